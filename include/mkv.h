@@ -1,0 +1,231 @@
+/*
+ * mkv.h — C ABI of libmuserve_kv.so, the MI355X (gfx950) KV-cache hot path.
+ *
+ * Every entry point takes caller-owned device pointers, sizes in elements or
+ * bytes, and a hipStream_t passed as `void*` (NULL = the default stream).
+ * Nothing here allocates device memory, synchronises, or throws: calls are
+ * asynchronous and return an int status (MKV_OK or a negative MKV_E_* code,
+ * with a message available from mkv_last_error() on the calling thread).
+ *
+ * Data-dependent faults that only the device can see (a slot or page id out of
+ * range, a sequence longer than its block table) never cause an out-of-bounds
+ * access: the kernel skips the offending row (writing zeros where it would
+ * have produced output) and ORs an MKV_DEVERR_* bit into the caller-owned
+ * int32 `err` word, which the caller reads at its next sync point.
+ *
+ * Layouts (all row-major, strides in BYTES unless named otherwise):
+ *   paged pool  [layers, 2, num_pages, 16, heads, head_dim]   (K plane, V plane)
+ *               — the reference layout of muserve/kv_cache.py:4-10,45-49; a
+ *               (layer, K|V) plane is an array of `num_pages*16` token rows.
+ *   fp8 scales  [layers, 2, num_pages, 16, heads] float32, one per (token, head).
+ *   block table [batch, table_width] int32 page ids, seq_lens [batch] int32.
+ *
+ * The names follow the reference's domain: a "page" is one 16-token block of
+ * the pool (muserve/kv_cache.py:77), a "slot" is page*16 + offset.
+ */
+#ifndef MUSERVE_KV_MKV_H
+#define MUSERVE_KV_MKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKV_ABI_VERSION 1
+#define MKV_PAGE_SIZE 16 /* muserve/config.py:36 KV_PAGE_SIZE */
+
+/* host-side status codes */
+#define MKV_OK 0
+#define MKV_E_INVALID -1   /* bad size / null pointer / negative count       */
+#define MKV_E_ALIGN -2     /* pointer or row size not 16-byte aligned        */
+#define MKV_E_UNSUPPORTED -3 /* shape outside what the kernels implement     */
+#define MKV_E_LAUNCH -4    /* the HIP runtime rejected the launch            */
+
+/* device error bits, OR-ed into the caller's int32 err word */
+#define MKV_DEVERR_SLOT 1        /* slot_mapping entry outside [-1, num_slots) */
+#define MKV_DEVERR_PAGE 2        /* block-table page id outside [0, num_pages) */
+#define MKV_DEVERR_TABLE 4       /* sequence needs more pages than the table holds */
+#define MKV_DEVERR_STATE_SLOT 8  /* state-pool slot outside [0, pool_slots)    */
+#define MKV_DEVERR_NEW_PAGE 16   /* decode step needed a page but none was given */
+
+/* ---- meta ------------------------------------------------------------- */
+
+/* ABI version (MKV_ABI_VERSION). No reference counterpart. */
+int mkv_version(void);
+
+/* Message of the last non-OK status returned on this thread ("" if none). */
+const char* mkv_last_error(void);
+
+/* ---- paged append / gather (bf16 or fp16 rows: plain byte copies) ------- */
+
+/*
+ * Slot-mapped append: for every layer l < num_layers and token t < num_tokens
+ * with s = slot_mapping[t] >= 0,
+ *   K-plane(l)[s] = k_src[l][t],  V-plane(l)[s] = v_src[l][t]
+ * where a row is `row_bytes` = heads*head_dim*elem bytes. slot = -1 skips the
+ * token; any other slot outside [0, num_slots) sets MKV_DEVERR_SLOT.
+ * Slots must be unique within one call (the reference's torch index_put_ with
+ * duplicate indices has no defined winner either).
+ *
+ * Replaces PagedKVCache.write_kv, muserve/kv_cache.py:102-112
+ * (cache[l,0,page,slot]=k; cache[l,1,page,slot]=v) with page/slot tensors
+ * folded into one int64 slot = page*16 + slot, and the decode-time
+ * torch.cat append of muserve/model/qwen35_layer_v2.py:485-492.
+ */
+int mkv_append_bf16(void* k_pool, void* v_pool, int64_t pool_layer_stride,
+                    int64_t num_slots, const void* k_src, const void* v_src,
+                    int64_t src_layer_stride, int64_t src_token_stride,
+                    const int64_t* slot_mapping, int64_t num_tokens,
+                    int32_t num_layers, int32_t row_bytes, int32_t* err,
+                    void* stream);
+
+/*
+ * Block-table gather into contiguous per-sequence rows. For layer l, sequence
+ * b and output row i < out_len, the source position is p = start_b + i
+ * (start_b = starts ? starts[b] : 0):
+ *   p <  seq_lens[b]:  out(l)[row(b,i)] = plane(l)[block_tables[b][p/16]*16 + p%16]
+ *   p >= seq_lens[b]:  padded mode (out_offsets == NULL): row is zero-filled;
+ *                      packed mode: row is not written.
+ * row(b,i) = b*out_len + i in padded mode ([batch, out_len, row] output, the
+ * [B,S,H,D] layout muserve/model/qwen35_model.py:223-249 hands to decode), or
+ * out_offsets[b] + i in packed mode (varlen [total, row] output).
+ * Output planes of consecutive layers are out_layer_stride bytes apart.
+ *
+ * Replaces SequenceKVState.to_page_table_tensor + the contiguous K/V that
+ * decode attention reads (muserve/kv_cache.py:149-158,
+ * muserve/model/qwen35_layer_v2.py:485-492).
+ */
+int mkv_gather_bf16(const void* k_pool, const void* v_pool,
+                    int64_t pool_layer_stride, int64_t num_pages,
+                    const int32_t* block_tables, int64_t table_stride,
+                    int32_t table_width, const int32_t* seq_lens,
+                    const int32_t* starts, int32_t batch, int64_t out_len,
+                    const int64_t* out_offsets, void* k_out, void* v_out,
+                    int64_t out_layer_stride, int32_t num_layers,
+                    int32_t row_bytes, int32_t* err, void* stream);
+
+/*
+ * Decode-step slot assignment for a batch, on the device. For b < batch:
+ *   len = seq_lens[b]; if len % 16 == 0 the sequence needs a page:
+ *     block_tables[b][len/16] = new_pages[b]   (MKV_DEVERR_NEW_PAGE if < 0)
+ *   slot_out[b] = block_tables[b][len/16]*16 + len%16;  seq_lens[b] = len + 1
+ * new_pages[b] is the page the host popped for sequence b (-1 when none is
+ * needed); the host pops them from the LIFO free list exactly as repeated
+ * PagedKVCache.alloc_pages(1) calls would (muserve/kv_cache.py:77-86, the
+ * per-token loop of muserve/scripts/test_kv_cache.py:88-92).
+ * Replaces SequenceKVState.needs_new_page/current_page/last_page_slot,
+ * muserve/kv_cache.py:133-147, for a whole batch in one launch.
+ */
+int mkv_decode_slots(int32_t* seq_lens, int32_t* block_tables,
+                     int64_t table_stride, int32_t table_width,
+                     const int32_t* new_pages, int32_t batch,
+                     int64_t num_pages, int64_t* slot_out, int32_t* err,
+                     void* stream);
+
+/* ---- fp8 e4m3fn quantize-on-append / dequant-gather --------------------- */
+
+/*
+ * Append with quantisation: each (token, head) row of head_dim bf16 values x
+ * becomes
+ *   scale = max(max_i |x_i|, 1e-12f) / 448.0f          (fp32, correctly rounded)
+ *   q_i   = e4m3fn_rne(clamp(x_i / scale, -448, 448))   (fp32 divide, RNE)
+ * written to the fp8 pool row at the slot, and scale to the scale plane. This
+ * is _fast_fp8_quantize(x, block_size=head_dim) of
+ * muserve/model/qwen35_layer_v2.py:71-86 applied to K and V separately.
+ * head_dim must be 256 (the Qwen3.5 attention head, muserve/config.py:9).
+ * Pool strides are in bytes; the scale planes are float arrays with
+ * `scale_layer_stride` bytes between layers.
+ */
+int mkv_append_fp8(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                   int64_t pool_layer_stride, int64_t scale_layer_stride,
+                   int64_t num_slots, const void* k_src, const void* v_src,
+                   int64_t src_layer_stride, int64_t src_token_stride,
+                   const int64_t* slot_mapping, int64_t num_tokens,
+                   int32_t num_layers, int32_t num_heads, int32_t head_dim,
+                   int32_t* err, void* stream);
+
+/*
+ * Dequant-gather: like mkv_gather_bf16 (same position/padding rules), with
+ * each output element bf16_rne(float(q) * scale) for its (token, head) scale.
+ * No reference counterpart (the reference keeps no fp8 KV); the formula is
+ * the inverse of _fast_fp8_quantize's scaling.
+ */
+int mkv_gather_dequant_fp8(const void* k_pool, const void* v_pool,
+                           const float* k_scale, const float* v_scale,
+                           int64_t pool_layer_stride,
+                           int64_t scale_layer_stride, int64_t num_pages,
+                           const int32_t* block_tables, int64_t table_stride,
+                           int32_t table_width, const int32_t* seq_lens,
+                           const int32_t* starts, int32_t batch,
+                           int64_t out_len, const int64_t* out_offsets,
+                           void* k_out, void* v_out, int64_t out_layer_stride,
+                           int32_t num_layers, int32_t num_heads,
+                           int32_t head_dim, int32_t* err, void* stream);
+
+/* ---- page copies (copy-on-write) ---------------------------------------- */
+
+/*
+ * For i < n and every plane q < num_planes:
+ *   plane(q)[dst_pages[i]] = plane(q)[src_pages[i]]   (page_bytes each)
+ * with plane(q) = pool + q*plane_stride. For the bf16 pool
+ * [L,2,P,16,H,D] pass num_planes = 2L, plane_stride = P*page_bytes; for the
+ * fp8 scales call again with their own plane geometry. Pages outside
+ * [0, num_pages) set MKV_DEVERR_PAGE. No reference counterpart: the reference
+ * has no copy-on-write; this is the copy a forked sequence needs before its
+ * first append into a shared partial page.
+ */
+int mkv_copy_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                    int64_t num_pages, int64_t page_bytes,
+                    const int32_t* src_pages, const int32_t* dst_pages,
+                    int32_t n, int32_t* err, void* stream);
+
+/* ---- GDN recurrent / conv state slot pools ------------------------------ */
+
+/*
+ * Slot gather: out[b] = pool[slots[b]] for b < n, each entry `entry_bytes`
+ * long, for up to two pools in one launch (pool1 may be NULL, e.g. the
+ * [8,128,128] fp32 recurrent state and the [2048,4] bf16 conv state of one
+ * GDN layer). Slots outside [0, pool_slots) set MKV_DEVERR_STATE_SLOT and
+ * their output is zero-filled. Replaces the per-request state lists the
+ * reference threads through forward_decode (muserve/model/qwen35_model.py:
+ * 94-126) and the .contiguous() of muserve/inference_loop.py:108.
+ */
+int mkv_state_gather(const void* pool0, int64_t entry_bytes0, void* out0,
+                     const void* pool1, int64_t entry_bytes1, void* out1,
+                     int64_t pool_slots, const int32_t* slots, int32_t n,
+                     int32_t* err, void* stream);
+
+/* Slot scatter: pool[slots[b]] = in[b]; the inverse of mkv_state_gather.
+ * Slots must be unique within one call. */
+int mkv_state_scatter(void* pool0, int64_t entry_bytes0, const void* in0,
+                      void* pool1, int64_t entry_bytes1, const void* in1,
+                      int64_t pool_slots, const int32_t* slots, int32_t n,
+                      int32_t* err, void* stream);
+
+/* ---- prefix hashing ------------------------------------------------------ */
+
+/*
+ * Per-page prefix hashes. Request r owns the token bytes
+ * tokens[tok_offsets[r]*token_bytes, tok_offsets[r+1]*token_bytes); for every
+ * full 16-token page i of it,
+ *   out[page_offsets[r] + i] = first 8 bytes, big-endian, of
+ *                              SHA-256(its first 16*(i+1) tokens)
+ * which is int(PrefixCache._hash_tokens(ids[:16*(i+1)]), 16) of
+ * muserve/model/prefix_cache.py:31-34 (sha256 of the ids' little-endian
+ * bytes, hexdigest()[:16]). token_bytes is 8 (int64 ids) or 4 (int32).
+ * page_offsets[r+1]-page_offsets[r] must equal the request's full-page count
+ * (floor(tokens/16)); a request where it does not is skipped and sets
+ * MKV_DEVERR_TABLE. One lane walks one request's chain, so a launch should
+ * carry many requests: a single long prefix is faster on a CPU core.
+ */
+int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
+                          const int64_t* page_offsets, int32_t num_requests,
+                          int32_t token_bytes, uint64_t* out, int32_t* err,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUSERVE_KV_MKV_H */

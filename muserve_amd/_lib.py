@@ -1,0 +1,155 @@
+"""ctypes binding of libmuserve_kv.so (C ABI in include/mkv.h).
+
+The library is loaded after torch, so its HIP runtime references bind to the
+runtime torch already mapped: a hipStream_t from torch and a device pointer
+from a torch tensor mean the same thing on both sides of the boundary.
+
+Every wrapper here launches asynchronously on the current torch stream of the
+tensors' device. Data-dependent faults are reported through a per-owner int32
+device word (``DeviceErrors``) that callers check at their sync points.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmuserve_kv.so")
+ABI_VERSION = 1
+
+# device error bits (include/mkv.h)
+DEVERR_SLOT = 1
+DEVERR_PAGE = 2
+DEVERR_TABLE = 4
+DEVERR_STATE_SLOT = 8
+DEVERR_NEW_PAGE = 16
+_DEVERR_TEXT = {
+    DEVERR_SLOT: "slot_mapping entry out of range",
+    DEVERR_PAGE: "page id out of range",
+    DEVERR_TABLE: "sequence longer than its block table (or inconsistent offsets)",
+    DEVERR_STATE_SLOT: "state-pool slot out of range",
+    DEVERR_NEW_PAGE: "decode step needed a new page but none was supplied",
+}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+
+# name -> argtypes, in the order of include/mkv.h
+SIGNATURES: dict[str, list] = {
+    "mkv_version": [],
+    "mkv_last_error": [],
+    "mkv_append_bf16": [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I32, _I32, _P, _P],
+    "mkv_gather_bf16": [_P, _P, _I64, _I64, _P, _I64, _I32, _P, _P, _I32, _I64, _P, _P, _P,
+                        _I64, _I32, _I32, _P, _P],
+    "mkv_decode_slots": [_P, _P, _I64, _I32, _P, _I32, _I64, _P, _P, _P],
+    "mkv_append_fp8": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I32,
+                       _I32, _I32, _P, _P],
+    "mkv_gather_dequant_fp8": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I32,
+                               _I64, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _P],
+    "mkv_copy_blocks": [_P, _I64, _I32, _I64, _I64, _P, _P, _I32, _P, _P],
+    "mkv_state_gather": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
+    "mkv_state_scatter": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
+    "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class MkvError(RuntimeError):
+    """A libmuserve_kv entry point returned a non-OK status."""
+
+
+class MkvDeviceError(RuntimeError):
+    """A kernel flagged a data-dependent fault in its device error word."""
+
+
+def _hip_runtimes() -> list[str]:
+    try:
+        with open("/proc/self/maps") as f:
+            return sorted({ln.split()[-1] for ln in f if "libamdhip64" in ln})
+    except OSError:
+        return []
+
+
+def load() -> ctypes.CDLL:
+    """Loads (once) and returns the library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH.name} is not built ({LIB_PATH}); build it with "
+                "`python -m muserve_amd.build` — there is no fallback path")
+        torch.zeros(1)  # make sure torch's HIP runtime is mapped before ours resolves
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name == "mkv_last_error" else ctypes.c_int
+        if lib.mkv_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH.name} ABI {lib.mkv_version()} != expected {ABI_VERSION}")
+        runtimes = _hip_runtimes()
+        if len(runtimes) > 1:
+            raise RuntimeError(f"two HIP runtimes are mapped ({runtimes}); load torch first")
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> None:
+    """Calls an entry point and raises MkvError on a non-OK status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.mkv_last_error().decode(errors="replace")
+        raise MkvError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one ROCm device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"muserve_amd kernels run on a ROCm GPU only; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise RuntimeError("no device tensor given")
+    return dev
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class DeviceErrors:
+    """An int32 device word the kernels OR fault bits into."""
+
+    def __init__(self, device: torch.device):
+        self.word = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def ptr(self) -> int:
+        return self.word.data_ptr()
+
+    def check(self, what: str = "kernel") -> None:
+        """Synchronises with the word's stream; raises and clears on any fault."""
+        bits = int(self.word.item())
+        if bits:
+            self.word.zero_()
+            text = "; ".join(t for b, t in _DEVERR_TEXT.items() if bits & b) or f"bits {bits:#x}"
+            raise MkvDeviceError(f"{what}: device fault: {text}")

@@ -1,0 +1,299 @@
+// mkv_paged.hip — paged-pool append, block-table gather, decode-step slot
+// assignment and page copies for gfx950.
+//
+// The pool keeps the reference layout [L, 2, P, 16, H, D]
+// (muserve/kv_cache.py:45-49): one (layer, K|V) plane is an array of P*16
+// token rows, and a page is 16 consecutive rows (8 KiB for one bf16 head of
+// 256). Every kernel here is a pure byte mover, so the design goal is HBM
+// streaming efficiency: 16-byte vector accesses, consecutive lanes on
+// consecutive addresses, all loads of a thread issued before its stores, and
+// non-temporal hints on data that is not re-read within the step.
+#include "mkv_device.h"
+
+namespace mkv {
+namespace {
+
+// ---------------------------------------------------------------------------
+// append: one thread per 16-byte chunk of a (layer, K|V, token) row.
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  uint8_t* k_pool;
+  uint8_t* v_pool;
+  int64_t pool_layer_stride;
+  int64_t num_slots;
+  const uint8_t* k_src;
+  const uint8_t* v_src;
+  int64_t src_layer_stride;
+  int64_t src_token_stride;
+  const int64_t* slots;
+  uint32_t num_tokens;
+  uint32_t row_chunks;
+  int32_t* err;
+};
+
+__global__ __launch_bounds__(kThreads) void append_rows_kernel(AppendArgs a) {
+  const uint32_t g = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t t = g / a.row_chunks;
+  if (t >= a.num_tokens) return;
+  const uint32_t col = g - t * a.row_chunks;
+  const uint32_t lkv = blockIdx.y;  // layer*2 + (0: K, 1: V)
+  const uint32_t l = lkv >> 1;
+  const bool is_v = lkv & 1u;
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.num_slots) {
+    if (slot != -1 && col == 0 && !is_v) raise_err(a.err, MKV_DEVERR_SLOT);
+    return;
+  }
+  const int64_t row_bytes = (int64_t)a.row_chunks * 16;
+  const uint8_t* src = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride +
+                       (int64_t)t * a.src_token_stride + (int64_t)col * 16;
+  uint8_t* dst = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride +
+                 slot * row_bytes + (int64_t)col * 16;
+  st16(dst, ld16(src));
+}
+
+// ---------------------------------------------------------------------------
+// gather: a workgroup moves ROWS consecutive output rows of one
+// (layer, K|V, sequence); each thread issues its CPT 16-byte loads (zero for
+// padding rows, no load at all) before any of its stores.
+// ---------------------------------------------------------------------------
+template <int ROW_BYTES, int ROWS>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(GatherArgs a) {
+  constexpr int RC = ROW_BYTES / 16;         // 16-byte chunks per row
+  constexpr int RSTEP = kThreads / RC;       // rows between a thread's chunks
+  constexpr int CPT = ROWS * RC / kThreads;  // chunks per thread
+  static_assert(RC * RSTEP == kThreads && CPT * kThreads == ROWS * RC, "tile shape");
+  const int col = threadIdx.x % RC;
+  const int rsub = threadIdx.x / RC;
+  const bool packed = a.out_offsets != nullptr;
+
+  for (uint64_t tile_id = blockIdx.x; tile_id < a.total_tiles; tile_id += gridDim.x) {
+    GatherTile<ROWS> t;
+    t.init(a, tile_id);
+    if (t.skip) continue;
+    const uint32_t l = t.lkv >> 1;
+    const bool is_v = t.lkv & 1u;
+    const uint8_t* plane = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
+    uint8_t* out = (is_v ? a.v_out : a.k_out) + (int64_t)l * a.out_layer_stride +
+                   t.out_row * ROW_BYTES + col * 16;
+
+    // Fast paths are branch-free between the loads and the stores, so the
+    // waitcnt pass can let the four stores overlap; a per-row guard would
+    // serialise them (vmcnt counts stores as well as loads).
+    u32x4 v[CPT];
+    if (t.full_data()) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int64_t p = t.p0 + rsub + i * RSTEP;
+        v[i] = ld_nt(plane + ((int64_t)t.page_of(p) * 16 + (p & 15)) * ROW_BYTES + col * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, v[i]);
+      continue;
+    }
+    if (t.full_pad(a.out_len)) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i)
+        st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, u32x4{0u, 0u, 0u, 0u});
+      continue;
+    }
+    // Boundary tile: per-row guards.
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int r = rsub + i * RSTEP;
+      v[i] = u32x4{0u, 0u, 0u, 0u};
+      if (t.row0 + r < t.nvalid) {
+        const int64_t p = t.p0 + r;
+        const int32_t page = t.page_of(p);
+        if (page >= 0)
+          v[i] = ld_nt(plane + ((int64_t)page * 16 + (p & 15)) * ROW_BYTES + col * 16);
+      }
+    }
+    const int64_t row_limit = packed ? t.nvalid : a.out_len;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int r = rsub + i * RSTEP;
+      if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * ROW_BYTES, v[i]);
+    }
+  }
+}
+
+template <int ROW_BYTES, int ROWS>
+int launch_gather(GatherArgs a, int32_t num_layers, hipStream_t stream) {
+  a.tiles_per_seq = (uint32_t)((a.out_len + ROWS - 1) / ROWS);
+  a.total_tiles = (uint64_t)num_layers * 2u * a.batch * a.tiles_per_seq;
+  if (a.total_tiles == 0) return MKV_OK;
+  const uint64_t wgs = a.total_tiles < kMaxGridWgs ? a.total_tiles : kMaxGridWgs;
+  hipLaunchKernelGGL((gather_rows_kernel<ROW_BYTES, ROWS>), dim3((unsigned)wgs), dim3(kThreads),
+                     0, stream, a);
+  return check_launch("mkv_gather_bf16");
+}
+
+// ---------------------------------------------------------------------------
+// decode-step slot assignment, one thread per sequence.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void decode_slots_kernel(
+    int32_t* seq_lens, int32_t* bt, int64_t stride, int32_t width, const int32_t* new_pages,
+    int32_t batch, int64_t num_pages, int64_t* slot_out, int32_t* err) {
+  const int b = blockIdx.x * kThreads + threadIdx.x;
+  if (b >= batch) return;
+  const int32_t len = seq_lens[b];
+  const int32_t j = len >> 4, off = len & 15;
+  if (len < 0 || j >= width) {
+    raise_err(err, MKV_DEVERR_TABLE);
+    slot_out[b] = -1;
+    return;
+  }
+  int32_t page;
+  if (off == 0) {
+    page = new_pages[b];
+    if (page < 0 || page >= num_pages) {
+      raise_err(err, page < 0 ? MKV_DEVERR_NEW_PAGE : MKV_DEVERR_PAGE);
+      slot_out[b] = -1;
+      return;
+    }
+    bt[(int64_t)b * stride + j] = page;
+  } else {
+    page = bt[(int64_t)b * stride + j];
+    if (page < 0 || page >= num_pages) {
+      raise_err(err, MKV_DEVERR_PAGE);
+      slot_out[b] = -1;
+      return;
+    }
+  }
+  slot_out[b] = (int64_t)page * 16 + off;
+  seq_lens[b] = len + 1;
+}
+
+// ---------------------------------------------------------------------------
+// page copies: one workgroup per (pair, plane).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void copy_pages_kernel(
+    uint8_t* pool, int64_t plane_stride, int32_t num_planes, int64_t num_pages,
+    int64_t page_bytes, const int32_t* src, const int32_t* dst, int32_t* err) {
+  const int32_t i = blockIdx.x / num_planes;
+  const int32_t q = blockIdx.x - i * num_planes;
+  const int32_t s = src[i], d = dst[i];
+  if (s < 0 || s >= num_pages || d < 0 || d >= num_pages) {
+    if (threadIdx.x == 0 && q == 0) raise_err(err, MKV_DEVERR_PAGE);
+    return;
+  }
+  const uint8_t* sp = pool + q * plane_stride + (int64_t)s * page_bytes;
+  uint8_t* dp = pool + q * plane_stride + (int64_t)d * page_bytes;
+  const int64_t chunks = page_bytes / 16;
+  constexpr int U = 4;
+  for (int64_t c0 = threadIdx.x; c0 < chunks; c0 += (int64_t)kThreads * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + (int64_t)u * kThreads;
+      if (c < chunks) v[u] = ld16(sp + c * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + (int64_t)u * kThreads;
+      if (c < chunks) st16(dp + c * 16, v[u]);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace mkv
+
+using namespace mkv;
+
+extern "C" int mkv_append_bf16(void* k_pool, void* v_pool, int64_t pool_layer_stride,
+                               int64_t num_slots, const void* k_src, const void* v_src,
+                               int64_t src_layer_stride, int64_t src_token_stride,
+                               const int64_t* slot_mapping, int64_t num_tokens,
+                               int32_t num_layers, int32_t row_bytes, int32_t* err,
+                               void* stream) {
+  clear_error();
+  MKV_REQUIRE(num_tokens >= 0 && num_layers >= 0 && num_slots >= 0, MKV_E_INVALID,
+              "mkv_append_bf16: negative size");
+  if (num_tokens == 0 || num_layers == 0) return MKV_OK;
+  MKV_REQUIRE(k_pool && v_pool && k_src && v_src && slot_mapping && err, MKV_E_INVALID,
+              "mkv_append_bf16: null pointer");
+  MKV_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0, MKV_E_ALIGN,
+              "mkv_append_bf16: row_bytes %d is not a positive multiple of 16", row_bytes);
+  MKV_REQUIRE(aligned16(k_pool) && aligned16(v_pool) && aligned16(k_src) && aligned16(v_src) &&
+                  pool_layer_stride % 16 == 0 && src_layer_stride % 16 == 0 &&
+                  src_token_stride % 16 == 0,
+              MKV_E_ALIGN, "mkv_append_bf16: pointers and strides must be 16-byte aligned");
+  const uint64_t chunks = (uint64_t)num_tokens * (uint64_t)(row_bytes / 16);
+  MKV_REQUIRE(chunks < (1ull << 31) && num_layers <= 32767, MKV_E_UNSUPPORTED,
+              "mkv_append_bf16: %lld tokens x %d-byte rows x %d layers is too large for one call",
+              (long long)num_tokens, row_bytes, num_layers);
+  AppendArgs a{(uint8_t*)k_pool, (uint8_t*)v_pool, pool_layer_stride, num_slots,
+               (const uint8_t*)k_src, (const uint8_t*)v_src, src_layer_stride, src_token_stride,
+               slot_mapping, (uint32_t)num_tokens, (uint32_t)(row_bytes / 16), err};
+  dim3 grid((unsigned)((chunks + kThreads - 1) / kThreads), (unsigned)(2 * num_layers));
+  hipLaunchKernelGGL(append_rows_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+  return check_launch("mkv_append_bf16");
+}
+
+extern "C" int mkv_gather_bf16(const void* k_pool, const void* v_pool, int64_t pool_layer_stride,
+                               int64_t num_pages, const int32_t* block_tables,
+                               int64_t table_stride, int32_t table_width,
+                               const int32_t* seq_lens, const int32_t* starts, int32_t batch,
+                               int64_t out_len, const int64_t* out_offsets, void* k_out,
+                               void* v_out, int64_t out_layer_stride, int32_t num_layers,
+                               int32_t row_bytes, int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(batch >= 0 && out_len >= 0 && num_layers >= 0 && num_pages >= 0 &&
+                  table_width >= 0,
+              MKV_E_INVALID, "mkv_gather_bf16: negative size");
+  if (batch == 0 || out_len == 0 || num_layers == 0) return MKV_OK;
+  GatherArgs a;
+  const int rc = fill_gather_args(a, "mkv_gather_bf16", k_pool, v_pool, pool_layer_stride,
+                                  num_pages, block_tables, table_stride, table_width, seq_lens,
+                                  starts, batch, out_len, out_offsets, k_out, v_out,
+                                  out_layer_stride, err);
+  if (rc != MKV_OK) return rc;
+  hipStream_t s = as_stream(stream);
+  switch (row_bytes) {
+    case 128: return launch_gather<128, 64>(a, num_layers, s);
+    case 256: return launch_gather<256, 64>(a, num_layers, s);
+    case 512: return launch_gather<512, 32>(a, num_layers, s);
+    case 1024: return launch_gather<1024, 16>(a, num_layers, s);
+    case 2048: return launch_gather<2048, 16>(a, num_layers, s);
+    default:
+      return set_error(MKV_E_UNSUPPORTED,
+                       "mkv_gather_bf16: row_bytes %d not in {128,256,512,1024,2048}", row_bytes);
+  }
+}
+
+extern "C" int mkv_decode_slots(int32_t* seq_lens, int32_t* block_tables, int64_t table_stride,
+                                int32_t table_width, const int32_t* new_pages, int32_t batch,
+                                int64_t num_pages, int64_t* slot_out, int32_t* err,
+                                void* stream) {
+  clear_error();
+  MKV_REQUIRE(batch >= 0 && table_width >= 0, MKV_E_INVALID, "mkv_decode_slots: negative size");
+  if (batch == 0) return MKV_OK;
+  MKV_REQUIRE(seq_lens && block_tables && new_pages && slot_out && err, MKV_E_INVALID,
+              "mkv_decode_slots: null pointer");
+  hipLaunchKernelGGL(decode_slots_kernel, dim3((batch + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, as_stream(stream), seq_lens, block_tables, table_stride,
+                     table_width, new_pages, batch, num_pages, slot_out, err);
+  return check_launch("mkv_decode_slots");
+}
+
+extern "C" int mkv_copy_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                               int64_t num_pages, int64_t page_bytes, const int32_t* src_pages,
+                               const int32_t* dst_pages, int32_t n, int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(n >= 0 && num_planes >= 0 && num_pages >= 0, MKV_E_INVALID,
+              "mkv_copy_blocks: negative size");
+  if (n == 0 || num_planes == 0) return MKV_OK;
+  MKV_REQUIRE(pool && src_pages && dst_pages && err, MKV_E_INVALID,
+              "mkv_copy_blocks: null pointer");
+  MKV_REQUIRE(aligned16(pool) && plane_stride % 16 == 0 && page_bytes > 0 && page_bytes % 16 == 0,
+              MKV_E_ALIGN,
+              "mkv_copy_blocks: pool, plane stride and page bytes must be 16-byte aligned");
+  MKV_REQUIRE((int64_t)n * num_planes < (1ll << 31), MKV_E_UNSUPPORTED,
+              "mkv_copy_blocks: too many pages for one call");
+  hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)(n * num_planes)), dim3(kThreads), 0,
+                     as_stream(stream), (uint8_t*)pool, plane_stride, num_planes, num_pages,
+                     page_bytes, src_pages, dst_pages, err);
+  return check_launch("mkv_copy_blocks");
+}

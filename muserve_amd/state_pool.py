@@ -1,0 +1,119 @@
+"""Slot pool for GDN linear-attention states (recurrent + conv), per rank.
+
+The reference threads GDN states through the model as per-request,
+per-layer tensors (muserve/model/qwen35_model.py:28-49,94-126; the
+``.contiguous()`` of muserve/inference_loop.py:108). For continuous batching
+this module keeps them resident in two pools indexed by a request slot:
+
+* recurrent ``state[L_gdn, num_slots, v_heads, v_dim, k_dim]`` fp32 — the
+  "VK" layout the decode kernel reads (muserve/model/qwen35_layer_v2.py:293),
+  8 heads x 128 x 128 per rank = 512 KiB per (layer, slot);
+* conv ``conv[L_gdn, num_slots, channels, width]`` bf16 (2048 x 4 = 16 KiB).
+
+``gather(layer, slots)`` copies a batch's entries into contiguous buffers and
+``scatter`` writes updated entries back, both layer's pools in one launch.
+Slot ids within a ``scatter`` must be unique.
+"""
+from __future__ import annotations
+
+import torch
+
+from muserve_amd import _lib
+from muserve_amd.config import GDN_CONV_KERNEL, GDN_KEY_DIM, GDN_VALUE_DIM
+
+GDN_V_HEADS_PER_RANK = 8   # 64 value heads / TP 8 (muserve/model/qwen35_layer_v2.py:46-47)
+CONV_CHANNELS_PER_RANK = 2048
+
+
+def gdn_ordinal(layer_idx: int) -> int:
+    """Index of a GDN layer among the 45 GDN layers of the 60-layer stack
+    (attention layers are those with layer % 4 == 3)."""
+    if layer_idx % 4 == 3:
+        raise ValueError(f"layer {layer_idx} is an attention layer")
+    return layer_idx - (layer_idx + 1) // 4
+
+
+class StatePool:
+    def __init__(self, num_layers: int = 45, num_slots: int = 1024,
+                 state_shape: tuple[int, ...] = (GDN_V_HEADS_PER_RANK, GDN_VALUE_DIM, GDN_KEY_DIM),
+                 state_dtype: torch.dtype = torch.float32,
+                 conv_shape: tuple[int, ...] | None = (CONV_CHANNELS_PER_RANK, GDN_CONV_KERNEL),
+                 conv_dtype: torch.dtype = torch.bfloat16, device: torch.device | str = "cuda"):
+        self.device = torch.device(device)
+        self.num_layers = num_layers
+        self.num_slots = num_slots
+        self.state = torch.zeros(num_layers, num_slots, *state_shape, dtype=state_dtype,
+                                 device=self.device)
+        self.conv = (torch.zeros(num_layers, num_slots, *conv_shape, dtype=conv_dtype,
+                                 device=self.device) if conv_shape is not None else None)
+        self._free = list(range(num_slots))
+        self._errors = _lib.DeviceErrors(self.device) if self.device.type == "cuda" else None
+
+    # slot bookkeeping: a LIFO stack, like the KV page free list
+    def alloc_slot(self) -> int:
+        if not self._free:
+            raise RuntimeError(f"state pool full: all {self.num_slots} slots in use")
+        return self._free.pop()
+
+    def free_slot(self, slot: int) -> None:
+        self._free.append(slot)
+
+    @property
+    def num_free_slots(self) -> int:
+        return len(self._free)
+
+    def _entry_bytes(self, t: torch.Tensor) -> int:
+        return t[0, 0].numel() * t.element_size()
+
+    def _check(self, slots: torch.Tensor) -> torch.Tensor:
+        if self.device.type != "cuda":
+            raise RuntimeError(f"StatePool on {self.device}: the slot kernels need a ROCm GPU")
+        if slots.dtype != torch.int32 or slots.device != self.device:
+            slots = slots.to(device=self.device, dtype=torch.int32)
+        return slots.contiguous()
+
+    def gather(self, layer: int, slots: torch.Tensor,
+               out: tuple[torch.Tensor, torch.Tensor | None] | None = None):
+        """(state[layer, slots], conv[layer, slots]) as contiguous [n, ...] buffers."""
+        slots = self._check(slots)
+        n = slots.numel()
+        if out is None:
+            st = torch.empty((n, *self.state.shape[2:]), dtype=self.state.dtype, device=self.device)
+            cv = (torch.empty((n, *self.conv.shape[2:]), dtype=self.conv.dtype, device=self.device)
+                  if self.conv is not None else None)
+        else:
+            st, cv = out
+        self._move("mkv_state_gather", layer, slots, st, cv)
+        return st, cv
+
+    def scatter(self, layer: int, slots: torch.Tensor, state: torch.Tensor,
+                conv: torch.Tensor | None = None) -> None:
+        """state[layer, slots] = state; conv[layer, slots] = conv (unique slots)."""
+        slots = self._check(slots)
+        self._move("mkv_state_scatter", layer, slots, state, conv)
+
+    def _move(self, fn: str, layer: int, slots: torch.Tensor, st: torch.Tensor,
+              cv: torch.Tensor | None) -> None:
+        n = slots.numel()
+        if not 0 <= layer < self.num_layers:
+            raise IndexError(f"GDN layer {layer} out of range (pool has {self.num_layers})")
+        if st.dtype != self.state.dtype or st.numel() != n * self.state[0, 0].numel():
+            raise ValueError("state buffer has the wrong dtype or size")
+        if not st.is_contiguous():
+            raise ValueError("state buffer must be contiguous")
+        use_conv = self.conv is not None and cv is not None
+        if use_conv and (cv.dtype != self.conv.dtype or cv.numel() != n * self.conv[0, 0].numel()
+                         or not cv.is_contiguous()):
+            raise ValueError("conv buffer has the wrong dtype, size or layout")
+        _lib.require_gpu(slots, st, self.state, *((cv,) if use_conv else ()))
+        if n == 0:
+            return
+        _lib.call(fn, self.state[layer].data_ptr(), self._entry_bytes(self.state), st.data_ptr(),
+                  self.conv[layer].data_ptr() if use_conv else None,
+                  self._entry_bytes(self.conv) if use_conv else 0,
+                  cv.data_ptr() if use_conv else None, self.num_slots, slots.data_ptr(), n,
+                  self._errors.ptr(), _lib.stream_of(self.device))
+
+    def check_errors(self) -> None:
+        if self._errors is not None:
+            self._errors.check("StatePool")
