@@ -198,7 +198,7 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
         "useful_GBps_without_padding_writes": round(useful / elapsed / 1e9, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "gather_rows_kernel<512,32> (mkv_gather_bf16)",
+            "kernel": "mkv_gather_bf16 = gather_pad_kernel<512> + gather_data_kernel<512>",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -53,8 +53,6 @@ struct GatherArgs {
   uint8_t* k_out;
   uint8_t* v_out;
   int64_t out_layer_stride;
-  uint32_t tiles_per_seq;
-  uint64_t total_tiles;
   int32_t* err;
 };
 
@@ -66,44 +64,56 @@ __device__ __forceinline__ int32_t pick_page(const int32_t (&pg)[NP], int j) {
   return r;
 }
 
-// One gather tile = ROWS consecutive output rows of one (layer, K|V,
-// sequence). Everything here depends only on the tile id and on scalar loads,
-// so it stays in scalar registers; pg[] holds the (at most NP) page ids the
-// tile's valid rows live in, -1 where a row must be zero.
+// Tile geometry of the two-kernel gather. A tile is ROWS consecutive output
+// rows (4 KiB of output) of one (layer, K|V, sequence); the grid is
+// (tile, sequence, layer*2 + K|V), so nothing is decoded by division.
+//
+// Output rows of a sequence split at data_end = min(roundup(nvalid, ROWS),
+// out_len): tiles below it belong to the data kernel (which also zero-fills
+// the padding rows of the last, partial tile), tiles at or above it to the
+// padding kernel. Both kernels use the same ROWS, so each row is written once.
 template <int ROWS>
 struct GatherTile {
-  static constexpr int NP = (ROWS + 14) / 16 + 1;
-  uint32_t lkv, b;
-  int64_t row0, nvalid, p0, first_page, out_row;
-  bool skip;
-  bool pages_ok;  // every page a valid row needs resolved to a real page id
+  static constexpr int NP = (ROWS + 14) / 16 + 1;  // pages ROWS rows can span
+  uint32_t b, layer;
+  bool is_v;
+  int64_t row0, nvalid, data_end, p0, first_page, out_row;
+  bool pages_ok;
   int32_t pg[NP];
 
-  __device__ __forceinline__ void init(const GatherArgs& a, uint64_t tile_id) {
-    const uint32_t tile = (uint32_t)(tile_id % a.tiles_per_seq);
-    const uint64_t rest = tile_id / a.tiles_per_seq;
-    b = (uint32_t)(rest % a.batch);
-    lkv = (uint32_t)(rest / a.batch);
-    const bool packed = a.out_offsets != nullptr;
+  // Sequence window (what the padding kernel needs): one or two scalar loads.
+  __device__ __forceinline__ void init(const GatherArgs& a) {
+    b = blockIdx.y;
+    layer = blockIdx.z >> 1;
+    is_v = blockIdx.z & 1u;
+    row0 = (int64_t)blockIdx.x * ROWS;
     const int64_t len = ld_const(a.seq_lens + b);
     int64_t start = a.starts ? (int64_t)ld_const(a.starts + b) : 0;
-    const int64_t out_base = packed ? ld_const(a.out_offsets + b) : (int64_t)b * a.out_len;
     nvalid = len - start;
     nvalid = nvalid < 0 ? 0 : (nvalid > a.out_len ? a.out_len : nvalid);
-    if (start < 0) {  // malformed window: emit padding only, never a negative page
+    if (start < 0) {  // malformed window: padding only, never a negative page
       nvalid = 0;
       start = 0;
     }
-    row0 = (int64_t)tile * ROWS;
-    skip = packed && row0 >= nvalid;
-    out_row = out_base + row0;
+    const int64_t up = (nvalid + ROWS - 1) / ROWS * ROWS;
+    data_end = up < a.out_len ? up : a.out_len;
     p0 = start + row0;
     first_page = p0 >> 4;
-    const int64_t end_pos = start + nvalid;  // one past the last valid position
-    // Issue every page-id load before inspecting any: the index is clamped
-    // into the table row so an unneeded load stays in bounds.
+  }
+
+  // Output row of this tile's first row (padded or packed layout).
+  __device__ __forceinline__ void locate(const GatherArgs& a) {
+    out_row = (a.out_offsets ? ld_const(a.out_offsets + b) : (int64_t)b * a.out_len) + row0;
+  }
+
+  // Page ids of the tile's valid rows (data kernel). All loads are issued
+  // before any is inspected; the index is clamped into the table row so an
+  // unneeded load stays in bounds. Bad ids become -1 (zero rows) and are
+  // reported through the error word.
+  __device__ __forceinline__ void load_pages(const GatherArgs& a) {
     const int32_t* row = a.block_tables + (int64_t)b * a.table_stride;
     const int64_t wmax = a.table_width > 0 ? a.table_width - 1 : 0;
+    const int64_t end_pos = p0 - row0 + nvalid;  // one past the last valid position
     int32_t raw[NP];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
@@ -115,7 +125,7 @@ struct GatherTile {
     for (int j = 0; j < NP; ++j) {
       const int64_t pj = first_page + j;
       int32_t page = -1;
-      if (!skip && pj * 16 < end_pos) {
+      if (pj * 16 < end_pos) {
         if (pj >= a.table_width) {
           bad |= MKV_DEVERR_TABLE;
         } else if (raw[j] < 0 || raw[j] >= a.num_pages) {
@@ -130,21 +140,39 @@ struct GatherTile {
     if (bad && threadIdx.x == 0) raise_err(a.err, bad);
   }
 
-  // All ROWS rows hold data from valid pages: straight-line loads and stores.
-  __device__ __forceinline__ bool full_data() const { return row0 + ROWS <= nvalid && pages_ok; }
-  // All ROWS rows are padding inside the output: straight-line zero stores.
-  __device__ __forceinline__ bool full_pad(int64_t out_len) const {
-    return row0 >= nvalid && row0 + ROWS <= out_len;
-  }
-
-  // Page of output row r of this tile (valid rows only).
   __device__ __forceinline__ int32_t page_of(int64_t p) const {
     return pick_page(pg, (int)((p >> 4) - first_page));
   }
+  __device__ __forceinline__ bool full_data() const { return row0 + ROWS <= nvalid && pages_ok; }
 };
 
-// Largest grid a gather launches; bigger jobs loop over tiles inside it.
-constexpr uint64_t kMaxGridWgs = 1u << 22;
+// Threads of the padding kernel (one 16-byte store each) and of the data
+// kernels (two 16-byte chunks each); both cover 4 KiB of output per tile.
+constexpr int kPadThreads = 256;
+constexpr int kDataThreads = 128;
+constexpr int kTileBytes = kPadThreads * 16;
+
+// Zero-fills the padding tiles of a padded gather: rows >= data_end of every
+// (layer, K|V, sequence). Write-only and register-light so that it streams
+// at the HBM write rate.
+template <int ROW_BYTES>
+__global__ __launch_bounds__(kPadThreads) void gather_pad_kernel(GatherArgs a) {
+  constexpr int ROWS = kTileBytes / ROW_BYTES;
+  constexpr int RC = ROW_BYTES / 16;
+  GatherTile<ROWS> t;
+  t.init(a);
+  if (t.row0 < t.data_end) return;  // a data tile
+  const int r = threadIdx.x / RC;
+  if (t.row0 + r >= a.out_len) return;
+  uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
+                 ((int64_t)t.b * a.out_len + t.row0 + r) * ROW_BYTES + (threadIdx.x % RC) * 16;
+  st_nt(out, u32x4{0u, 0u, 0u, 0u});
+}
+
+// Grid of a gather kernel with ROWS-row tiles; 0 tiles when nothing to do.
+inline dim3 gather_grid(const GatherArgs& a, int rows, int32_t num_layers) {
+  return dim3((unsigned)((a.out_len + rows - 1) / rows), a.batch, (unsigned)(2 * num_layers));
+}
 
 // Fills the argument block common to mkv_gather_bf16 and mkv_gather_dequant_fp8.
 inline int fill_gather_args(GatherArgs& a, const char* fn, const void* k_pool, const void* v_pool,
@@ -158,7 +186,8 @@ inline int fill_gather_args(GatherArgs& a, const char* fn, const void* k_pool, c
   if (!(aligned16(k_pool) && aligned16(v_pool) && aligned16(k_out) && aligned16(v_out) &&
         pool_layer_stride % 16 == 0 && out_layer_stride % 16 == 0))
     return set_error(MKV_E_ALIGN, "%s: pointers and strides must be 16-byte aligned", fn);
-  if (out_len >= (1ll << 40)) return set_error(MKV_E_UNSUPPORTED, "%s: out_len too large", fn);
+  if (out_len >= (1ll << 31)) return set_error(MKV_E_UNSUPPORTED, "%s: out_len too large", fn);
+  if (batch > 65535) return set_error(MKV_E_UNSUPPORTED, "%s: batch %d > 65535", fn, batch);
   a = GatherArgs{};
   a.k_pool = (const uint8_t*)k_pool;
   a.v_pool = (const uint8_t*)v_pool;

@@ -104,88 +104,85 @@ __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// dequant-gather: the bf16 gather's tile walk with fp8 rows in and bf16 rows
-// out. A thread turns 8 fp8 bytes and its head's scale into 16 output bytes.
+// dequant-gather: the bf16 gather's tiles with fp8 rows in and bf16 rows out
+// (the padding tiles go to the shared gather_pad_kernel). A thread turns 8
+// fp8 bytes and its head's scale into 16 output bytes.
 // ---------------------------------------------------------------------------
-template <int HEADS, int ROWS>
-__global__ __launch_bounds__(kThreads) void gather_dequant_kernel(GatherArgs a) {
+template <int HEADS>
+__global__ __launch_bounds__(kDataThreads) void gather_dequant_kernel(GatherArgs a) {
   constexpr int OUT_ROW = HEADS * kHeadDim * 2;  // bf16 bytes per output row
   constexpr int IN_ROW = HEADS * kHeadDim;       // fp8 bytes per pool row
+  constexpr int ROWS = kTileBytes / OUT_ROW;
   constexpr int RC = OUT_ROW / 16;               // output chunks per row
-  constexpr int RSTEP = kThreads / RC;
-  constexpr int CPT = ROWS * RC / kThreads;
-  static_assert(RC * RSTEP == kThreads && CPT * kThreads == ROWS * RC, "tile shape");
+  constexpr int RSTEP = kDataThreads / RC;
+  constexpr int CPT = ROWS * RC / kDataThreads;
+  static_assert(RC * RSTEP == kDataThreads && CPT * kDataThreads == ROWS * RC, "tile shape");
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  GatherTile<ROWS> t;
+  t.init(a);
+  if (t.row0 >= t.nvalid) return;  // padding tile: gather_pad_kernel's
+  t.locate(a);
+  t.load_pages(a);
   const int col = threadIdx.x % RC;
   const int head = col / (kHeadDim / 8);
   const int rsub = threadIdx.x / RC;
-  const bool packed = a.out_offsets != nullptr;
+  const uint8_t* plane = (t.is_v ? a.v_pool : a.k_pool) + (int64_t)t.layer * a.pool_layer_stride;
+  const float* splane = reinterpret_cast<const float*>(
+      reinterpret_cast<const uint8_t*>(t.is_v ? a.v_scale : a.k_scale) +
+      (int64_t)t.layer * a.scale_layer_stride);
+  uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
+                 t.out_row * OUT_ROW + col * 16;
 
-  for (uint64_t tile_id = blockIdx.x; tile_id < a.total_tiles; tile_id += gridDim.x) {
-    GatherTile<ROWS> t;
-    t.init(a, tile_id);
-    if (t.skip) continue;
-    const uint32_t l = t.lkv >> 1;
-    const bool is_v = t.lkv & 1u;
-    const uint8_t* plane = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
-    const float* splane = reinterpret_cast<const float*>(
-        reinterpret_cast<const uint8_t*>(is_v ? a.v_scale : a.k_scale) +
-        (int64_t)l * a.scale_layer_stride);
-    uint8_t* out = (is_v ? a.v_out : a.k_out) + (int64_t)l * a.out_layer_stride +
-                   t.out_row * OUT_ROW + col * 16;
-
-    u32x2 q[CPT];
-    float s[CPT];
-    bool valid[CPT];
+  u32x2 q[CPT];
+  float s[CPT];
+  bool valid[CPT];
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int r = rsub + i * RSTEP;
-      valid[i] = false;
-      q[i] = u32x2{0u, 0u};
-      s[i] = 0.0f;
-      if (t.row0 + r < t.nvalid) {
-        const int64_t p = t.p0 + r;
-        const int32_t page = t.page_of(p);
-        if (page >= 0) {
-          const int64_t slot = (int64_t)page * 16 + (p & 15);
-          q[i] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x2*>(plane + slot * IN_ROW + col * 8));
-          s[i] = splane[slot * HEADS + head];
-          valid[i] = true;
-        }
+  for (int i = 0; i < CPT; ++i) {
+    const int r = rsub + i * RSTEP;
+    valid[i] = false;
+    q[i] = u32x2{0u, 0u};
+    s[i] = 0.0f;
+    if (t.row0 + r < t.nvalid) {
+      const int64_t p = t.p0 + r;
+      const int32_t page = t.page_of(p);
+      if (page >= 0) {
+        const int64_t slot = (int64_t)page * 16 + (p & 15);
+        q[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2*>(plane + slot * IN_ROW + col * 8));
+        s[i] = splane[slot * HEADS + head];
+        valid[i] = true;
       }
     }
-    const int64_t row_limit = packed ? t.nvalid : a.out_len;
+  }
+  const int64_t row_limit = a.out_offsets ? t.nvalid : a.out_len;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int r = rsub + i * RSTEP;
-      u32x4 o = u32x4{0u, 0u, 0u, 0u};
-      if (valid[i]) {
-        uint32_t w[4];
+  for (int i = 0; i < CPT; ++i) {
+    const int r = rsub + i * RSTEP;
+    u32x4 o = u32x4{0u, 0u, 0u, 0u};
+    if (valid[i]) {
+      uint32_t w[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t word = k < 2 ? q[i].x : q[i].y;
-          const uint32_t b0 = (word >> (16 * (k & 1))) & 0xffu;
-          const uint32_t b1 = (word >> (16 * (k & 1) + 8)) & 0xffu;
-          const uint32_t e0 = f32_to_bf16_rne(e4m3fn_to_f32(b0) * s[i]);
-          const uint32_t e1 = f32_to_bf16_rne(e4m3fn_to_f32(b1) * s[i]);
-          w[k] = e0 | (e1 << 16);
-        }
-        o = u32x4{w[0], w[1], w[2], w[3]};
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t word = k < 2 ? q[i].x : q[i].y;
+        const uint32_t b0 = (word >> (16 * (k & 1))) & 0xffu;
+        const uint32_t b1 = (word >> (16 * (k & 1) + 8)) & 0xffu;
+        const uint32_t e0 = f32_to_bf16_rne(e4m3fn_to_f32(b0) * s[i]);
+        const uint32_t e1 = f32_to_bf16_rne(e4m3fn_to_f32(b1) * s[i]);
+        w[k] = e0 | (e1 << 16);
       }
-      if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * OUT_ROW, o);
+      o = u32x4{w[0], w[1], w[2], w[3]};
     }
+    if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * OUT_ROW, o);
   }
 }
 
-template <int HEADS, int ROWS>
-int launch_dequant(GatherArgs a, int32_t num_layers, hipStream_t stream) {
-  a.tiles_per_seq = (uint32_t)((a.out_len + ROWS - 1) / ROWS);
-  a.total_tiles = (uint64_t)num_layers * 2u * a.batch * a.tiles_per_seq;
-  if (a.total_tiles == 0) return MKV_OK;
-  const uint64_t wgs = a.total_tiles < kMaxGridWgs ? a.total_tiles : kMaxGridWgs;
-  hipLaunchKernelGGL((gather_dequant_kernel<HEADS, ROWS>), dim3((unsigned)wgs), dim3(kThreads), 0,
-                     stream, a);
+template <int HEADS>
+int launch_dequant(const GatherArgs& a, int32_t num_layers, hipStream_t stream) {
+  constexpr int OUT_ROW = HEADS * kHeadDim * 2;
+  const dim3 grid = gather_grid(a, kTileBytes / OUT_ROW, num_layers);
+  if (!a.out_offsets)
+    hipLaunchKernelGGL(gather_pad_kernel<OUT_ROW>, grid, dim3(kPadThreads), 0, stream, a);
+  hipLaunchKernelGGL(gather_dequant_kernel<HEADS>, grid, dim3(kDataThreads), 0, stream, a);
   return check_launch("mkv_gather_dequant_fp8");
 }
 
@@ -243,6 +240,7 @@ extern "C" int mkv_gather_dequant_fp8(const void* k_pool, const void* v_pool, co
               "mkv_gather_dequant_fp8: heads=%d head_dim=%d unsupported (1 or 2 heads of 256)",
               num_heads, head_dim);
   if (batch == 0 || out_len == 0 || num_layers == 0) return MKV_OK;
+  MKV_REQUIRE(num_layers <= 32767, MKV_E_UNSUPPORTED, "mkv_gather_dequant_fp8: too many layers for one call");
   MKV_REQUIRE(k_scale && v_scale && scale_layer_stride % 4 == 0, MKV_E_INVALID,
               "mkv_gather_dequant_fp8: bad scale planes");
   GatherArgs a;
@@ -255,6 +253,5 @@ extern "C" int mkv_gather_dequant_fp8(const void* k_pool, const void* v_pool, co
   a.v_scale = v_scale;
   a.scale_layer_stride = scale_layer_stride;
   hipStream_t s = as_stream(stream);
-  return num_heads == 1 ? launch_dequant<1, 32>(a, num_layers, s)
-                        : launch_dequant<2, 16>(a, num_layers, s);
+  return num_heads == 1 ? launch_dequant<1>(a, num_layers, s) : launch_dequant<2>(a, num_layers, s);
 }

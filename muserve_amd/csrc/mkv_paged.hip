@@ -8,6 +8,12 @@
 // streaming efficiency: 16-byte vector accesses, consecutive lanes on
 // consecutive addresses, all loads of a thread issued before its stores, and
 // non-temporal hints on data that is not re-read within the step.
+//
+// A padded gather is two launches: a write-only padding kernel shaped like a
+// fill (one 16-byte store per thread, few registers, so full occupancy) and a
+// data kernel for the rows that exist. Fused into one kernel the padding
+// tiles carried the data path's registers and latency and the whole gather
+// ran about 10 points of HBM peak slower.
 #include "mkv_device.h"
 
 namespace mkv {
@@ -53,79 +59,67 @@ __global__ __launch_bounds__(kThreads) void append_rows_kernel(AppendArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// gather: a workgroup moves ROWS consecutive output rows of one
-// (layer, K|V, sequence); each thread issues its CPT 16-byte loads (zero for
-// padding rows, no load at all) before any of its stores.
+// gather, data part: one 4 KiB tile of one (layer, K|V, sequence) per
+// workgroup of 128 threads; each thread issues both of its 16-byte loads
+// before either store. Tiles past the sequence's data belong to
+// gather_pad_kernel (mkv_device.h) and return at once.
 // ---------------------------------------------------------------------------
-template <int ROW_BYTES, int ROWS>
-__global__ __launch_bounds__(kThreads) void gather_rows_kernel(GatherArgs a) {
-  constexpr int RC = ROW_BYTES / 16;         // 16-byte chunks per row
-  constexpr int RSTEP = kThreads / RC;       // rows between a thread's chunks
-  constexpr int CPT = ROWS * RC / kThreads;  // chunks per thread
-  static_assert(RC * RSTEP == kThreads && CPT * kThreads == ROWS * RC, "tile shape");
+template <int ROW_BYTES>
+__global__ __launch_bounds__(kDataThreads) void gather_data_kernel(GatherArgs a) {
+  constexpr int ROWS = kTileBytes / ROW_BYTES;
+  constexpr int RC = ROW_BYTES / 16;            // 16-byte chunks per row
+  constexpr int RSTEP = kDataThreads / RC;      // rows between a thread's chunks
+  constexpr int CPT = ROWS * RC / kDataThreads; // chunks per thread
+  static_assert(CPT * kDataThreads == ROWS * RC && RSTEP * RC == kDataThreads, "tile shape");
+  GatherTile<ROWS> t;
+  t.init(a);
+  if (t.row0 >= t.nvalid) return;
+  t.locate(a);
+  t.load_pages(a);
   const int col = threadIdx.x % RC;
   const int rsub = threadIdx.x / RC;
-  const bool packed = a.out_offsets != nullptr;
-
-  for (uint64_t tile_id = blockIdx.x; tile_id < a.total_tiles; tile_id += gridDim.x) {
-    GatherTile<ROWS> t;
-    t.init(a, tile_id);
-    if (t.skip) continue;
-    const uint32_t l = t.lkv >> 1;
-    const bool is_v = t.lkv & 1u;
-    const uint8_t* plane = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
-    uint8_t* out = (is_v ? a.v_out : a.k_out) + (int64_t)l * a.out_layer_stride +
-                   t.out_row * ROW_BYTES + col * 16;
-
-    // Fast paths are branch-free between the loads and the stores, so the
-    // waitcnt pass can let the four stores overlap; a per-row guard would
-    // serialise them (vmcnt counts stores as well as loads).
-    u32x4 v[CPT];
-    if (t.full_data()) {
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const int64_t p = t.p0 + rsub + i * RSTEP;
-        v[i] = ld_nt(plane + ((int64_t)t.page_of(p) * 16 + (p & 15)) * ROW_BYTES + col * 16);
-      }
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, v[i]);
-      continue;
-    }
-    if (t.full_pad(a.out_len)) {
-#pragma unroll
-      for (int i = 0; i < CPT; ++i)
-        st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, u32x4{0u, 0u, 0u, 0u});
-      continue;
-    }
-    // Boundary tile: per-row guards.
+  const uint8_t* plane = (t.is_v ? a.v_pool : a.k_pool) + (int64_t)t.layer * a.pool_layer_stride;
+  uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
+                 t.out_row * ROW_BYTES + col * 16;
+  u32x4 v[CPT];
+  if (t.full_data()) {
+    // Straight-line: the waitcnt pass can overlap the stores (vmcnt counts
+    // stores as well as loads, so a per-row guard would serialise them).
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int r = rsub + i * RSTEP;
-      v[i] = u32x4{0u, 0u, 0u, 0u};
-      if (t.row0 + r < t.nvalid) {
-        const int64_t p = t.p0 + r;
-        const int32_t page = t.page_of(p);
-        if (page >= 0)
-          v[i] = ld_nt(plane + ((int64_t)page * 16 + (p & 15)) * ROW_BYTES + col * 16);
-      }
+      const int64_t p = t.p0 + rsub + i * RSTEP;
+      v[i] = ld_nt(plane + ((int64_t)t.page_of(p) * 16 + (p & 15)) * ROW_BYTES + col * 16);
     }
-    const int64_t row_limit = packed ? t.nvalid : a.out_len;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int r = rsub + i * RSTEP;
-      if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * ROW_BYTES, v[i]);
+    for (int i = 0; i < CPT; ++i) st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, v[i]);
+    return;
+  }
+  // Last data tile (or one with a bad page id): per-row guards.
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int r = rsub + i * RSTEP;
+    v[i] = u32x4{0u, 0u, 0u, 0u};
+    if (t.row0 + r < t.nvalid) {
+      const int64_t p = t.p0 + r;
+      const int32_t page = t.page_of(p);
+      if (page >= 0)
+        v[i] = ld_nt(plane + ((int64_t)page * 16 + (p & 15)) * ROW_BYTES + col * 16);
     }
+  }
+  const int64_t row_limit = a.out_offsets ? t.nvalid : a.out_len;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int r = rsub + i * RSTEP;
+    if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * ROW_BYTES, v[i]);
   }
 }
 
-template <int ROW_BYTES, int ROWS>
-int launch_gather(GatherArgs a, int32_t num_layers, hipStream_t stream) {
-  a.tiles_per_seq = (uint32_t)((a.out_len + ROWS - 1) / ROWS);
-  a.total_tiles = (uint64_t)num_layers * 2u * a.batch * a.tiles_per_seq;
-  if (a.total_tiles == 0) return MKV_OK;
-  const uint64_t wgs = a.total_tiles < kMaxGridWgs ? a.total_tiles : kMaxGridWgs;
-  hipLaunchKernelGGL((gather_rows_kernel<ROW_BYTES, ROWS>), dim3((unsigned)wgs), dim3(kThreads),
-                     0, stream, a);
+template <int ROW_BYTES>
+int launch_gather(const GatherArgs& a, int32_t num_layers, hipStream_t stream) {
+  const dim3 grid = gather_grid(a, kTileBytes / ROW_BYTES, num_layers);
+  if (!a.out_offsets)  // padded layout: zero tiles first, then the data tiles
+    hipLaunchKernelGGL(gather_pad_kernel<ROW_BYTES>, grid, dim3(kPadThreads), 0, stream, a);
+  hipLaunchKernelGGL(gather_data_kernel<ROW_BYTES>, grid, dim3(kDataThreads), 0, stream, a);
   return check_launch("mkv_gather_bf16");
 }
 
@@ -244,6 +238,7 @@ extern "C" int mkv_gather_bf16(const void* k_pool, const void* v_pool, int64_t p
                   table_width >= 0,
               MKV_E_INVALID, "mkv_gather_bf16: negative size");
   if (batch == 0 || out_len == 0 || num_layers == 0) return MKV_OK;
+  MKV_REQUIRE(num_layers <= 32767, MKV_E_UNSUPPORTED, "mkv_gather_bf16: too many layers for one call");
   GatherArgs a;
   const int rc = fill_gather_args(a, "mkv_gather_bf16", k_pool, v_pool, pool_layer_stride,
                                   num_pages, block_tables, table_stride, table_width, seq_lens,
@@ -252,11 +247,11 @@ extern "C" int mkv_gather_bf16(const void* k_pool, const void* v_pool, int64_t p
   if (rc != MKV_OK) return rc;
   hipStream_t s = as_stream(stream);
   switch (row_bytes) {
-    case 128: return launch_gather<128, 64>(a, num_layers, s);
-    case 256: return launch_gather<256, 64>(a, num_layers, s);
-    case 512: return launch_gather<512, 32>(a, num_layers, s);
-    case 1024: return launch_gather<1024, 16>(a, num_layers, s);
-    case 2048: return launch_gather<2048, 16>(a, num_layers, s);
+    case 128: return launch_gather<128>(a, num_layers, s);
+    case 256: return launch_gather<256>(a, num_layers, s);
+    case 512: return launch_gather<512>(a, num_layers, s);
+    case 1024: return launch_gather<1024>(a, num_layers, s);
+    case 2048: return launch_gather<2048>(a, num_layers, s);
     default:
       return set_error(MKV_E_UNSUPPORTED,
                        "mkv_gather_bf16: row_bytes %d not in {128,256,512,1024,2048}", row_bytes);

@@ -13,6 +13,7 @@ namespace mkv {
 namespace {
 
 constexpr int kUnroll = 4;
+constexpr int64_t kMaxGridWgs = 1 << 22;  // bigger jobs loop inside the grid
 constexpr int64_t kPiece = (int64_t)kThreads * 16 * kUnroll;  // 16 KiB
 
 struct StateArgs {
@@ -93,7 +94,7 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   a.pool_slots = pool_slots;
   a.slots = slots;
   a.err = err;
-  const int64_t wgs = a.total_pieces < (int64_t)kMaxGridWgs ? a.total_pieces : (int64_t)kMaxGridWgs;
+  const int64_t wgs = a.total_pieces < kMaxGridWgs ? a.total_pieces : kMaxGridWgs;
   hipLaunchKernelGGL((state_move_kernel<GATHER>), dim3((unsigned)wgs), dim3(kThreads), 0, stream,
                      a);
   return check_launch(fn);
