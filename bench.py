@@ -87,6 +87,25 @@ def cpu_baseline(cache, bt, lens_now: np.ndarray, gpu_out) -> dict:
     }
 
 
+PMC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "gather_decode_b256_hbm_counters.md")
+
+
+def counter_traffic() -> tuple[float | None, float | None]:
+    """(HBM bytes per gather launch, traffic/algorithmic ratio) recorded from
+    the FETCH_SIZE/WRITE_SIZE runs of this workload, if that summary exists."""
+    vals = {}
+    try:
+        for line in open(PMC_PROFILE):
+            if ":" in line and line.split(":", 1)[0].strip() in (
+                    "traffic_bytes_per_gather_launch", "traffic_to_algorithmic_ratio"):
+                k, v = line.split(":", 1)
+                vals[k.strip()] = float(v)
+    except OSError:
+        pass
+    return vals.get("traffic_bytes_per_gather_launch"), vals.get("traffic_to_algorithmic_ratio")
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -169,6 +188,7 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     mean_gather_bytes = gather_bytes / steps
     lens_now = bt._lens.copy()
 
+    traffic, ratio = counter_traffic()
     step_s = elapsed / steps
     value = all_bytes / elapsed / 1e9
     achieved = mean_gather_bytes / mean_gather_s / 1e9
@@ -203,7 +223,10 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_to_algorithmic": ratio,
+            "traffic_source": ("rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 (scales from a 1 GiB copy), "
+                               "profiles/gather_decode_b256_hbm_counters.md"),
             "mean_launch_us": round(mean_gather_s * 1e6, 2),
             "algorithmic_bytes_per_launch": round(mean_gather_bytes),
         },
@@ -214,8 +237,31 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
+def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
+    """A plain device copy of known size (one 1 GiB state-pool entry through
+    mkv_state_gather): the reference point for scaling rocprof's FETCH_SIZE and
+    WRITE_SIZE counters to bytes."""
+    from muserve_amd import _lib
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    slots = torch.zeros(1, dtype=torch.int32, device=dev)
+    err = _lib.DeviceErrors(dev)
+    for _ in range(reps):
+        _lib.call("mkv_state_gather", src.data_ptr(), nbytes, dst.data_ptr(), None, 0, None, 1,
+                  slots.data_ptr(), 1, err.ptr(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    err.check("calibration copy")
+    assert torch.equal(src, dst)
+    return {"calibration": "state_move_kernel<true> copy", "bytes_read": nbytes,
+            "bytes_written": nbytes, "launches": reps}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
+    ap.add_argument("--calibrate", action="store_true",
+                    help="run only a 1 GiB plain copy (for rocprof counter scaling)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
@@ -229,6 +275,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.calibrate:
+        print(json.dumps(run_calibration()), flush=True)
+        return 0
     res = run_decode(args.steps, args.warmup, not args.no_cpu_baseline)
     print(json.dumps(res), flush=True)
     return 0
