@@ -237,6 +237,312 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
+def _timed(events_per_step: list, label: str) -> float:
+    """Mean milliseconds of the (start, end) event pairs recorded under label."""
+    ms = [a.elapsed_time(b) for step in events_per_step for (lab, a, b) in step if lab == label]
+    return float(np.mean(ms)) if ms else float("nan")
+
+
+def _pair(stream):
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    return a, b
+
+
+def _kernel_roofline(name: str, nbytes: float, ms: float) -> dict:
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"kernel": name, "algorithmic_bytes_per_launch": round(nbytes), "mean_launch_us":
+            round(ms * 1e3, 2), "achieved": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Chunked prefill into an fp8 pool: 32 requests append 2048-token chunks
+    (bf16 ~N(0,1), 1 % of elements x20) into 128k-token contexts, quantised on
+    append (per-token absmax/448 scale), then a dequant-gather of the last 8192
+    tokens of every request; 15 layers, 1 KV head x 256."""
+    from muserve_amd.kv_cache import PagedKVCache, SequenceKVState, reserve_tokens, slot_mapping_for
+
+    R, CHUNK, CTX, WIN, L = 32, 2048, 131072, 8192, LAYERS
+    n_chunks = warmup + steps
+    if CHUNK * n_chunks > CTX - WIN:
+        raise SystemExit(f"at most {(CTX - WIN) // CHUNK} chunks fit in a {CTX}-token context")
+    prior = CTX - CHUNK * n_chunks
+    dev = torch.device("cuda:0")
+    pages = R * CTX // 16 + 16
+    cache = PagedKVCache(pages, num_layers=L, kv_heads=1, head_dim=HEAD_DIM,
+                         dtype=torch.float8_e4m3fn, device=dev, verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(103))
+    gen = torch.Generator(device=dev).manual_seed(103)
+
+    def kv_batch(t: int) -> torch.Tensor:
+        x = torch.randn(L, t, 1, HEAD_DIM, generator=gen, device=dev)
+        boost = torch.rand(L, t, 1, HEAD_DIM, generator=gen, device=dev) < 0.01
+        return torch.where(boost, x * 20.0, x).bfloat16()
+
+    seqs = [SequenceKVState() for _ in range(R)]
+    log(f"fp8 pool {pages} pages; prefilling {prior} tokens x {R} requests")
+    step = 8192
+    for s0 in range(0, prior, step):
+        n = min(step, prior - s0)
+        slots = np.concatenate([slot_mapping_for(sq, reserve_tokens(cache, sq, n), n) for sq in seqs])
+        sl = torch.from_numpy(slots).to(dev)
+        cache.append(sl, kv_batch(len(slots)), kv_batch(len(slots)))
+    # the chunks' pages and slot mappings, resident before timing
+    slot_steps, lens_steps = [], []
+    for _ in range(n_chunks):
+        slot_steps.append(np.concatenate(
+            [slot_mapping_for(sq, reserve_tokens(cache, sq, CHUNK), CHUNK) for sq in seqs]))
+        lens_steps.append([sq.seq_len for sq in seqs])
+    width = CTX // 16
+    bt = torch.zeros(R, width, dtype=torch.int32)
+    for b, sq in enumerate(seqs):
+        bt[b, :len(sq.page_table)] = torch.tensor(sq.page_table, dtype=torch.int32)
+    bt = bt.to(dev)
+    slots_dev = torch.from_numpy(np.stack(slot_steps)).to(dev)
+    lens_dev = torch.tensor(lens_steps, dtype=torch.int32, device=dev)
+    starts_dev = (lens_dev - WIN).clamp(min=0).contiguous()
+    # every request holds more than WIN tokens, so the windows are full and the
+    # packed layout at row offsets b*WIN is the padded [R, WIN, 1, 256] output
+    assert min(min(x) for x in lens_steps) >= WIN
+    cu_out = torch.arange(R + 1, dtype=torch.int64, device=dev) * WIN
+    T = R * CHUNK
+    kin = torch.stack([kv_batch(T) for _ in range(n_chunks)])
+    vin = torch.stack([kv_batch(T) for _ in range(n_chunks)])
+    kbuf = torch.empty(R, WIN, 1, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vbuf = torch.empty_like(kbuf)
+    torch.cuda.synchronize()
+    cache.check_errors()
+    stream = torch.cuda.current_stream(dev)
+
+    def one_step(i: int, rec=None):
+        for l in range(L):
+            if rec is not None:
+                a, b = _pair(stream)
+            cache.append(slots_dev[i], kin[i, l], vin[i, l], layer=l)
+            if rec is not None:
+                b.record(stream)
+                rec.append(("append", a, b))
+                a, b = _pair(stream)
+            cache.gather(l, bt, lens_dev[i], out_len=WIN, starts=starts_dev[i], out=(kbuf, vbuf),
+                         cu_out=cu_out)
+            if rec is not None:
+                b.record(stream)
+                rec.append(("gather", a, b))
+
+    for i in range(warmup):
+        one_step(i)
+    torch.cuda.synchronize()
+    recs = [[] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(warmup + j, recs[j])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    cache.check_errors()
+    append_bytes = T * (1024 + 512 + 8 + 8)
+    gather_bytes = R * WIN * (520 + 1024) + R * (WIN // 16 + 1) * 4 + 8 * R
+    step_bytes_ = L * (append_bytes + gather_bytes)
+    step_s = elapsed / steps
+    res = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) for fp8 quantize-on-append + dequant-gather",
+        "value": round(step_bytes_ / step_s / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8_e4m3fn",
+        "data": "synthetic (seeded ~N(0,1) bf16 K/V with 1% x20 outliers)",
+        "config": {"workload": ("fp8 chunked prefill: 32 requests x 2048-token chunks into 128k "
+                                "contexts, 15 layers, 1 KV head x 256, e4m3fn + fp32 per-token "
+                                "scale, then dequant-gather of the last 8192 tokens; seed 103")},
+        "appended_tokens_per_s": round(T / step_s, 1),
+        "pct_of_hbm_peak": round(100 * step_bytes_ / step_s / 1e9 / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
+            _kernel_roofline("append_fp8_kernel (mkv_append_fp8)", append_bytes,
+                             _timed(recs, "append")),
+            _kernel_roofline("gather_dequant_kernel<1> (mkv_gather_dequant_fp8)", gather_bytes,
+                             _timed(recs, "gather"))]},
+    }
+    if with_cpu:
+        from oracle import fp8 as ref
+        n = 2048
+        x = kin[warmup + steps - 1, 0, :n].cpu()
+        t1 = time.perf_counter()
+        q, sc = ref.quantize_rows(x)
+        dt = time.perf_counter() - t1
+        pg = slots_dev[warmup + steps - 1, :n].cpu()
+        got_q = cache.cache[0, 0].view(torch.uint8).reshape(-1, 1, HEAD_DIM)[pg].cpu()
+        got_s = cache.scales[0, 0].reshape(-1, 1)[pg].cpu()
+        res["cpu_baseline"] = {
+            "value": round(n * (1024 + 512 + 8) / 2 / dt / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle quantize_rows (torch-CPU) of {n} K rows of one layer: {dt*1e3:.1f} ms",
+            "gpu_matches_cpu_on_sample": bool(torch.equal(got_q, q) and torch.equal(
+                got_s.view(torch.int32), sc.view(torch.int32)))}
+    return res
+
+
+def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Decode step of the hybrid stack: 45 GDN layers gather their 256 active
+    requests' recurrent [8,128,128] fp32 + conv [2048,4] bf16 states from a
+    1024-slot pool (seeded permuted slots), apply a synthetic update (+1, timed
+    apart) and scatter them back; the 15 attention layers append one decode
+    token per request (the headline workload's appends)."""
+    from muserve_amd.kv_cache import BlockTables, PagedKVCache, SequenceKVState, reserve_tokens
+    from muserve_amd.state_pool import StatePool, gdn_ordinal
+
+    dev = torch.device("cuda:0")
+    S, G = 1024, 45
+    pool = StatePool(num_layers=G, num_slots=S, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(105)
+    pool.state.normal_(generator=gen)
+    pool.conv.normal_(generator=gen)
+    slots = torch.randperm(S, generator=torch.Generator().manual_seed(105))[:B].to(
+        torch.int32).to(dev)
+    ctx = context_lengths()
+    total = warmup + steps
+    pages = int(np.sum(-(-(ctx + total) // 16))) + 64
+    cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
+                         dtype=torch.bfloat16, device=dev, verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(SEED))
+    seqs = [SequenceKVState() for _ in range(B)]
+    for s_, n in zip(seqs, ctx):
+        reserve_tokens(cache, s_, int(n))
+    bt = BlockTables(cache, seqs, max_pages=int(-(-(int(ctx.max()) + total) // 16)))
+    kin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
+    vin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
+    sbuf = torch.empty((B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
+    cbuf = torch.empty((B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def one_step(i: int, rec=None):
+        kv_slots = bt.decode_step()
+        for layer in range(60):
+            if layer % 4 == 3:
+                a = layer // 4
+                cache.append(kv_slots, kin[i, a], vin[i, a], layer=a)
+                continue
+            g = gdn_ordinal(layer)
+            ev = _pair(stream) if rec is not None else None
+            pool.gather(g, slots, out=(sbuf, cbuf))
+            if rec is not None:
+                ev[1].record(stream)
+                rec.append(("gather",) + ev)
+                ev = _pair(stream)
+            sbuf.add_(1.0)
+            cbuf.add_(1.0)
+            if rec is not None:
+                ev[1].record(stream)
+                rec.append(("update",) + ev)
+                ev = _pair(stream)
+            pool.scatter(g, slots, sbuf, cbuf)
+            if rec is not None:
+                ev[1].record(stream)
+                rec.append(("scatter",) + ev)
+
+    for i in range(warmup):
+        one_step(i)
+    torch.cuda.synchronize()
+    recs = [[] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(warmup + j, recs[j])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    pool.check_errors()
+    cache.check_errors()
+    entry = 8 * 128 * 128 * 4 + 2048 * 4 * 2
+    move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
+    g_ms, s_ms, u_ms = _timed(recs, "gather"), _timed(recs, "scatter"), _timed(recs, "update")
+    state_s = G * (g_ms + s_ms) / 1e3
+    step_s = elapsed / steps
+    per_step_state = 4 * G * B * entry
+    res = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) for GDN state slot gather+scatter",
+        "value": round(per_step_state / state_s / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32+bf16",
+        "data": "synthetic (seeded ~N(0,1) states, seeded permuted slots)",
+        "config": {"workload": ("GDN state slots at decode: 45 layers x [8,128,128] fp32 + "
+                                "[2048,4] bf16, 1024-slot pool, batch 256, gather -> +1 -> "
+                                "scatter, interleaved with decode appends on 15 attention "
+                                "layers; seed 105")},
+        "state_move_ms_per_step": round(state_s * 1e3, 3),
+        "synthetic_update_ms_per_step": round(G * u_ms, 3),
+        "pct_of_hbm_peak": round(100 * per_step_state / state_s / 1e9 / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
+            _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms),
+            _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms)]},
+    }
+    if with_cpu:
+        from oracle import state as ref
+        n = 32
+        cpu_pool = pool.state[0, :S].cpu()
+        idx = slots[:n].cpu()
+        t1 = time.perf_counter()
+        x = ref.gather(cpu_pool.unsqueeze(0), 0, idx)
+        ref.scatter(cpu_pool.unsqueeze(0), 0, idx, x)
+        dt = time.perf_counter() - t1
+        res["cpu_baseline"] = {
+            "value": round(4 * n * 8 * 128 * 128 * 4 / dt / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"oracle index_select + index_copy_ (torch-CPU) of {n} recurrent "
+                       f"states of one layer: {dt*1e3:.1f} ms")}
+    return res
+
+
+def run_plumbing(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """1 attention layer, 512 pages x 16, 1 KV head x 256 bf16, 8 prompts of
+    randint(1,513) tokens on a seeded shuffled free list: append all prompt
+    tokens by slot mapping, gather each back to [len,1,256] (bit-exact check)."""
+    from muserve_amd.kv_cache import PagedKVCache, SequenceKVState, prefill_slot_mapping
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(101)
+    lens = torch.randint(1, 513, (8,), generator=g).tolist()
+    cache = PagedKVCache(512, num_layers=1, dtype=torch.bfloat16, device=dev, verbose=False)
+    cache.shuffle_free_list(g)
+    seqs = [SequenceKVState() for _ in lens]
+    slots = prefill_slot_mapping(cache, seqs, lens)
+    T = sum(lens)
+    k = torch.randn(T, 1, HEAD_DIM, generator=g).bfloat16().to(dev)
+    v = torch.randn(T, 1, HEAD_DIM, generator=g).bfloat16().to(dev)
+    width = max(len(s_.page_table) for s_ in seqs)
+    bt = torch.zeros(8, width, dtype=torch.int32)
+    for b, s_ in enumerate(seqs):
+        bt[b, :len(s_.page_table)] = torch.tensor(s_.page_table, dtype=torch.int32)
+    bt = bt.to(dev)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=dev)
+    kout = torch.empty_like(k)
+    vout = torch.empty_like(v)
+
+    def one_step():
+        cache.append(slots, k, v, layer=0)
+        cache.gather(0, bt, sl, out_len=max(lens), cu_out=cu, out=(kout, vout))
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    cache.check_errors()
+    exact = bool(torch.equal(kout.view(torch.int16), k.view(torch.int16)) and
+                 torch.equal(vout.view(torch.int16), v.view(torch.int16)))
+    nbytes = 4 * 512 * T + 8 * T + 4 * 512 * T
+    step_s = elapsed / steps
+    return {
+        "metric": "append + packed gather round trip (us per step; launch-bound, no roofline claim)",
+        "value": round(step_s * 1e6, 2), "unit": "us", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "plumbing: 1 layer, 512x16 pool, 8 prompts randint(1,513), seed 101",
+                   "tokens": T},
+        "GBps": round(nbytes / step_s / 1e9, 2), "bit_exact_round_trip": exact,
+    }
+
+
 def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
     """A plain device copy of known size (one 1 GiB state-pool entry through
     mkv_state_gather): the reference point for scaling rocprof's FETCH_SIZE and
@@ -266,6 +572,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "fp8_prefill", "gdn_state", "plumbing"],
+                    help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this path has no cross-GPU traffic "
@@ -278,7 +587,12 @@ def main() -> int:
     if args.calibrate:
         print(json.dumps(run_calibration()), flush=True)
         return 0
-    res = run_decode(args.steps, args.warmup, not args.no_cpu_baseline)
+    runner = {"decode": run_decode, "fp8_prefill": run_fp8_prefill,
+              "gdn_state": run_gdn_state, "plumbing": run_plumbing}[args.workload]
+    steps, warmup = args.steps, args.warmup
+    if args.workload == "fp8_prefill" and steps == 1000:
+        steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
+    res = runner(steps, warmup, not args.no_cpu_baseline)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -224,6 +224,21 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
                           int32_t token_bytes, uint64_t* out, int32_t* err,
                           void* stream);
 
+/* ---- self-test ------------------------------------------------------------ */
+
+/*
+ * On-device check of what the fp8 kernels rely on. Adds into counts[7]
+ * (device uint64, caller-zeroed): [0] v_cvt_pk_fp8_f32 results that differ
+ * from RNE e4m3fn (|x| <= 448, or not NaN for NaN), [1] v_cvt_pk_bf16_f32
+ * results that differ from RNE bf16, [2] v_cvt_pk_f32_fp8 decodes that differ
+ * from the OCP value, [3] fp8 codes where the quantiser's reciprocal divide
+ * differs from x / scale, [4] such quotients with |x/scale| >= 2^-12 whose
+ * bits differ, [5] fp32 patterns checked (2^32), [6] (absmax, x) pairs
+ * checked. Every mismatch count is 0 on a correct gfx950. No reference
+ * counterpart: it pins the hardware conversions to torch's CPU semantics.
+ */
+int mkv_check_conversions(uint64_t* counts, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

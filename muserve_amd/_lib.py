@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "mkv_state_gather": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
     "mkv_state_scatter": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
     "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],
+    "mkv_check_conversions": [_P, _P],
 }
 
 _lock = threading.Lock()
@@ -135,6 +136,18 @@ def require_gpu(*tensors: torch.Tensor) -> torch.device:
 
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+CONVERSION_COUNTERS = ("fp8_encode_mismatch", "bf16_mismatch", "fp8_decode_mismatch",
+                       "div_code_mismatch", "div_quotient_mismatch", "fp32_values", "div_pairs")
+
+
+def check_conversions(device: torch.device | str = "cuda") -> dict[str, int]:
+    """Runs mkv_check_conversions on ``device`` and returns its counters."""
+    dev = torch.device(device)
+    counts = torch.zeros(len(CONVERSION_COUNTERS), dtype=torch.int64, device=dev)
+    call("mkv_check_conversions", counts.data_ptr(), stream_of(dev))
+    return dict(zip(CONVERSION_COUNTERS, counts.cpu().tolist()))
 
 
 class DeviceErrors:

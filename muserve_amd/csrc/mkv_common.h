@@ -65,6 +65,29 @@ MKV_HD float e4m3fn_to_f32(uint32_t q) {
   return bits_f32(sign | ((e + 120u) << 23) | (m << 20));
 }
 
+// x / b, correctly rounded, given y = 1/b correctly rounded (Markstein's
+// correction step: q = RN(x*y) is within an ulp of x/b, r = x - q*b is exact
+// through the fma, and RN(q + r*y) = RN(x/b)). Intermediates must be normal,
+// which holds wherever the quotient can reach an fp8 code other than +-0. The
+// step is skipped when r is 0 (q is exact; this also keeps the sign of -0) or
+// NaN, which happens only for b = inf (y = 0: q = x*0 is already x/b, +-0 or
+// NaN for x = +-inf) or b = NaN (q is NaN), so no separate path is needed.
+// The fp8 quantiser's whole domain (every bf16 row absmax, including inf and
+// NaN, as divisor source; every bf16 x with |x| <= absmax) is checked
+// exhaustively against x / b, on the CPU and on the device.
+MKV_HD float div_by_recip(float x, float b, float y) {
+#pragma clang fp contract(off)
+  const float q = x * y;
+  const float r = __builtin_fmaf(-q, b, x);
+  const float ar = r < 0.0f ? -r : r;
+  return ar > 0.0f ? __builtin_fmaf(r, y, q) : q;
+}
+
+// e4m3fn codes equal, counting every NaN code (0x7F, 0xFF) as equal.
+MKV_HD bool same_fp8(uint32_t a, uint32_t b) {
+  return a == b || ((a & 0x7fu) == 0x7fu && (b & 0x7fu) == 0x7fu);
+}
+
 // fp32 -> bf16 bits, round to nearest even; every NaN becomes 0x7FC0 (the
 // conversion torch's .to(torch.bfloat16) performs).
 MKV_HD uint16_t f32_to_bf16_rne(float f) {

@@ -64,14 +64,14 @@ __device__ __forceinline__ int32_t pick_page(const int32_t (&pg)[NP], int j) {
   return r;
 }
 
-// Tile geometry of the two-kernel gather. A tile is ROWS consecutive output
-// rows (4 KiB of output) of one (layer, K|V, sequence); the grid is
+// Tile geometry of the data kernels of the two-kernel gather. A tile is ROWS
+// consecutive output rows of one (layer, K|V, sequence); the grid is
 // (tile, sequence, layer*2 + K|V), so nothing is decoded by division.
 //
 // Output rows of a sequence split at data_end = min(roundup(nvalid, ROWS),
 // out_len): tiles below it belong to the data kernel (which also zero-fills
-// the padding rows of the last, partial tile), tiles at or above it to the
-// padding kernel. Both kernels use the same ROWS, so each row is written once.
+// the padding rows of the last, partial tile), rows at or above it to
+// gather_pad_kernel<.., ROWS>, so each row is written exactly once.
 template <int ROWS>
 struct GatherTile {
   static constexpr int NP = (ROWS + 14) / 16 + 1;  // pages ROWS rows can span
@@ -146,27 +146,43 @@ struct GatherTile {
   __device__ __forceinline__ bool full_data() const { return row0 + ROWS <= nvalid && pages_ok; }
 };
 
-// Threads of the padding kernel (one 16-byte store each) and of the data
-// kernels (two 16-byte chunks each); both cover 4 KiB of output per tile.
+// Threads of the padding kernel (one 16-byte store per tile each) and of the
+// bf16 data kernel (two 16-byte chunks each); both tiles are 4 KiB of output.
 constexpr int kPadThreads = 256;
 constexpr int kDataThreads = 128;
 constexpr int kTileBytes = kPadThreads * 16;
 
-// Zero-fills the padding tiles of a padded gather: rows >= data_end of every
-// (layer, K|V, sequence). Write-only and register-light so that it streams
-// at the HBM write rate.
-template <int ROW_BYTES>
+// Zero-fills the padding rows of a padded gather: rows >= data_end of every
+// (layer, K|V, sequence), where data_end rounds the sequence's valid rows up
+// to the DATA_ROWS tiles of the data kernel that writes everything below it.
+// One 4 KiB tile per workgroup, one 16-byte store per thread, few registers:
+// shaped like the fastest fill on MI355X (6.8-7.0 TB/s). A workgroup that
+// loops over several tiles, or stores several chunks per thread, streams
+// measurably slower.
+template <int ROW_BYTES, int DATA_ROWS>
 __global__ __launch_bounds__(kPadThreads) void gather_pad_kernel(GatherArgs a) {
-  constexpr int ROWS = kTileBytes / ROW_BYTES;
+  constexpr int ROWS = kTileBytes / ROW_BYTES;  // rows per padding tile
   constexpr int RC = ROW_BYTES / 16;
-  GatherTile<ROWS> t;
-  t.init(a);
-  if (t.row0 < t.data_end) return;  // a data tile
-  const int r = threadIdx.x / RC;
-  if (t.row0 + r >= a.out_len) return;
-  uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
-                 ((int64_t)t.b * a.out_len + t.row0 + r) * ROW_BYTES + (threadIdx.x % RC) * 16;
+  static_assert(DATA_ROWS % ROWS == 0, "data tiles must be whole padding tiles");
+  const uint32_t b = blockIdx.y;
+  int64_t nvalid = ld_const(a.seq_lens + b);
+  const int64_t start = a.starts ? (int64_t)ld_const(a.starts + b) : 0;
+  nvalid = start < 0 ? 0 : nvalid - start;
+  nvalid = nvalid < 0 ? 0 : (nvalid > a.out_len ? a.out_len : nvalid);
+  const int64_t up = (nvalid + DATA_ROWS - 1) / DATA_ROWS * DATA_ROWS;
+  const int64_t data_end = up < a.out_len ? up : a.out_len;
+  const int64_t row = (int64_t)blockIdx.x * ROWS + threadIdx.x / RC;
+  if (row < data_end || row >= a.out_len) return;
+  uint8_t* out = ((blockIdx.z & 1u) ? a.v_out : a.k_out) +
+                 (int64_t)(blockIdx.z >> 1) * a.out_layer_stride +
+                 ((int64_t)b * a.out_len + row) * ROW_BYTES + (threadIdx.x % RC) * 16;
   st_nt(out, u32x4{0u, 0u, 0u, 0u});
+}
+
+// Grid of the padding kernel (one 4 KiB tile per workgroup).
+inline dim3 pad_grid(const GatherArgs& a, int row_bytes, int32_t num_layers) {
+  const int64_t rows = kTileBytes / row_bytes;
+  return dim3((unsigned)((a.out_len + rows - 1) / rows), a.batch, (unsigned)(2 * num_layers));
 }
 
 // Grid of a gather kernel with ROWS-row tiles; 0 tiles when nothing to do.

@@ -116,10 +116,12 @@ __global__ __launch_bounds__(kDataThreads) void gather_data_kernel(GatherArgs a)
 
 template <int ROW_BYTES>
 int launch_gather(const GatherArgs& a, int32_t num_layers, hipStream_t stream) {
-  const dim3 grid = gather_grid(a, kTileBytes / ROW_BYTES, num_layers);
+  constexpr int ROWS = kTileBytes / ROW_BYTES;
   if (!a.out_offsets)  // padded layout: zero tiles first, then the data tiles
-    hipLaunchKernelGGL(gather_pad_kernel<ROW_BYTES>, grid, dim3(kPadThreads), 0, stream, a);
-  hipLaunchKernelGGL(gather_data_kernel<ROW_BYTES>, grid, dim3(kDataThreads), 0, stream, a);
+    hipLaunchKernelGGL((gather_pad_kernel<ROW_BYTES, ROWS>), pad_grid(a, ROW_BYTES, num_layers),
+                       dim3(kPadThreads), 0, stream, a);
+  hipLaunchKernelGGL(gather_data_kernel<ROW_BYTES>, gather_grid(a, ROWS, num_layers),
+                     dim3(kDataThreads), 0, stream, a);
   return check_launch("mkv_gather_bf16");
 }
 

@@ -44,3 +44,40 @@ void hc_page_hashes(const uint8_t* tokens, int64_t ntok, int32_t token_bytes, ui
 }
 
 }  // extern "C"
+
+// Exhaustive check of the fp8 quantiser's division over its reachable domain:
+// for every non-negative bf16 absmax a (the divisor is
+// b = max(a, 1e-12f) / 448) and every bf16 x with |x| <= a, compares
+// div_by_recip(x, b, 1/b) with x / b: the e4m3fn code of the clamped quotient
+// everywhere, and the quotient bits wherever |x / b| >= 2^-12 (below that the
+// residual may underflow, and every such quotient encodes to +-0). Returns the
+// number of code mismatches; quotient mismatches go to *quot_bad.
+// Infinite and NaN absmax rows are included (codes compared with every NaN
+// code equal to every other).
+extern "C" int64_t hc_check_div_by_recip(uint32_t a_lo, uint32_t a_hi, int64_t* quot_bad,
+                                         int64_t* pairs) {
+  int64_t bad = 0, qb = 0, n = 0;
+  for (uint32_t ah = a_lo; ah < a_hi; ++ah) {  // bf16 bit patterns of the absmax
+    const float a = mkv::bits_f32(ah << 16);
+    const bool nan_row = !(a == a);  // a NaN absmax: the row's x may be anything
+    const float amax = a < 1e-12f ? 1e-12f : a;
+    const float b = amax / 448.0f;
+    const float y = 1.0f / b;
+    for (uint32_t xh = 0; xh < 65536; ++xh) {
+      const float x = mkv::bits_f32(xh << 16);
+      if (!nan_row && !(x == x)) continue;
+      const float ax = x < 0 ? -x : x;
+      if (!nan_row && ax > a) continue;
+      const float want = x / b;
+      const float got = mkv::div_by_recip(x, b, y);
+      ++n;
+      const float aw = want < 0 ? -want : want;
+      if (aw >= 0.000244140625f && mkv::f32_bits(want) != mkv::f32_bits(got)) ++qb;
+      auto cl = [](float v) { return v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v); };
+      if (!mkv::same_fp8(mkv::f32_to_e4m3fn(cl(want)), mkv::f32_to_e4m3fn(cl(got)))) ++bad;
+    }
+  }
+  *quot_bad = qb;
+  *pairs = n;
+  return bad;
+}

@@ -123,3 +123,16 @@ def test_chunked_prefill_then_dequant_gather_window():
             want = pref.gather_padded(plane, bt, sl, N, starts)
             assert torch.equal(bits16(got), want.view(torch.int16)), (l, kv)
     cache.check_errors()
+
+
+def test_hardware_conversions_and_divide_match_cpu_semantics():
+    """mkv_check_conversions: v_cvt_pk_fp8_f32 / v_cvt_pk_bf16_f32 on all 2^32
+    fp32 patterns, v_cvt_pk_f32_fp8 on all 256 codes, and the quantiser's
+    reciprocal divide on its whole domain, all on the device."""
+    from muserve_amd import _lib
+    case("exhaustive conversion self-test")
+    c = _lib.check_conversions(DEV)
+    assert c["fp32_values"] == 1 << 32 and c["div_pairs"] == 1073790594, c
+    for k in ("fp8_encode_mismatch", "bf16_mismatch", "fp8_decode_mismatch",
+              "div_code_mismatch", "div_quotient_mismatch"):
+        assert c[k] == 0, c

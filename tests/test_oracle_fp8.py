@@ -132,3 +132,26 @@ def test_quantize_rows_is_fast_fp8_quantize_with_row_blocks(shape):
     s2 = flat.abs().amax(-1).clamp(min=1e-12) / 448.0
     q2 = (flat / s2[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
     assert torch.equal(q.reshape(-1, 256), q2) and torch.equal(s.reshape(-1), s2)
+
+
+def test_reciprocal_divide_equals_division_on_the_quantiser_domain():
+    """div_by_recip (mkv_common.h, host build) vs x / scale for every bf16 row
+    absmax (hence every reachable scale) and every bf16 x with |x| <= absmax:
+    identical e4m3fn codes everywhere, identical quotients where |x/scale| >= 2^-12."""
+    import ctypes
+    from concurrent.futures import ThreadPoolExecutor
+
+    fn = hostcheck().hc_check_div_by_recip
+    fn.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int64
+
+    def run(lo):
+        qb, n = ctypes.c_int64(), ctypes.c_int64()
+        bad = fn(lo, lo + 0x800, ctypes.addressof(qb), ctypes.addressof(n))
+        return bad, qb.value, n.value
+
+    with ThreadPoolExecutor(8) as ex:
+        res = list(ex.map(run, range(0, 0x8000, 0x800)))
+    assert sum(r[0] for r in res) == 0
+    assert sum(r[1] for r in res) == 0
+    assert sum(r[2] for r in res) == 1073790594
