@@ -44,6 +44,30 @@ def context_lengths(seed: int = SEED) -> np.ndarray:
     return np.clip(np.round(rng.lognormal(np.log(4096.0), 1.0, B)), 1, 32768).astype(np.int64)
 
 
+def prefix_requests(n_requests: int, seed: int = 104, n_templates: int = 64,
+                    template_len: int = 4096, suffix: tuple[int, int] = (64, 1024),
+                    zipf_s: float = 1.1, vocab: int = 151936) -> list[np.ndarray]:
+    """Prompts = one of n_templates seeded templates of template_len random
+    token ids in [0, vocab), drawn by a bounded Zipf(s) law over the templates,
+    plus a random suffix of suffix[0]..suffix[1] ids (int64)."""
+    rng = np.random.default_rng(seed)
+    templates = rng.integers(0, vocab, (n_templates, template_len), dtype=np.int64)
+    p = np.arange(1, n_templates + 1, dtype=np.float64) ** -zipf_s
+    choice = rng.choice(n_templates, size=n_requests, p=p / p.sum())
+    lens = rng.integers(suffix[0], suffix[1] + 1, n_requests)
+    return [np.concatenate([templates[c], rng.integers(0, vocab, int(n), dtype=np.int64)])
+            for c, n in zip(choice, lens)]
+
+
+def prefix_ops(n_requests: int, batch: int) -> list[list[int]]:
+    """Per batch: release the previous batch's requests, then admit this one's."""
+    out = []
+    for b0 in range(0, n_requests, batch):
+        prev = range(max(0, b0 - batch), b0)
+        out.append([-(r + 1) for r in prev] + list(range(b0, min(n_requests, b0 + batch))))
+    return out
+
+
 def step_bytes(lens: np.ndarray) -> tuple[float, float, float]:
     """(all algorithmic bytes of one step, of one gather launch, useful bytes of
     one step without padding writes) for post-append lengths ``lens``."""

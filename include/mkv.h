@@ -48,6 +48,7 @@ extern "C" {
 #define MKV_DEVERR_TABLE 4       /* sequence needs more pages than the table holds */
 #define MKV_DEVERR_STATE_SLOT 8  /* state-pool slot outside [0, pool_slots)    */
 #define MKV_DEVERR_NEW_PAGE 16   /* decode step needed a page but none was given */
+#define MKV_DEVERR_BM 32         /* block manager: malformed request or op order */
 
 /* ---- meta ------------------------------------------------------------- */
 
@@ -170,8 +171,9 @@ int mkv_gather_dequant_fp8(const void* k_pool, const void* v_pool,
  *   plane(q)[dst_pages[i]] = plane(q)[src_pages[i]]   (page_bytes each)
  * with plane(q) = pool + q*plane_stride. For the bf16 pool
  * [L,2,P,16,H,D] pass num_planes = 2L, plane_stride = P*page_bytes; for the
- * fp8 scales call again with their own plane geometry. Pages outside
- * [0, num_pages) set MKV_DEVERR_PAGE. No reference counterpart: the reference
+ * fp8 scales call again with their own plane geometry. A pair with a negative
+ * id is skipped (so mkv_bm_step's cow_src/cow_dst columns can be passed as
+ * they are); ids >= num_pages set MKV_DEVERR_PAGE. No reference counterpart: the reference
  * has no copy-on-write; this is the copy a forked sequence needs before its
  * first append into a shared partial page.
  */
@@ -223,6 +225,60 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
                           const int64_t* page_offsets, int32_t num_requests,
                           int32_t token_bytes, uint64_t* out, int32_t* err,
                           void* stream);
+
+/* ---- block manager (prefix caching, refcounts, copy-on-write, LRU) ------- */
+
+/*
+ * Device-resident page bookkeeping for prefix caching. No reference
+ * counterpart for the block level: the reference caches whole prefixes
+ * (muserve/model/prefix_cache.py:46-105); this keeps its key (the SHA-256
+ * prefix hash, here per 16-token page from mkv_block_hash_sha256), its LRU
+ * order (OrderedDict move-to-end / popitem(last=False)) and the LIFO free list
+ * of muserve/kv_cache.py:77-91, at page granularity.
+ *
+ * The state is one caller-owned device buffer of mkv_bm_state_bytes(P) bytes
+ * (256-byte aligned), initialised by mkv_bm_init with the free stack
+ * free_order[0..P) (popped from the end; NULL = 0..P-1). mkv_bm_layout
+ * writes 13 int64: table capacity C, ring capacity Q, then the byte offsets of
+ * counters, table keys, table values, refcounts, flags, stamps, free stack,
+ * page hashes, ring pages, ring stamps, and the total size.
+ *
+ * mkv_bm_step runs ops[0..num_ops) in order on one workgroup: op r >= 0
+ * admits request r, op -(r+1) releases it (r < num_requests, the length of
+ * the per-request arrays; hash_offsets has num_requests+1 entries, tables
+ * num_requests rows). Request r has num_tokens[r]
+ * tokens whose floor(n/16) page hashes are page_hashes[hash_offsets[r] ..
+ * hash_offsets[r+1]). Admit:
+ *   k = number of leading page hashes found in the table;
+ *   take = ceil(n/16) - k + (n % 16 != 0); if take > free + evictable - (hits
+ *     now evictable): status OOM, nothing changes;
+ *   hits: refcount += 1 (leaving the LRU); the other pages come from the free
+ *     stack's top, then from evicting the LRU's oldest pages (their hashes
+ *     leave the table; each is appended to evict_log while it has room);
+ *   pages k.. of the full pages register their hash unless already present;
+ *   fork: a child shares every page (refcount += 1); with a partial last page
+ *     the child's first append needs a private copy: cow_src/cow_dst[r] name
+ *     the pages to copy (mkv_copy_blocks) and child_last[r] the child's page.
+ * tables[r][0..ceil(n/16)) receives the parent's page ids, hits[r] = k,
+ * status[r] = 0 (admitted), 1 (OOM) or 2 (malformed request: hash count not
+ * floor(n/16) or more pages than table_width; sets MKV_DEVERR_BM).
+ * Release (child then parent, each from its last page): refcount -= 1; a page
+ * reaching 0 goes to the LRU's newest end if cached, else onto the free stack;
+ * status[r] becomes 3. Releasing a request that got OOM does nothing;
+ * releasing one that is neither admitted nor OOM (never admitted, already
+ * released), or an op with r >= num_requests, sets MKV_DEVERR_BM and does
+ * nothing.
+ */
+int64_t mkv_bm_state_bytes(int32_t num_pages);
+int mkv_bm_layout(int32_t num_pages, int64_t* out);
+int mkv_bm_init(void* state, int32_t num_pages, const int32_t* free_order, void* stream);
+int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_ops,
+                int32_t num_requests, const uint64_t* page_hashes, const int64_t* hash_offsets,
+                const int32_t* num_tokens, int32_t* tables, int64_t table_stride,
+                int32_t table_width, int32_t* hits, int32_t* child_last,
+                int32_t* cow_src, int32_t* cow_dst, int32_t* status,
+                int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
+                void* stream);
 
 /* ---- self-test ------------------------------------------------------------ */
 

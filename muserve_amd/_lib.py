@@ -25,12 +25,14 @@ DEVERR_PAGE = 2
 DEVERR_TABLE = 4
 DEVERR_STATE_SLOT = 8
 DEVERR_NEW_PAGE = 16
+DEVERR_BM = 32
 _DEVERR_TEXT = {
     DEVERR_SLOT: "slot_mapping entry out of range",
     DEVERR_PAGE: "page id out of range",
     DEVERR_TABLE: "sequence longer than its block table (or inconsistent offsets)",
     DEVERR_STATE_SLOT: "state-pool slot out of range",
     DEVERR_NEW_PAGE: "decode step needed a new page but none was supplied",
+    DEVERR_BM: "block manager: malformed request or release of a request not admitted",
 }
 
 _P = ctypes.c_void_p
@@ -54,6 +56,11 @@ SIGNATURES: dict[str, list] = {
     "mkv_state_scatter": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
     "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],
     "mkv_check_conversions": [_P, _P],
+    "mkv_bm_state_bytes": [_I32],
+    "mkv_bm_layout": [_I32, _P],
+    "mkv_bm_init": [_P, _I32, _P, _P],
+    "mkv_bm_step": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P,
+                    _I64, _P, _P],
 }
 
 _lock = threading.Lock()
@@ -93,7 +100,8 @@ def load() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == "mkv_last_error" else ctypes.c_int
+            fn.restype = (ctypes.c_char_p if name == "mkv_last_error" else
+                          ctypes.c_int64 if name == "mkv_bm_state_bytes" else ctypes.c_int)
         if lib.mkv_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH.name} ABI {lib.mkv_version()} != expected {ABI_VERSION}")
         runtimes = _hip_runtimes()

@@ -1,0 +1,146 @@
+"""GPU-resident block manager for prefix caching (refcounts, copy-on-write,
+LRU eviction), driving mkv_bm_step.
+
+The reference caches whole prefixes in an OrderedDict
+(muserve/model/prefix_cache.py:46-105) and hands out pages from a LIFO list
+(muserve/kv_cache.py:77-91). ``BlockManager`` does both at page granularity
+on the device: a request's full 16-token pages are keyed by the SHA-256 prefix
+hash of ``PrefixCache._hash_tokens`` (``prefix_hash.page_hashes``), the
+longest run of leading cached pages is shared (refcounted), the rest come from
+the free stack or by evicting the least recently released cached page, and a
+forked request's partial last page is copied on write. Requests are processed
+in op order by one workgroup, so eviction order is deterministic and equal to
+the sequential OrderedDict model.
+
+Typical step for a batch of requests (all on the stream, no host sync)::
+
+    hashes, cu_pages = prefix_hash.page_hashes(tokens, cu_tokens)
+    bm.step(ops, hashes, cu_pages_dev, num_tokens_dev)
+    bm.copy_on_write(cache, first_request, last_request)
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from muserve_amd import _lib
+
+STATUS_ADMITTED, STATUS_OOM, STATUS_BAD, STATUS_RELEASED = 0, 1, 2, 3
+_FREE_TOP, _HEAD, _TAIL, _NEXT_STAMP, _EVICTABLE, _TOMBS, _LOG_LEN = range(7)
+
+
+def admit_op(r: int) -> int:
+    return r
+
+
+def release_op(r: int) -> int:
+    return -(r + 1)
+
+
+class BlockManager:
+    def __init__(self, num_pages: int, max_requests: int, max_pages_per_request: int,
+                 device: torch.device | str = "cuda", free_order=None,
+                 evict_log_capacity: int = 0):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("BlockManager runs on a ROCm GPU only")
+        self.num_pages = num_pages
+        lib = _lib.load()
+        nbytes = lib.mkv_bm_state_bytes(num_pages)
+        if nbytes <= 0:
+            raise ValueError(f"bad page count {num_pages}")
+        lay = (ctypes.c_int64 * 13)()
+        _lib.call("mkv_bm_layout", num_pages, ctypes.addressof(lay))
+        self.layout = list(lay)
+        self.state = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        if self.state.data_ptr() % 256:
+            raise RuntimeError("state buffer is not 256-byte aligned")
+        order = None
+        if free_order is not None:
+            order = torch.as_tensor(np.asarray(free_order, dtype=np.int32)).to(self.device)
+            if order.numel() != num_pages:
+                raise ValueError("free_order must list every page once")
+        stream = _lib.stream_of(self.device)
+        _lib.call("mkv_bm_init", self.state.data_ptr(), num_pages, _lib.ptr(order), stream)
+        R, W = max_requests, max_pages_per_request
+        i32 = dict(dtype=torch.int32, device=self.device)
+        self.tables = torch.full((R, W), -1, **i32)
+        self.hits = torch.full((R,), -1, **i32)
+        self.child_last = torch.full((R,), -1, **i32)
+        self.cow_src = torch.full((R,), -1, **i32)
+        self.cow_dst = torch.full((R,), -1, **i32)
+        self.status = torch.full((R,), -1, **i32)
+        self.evict_log = torch.full((max(evict_log_capacity, 1),), -1, **i32)
+        self.evict_log_capacity = evict_log_capacity
+        self.errors = _lib.DeviceErrors(self.device)
+
+    def step(self, ops: torch.Tensor, page_hashes: torch.Tensor, hash_offsets: torch.Tensor,
+             num_tokens: torch.Tensor) -> None:
+        """Runs ops (int32: r admits request r, -(r+1) releases it) in order.
+        page_hashes: int64 device tensor of u64 page-hash bit patterns;
+        hash_offsets: int64 [max_requests+1] offsets into it per request id;
+        num_tokens: int32 [max_requests] prompt lengths."""
+        if not (isinstance(ops, torch.Tensor) and ops.device.type == "cuda"):
+            host = np.asarray(ops.cpu() if isinstance(ops, torch.Tensor) else ops, dtype=np.int64)
+            req = np.where(host >= 0, host, -(host + 1))
+            if host.size and (req.max() >= self.tables.shape[0]):
+                raise IndexError(f"op names request {int(req.max())} >= {self.tables.shape[0]}")
+            ops = torch.from_numpy(host.astype(np.int32))
+        if hash_offsets.numel() != self.tables.shape[0] + 1 or num_tokens.numel() != self.tables.shape[0]:
+            raise ValueError("hash_offsets needs max_requests+1 entries and num_tokens max_requests")
+        ops = ops.to(device=self.device, dtype=torch.int32).contiguous()
+        hash_offsets = hash_offsets.to(device=self.device, dtype=torch.int64).contiguous()
+        num_tokens = num_tokens.to(device=self.device, dtype=torch.int32).contiguous()
+        page_hashes = page_hashes.to(device=self.device).contiguous()
+        if page_hashes.dtype != torch.int64:
+            raise TypeError("page_hashes must hold u64 bit patterns in an int64 tensor")
+        _lib.require_gpu(ops, hash_offsets, num_tokens, self.state)
+        _lib.call("mkv_bm_step", self.state.data_ptr(), self.num_pages, ops.data_ptr(),
+                  ops.numel(), self.tables.shape[0], page_hashes.data_ptr(), hash_offsets.data_ptr(),
+                  num_tokens.data_ptr(), self.tables.data_ptr(), self.tables.stride(0),
+                  self.tables.shape[1], self.hits.data_ptr(), self.child_last.data_ptr(),
+                  self.cow_src.data_ptr(), self.cow_dst.data_ptr(), self.status.data_ptr(),
+                  self.evict_log.data_ptr(), self.evict_log_capacity, self.errors.ptr(),
+                  _lib.stream_of(self.device))
+
+    def copy_on_write(self, cache, first: int = 0, last: int | None = None) -> None:
+        """Copies every admitted request's shared partial page to its child's
+        private page (requests first..last-1; pairs without a copy are -1)."""
+        cache.copy_pages(self.cow_src[first:last], self.cow_dst[first:last])
+
+    def check_errors(self) -> None:
+        self.errors.check("BlockManager")
+
+    # -- inspection (synchronises) --
+    def _arr(self, idx: int, count: int, dtype: torch.dtype) -> torch.Tensor:
+        off = self.layout[idx]
+        esz = torch.empty((), dtype=dtype).element_size()
+        return self.state[off:off + count * esz].view(dtype)
+
+    def counters(self) -> list[int]:
+        return self._arr(2, 16, torch.int64).cpu().tolist()
+
+    def snapshot(self) -> dict:
+        """Host copy of the bookkeeping: free stack (bottom..top), live LRU
+        order (oldest first), refcounts, cached flags, page hashes (u64)."""
+        P, Q = self.num_pages, self.layout[1]
+        ctr = self.counters()
+        ref = self._arr(5, P, torch.int32).cpu().numpy()
+        flag = self._arr(6, P, torch.int32).cpu().numpy()
+        stamp = self._arr(7, P, torch.int32).cpu().numpy().view(np.uint32)
+        free = self._arr(8, P, torch.int32).cpu().numpy()[:ctr[_FREE_TOP]]
+        phash = self._arr(9, P, torch.int64).cpu().numpy().view(np.uint64)
+        rpg = self._arr(10, Q, torch.int32).cpu().numpy()
+        rst = self._arr(11, Q, torch.int32).cpu().numpy().view(np.uint32)
+        lru = []
+        for pos in range(ctr[_HEAD], ctr[_TAIL]):
+            pg, st = int(rpg[pos % Q]), int(rst[pos % Q])
+            if flag[pg] & 1 and ref[pg] == 0 and stamp[pg] == st:
+                lru.append(pg)
+        cached = flag & 1
+        return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(),
+                "cached": cached.tolist(),
+                "hash": [int(phash[p]) if cached[p] else None for p in range(P)],
+                "evictable": ctr[_EVICTABLE], "log_len": ctr[_LOG_LEN]}

@@ -170,7 +170,8 @@ __global__ __launch_bounds__(kThreads) void copy_pages_kernel(
   const int32_t i = blockIdx.x / num_planes;
   const int32_t q = blockIdx.x - i * num_planes;
   const int32_t s = src[i], d = dst[i];
-  if (s < 0 || s >= num_pages || d < 0 || d >= num_pages) {
+  if (s < 0 || d < 0) return;  // a negative id marks "no copy" for this pair
+  if (s >= num_pages || d >= num_pages) {
     if (threadIdx.x == 0 && q == 0) raise_err(err, MKV_DEVERR_PAGE);
     return;
   }

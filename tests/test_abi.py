@@ -13,7 +13,7 @@ HEADER = ROOT / "include" / "mkv.h"
 
 def declared() -> list[str]:
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:int|const char\*)\s+(mkv_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(mkv_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_the_bound_functions():

@@ -1,0 +1,105 @@
+"""GPU block manager (mkv_bm_step) vs the OrderedDict model, request by request:
+status, hits, page tables, copy-on-write pairs, eviction order, and the final
+free stack / LRU order / refcounts / cached hashes; plus the copied pages."""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from muserve_amd import _lib
+from muserve_amd.block_manager import BlockManager
+from muserve_amd.kv_cache import PagedKVCache
+from muserve_amd.prefix_hash import as_u64, page_hashes
+from oracle.blocks import OK, OOM, BlockManagerModel
+from oracle.sha import page_hashes as cpu_page_hashes
+from tests.gpu_util import DEV, bits16, case
+
+pytestmark = pytest.mark.gpu
+
+
+def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False):
+    reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
+                                 template_len=template_len, suffix=suffix)
+    lens = [len(x) for x in reqs]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    flat = torch.from_numpy(np.concatenate(reqs)).to(DEV)
+    hashes, cu_pages = page_hashes(flat, cu)
+    hu = as_u64(hashes)
+    for r in (0, n // 2, n - 1):  # the GPU hashes are the prefix keys
+        assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r])
+    free = np.random.default_rng(seed).permutation(P).tolist()
+    bm = BlockManager(P, n, width, DEV, free_order=free, evict_log_capacity=1 << 16)
+    model = BlockManagerModel(P, free)
+    cache = cpu = None
+    if with_data:
+        cache = PagedKVCache(P, num_layers=2, dtype=torch.bfloat16, device=DEV, verbose=False)
+        cpu = torch.randn(cache.cache.shape, generator=torch.Generator().manual_seed(seed)).bfloat16()
+        cache.cache.copy_(cpu.to(DEV))
+    off = torch.from_numpy(cu_pages).to(DEV)
+    ntok = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    want = {}
+    for ops in bench.prefix_ops(n, batch):
+        bm.step(torch.tensor(ops, dtype=torch.int32), hashes, off, ntok)
+        pairs = []
+        for op in ops:
+            if op >= 0:
+                h = [int(v) for v in hu[cu_pages[op]:cu_pages[op + 1]]]
+                want[op] = model.admit(op, h, lens[op])
+                if want[op]["cow_src"] >= 0:
+                    pairs.append((want[op]["cow_src"], want[op]["cow_dst"]))
+            elif -op - 1 in model.reqs:
+                model.release(-op - 1)
+        if with_data:
+            first = min(o for o in ops if o >= 0)
+            bm.copy_on_write(cache, first, first + sum(1 for o in ops if o >= 0))
+            for s, d in pairs:
+                cpu[:, :, d] = cpu[:, :, s]
+    bm.check_errors()
+    status = bm.status.cpu().tolist()
+    hits, cl = bm.hits.cpu().tolist(), bm.child_last.cpu().tolist()
+    cs, cd = bm.cow_src.cpu().tolist(), bm.cow_dst.cpu().tolist()
+    tables = bm.tables.cpu()
+    for r in range(n):
+        w = want[r]
+        released = status[r] == 3
+        assert (OK if released else status[r]) == w["status"], r
+        if w["status"] != OK:
+            continue
+        assert hits[r] == w["hits"], r
+        npg = -(-lens[r] // 16)
+        assert tables[r, :npg].tolist() == w["table"], r
+        assert (cl[r], cs[r], cd[r]) == (w["child_last"], w["cow_src"], w["cow_dst"]), r
+    snap = bm.snapshot()
+    assert snap["free"] == model.free
+    assert snap["lru"] == model.lru_order()
+    assert snap["ref"] == model.ref
+    assert snap["hash"] == model.hash
+    log = bm.evict_log.cpu().tolist()[:snap["log_len"]]
+    assert log == model.evicted
+    if with_data:
+        assert torch.equal(bits16(cache.cache), cpu.view(torch.int16))
+        cache.check_errors()
+    return status, model
+
+
+def test_small_pool_evictions_oom_and_cow():
+    case("block manager: 72-page pool, 240 requests, batches of 6")
+    status, model = run(P=72, n=240, batch=6, seed=104, n_templates=6, template_len=128,
+                        suffix=(1, 120), width=32, with_data=True)
+    assert OOM in status and len(model.evicted) > 100
+
+
+def test_larger_trace_with_ring_compaction():
+    case("block manager: 3000-page pool, 1200 requests, batches of 32")
+    status, model = run(P=3000, n=1200, batch=32, seed=7, n_templates=24, template_len=512,
+                        suffix=(16, 600), width=96)
+    assert len(model.evicted) > 1000
+
+
+def test_release_of_unknown_request_is_flagged():
+    case("block manager: release of a request never admitted")
+    bm = BlockManager(64, 4, 8, DEV)
+    z = torch.zeros(5, dtype=torch.int64, device=DEV)
+    bm.step(torch.tensor([-(2 + 1)], dtype=torch.int32), z[:0], z, torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(_lib.MkvDeviceError, match="block manager"):
+        bm.check_errors()
