@@ -239,9 +239,9 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * The state is one caller-owned device buffer of mkv_bm_state_bytes(P) bytes
  * (256-byte aligned), initialised by mkv_bm_init with the free stack
  * free_order[0..P) (popped from the end; NULL = 0..P-1). mkv_bm_layout
- * writes 13 int64: table capacity C, ring capacity Q, then the byte offsets of
+ * writes 14 int64: table capacity C, ring capacity Q, then the byte offsets of
  * counters, table keys, table values, refcounts, flags, stamps, free stack,
- * page hashes, ring pages, ring stamps, and the total size.
+ * page hashes, ring pages, ring stamps, key slots, and the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) in order on one workgroup: op r >= 0
  * admits request r, op -(r+1) releases it (r < num_requests, the length of

@@ -51,7 +51,7 @@ class BlockManager:
         nbytes = lib.mkv_bm_state_bytes(num_pages)
         if nbytes <= 0:
             raise ValueError(f"bad page count {num_pages}")
-        lay = (ctypes.c_int64 * 13)()
+        lay = (ctypes.c_int64 * 14)()
         _lib.call("mkv_bm_layout", num_pages, ctypes.addressof(lay))
         self.layout = list(lay)
         self.state = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)

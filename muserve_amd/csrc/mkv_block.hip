@@ -14,7 +14,8 @@
 //   table     open addressing, linear probing: key[C] u64, val[C] i32
 //             (-1 empty, -2 tombstone, -3 being written, >= 0 page id);
 //             rebuilt when tombstones exceed C/4
-//   per page  ref[P], flag[P] (bit 0: cached), stamp[P], hash[P]
+//   per page  ref[P], flag[P] (bit 0: cached), stamp[P], hash[P], slot[P]
+//             (the table slot of a cached page's key, so eviction needs no probe)
 //   free      stack free[P] (pop from the top, like PagedKVCache.alloc_pages)
 //   LRU       ring of (page, stamp) entries with lazy deletion: an entry is
 //             live iff its page is cached, unreferenced and still carries that
@@ -38,7 +39,7 @@ constexpr int32_t kEmpty = -1, kTomb = -2, kBusy = -3;
 struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
   int64_t off_ctr, off_key, off_val, off_ref, off_flag, off_stamp, off_free, off_hash, off_ring_pg,
-      off_ring_st, bytes;
+      off_ring_st, off_slot, bytes;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -67,6 +68,7 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.off_hash = take((int64_t)P * 8);
   l.off_ring_pg = take(l.Q * 4);
   l.off_ring_st = take(l.Q * 4);
+  l.off_slot = take((int64_t)P * 4);
   l.bytes = o;
   return l;
 }
@@ -82,6 +84,7 @@ struct BmState {
   uint64_t* hash;
   int32_t* ring_pg;
   uint32_t* ring_st;
+  int32_t* slot;  // table slot holding a cached page's key
   int64_t C, Q;
   int32_t P;
 };
@@ -100,6 +103,7 @@ inline BmState bm_state(void* base, int32_t P) {
   s.hash = reinterpret_cast<uint64_t*>(b + l.off_hash);
   s.ring_pg = reinterpret_cast<int32_t*>(b + l.off_ring_pg);
   s.ring_st = reinterpret_cast<uint32_t*>(b + l.off_ring_st);
+  s.slot = reinterpret_cast<int32_t*>(b + l.off_slot);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -175,9 +179,10 @@ __device__ int32_t tab_find(const BmState& s, uint64_t h, int64_t* slot_out = nu
   return -1;
 }
 
-// Inserts h -> page; other lanes may insert other keys at the same time.
-// Returns 1 if it reused a tombstone, 0 if it took an empty slot, -1 if the
-// table was full (cannot happen below 3/4 load).
+// Inserts h -> page (other lanes may insert other keys at the same time) and
+// records the slot in slot[page]. Returns 1 if it reused a tombstone, 0 if it
+// took an empty slot, -1 if the table was full (cannot happen: the load stays
+// below 1/2 because of the rebuild threshold).
 __device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page) {
   const int64_t mask = s.C - 1;
   int64_t i = slot_of(h) & mask;
@@ -185,6 +190,7 @@ __device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page) {
     const int32_t v = __hip_atomic_load(&s.val[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if ((v == kEmpty || v == kTomb) && atomicCAS(&s.val[i], v, kBusy) == v) {
       s.key[i] = h;
+      s.slot[page] = (int32_t)i;
       __threadfence_block();
       __hip_atomic_store(&s.val[i], page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       return v == kTomb ? 1 : 0;
@@ -242,6 +248,11 @@ __device__ void tab_rebuild(const BmArgs& a, Ctrs& c) {
   c.tombs = 0;
 }
 
+// Probe results a thread keeps in registers for the pages it owns
+// (i = tid + j*kBmThreads); requests longer than kHeld*kBmThreads pages re-read
+// the rest from memory.
+constexpr int kHeld = 4;
+
 __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
   const BmState& s = a.s;
   const int tid = threadIdx.x;
@@ -262,24 +273,39 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
   }
   if (c.tombs > s.C / 4) tab_rebuild(a, c);
 
-  // 1. probe every page hash; k = first miss
+  // 1. probe every page hash; k = first miss. Each lane keeps the page and its
+  //    current refcount for its first kHeld hashes.
   if (tid == 0) {
     sh.first_miss = (int32_t)m;
     sh.count = 0;
     sh.tomb_reused = 0;
   }
   __syncthreads();
-  for (int64_t i = tid; i < m; i += kBmThreads) {
+  int32_t held_pg[kHeld], held_ref[kHeld];
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    held_pg[j] = -1;
+    held_ref[j] = 0;
+  }
+  for (int64_t i = tid, j = 0; i < m; i += kBmThreads, ++j) {
     const int32_t p = tab_find(s, a.hashes[h0 + i]);
     row[i] = p;
     if (p < 0) atomicMin(&sh.first_miss, (int32_t)i);
+    if (j < kHeld) {
+      held_pg[j] = p;
+      held_ref[j] = p >= 0 ? s.ref[p] : 0;
+    }
   }
   __syncthreads();
   const int64_t k = sh.first_miss;
 
   // 2. hits that are evictable now will be pinned: count them for the OOM check
-  for (int64_t i = tid; i < k; i += kBmThreads)
-    if (s.ref[row[i]] == 0) atomicAdd(&sh.count, 1);
+  {
+    int32_t cnt = 0;
+    for (int64_t i = tid, j = 0; i < k; i += kBmThreads, ++j)
+      cnt += (j < kHeld ? held_ref[j] : s.ref[row[i]]) == 0;
+    if (cnt) atomicAdd(&sh.count, cnt);
+  }
   __syncthreads();
   const int64_t pinned = sh.count;
   const int64_t take = n_pages - k + (cow ? 1 : 0);
@@ -293,19 +319,30 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
     return;
   }
 
-  // 3. pin the hits
-  for (int64_t i = tid; i < k; i += kBmThreads) s.ref[row[i]] += 1;
+  // 3. pin the hits, for the parent and the forked child at once (+2)
+  for (int64_t i = tid, j = 0; i < k; i += kBmThreads, ++j) {
+    if (j < kHeld)
+      s.ref[held_pg[j]] = held_ref[j] + 2;
+    else
+      s.ref[row[i]] += 2;
+  }
   c.evictable -= pinned;
 
   // 4. take pages: the free stack's top first, then LRU victims in order. The
-  //    first n_pages-k go to the table, the last (if any) is the COW target.
+  //    first n_pages-k go to the table (held by parent and child: refcount 2,
+  //    except a partial last page, which the child copies: 1), the last (if
+  //    any) is the child's copy (refcount 1).
   const int64_t from_free = take < c.free_top ? take : c.free_top;
   const int64_t table_new = n_pages - k;
   for (int64_t j = tid; j < from_free; j += kBmThreads) {
     const int32_t p = s.free_list[c.free_top - 1 - j];
-    s.ref[p] = 1;
-    if (j < table_new) row[k + j] = p;
-    else a.cow_dst[r] = p;
+    if (j < table_new) {
+      row[k + j] = p;
+      s.ref[p] = (cow && k + j == n_pages - 1) ? 1 : 2;
+    } else {
+      a.cow_dst[r] = p;
+      s.ref[p] = 1;
+    }
   }
   c.free_top -= from_free;
   int64_t done = from_free;
@@ -325,15 +362,17 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
     int32_t total;
     const int32_t rank = block_rank(live, total, sh);
     const int64_t want = take - done;
-    const bool evict = live && rank < want;
-    if (evict) {
+    if (live && rank < want) {
       const int64_t j = done + rank;
-      int64_t slot;
-      if (tab_find(s, s.hash[pg], &slot) == pg) s.val[slot] = kTomb;
+      s.val[s.slot[pg]] = kTomb;  // the page's key leaves the table
       s.flag[pg] &= ~1;
-      s.ref[pg] = 1;
-      if (j < table_new) row[k + j] = pg;
-      else a.cow_dst[r] = pg;
+      if (j < table_new) {
+        row[k + j] = pg;
+        s.ref[pg] = (cow && k + j == n_pages - 1) ? 1 : 2;
+      } else {
+        a.cow_dst[r] = pg;
+        s.ref[pg] = 1;
+      }
       if (c.log_len + (j - from_free) < a.evict_cap)
         a.evict_log[c.log_len + (j - from_free)] = pg;
       if (rank == want - 1) sh.new_head = pos + 1;
@@ -347,26 +386,40 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
     done += got;
     __syncthreads();
   }
-  const int64_t evicted = done - from_free;
-  c.log_len += evicted;
-  __syncthreads();
+  c.log_len += done - from_free;
 
-  // 5. register the new full pages' hashes (unless already present)
-  for (int64_t i = k + tid; i < m; i += kBmThreads) {
-    const uint64_t h = a.hashes[h0 + i];
-    if (tab_find(s, h) < 0) {
+  // 5. register the new full pages' hashes unless already present. A key the
+  //    probe did not find is still absent (only evictions ran since); a key
+  //    it found is present unless its page was just evicted. All presence
+  //    checks of a chunk finish before any of its inserts (barrier), so no
+  //    check reads a page another lane is registering.
+  for (int64_t base = 0; base < m; base += (int64_t)kHeld * kBmThreads) {
+    bool reg[kHeld];
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      const int64_t i = base + tid + (int64_t)j * kBmThreads;
+      reg[j] = false;
+      if (i < m && i >= k) {
+        const uint64_t h = a.hashes[h0 + i];
+        const int32_t seen = base == 0 ? held_pg[j] : tab_find(s, h);
+        reg[j] = !(seen >= 0 && (s.flag[seen] & 1) && s.hash[seen] == h);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      if (!reg[j]) continue;
+      const int64_t i = base + tid + (int64_t)j * kBmThreads;
+      const uint64_t h = a.hashes[h0 + i];
       const int32_t p = row[i];
       s.hash[p] = h;
       s.flag[p] |= 1;
       if (tab_insert(s, h, p) == 1) atomicAdd(&sh.tomb_reused, 1);
     }
+    __syncthreads();
   }
-  __syncthreads();
   c.tombs -= sh.tomb_reused;
 
-  // 6. fork: the child shares every page but a copied partial last page
-  const int64_t shared = cow ? n_pages - 1 : n_pages;
-  for (int64_t i = tid; i < shared; i += kBmThreads) s.ref[row[i]] += 1;
   if (tid == 0) {
     a.hits[r] = (int32_t)k;
     a.status[r] = kStOk;
@@ -381,45 +434,17 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
   __syncthreads();
 }
 
-// Drops one table (child or parent), tail first: refcount -= 1; at zero a
-// cached page goes to the LRU's newest end, any other page onto the free stack.
-__device__ void release_table(const BmArgs& a, const int32_t* row, int64_t n_pages,
-                              int32_t last_override, Ctrs& c, Shared& sh) {
-  const BmState& s = a.s;
-  const int64_t qm = s.Q - 1;
-  if (c.tail - c.head + n_pages > s.Q) ring_compact(a, c, sh);
-  for (int64_t base = 0; base < n_pages; base += kBmThreads) {
-    const int64_t j = base + threadIdx.x;  // j-th page from the tail
-    bool to_lru = false, to_free = false;
-    int32_t page = 0;
-    if (j < n_pages) {
-      const int64_t i = n_pages - 1 - j;
-      page = (i == n_pages - 1 && last_override >= 0) ? last_override : row[i];
-      const int32_t left = --s.ref[page];
-      if (left == 0) {
-        to_lru = (s.flag[page] & 1) != 0;
-        to_free = !to_lru;
-      }
-    }
-    int32_t n_lru, n_free;
-    const int32_t rl = block_rank(to_lru, n_lru, sh);
-    const int32_t rf = block_rank(to_free, n_free, sh);
-    if (to_lru) {
-      const uint32_t st = (uint32_t)(c.next_stamp + rl);
-      s.ring_pg[(c.tail + rl) & qm] = page;
-      s.ring_st[(c.tail + rl) & qm] = st;
-      s.stamp[page] = st;
-    }
-    if (to_free) s.free_list[c.free_top + rf] = page;
-    c.tail += n_lru;
-    c.next_stamp += n_lru;
-    c.evictable += n_lru;
-    c.free_top += n_free;
-    __syncthreads();
-  }
-}
-
+// Releases a forked request in one pass. Sequentially that is the child's
+// table then the parent's, each from its last page: refcount -= 1; at zero a
+// cached page goes to the LRU's newest end, any other page onto the free
+// stack. The child shares every page of the parent except, after a
+// copy-on-write, the last (its own copy), so in one pass over the table from
+// the last page: the child's copy (if any) reaches zero first and goes to the
+// free stack; then every shared page loses both references at once, and the
+// parent's own partial last page (after a copy) loses one. Pages reach zero
+// in the same order as in the two sequential passes.
 __device__ void release(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
+  const BmState& s = a.s;
   const int32_t st = a.status[r];
   if (st != kStOk) {  // an OOM request holds nothing; anything else is a caller error
     if (st != kStOom && threadIdx.x == 0) raise_err(a.err, MKV_DEVERR_BM);
@@ -429,8 +454,47 @@ __device__ void release(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
   const int64_t n_pages = (n + 15) / 16;
   const bool cow = (n & 15) != 0;
   const int32_t* row = a.tables + (int64_t)r * a.tstride;
-  release_table(a, row, n_pages, cow ? a.child_last[r] : -1, c, sh);  // child
-  release_table(a, row, n_pages, -1, c, sh);                           // parent
+  const int64_t qm = s.Q - 1;
+  if (cow) {  // the child's private copy: uncached, refcount 1 -> free stack
+    if (threadIdx.x == 0) {
+      const int32_t p = a.child_last[r];
+      s.ref[p] = 0;
+      s.free_list[c.free_top] = p;
+    }
+    c.free_top += 1;
+  }
+  if (c.tail - c.head + n_pages > s.Q) ring_compact(a, c, sh);
+  for (int64_t base = 0; base < n_pages; base += kBmThreads) {
+    const int64_t j = base + threadIdx.x;  // j-th page from the tail
+    bool to_lru = false, to_free = false;
+    int32_t page = 0;
+    if (j < n_pages) {
+      const int64_t i = n_pages - 1 - j;
+      page = row[i];
+      const int32_t drop = (cow && i == n_pages - 1) ? 1 : 2;
+      const int32_t left = s.ref[page] - drop;
+      s.ref[page] = left;
+      if (left == 0) {
+        to_lru = (s.flag[page] & 1) != 0;
+        to_free = !to_lru;
+      }
+    }
+    int32_t n_lru, n_free;
+    const int32_t rl = block_rank(to_lru, n_lru, sh);
+    const int32_t rf = block_rank(to_free, n_free, sh);
+    if (to_lru) {
+      const uint32_t stamp = (uint32_t)(c.next_stamp + rl);
+      s.ring_pg[(c.tail + rl) & qm] = page;
+      s.ring_st[(c.tail + rl) & qm] = stamp;
+      s.stamp[page] = stamp;
+    }
+    if (to_free) s.free_list[c.free_top + rf] = page;
+    c.tail += n_lru;
+    c.next_stamp += n_lru;
+    c.evictable += n_lru;
+    c.free_top += n_free;
+    __syncthreads();
+  }
   if (threadIdx.x == 0) a.status[r] = kStReleased;
   __syncthreads();
 }
@@ -496,10 +560,10 @@ extern "C" int mkv_bm_layout(int32_t num_pages, int64_t* out) {
   MKV_REQUIRE(num_pages > 0 && num_pages <= (1 << 28) && out, MKV_E_INVALID,
               "mkv_bm_layout: bad arguments");
   const BmLayout l = bm_layout(num_pages);
-  const int64_t v[13] = {l.C,        l.Q,        l.off_ctr,   l.off_key,   l.off_val,
-                         l.off_ref,  l.off_flag, l.off_stamp, l.off_free,  l.off_hash,
-                         l.off_ring_pg, l.off_ring_st, l.bytes};
-  for (int i = 0; i < 13; ++i) out[i] = v[i];
+  const int64_t v[14] = {l.C,        l.Q,        l.off_ctr,   l.off_key,     l.off_val,
+                         l.off_ref,  l.off_flag, l.off_stamp, l.off_free,    l.off_hash,
+                         l.off_ring_pg, l.off_ring_st, l.off_slot, l.bytes};
+  for (int i = 0; i < 14; ++i) out[i] = v[i];
   return MKV_OK;
 }
 

@@ -7,8 +7,9 @@
 // page i, finalised with one constant padding block. A request's pages form a
 // dependent chain; requests are independent, so one lane walks one request
 // and a launch covers a whole batch of requests. The work is integer ALU and
-// latency bound (two chained compressions per page plus one to finalise),
-// not HBM bound.
+// latency bound, not HBM bound: per page two chained compressions, plus a
+// finalisation that runs interleaved with the next page's first compression,
+// while the next block's words are already being loaded.
 #include "mkv_device.h"
 
 namespace mkv {
@@ -34,20 +35,49 @@ __global__ __launch_bounds__(kThreads) void block_hash_kernel(const uint8_t* tok
     return;
   }
   const uint32_t* p = reinterpret_cast<const uint32_t*>(tokens + t0 * token_bytes);
-  const int blocks_per_page = token_bytes * 16 / 64;  // 2 for int64 ids, 1 for int32
+  const int64_t bpp = token_bytes * 16 / 64;  // 64-byte blocks per page: 2 (int64), 1 (int32)
+  const int64_t nblocks = pages * bpp;
   const uint64_t page_bytes = (uint64_t)token_bytes * 16u;
   Sha256 s;
   sha256_init(s);
-  for (int64_t i = 0; i < pages; ++i) {
-    for (int k = 0; k < blocks_per_page; ++k) {
-      uint32_t w[16];
+  // Block b+1's words are loaded while block b is compressed; a page's
+  // finalisation (one more compression of a copy of the state) runs
+  // interleaved with the next block's compression.
+  uint32_t next[16];
+  if (nblocks > 0) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) w[j] = bswap32(p[j]);
-      sha256_compress(s, w);
-      p += 16;
-    }
-    out[o0 + i] = sha256_final_aligned_u64(s, (uint64_t)(i + 1) * page_bytes);
+    for (int j = 0; j < 16; ++j) next[j] = p[j];
   }
+  Sha256 fin;
+  uint32_t pad[16];
+  bool pending = false;  // fin holds a page state awaiting its padding block
+  int64_t pending_page = 0;
+  for (int64_t b = 0; b < nblocks; ++b) {
+    uint32_t w[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = bswap32(next[j]);
+    if (b + 1 < nblocks) {
+      const uint32_t* q = p + 16 * (b + 1);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) next[j] = q[j];
+    }
+    if (pending) {
+      sha256_compress2(s, w, fin, pad);
+      out[o0 + pending_page] = ((uint64_t)fin.h[0] << 32) | fin.h[1];
+      pending = false;
+    } else {
+      sha256_compress(s, w);
+    }
+    if (bpp == 1 || (b & 1)) {  // block b ends a page
+      pending_page = bpp == 1 ? b : b >> 1;
+      fin = s;
+      sha256_pad_block(pad, (uint64_t)(pending_page + 1) * page_bytes);
+      pending = true;
+    }
+  }
+  if (pending)
+    out[o0 + pending_page] =
+        sha256_final_aligned_u64(fin, (uint64_t)(pending_page + 1) * page_bytes);
 }
 
 }  // namespace

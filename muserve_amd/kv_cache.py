@@ -325,10 +325,15 @@ class PagedKVCache:
     def copy_pages(self, src_pages, dst_pages) -> None:
         """For every pair, page dst := page src in all layers and both K and V
         (and the fp8 scales): the copy a copy-on-write fork needs. The dst set
-        must not overlap the src set."""
+        must not overlap the src set; a pair with a negative id is skipped."""
         dev = self._gpu()
-        src = _as_index(src_pages, dev).to(torch.int32).contiguous()
-        dst = _as_index(dst_pages, dev).to(torch.int32).contiguous()
+
+        def ids(x):
+            if isinstance(x, torch.Tensor) and x.dtype == torch.int32 and x.device == dev:
+                return x.contiguous()
+            return _as_index(x, dev).to(torch.int32).contiguous()
+
+        src, dst = ids(src_pages), ids(dst_pages)
         if src.numel() != dst.numel():
             raise ValueError("src_pages and dst_pages differ in length")
         n = src.numel()

@@ -52,6 +52,22 @@ def page_hashes(tokens: torch.Tensor, cu_tokens, errors: _lib.DeviceErrors | Non
     return out[:total], cu_p
 
 
+def page_hashes_range(tokens: torch.Tensor, tok_offsets: torch.Tensor,
+                      page_offsets: torch.Tensor, first: int, count: int, out: torch.Tensor,
+                      errors: _lib.DeviceErrors) -> None:
+    """Hashes requests first..first+count-1 with offsets already on the device
+    (tok_offsets/page_offsets: int64 [R+1], global indices into tokens and
+    out); no host work, no synchronisation."""
+    if count <= 0:
+        return
+    if first < 0 or first + count + 1 > tok_offsets.numel() or \
+            tok_offsets.numel() != page_offsets.numel():
+        raise IndexError("request range outside the offset arrays")
+    _lib.call("mkv_block_hash_sha256", tokens.data_ptr(), tok_offsets[first:].data_ptr(),
+              page_offsets[first:].data_ptr(), count, tokens.element_size(), out.data_ptr(),
+              errors.ptr(), _lib.stream_of(tokens.device))
+
+
 def as_u64(h: torch.Tensor) -> np.ndarray:
     """Device int64 bit patterns -> host numpy uint64."""
     return h.cpu().numpy().view(np.uint64)
