@@ -339,20 +339,25 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
     cache.check_errors()
     stream = torch.cuda.current_stream(dev)
 
+    # A step appends the chunk to every layer, then dequant-gathers every
+    # layer's window (each gather follows its own layer's append, as in a layer
+    # loop). One event pair brackets each group of 15 launches, so the mean
+    # launch time carries no per-launch event overhead.
     def one_step(i: int, rec=None):
+        if rec is not None:
+            a, b = _pair(stream)
         for l in range(L):
-            if rec is not None:
-                a, b = _pair(stream)
             cache.append(slots_dev[i], kin[i, l], vin[i, l], layer=l)
-            if rec is not None:
-                b.record(stream)
-                rec.append(("append", a, b))
-                a, b = _pair(stream)
+        if rec is not None:
+            b.record(stream)
+            rec.append(("append", a, b))
+            a, b = _pair(stream)
+        for l in range(L):
             cache.gather(l, bt, lens_dev[i], out_len=WIN, starts=starts_dev[i], out=(kbuf, vbuf),
                          cu_out=cu_out)
-            if rec is not None:
-                b.record(stream)
-                rec.append(("gather", a, b))
+        if rec is not None:
+            b.record(stream)
+            rec.append(("gather", a, b))
 
     for i in range(warmup):
         one_step(i)
@@ -381,9 +386,9 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
         "pct_of_hbm_peak": round(100 * step_bytes_ / step_s / 1e9 / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
             _kernel_roofline("append_fp8_kernel (mkv_append_fp8)", append_bytes,
-                             _timed(recs, "append")),
+                             _timed(recs, "append") / L),
             _kernel_roofline("gather_dequant_kernel<1> (mkv_gather_dequant_fp8)", gather_bytes,
-                             _timed(recs, "gather"))]},
+                             _timed(recs, "gather") / L)]},
     }
     if with_cpu:
         from oracle import fp8 as ref
@@ -405,13 +410,13 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
 
 
 def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
-    """Decode step of the hybrid stack: 45 GDN layers gather their 256 active
-    requests' recurrent [8,128,128] fp32 + conv [2048,4] bf16 states from a
-    1024-slot pool (seeded permuted slots), apply a synthetic update (+1, timed
-    apart) and scatter them back; the 15 attention layers append one decode
-    token per request (the headline workload's appends)."""
+    """Decode step of the hybrid stack: the 256 active requests' recurrent
+    [8,128,128] fp32 + conv [2048,4] bf16 states of all 45 GDN layers are
+    gathered from a 1024-slot pool (seeded permuted slots), updated (a
+    synthetic +1, timed apart) and scattered back; the 15 attention layers
+    append one decode token per request (the headline workload's appends)."""
     from muserve_amd.kv_cache import BlockTables, PagedKVCache, SequenceKVState, reserve_tokens
-    from muserve_amd.state_pool import StatePool, gdn_ordinal
+    from muserve_amd.state_pool import StatePool
 
     dev = torch.device("cuda:0")
     S, G = 1024, 45
@@ -433,34 +438,38 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     bt = BlockTables(cache, seqs, max_pages=int(-(-(int(ctx.max()) + total) // 16)))
     kin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
     vin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
-    sbuf = torch.empty((B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
-    cbuf = torch.empty((B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+    # the step's working set: every GDN layer's states of the batch, contiguous
+    sbuf = torch.empty((G, B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
+    cbuf = torch.empty((G, B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
     stream = torch.cuda.current_stream(dev)
 
+    # A decode step gathers the batch's states of all 45 GDN layers into the
+    # working set, updates them (a synthetic +1 stands in for the recurrence),
+    # and scatters them back, besides one KV append per attention layer. One
+    # event pair brackets each phase of 45 launches, so the mean launch time
+    # carries no per-launch event overhead.
     def one_step(i: int, rec=None):
         kv_slots = bt.decode_step()
-        for layer in range(60):
-            if layer % 4 == 3:
-                a = layer // 4
-                cache.append(kv_slots, kin[i, a], vin[i, a], layer=a)
-                continue
-            g = gdn_ordinal(layer)
-            ev = _pair(stream) if rec is not None else None
-            pool.gather(g, slots, out=(sbuf, cbuf))
-            if rec is not None:
-                ev[1].record(stream)
-                rec.append(("gather",) + ev)
-                ev = _pair(stream)
-            sbuf.add_(1.0)
-            cbuf.add_(1.0)
-            if rec is not None:
-                ev[1].record(stream)
-                rec.append(("update",) + ev)
-                ev = _pair(stream)
-            pool.scatter(g, slots, sbuf, cbuf)
-            if rec is not None:
-                ev[1].record(stream)
-                rec.append(("scatter",) + ev)
+        for a in range(LAYERS):
+            cache.append(kv_slots, kin[i, a], vin[i, a], layer=a)
+        ev = _pair(stream) if rec is not None else None
+        for g in range(G):
+            pool.gather(g, slots, out=(sbuf[g], cbuf[g]))
+        if rec is not None:
+            ev[1].record(stream)
+            rec.append(("gather",) + ev)
+            ev = _pair(stream)
+        sbuf.add_(1.0)
+        cbuf.add_(1.0)
+        if rec is not None:
+            ev[1].record(stream)
+            rec.append(("update",) + ev)
+            ev = _pair(stream)
+        for g in range(G):
+            pool.scatter(g, slots, sbuf[g], cbuf[g])
+        if rec is not None:
+            ev[1].record(stream)
+            rec.append(("scatter",) + ev)
 
     for i in range(warmup):
         one_step(i)
@@ -475,7 +484,8 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     cache.check_errors()
     entry = 8 * 128 * 128 * 4 + 2048 * 4 * 2
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
-    g_ms, s_ms, u_ms = _timed(recs, "gather"), _timed(recs, "scatter"), _timed(recs, "update")
+    g_ms, s_ms = _timed(recs, "gather") / G, _timed(recs, "scatter") / G
+    u_ms = _timed(recs, "update")
     state_s = G * (g_ms + s_ms) / 1e3
     step_s = elapsed / steps
     per_step_state = 4 * G * B * entry
@@ -486,11 +496,11 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32+bf16",
         "data": "synthetic (seeded ~N(0,1) states, seeded permuted slots)",
         "config": {"workload": ("GDN state slots at decode: 45 layers x [8,128,128] fp32 + "
-                                "[2048,4] bf16, 1024-slot pool, batch 256, gather -> +1 -> "
-                                "scatter, interleaved with decode appends on 15 attention "
-                                "layers; seed 105")},
+                                "[2048,4] bf16, 1024-slot pool, batch 256: per decode step "
+                                "gather all layers -> +1 -> scatter all layers, plus decode "
+                                "appends on 15 attention layers; seed 105")},
         "state_move_ms_per_step": round(state_s * 1e3, 3),
-        "synthetic_update_ms_per_step": round(G * u_ms, 3),
+        "synthetic_update_ms_per_step": round(u_ms, 3),
         "pct_of_hbm_peak": round(100 * per_step_state / state_s / 1e9 / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
             _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms),

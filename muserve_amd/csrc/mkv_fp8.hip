@@ -1,12 +1,13 @@
 // mkv_fp8.hip — bf16 -> fp8 e4m3fn quantize-on-append and fp8 -> bf16
 // dequant-gather for gfx950.
 //
-// A quantisation row is one (token, head) of head_dim = 256 bf16 values. A
-// half-wave (32 lanes) owns a row at a time: each lane holds 16 bytes (8
-// values), the row absmax is a 5-step xor-shuffle reduction inside the
-// half-wave, and each lane stores 8 fp8 bytes, so the 256-byte fp8 row is one
-// coalesced 8-byte-per-lane store. Each half-wave takes 4 rows and loads all
-// of them before quantising any, to keep enough bytes in flight.
+// A quantisation row is one (token, head) of head_dim = 256 bf16 values. 16
+// lanes own a row: each lane loads 32 bytes (16 values), the row absmax is a
+// 4-step xor-shuffle inside the 16 lanes, and each lane stores its 16 codes
+// with one 16-byte store, so the 256-byte fp8 row is one coalesced store and
+// the row's scale one 4-byte store by the group's first lane. On the
+// chunked-prefill shape this runs as fast as a plain scattered copy of the
+// same bytes: the arithmetic is hidden under the memory traffic.
 //
 // Exactness: the scale is a correctly rounded fp32 division (hipcc keeps
 // division correctly rounded unless fast-math is requested, and this library
@@ -23,6 +24,8 @@ namespace mkv {
 namespace {
 
 constexpr int kHeadDim = 256;
+constexpr int kLanesPerRow = 16;                         // lanes per quantisation row
+constexpr int kRowsPerWg = kThreads / kLanesPerRow;      // 16 rows per workgroup
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -57,149 +60,164 @@ __device__ __forceinline__ float clamp448(float x) {
   return x < -448.0f ? -448.0f : (x > 448.0f ? 448.0f : x);
 }
 
-// Quantises one 256-value row held as 8 values per lane of a half-wave and
-// returns the lane's 8 codes packed in two words, plus the row's scale.
-__device__ __forceinline__ void quantise_row(const u32x4 raw, uint32_t& lo, uint32_t& hi,
-                                             float& scale_out) {
-  float x[8];
-  x[0] = bf16_lo(raw.x); x[1] = bf16_hi(raw.x);
-  x[2] = bf16_lo(raw.y); x[3] = bf16_hi(raw.y);
-  x[4] = bf16_lo(raw.z); x[5] = bf16_hi(raw.z);
-  x[6] = bf16_lo(raw.w); x[7] = bf16_hi(raw.w);
+// Quantises one 256-value row held as 16 values per lane of a 16-lane group
+// and returns the lane's 16 codes, plus the row's scale.
+__device__ __forceinline__ u32x4 quantise_row(const u32x4 r0, const u32x4 r1, float& scale_out) {
+  const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    x[2 * i] = bf16_lo(w[i]);
+    x[2 * i + 1] = bf16_hi(w[i]);
+  }
   // absmax over the row. On |x| bit patterns integer max is float max, and
   // any NaN (above +inf as an integer) wins, as torch's amax propagates NaN.
   uint32_t m = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 16; ++i) {
     const uint32_t ab = f32_bits(x[i]) & 0x7fffffffu;
     m = ab > m ? ab : m;
   }
 #pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)m, off, 32);
+  for (int off = kLanesPerRow / 2; off >= 1; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)m, off, kLanesPerRow);
     m = o > m ? o : m;
   }
   const float amax = bits_f32(m);
   const float clamped = amax < 1e-12f ? 1e-12f : amax;  // .clamp(min=1e-12); NaN stays
   const float scale = clamped / 448.0f;
   const float recip = 1.0f / scale;
-  float q[8];
+  float q[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = clamp448(div_by_recip(x[i], scale, recip));
-  int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-  w0 = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w0, true);
-  int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
-  w1 = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], w1, true);
-  lo = (uint32_t)w0;
-  hi = (uint32_t)w1;
+  for (int i = 0; i < 16; ++i) q[i] = clamp448(div_by_recip(x[i], scale, recip));
+  uint32_t c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i], q[4 * i + 1], 0, false);
+    c[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * i + 2], q[4 * i + 3], lo, true);
+  }
   scale_out = scale;
+  return u32x4{c[0], c[1], c[2], c[3]};
 }
 
-// A half-wave quantises kRowsPerHalfWave consecutive (token, head) rows of
-// one (layer, K|V): all their loads are issued first, so each lane keeps four
-// 16-byte loads in flight.
-constexpr int kRowsPerHalfWave = 4;
-constexpr int kRowsPerWg = (kThreads / 32) * kRowsPerHalfWave;  // 32 rows per workgroup
-
+// One 16-lane group per (token, head) row of one (layer, K|V): grid.x covers
+// the rows, grid.y is layer * 2 + K|V. The slot and both source loads are
+// issued together; a group whose row is past the end exits as a whole, so the
+// shuffles only ever read lanes of the same live row.
 __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
-  const uint32_t lane = threadIdx.x & 31u;
-  const uint32_t row0 = blockIdx.x * kRowsPerWg + (threadIdx.x >> 5) * kRowsPerHalfWave;
-  const uint32_t lkv = blockIdx.y;
-  const uint32_t l = lkv >> 1;
-  const bool is_v = lkv & 1u;
-  const uint8_t* src_base = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride;
-  int64_t slot[kRowsPerHalfWave];
-  u32x4 raw[kRowsPerHalfWave];
-#pragma unroll
-  for (int k = 0; k < kRowsPerHalfWave; ++k) {
-    const uint32_t row = row0 + k;
-    slot[k] = -1;
-    raw[k] = u32x4{0u, 0u, 0u, 0u};
-    if (row < a.num_rows) {
-      const uint32_t t = row / a.num_heads;
-      const uint32_t h = row - t * a.num_heads;
-      slot[k] = a.slots[t];
-      raw[k] = ld16(src_base + (int64_t)t * a.src_token_stride + (int64_t)h * (kHeadDim * 2) +
-                    lane * 16);
-    }
+  const uint32_t lane = threadIdx.x & (kLanesPerRow - 1);
+  const uint32_t row = blockIdx.x * kRowsPerWg + threadIdx.x / kLanesPerRow;
+  if (row >= a.num_rows) return;
+  const uint32_t l = blockIdx.y >> 1;
+  const bool is_v = blockIdx.y & 1u;
+  const uint32_t t = row / a.num_heads;
+  const uint32_t h = row - t * a.num_heads;
+  const int64_t slot = a.slots[t];
+  const uint8_t* src = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride +
+                       (int64_t)t * a.src_token_stride + (int64_t)h * (kHeadDim * 2) + lane * 32;
+  const u32x4 r0 = ld16(src), r1 = ld16(src + 16);
+  if (slot < 0 || slot >= a.num_slots) {  // -1 skips the token; anything else is an error
+    if (slot != -1 && lane == 0 && h == 0 && !is_v) raise_err(a.err, MKV_DEVERR_SLOT);
+    return;
   }
-  const int64_t row_bytes = (int64_t)a.num_heads * kHeadDim;  // fp8 row of all heads
+  float scale;
+  const u32x4 codes = quantise_row(r0, r1, scale);
   uint8_t* pool = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
-  float* sp = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(is_v ? a.v_scale : a.k_scale) +
-                                       (int64_t)l * a.scale_layer_stride);
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-  for (int k = 0; k < kRowsPerHalfWave; ++k) {
-    const uint32_t row = row0 + k;
-    if (row >= a.num_rows) break;  // the half-wave's rows run out together
-    const uint32_t t = row / a.num_heads;
-    const uint32_t h = row - t * a.num_heads;
-    if (slot[k] < 0 || slot[k] >= a.num_slots) {
-      if (slot[k] != -1 && lane == 0 && h == 0 && !is_v) raise_err(a.err, MKV_DEVERR_SLOT);
-      continue;
-    }
-    uint32_t lo, hi;
-    float scale;
-    quantise_row(raw[k], lo, hi, scale);
-    *reinterpret_cast<u32x2*>(pool + slot[k] * row_bytes + (int64_t)h * kHeadDim + lane * 8) =
-        u32x2{lo, hi};
-    if (lane == 0) sp[slot[k] * a.num_heads + h] = scale;
+  st16(pool + slot * ((int64_t)a.num_heads * kHeadDim) + (int64_t)h * kHeadDim + lane * 16, codes);
+  if (lane == 0) {
+    float* sp = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(is_v ? a.v_scale : a.k_scale) +
+                                         (int64_t)l * a.scale_layer_stride);
+    sp[slot * a.num_heads + h] = scale;
   }
 }
 
 // ---------------------------------------------------------------------------
 // dequant-gather: the bf16 gather's tiles with fp8 rows in and bf16 rows out
-// (the padding tiles go to the shared gather_pad_kernel). A thread turns 8
-// fp8 bytes and its head's scale into 16 output bytes.
+// (the padding tiles go to the shared gather_pad_kernel). A tile is 4096 fp8
+// codes (16 rows of one head, 8 rows of two) and 8 KiB of output; each wave
+// owns a contiguous quarter. A lane loads two runs of 8 codes 512 codes apart
+// (8-byte non-temporal loads) and writes each as one 16-byte bf16 store, so
+// every store instruction of a wave covers 1 KiB of output without gaps.
+// Against one 16-byte load and two 16-byte stores per lane (stride-32 store
+// addresses), this is 1.3x faster on MI355X; the loads stay non-temporal, the
+// stores stay ordinary (both measured faster than the alternatives here).
 // ---------------------------------------------------------------------------
-// One thread per 16 fp8 bytes (one 16-byte load, two 16-byte stores) and 256
-// threads per tile: the shape that streamed fastest on MI355X.
 constexpr int kDequantThreads = 256;
+constexpr int kDequantTileCodes = 4096;
 
 template <int HEADS>
 __global__ __launch_bounds__(kDequantThreads) void gather_dequant_kernel(GatherArgs a) {
-  constexpr int OUT_ROW = HEADS * kHeadDim * 2;  // bf16 bytes per output row
-  constexpr int IN_ROW = HEADS * kHeadDim;       // fp8 bytes per pool row
-  constexpr int RC = IN_ROW / 16;                // 16-byte fp8 chunks per row
-  constexpr int ROWS = kDequantThreads / RC;     // one chunk per thread
+  constexpr int IN_ROW = HEADS * kHeadDim;           // fp8 bytes per pool row
+  constexpr int OUT_ROW = 2 * IN_ROW;                // bf16 bytes per output row
+  constexpr int ROWS = kDequantTileCodes / IN_ROW;   // rows per tile
+  constexpr int WAVE_CODES = kDequantTileCodes / (kDequantThreads / 64);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   GatherTile<ROWS> t;
   t.init(a);
   if (t.row0 >= t.nvalid) return;  // padding tile: gather_pad_kernel's
   t.locate(a);
   t.load_pages(a);
-  const int col = threadIdx.x % RC;
-  const int head = col / (kHeadDim / 16);
-  const int r = threadIdx.x / RC;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = wave * WAVE_CODES + lane * 8;     // first run's code index in the tile
+  const int c1 = c0 + WAVE_CODES / 2;              // second run
+  const int r0 = c0 / IN_ROW, r1 = c1 / IN_ROW;    // tile rows of the two runs
+  const int col = c0 % IN_ROW;                     // same column for both runs
+  const int head = col / kHeadDim;
   const uint8_t* plane = (t.is_v ? a.v_pool : a.k_pool) + (int64_t)t.layer * a.pool_layer_stride;
   const float* splane = reinterpret_cast<const float*>(
       reinterpret_cast<const uint8_t*>(t.is_v ? a.v_scale : a.k_scale) +
       (int64_t)t.layer * a.scale_layer_stride);
   uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
-                 (t.out_row + r) * OUT_ROW + col * 32;
-  u32x4 o0 = u32x4{0u, 0u, 0u, 0u}, o1 = o0;
-  if (t.row0 + r < t.nvalid) {
-    const int64_t p = t.p0 + r;
+                 t.out_row * OUT_ROW;
+  u32x2 q0 = u32x2{0u, 0u}, q1 = q0;
+  float s0 = 0.0f, s1 = 0.0f;
+  if (t.full_data()) {
+    const int64_t p0 = t.p0 + r0, p1 = t.p0 + r1;
+    const int64_t slot0 = (int64_t)t.page_of(p0) * 16 + (p0 & 15);
+    const int64_t slot1 = (int64_t)t.page_of(p1) * 16 + (p1 & 15);
+    q0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(plane + slot0 * IN_ROW + col));
+    q1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(plane + slot1 * IN_ROW + col));
+    s0 = splane[slot0 * HEADS + head];
+    s1 = splane[slot1 * HEADS + head];
+    st16(out + 2 * c0, u32x4{dequant2(q0.x, false, s0), dequant2(q0.x, true, s0),
+                             dequant2(q0.y, false, s0), dequant2(q0.y, true, s0)});
+    st16(out + 2 * c1, u32x4{dequant2(q1.x, false, s1), dequant2(q1.x, true, s1),
+                             dequant2(q1.y, false, s1), dequant2(q1.y, true, s1)});
+    return;
+  }
+  // Last data tile (or one with a bad page id): rows past the data are zeros.
+  if (t.row0 + r0 < t.nvalid) {
+    const int64_t p = t.p0 + r0;
     const int32_t page = t.page_of(p);
     if (page >= 0) {
       const int64_t slot = (int64_t)page * 16 + (p & 15);
-      const u32x4 q = ld_nt(plane + slot * IN_ROW + col * 16);
-      const float s = splane[slot * HEADS + head];
-      o0 = u32x4{dequant2(q.x, false, s), dequant2(q.x, true, s), dequant2(q.y, false, s),
-                 dequant2(q.y, true, s)};
-      o1 = u32x4{dequant2(q.z, false, s), dequant2(q.z, true, s), dequant2(q.w, false, s),
-                 dequant2(q.w, true, s)};
+      q0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(plane + slot * IN_ROW + col));
+      s0 = splane[slot * HEADS + head];
     }
   }
-  if (t.row0 + r < (a.out_offsets ? t.nvalid : a.out_len)) {
-    st_nt(out, o0);
-    st_nt(out + 16, o1);
+  if (t.row0 + r1 < t.nvalid) {
+    const int64_t p = t.p0 + r1;
+    const int32_t page = t.page_of(p);
+    if (page >= 0) {
+      const int64_t slot = (int64_t)page * 16 + (p & 15);
+      q1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(plane + slot * IN_ROW + col));
+      s1 = splane[slot * HEADS + head];
+    }
   }
+  // A zero code times a zero scale is +0, the bytes of a zero row.
+  const int64_t row_limit = a.out_offsets ? t.nvalid : a.out_len;
+  if (t.row0 + r0 < row_limit)
+    st16(out + 2 * c0, u32x4{dequant2(q0.x, false, s0), dequant2(q0.x, true, s0),
+                             dequant2(q0.y, false, s0), dequant2(q0.y, true, s0)});
+  if (t.row0 + r1 < row_limit)
+    st16(out + 2 * c1, u32x4{dequant2(q1.x, false, s1), dequant2(q1.x, true, s1),
+                             dequant2(q1.y, false, s1), dequant2(q1.y, true, s1)});
 }
 
 template <int HEADS>
 int launch_dequant(const GatherArgs& a, int32_t num_layers, hipStream_t stream) {
   constexpr int OUT_ROW = HEADS * kHeadDim * 2;
-  constexpr int ROWS = kDequantThreads / (HEADS * kHeadDim / 16);
+  constexpr int ROWS = kDequantTileCodes / (HEADS * kHeadDim);
   if (!a.out_offsets)
     hipLaunchKernelGGL((gather_pad_kernel<OUT_ROW, ROWS>), pad_grid(a, OUT_ROW, num_layers),
                        dim3(kPadThreads), 0, stream, a);

@@ -75,6 +75,29 @@ def test_append_fp8_nan_rows_stay_nan():
     assert torch.isnan(cache.scales[0, 0, 0, 0]).item()
 
 
+def test_append_fp8_skip_and_bad_slots():
+    case("fp8 append: slot -1 skips, out-of-range slot flagged, 2 heads")
+    from muserve_amd import _lib
+    g = torch.Generator().manual_seed(5)
+    cache = PagedKVCache(4, num_layers=1, kv_heads=2, dtype=torch.float8_e4m3fn, device=DEV,
+                         verbose=False)
+    x = outlier_kv(g, (3, 2, 256))
+    cache.append(torch.tensor([5, -1, 63], device=DEV), x.to(DEV), x.to(DEV), layer=0)
+    cache.check_errors()
+    q, s = ref.quantize_rows(x)
+    pool = cache.cache.view(torch.uint8)[0, 0].reshape(64, 2, 256).cpu()
+    scales = cache.scales[0, 0].reshape(64, 2).cpu()
+    assert torch.equal(pool[5], q[0]) and torch.equal(pool[63], q[2])
+    assert torch.equal(scales[5].view(torch.int32), s[0].view(torch.int32))
+    untouched = torch.ones(64, dtype=torch.bool)
+    untouched[[5, 63]] = False
+    assert pool[untouched].sum().item() == 0 and scales[untouched].abs().sum().item() == 0
+    cache.append(torch.tensor([7, 64], device=DEV), x[:2].to(DEV), x[:2].to(DEV), layer=0)
+    with pytest.raises(_lib.MkvDeviceError, match="slot_mapping"):
+        cache.check_errors()
+    assert torch.equal(cache.cache.view(torch.uint8)[0, 1].reshape(64, 2, 256)[7].cpu(), q[0])
+
+
 def test_chunked_prefill_then_dequant_gather_window():
     """Chunks appended into long contexts, then the last N tokens of every
     request dequant-gathered to bf16 (a scaled-down fp8 chunked-prefill case)."""
@@ -123,6 +146,50 @@ def test_chunked_prefill_then_dequant_gather_window():
             want = pref.gather_padded(plane, bt, sl, N, starts)
             assert torch.equal(bits16(got), want.view(torch.int16)), (l, kv)
     cache.check_errors()
+
+
+@pytest.mark.parametrize("H", [1, 2])
+@pytest.mark.parametrize("packed", [False, True])
+def test_dequant_gather_ragged(H, packed):
+    """Ragged lengths (0, partial tiles, longer than out_len, unaligned window
+    starts) in the padded and the packed layout, one and two heads."""
+    case(f"fp8 dequant-gather ragged H={H} packed={packed}")
+    from muserve_amd import _lib
+    g = torch.Generator().manual_seed(31 + H)
+    rng = np.random.default_rng(31 + H)
+    P, L = 48, 2
+    cache = PagedKVCache(P, num_layers=L, kv_heads=H, dtype=torch.float8_e4m3fn, device=DEV,
+                         verbose=False)
+    x = outlier_kv(g, (L, P * 16, H, 256))
+    cache.append(torch.arange(P * 16, device=DEV), x.to(DEV), outlier_kv(g, x.shape).to(DEV))
+    lens = torch.tensor([0, 1, 15, 16, 17, 100, 161, 200], dtype=torch.int32)
+    starts = torch.tensor([0, 0, 3, 0, 1, 40, 7, 9], dtype=torch.int32)
+    out_len = 150
+    W = 13
+    bt = torch.from_numpy(rng.integers(0, P, size=(lens.numel(), W)).astype(np.int32))
+    win = torch.clamp(torch.minimum(lens - starts, torch.tensor(out_len)), min=0)
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(win.to(torch.int64), 0)])
+    kd, vd = cache.gather(None, bt.to(DEV), lens.to(DEV), out_len=out_len, starts=starts.to(DEV),
+                          num_layers=L, cu_out=cu.to(DEV) if packed else None)
+    cache.check_errors()
+    qpool = cache.cache.view(torch.uint8).cpu()
+    spool = cache.scales.cpu()
+    for l in range(L):
+        for kv, got in ((0, kd[l]), (1, vd[l])):
+            deq = ref.dequant_rows(qpool[l, kv].reshape(P * 16, H, 256),
+                                   spool[l, kv].reshape(P * 16, H))
+            want = pref.gather_padded(deq.view(P, 16, H, 256), bt, lens, out_len, starts)
+            if packed:
+                want = torch.cat([want[b, :int(win[b])] for b in range(lens.numel())])
+            assert torch.equal(bits16(got), want.view(torch.int16)), (l, kv)
+    bad = bt.clone()
+    bad[5, 4] = P + 3  # a page id past the pool: its rows come back as zeros
+    kd, _ = cache.gather(0, bad.to(DEV), lens.to(DEV), out_len=out_len, starts=starts.to(DEV))
+    with pytest.raises(_lib.MkvDeviceError, match="page id"):
+        cache.check_errors()
+    rows = torch.arange(out_len) + int(starts[5])
+    on_bad = (rows // 16 == 4) & (rows < int(lens[5]))
+    assert on_bad.any() and kd[5, on_bad.nonzero().squeeze(1)].cpu().float().abs().sum().item() == 0
 
 
 def test_hardware_conversions_and_divide_match_cpu_semantics():
