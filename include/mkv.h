@@ -239,16 +239,21 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * The state is one caller-owned device buffer of mkv_bm_state_bytes(P) bytes
  * (256-byte aligned), initialised by mkv_bm_init with the free stack
  * free_order[0..P) (popped from the end; NULL = 0..P-1). mkv_bm_layout
- * writes 14 int64: table capacity C, ring capacity Q, then the byte offsets of
- * counters, table keys, table values, refcounts, flags, stamps, free stack,
- * page hashes, ring pages, ring stamps, key slots, and the total size.
+ * writes 8 int64: table capacity C, ring capacity Q, then the byte offsets of
+ * the counters (16 int64: free-stack top, ring head, ring tail, next stamp,
+ * evictable pages, tombstones, eviction-log length), the table (C entries of
+ * {u64 key, i32 page}), the page records (P x 32 bytes: i32 refcount, i32
+ * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
+ * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), and the
+ * total size.
  *
  * mkv_bm_step runs ops[0..num_ops) in order on one workgroup: op r >= 0
  * admits request r, op -(r+1) releases it (r < num_requests, the length of
  * the per-request arrays; hash_offsets has num_requests+1 entries, tables
  * num_requests rows). Request r has num_tokens[r]
  * tokens whose floor(n/16) page hashes are page_hashes[hash_offsets[r] ..
- * hash_offsets[r+1]). Admit:
+ * hash_offsets[r+1]); the hashes of one request must be distinct (prefix
+ * hashes of different lengths are). Admit:
  *   k = number of leading page hashes found in the table;
  *   take = ceil(n/16) - k + (n % 16 != 0); if take > free + evictable - (hits
  *     now evictable): status OOM, nothing changes;

@@ -51,9 +51,11 @@ class BlockManager:
         nbytes = lib.mkv_bm_state_bytes(num_pages)
         if nbytes <= 0:
             raise ValueError(f"bad page count {num_pages}")
-        lay = (ctypes.c_int64 * 14)()
+        lay = (ctypes.c_int64 * 8)()
         _lib.call("mkv_bm_layout", num_pages, ctypes.addressof(lay))
-        self.layout = list(lay)
+        # table capacity, ring capacity, byte offsets of counters, table, page
+        # records, free stack, ring; total bytes
+        self.layout = dict(zip(("C", "Q", "ctr", "ent", "rec", "free", "ring", "bytes"), lay))
         self.state = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         if self.state.data_ptr() % 256:
             raise RuntimeError("state buffer is not 256-byte aligned")
@@ -114,30 +116,32 @@ class BlockManager:
         self.errors.check("BlockManager")
 
     # -- inspection (synchronises) --
-    def _arr(self, idx: int, count: int, dtype: torch.dtype) -> torch.Tensor:
-        off = self.layout[idx]
+    def _arr(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:
+        off = self.layout[name]
         esz = torch.empty((), dtype=dtype).element_size()
         return self.state[off:off + count * esz].view(dtype)
 
     def counters(self) -> list[int]:
-        return self._arr(2, 16, torch.int64).cpu().tolist()
+        return self._arr("ctr", 16, torch.int64).cpu().tolist()
 
     def snapshot(self) -> dict:
         """Host copy of the bookkeeping: free stack (bottom..top), live LRU
         order (oldest first), refcounts, cached flags, page hashes (u64)."""
-        P, Q = self.num_pages, self.layout[1]
+        P, Q = self.num_pages, self.layout["Q"]
         ctr = self.counters()
-        ref = self._arr(5, P, torch.int32).cpu().numpy()
-        flag = self._arr(6, P, torch.int32).cpu().numpy()
-        stamp = self._arr(7, P, torch.int32).cpu().numpy().view(np.uint32)
-        free = self._arr(8, P, torch.int32).cpu().numpy()[:ctr[_FREE_TOP]]
-        phash = self._arr(9, P, torch.int64).cpu().numpy().view(np.uint64)
-        rpg = self._arr(10, Q, torch.int32).cpu().numpy()
-        rst = self._arr(11, Q, torch.int32).cpu().numpy().view(np.uint32)
+        # page record: i32 ref, i32 flag, u32 stamp, i32 table slot, u64 hash, u64 unused
+        rec = self._arr("rec", P * 8, torch.int32).cpu().numpy().reshape(P, 8)
+        ref, flag = rec[:, 0], rec[:, 1]
+        stamp = rec[:, 2].view(np.uint32)
+        phash = rec.view(np.uint64).reshape(P, 4)[:, 2]
+        free = self._arr("free", P, torch.int32).cpu().numpy()[:ctr[_FREE_TOP]]
+        ring = self._arr("ring", Q, torch.int64).cpu().numpy().view(np.uint64)
+        rpg = (ring & 0xFFFFFFFF).astype(np.int64)
+        rst = (ring >> 32).astype(np.int64)
         lru = []
         for pos in range(ctr[_HEAD], ctr[_TAIL]):
             pg, st = int(rpg[pos % Q]), int(rst[pos % Q])
-            if flag[pg] & 1 and ref[pg] == 0 and stamp[pg] == st:
+            if flag[pg] & 1 and ref[pg] == 0 and int(stamp[pg]) == st:
                 lru.append(pg)
         cached = flag & 1
         return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(),

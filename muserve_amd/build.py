@@ -26,12 +26,14 @@ ARCH = "gfx950"
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (some forms have given
 # wrong results on this hardware). No fast-math anywhere: the fp8 quantiser
-# relies on correctly rounded fp32 division.
+# relies on correctly rounded fp32 division. -fno-strict-aliasing: kernels read
+# byte buffers and packed records through vector types.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
+    "-fno-strict-aliasing",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",

@@ -8,21 +8,38 @@
 // refcount updates are one lane per page, and allocation / release positions
 // come from wavefront ballots + popcount prefix ranks.
 //
+// A request costs a few dependent memory round trips, so the layout keeps
+// that chain short:
+//   * a table entry holds key and page id in 16 bytes: one load per probe step;
+//   * a page's refcount, flags, LRU stamp and the table slot of its key are the
+//     first 16 bytes of its 32-byte record: one load tells whether the page is
+//     evictable and where its key lives;
+//   * an LRU ring entry is one 8-byte (page, stamp) pair;
+//   * the ops' request metadata is staged in LDS, the next request's page
+//     hashes are loaded while the current request runs, and the free-stack
+//     entries a request may take are loaded with its probe;
+//   * the probe remembers where a missing key would go, so registering it is
+//     one compare-and-swap;
+//   * the number of hits that leave the LRU comes from per-wave ballots kept
+//     in LDS, without another reduction.
+//
 // State (one caller-owned device buffer, layout from bm_layout):
 //   counters  free_top, ring head/tail, next stamp, #evictable, tombstones,
 //             eviction-log length
-//   table     open addressing, linear probing: key[C] u64, val[C] i32
-//             (-1 empty, -2 tombstone, -3 being written, >= 0 page id);
-//             rebuilt when tombstones exceed C/4
-//   per page  ref[P], flag[P] (bit 0: cached), stamp[P], hash[P], slot[P]
-//             (the table slot of a cached page's key, so eviction needs no probe)
+//   table     ent[C] {u64 key, i32 page (-1 empty, -2 tombstone, -3 being
+//             written), i32 unused}: open addressing, linear probing; rebuilt
+//             when tombstones exceed C/4
+//   pages     rec[P] {i32 ref, i32 flag (bit 0: cached), u32 stamp, i32 table
+//             slot of the page's key, u64 hash, u64 unused}
 //   free      stack free[P] (pop from the top, like PagedKVCache.alloc_pages)
-//   LRU       ring of (page, stamp) entries with lazy deletion: an entry is
+//   LRU       ring[Q] of page | stamp << 32 with lazy deletion: an entry is
 //             live iff its page is cached, unreferenced and still carries that
 //             stamp, so a page re-released later simply gets a newer entry —
 //             exactly OrderedDict's move-to-end; eviction takes live entries
 //             from the head (popitem(last=False)). Compacted in place (ballot
 //             ranks) when full.
+#include <climits>
+
 #include "mkv_device.h"
 
 namespace mkv {
@@ -30,16 +47,20 @@ namespace {
 
 constexpr int kBmThreads = 1024;
 constexpr int kBmWaves = kBmThreads / 64;
+constexpr int kOpChunk = 1024;  // ops whose request metadata is staged in LDS at once
+// Page hashes (and probe results) a thread keeps in registers: pages
+// tid + j*kBmThreads for j < kHeld. Longer requests re-read the rest.
+constexpr int kHeld = 2;
 
 enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen, kNumCtr = 16 };
 enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
 
 constexpr int32_t kEmpty = -1, kTomb = -2, kBusy = -3;
+constexpr int64_t kEntBytes = 16, kRecBytes = 32;
 
 struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
-  int64_t off_ctr, off_key, off_val, off_ref, off_flag, off_stamp, off_free, off_hash, off_ring_pg,
-      off_ring_st, off_slot, bytes;
+  int64_t off_ctr, off_ent, off_rec, off_free, off_ring, bytes;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -59,32 +80,20 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
     return at;
   };
   l.off_ctr = take(kNumCtr * 8);
-  l.off_key = take(l.C * 8);
-  l.off_val = take(l.C * 4);
-  l.off_ref = take((int64_t)P * 4);
-  l.off_flag = take((int64_t)P * 4);
-  l.off_stamp = take((int64_t)P * 4);
+  l.off_ent = take(l.C * kEntBytes);
+  l.off_rec = take((int64_t)P * kRecBytes);
   l.off_free = take((int64_t)P * 4);
-  l.off_hash = take((int64_t)P * 8);
-  l.off_ring_pg = take(l.Q * 4);
-  l.off_ring_st = take(l.Q * 4);
-  l.off_slot = take((int64_t)P * 4);
+  l.off_ring = take(l.Q * 8);
   l.bytes = o;
   return l;
 }
 
 struct BmState {
   int64_t* ctr;
-  uint64_t* key;
-  int32_t* val;
-  int32_t* ref;
-  int32_t* flag;
-  uint32_t* stamp;
+  uint8_t* ent;  // C x 16 bytes
+  uint8_t* rec;  // P x 32 bytes
   int32_t* free_list;
-  uint64_t* hash;
-  int32_t* ring_pg;
-  uint32_t* ring_st;
-  int32_t* slot;  // table slot holding a cached page's key
+  uint64_t* ring;
   int64_t C, Q;
   int32_t P;
 };
@@ -94,20 +103,49 @@ inline BmState bm_state(void* base, int32_t P) {
   uint8_t* b = static_cast<uint8_t*>(base);
   BmState s;
   s.ctr = reinterpret_cast<int64_t*>(b + l.off_ctr);
-  s.key = reinterpret_cast<uint64_t*>(b + l.off_key);
-  s.val = reinterpret_cast<int32_t*>(b + l.off_val);
-  s.ref = reinterpret_cast<int32_t*>(b + l.off_ref);
-  s.flag = reinterpret_cast<int32_t*>(b + l.off_flag);
-  s.stamp = reinterpret_cast<uint32_t*>(b + l.off_stamp);
+  s.ent = b + l.off_ent;
+  s.rec = b + l.off_rec;
   s.free_list = reinterpret_cast<int32_t*>(b + l.off_free);
-  s.hash = reinterpret_cast<uint64_t*>(b + l.off_hash);
-  s.ring_pg = reinterpret_cast<int32_t*>(b + l.off_ring_pg);
-  s.ring_st = reinterpret_cast<uint32_t*>(b + l.off_ring_st);
-  s.slot = reinterpret_cast<int32_t*>(b + l.off_slot);
+  s.ring = reinterpret_cast<uint64_t*>(b + l.off_ring);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
   return s;
+}
+
+// --- field access ---------------------------------------------------------
+__device__ __forceinline__ int32_t* ent_page(const BmState& s, int64_t i) {
+  return reinterpret_cast<int32_t*>(s.ent + i * kEntBytes + 8);
+}
+__device__ __forceinline__ uint64_t* ent_key(const BmState& s, int64_t i) {
+  return reinterpret_cast<uint64_t*>(s.ent + i * kEntBytes);
+}
+struct RecHead {
+  int32_t ref, flag;
+  uint32_t stamp;
+  int32_t slot;
+};
+__device__ __forceinline__ RecHead rec_head(const BmState& s, int32_t p) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(s.rec + (int64_t)p * kRecBytes);
+  return RecHead{(int32_t)v.x, (int32_t)v.y, v.z, (int32_t)v.w};
+}
+__device__ __forceinline__ int32_t* rec_ref(const BmState& s, int32_t p) {
+  return reinterpret_cast<int32_t*>(s.rec + (int64_t)p * kRecBytes);
+}
+__device__ __forceinline__ int32_t* rec_flag(const BmState& s, int32_t p) {
+  return reinterpret_cast<int32_t*>(s.rec + (int64_t)p * kRecBytes + 4);
+}
+__device__ __forceinline__ uint32_t* rec_stamp(const BmState& s, int32_t p) {
+  return reinterpret_cast<uint32_t*>(s.rec + (int64_t)p * kRecBytes + 8);
+}
+__device__ __forceinline__ int32_t* rec_slot(const BmState& s, int32_t p) {
+  return reinterpret_cast<int32_t*>(s.rec + (int64_t)p * kRecBytes + 12);
+}
+__device__ __forceinline__ uint64_t* rec_hash(const BmState& s, int32_t p) {
+  return reinterpret_cast<uint64_t*>(s.rec + (int64_t)p * kRecBytes + 16);
+}
+__device__ __forceinline__ bool live(const RecHead& h, uint32_t stamp) {
+  return (h.flag & 1) && h.ref == 0 && h.stamp == stamp;
 }
 
 struct BmArgs {
@@ -131,78 +169,128 @@ struct BmArgs {
   int32_t* err;
 };
 
+// Request metadata of a chunk of ops, staged in LDS.
+struct OpMeta {
+  int32_t op[kOpChunk];
+  int32_t ntok[kOpChunk];
+  int32_t nhash[kOpChunk];  // admits: page-hash count, -1 if it disagrees with ntok
+  int64_t h0[kOpChunk];     // admits: index of the first page hash
+};
+
 // Per-workgroup scratch.
 struct Shared {
-  int32_t wave_sum[kBmWaves];
-  int32_t first_miss;
-  int32_t count;
-  int32_t tomb_reused;
+  int32_t wave_sum[2][2][kBmWaves];  // block_rank2: [buffer][flag][wave]
+  uint64_t evmask[kHeld][kBmWaves];  // probe: which held hits are evictable now
+  // Per-op accumulators, two sets used by alternate ops: thread 0 clears the
+  // previous op's set while the current op runs, so no clear can race with
+  // an update of the op that uses the set.
+  int32_t first_miss[2];
+  int32_t count[2];
+  int32_t tomb_reused[2];
   int64_t new_head;
 };
 
 __device__ __forceinline__ uint32_t slot_of(uint64_t h) { return (uint32_t)(h ^ (h >> 29)); }
 
-// Block-wide exclusive rank of a 0/1 flag (wavefront ballot + popcount, then
-// the waves' totals through LDS). Every thread gets the block total. Contains
-// barriers: every thread must call it.
-__device__ __forceinline__ int32_t block_rank(bool flag, int32_t& total, Shared& sh) {
-  const uint64_t m = __ballot(flag);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int32_t below = __popcll(m & ((1ull << lane) - 1ull));
-  if (lane == 0) sh.wave_sum[wave] = __popcll(m);
-  __syncthreads();
-  int32_t before = 0, all = 0;
+__device__ __forceinline__ int32_t wave_min(int32_t v) {
 #pragma unroll
-  for (int w = 0; w < kBmWaves; ++w) {
-    const int32_t c = sh.wave_sum[w];
-    before += w < wave ? c : 0;
-    all += c;
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int32_t o = __shfl_xor(v, off);
+    v = o < v ? o : v;
   }
-  __syncthreads();
-  total = all;
-  return before + below;
+  return v;
+}
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
 }
 
-// Page id under key h, or -1. Never runs concurrently with a writer of h.
-__device__ int32_t tab_find(const BmState& s, uint64_t h, int64_t* slot_out = nullptr) {
+// Block-wide exclusive ranks of two 0/1 flags (wavefront ballots + popcount,
+// then the waves' totals through LDS); every thread gets both totals. One
+// barrier per call: consecutive calls alternate between two LDS buffers
+// (`buf` flips), and a buffer is rewritten only after the next call's barrier,
+// which no thread passes before every thread has read it. Every thread must
+// call it.
+__device__ __forceinline__ void block_rank2(bool fa, bool fb, int32_t& ra, int32_t& rb,
+                                            int32_t& ta, int32_t& tb, Shared& sh, int& buf) {
+  const uint64_t ma = __ballot(fa), mb = __ballot(fb);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sh.wave_sum[buf][0][wave] = __popcll(ma);
+    sh.wave_sum[buf][1][wave] = __popcll(mb);
+  }
+  __syncthreads();
+  int32_t ba = 0, bb = 0, aa = 0, ab = 0;
+#pragma unroll
+  for (int w = 0; w < kBmWaves; ++w) {
+    const int32_t ca = sh.wave_sum[buf][0][w], cb = sh.wave_sum[buf][1][w];
+    ba += w < wave ? ca : 0;
+    bb += w < wave ? cb : 0;
+    aa += ca;
+    ab += cb;
+  }
+  buf ^= 1;
+  const uint64_t below = (1ull << lane) - 1ull;
+  ra = ba + __popcll(ma & below);
+  rb = bb + __popcll(mb & below);
+  ta = aa;
+  tb = ab;
+}
+
+// Page id under key h, or -1; *free_out (if given) receives the first empty or
+// tombstoned slot on h's probe path, where h would be inserted. Never runs
+// concurrently with a writer of the table.
+__device__ int32_t tab_find(const BmState& s, uint64_t h, int64_t* free_out = nullptr) {
   const int64_t mask = s.C - 1;
   int64_t i = slot_of(h) & mask;
+  int64_t first_free = -1;
   for (int64_t n = 0; n < s.C; ++n) {
-    const int32_t v = __hip_atomic_load(&s.val[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (v == kEmpty) return -1;
-    if (v >= 0 && s.key[i] == h) {
-      if (slot_out) *slot_out = i;
-      return v;
+    const u32x4 e = *reinterpret_cast<const u32x4*>(s.ent + i * kEntBytes);
+    const int32_t v = (int32_t)e.z;
+    if (v == kEmpty) {
+      if (free_out) *free_out = first_free >= 0 ? first_free : i;
+      return -1;
     }
+    if (v >= 0 && ((uint64_t)e.y << 32 | e.x) == h) return v;
+    if (v == kTomb && first_free < 0) first_free = i;
     i = (i + 1) & mask;
   }
+  if (free_out) *free_out = first_free;
   return -1;
 }
 
+// Claims slot i for (h, page) if it still holds `expect` (empty or tombstone).
+__device__ __forceinline__ bool tab_claim(const BmState& s, int64_t i, int32_t expect, uint64_t h,
+                                          int32_t page) {
+  if (atomicCAS(ent_page(s, i), expect, kBusy) != expect) return false;
+  *ent_key(s, i) = h;
+  *rec_slot(s, page) = (int32_t)i;
+  __threadfence_block();
+  __hip_atomic_store(ent_page(s, i), page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return true;
+}
+
 // Inserts h -> page (other lanes may insert other keys at the same time) and
-// records the slot in slot[page]. Returns 1 if it reused a tombstone, 0 if it
-// took an empty slot, -1 if the table was full (cannot happen: the load stays
-// below 1/2 because of the rebuild threshold).
-__device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page) {
+// records the slot in the page's record. Returns 1 if it reused a tombstone,
+// 0 if it took an empty slot, -1 if the table was full (cannot happen: the
+// load stays below 1/2 because of the rebuild threshold). `hint` is a slot on
+// h's probe path at or before which nothing is free (from tab_find), or -1.
+__device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page, int64_t hint = -1) {
   const int64_t mask = s.C - 1;
+  if (hint >= 0) {  // usually still free: one compare-and-swap
+    if (tab_claim(s, hint, kEmpty, h, page)) return 0;
+    if (tab_claim(s, hint, kTomb, h, page)) return 1;
+  }
   int64_t i = slot_of(h) & mask;
   for (int64_t n = 0; n < 2 * s.C; ++n) {
-    const int32_t v = __hip_atomic_load(&s.val[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if ((v == kEmpty || v == kTomb) && atomicCAS(&s.val[i], v, kBusy) == v) {
-      s.key[i] = h;
-      s.slot[page] = (int32_t)i;
-      __threadfence_block();
-      __hip_atomic_store(&s.val[i], page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      return v == kTomb ? 1 : 0;
-    }
+    const int32_t v =
+        __hip_atomic_load(ent_page(s, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if ((v == kEmpty || v == kTomb) && tab_claim(s, i, v, h, page)) return v == kTomb ? 1 : 0;
     if (v == kEmpty || v == kTomb) continue;  // lost the race for this slot: look again
     i = (i + 1) & mask;
   }
   return -1;
-}
-
-__device__ __forceinline__ bool ring_live(const BmState& s, int32_t pg, uint32_t st) {
-  return (s.flag[pg] & 1) && s.ref[pg] == 0 && s.stamp[pg] == st;
 }
 
 // Counters every thread keeps in registers (all threads compute them alike).
@@ -211,28 +299,24 @@ struct Ctrs {
 };
 
 // Moves the live ring entries [head, tail) to the front, in order.
-__device__ void ring_compact(const BmArgs& a, Ctrs& c, Shared& sh) {
+__device__ void ring_compact(const BmArgs& a, Ctrs& c, Shared& sh, int& buf) {
   const BmState& s = a.s;
   const int64_t qm = s.Q - 1;
   int64_t out = c.head;
   for (int64_t base = c.head; base < c.tail; base += kBmThreads) {
     const int64_t pos = base + threadIdx.x;
-    bool live = false;
-    int32_t pg = 0;
-    uint32_t st = 0;
+    bool keep = false;
+    uint64_t e = 0;
     if (pos < c.tail) {
-      pg = s.ring_pg[pos & qm];
-      st = s.ring_st[pos & qm];
-      live = ring_live(s, pg, st);
+      e = s.ring[pos & qm];
+      keep = live(rec_head(s, (int32_t)(uint32_t)e), (uint32_t)(e >> 32));
     }
-    int32_t total;
-    const int32_t rank = block_rank(live, total, sh);  // all reads of this chunk are done
-    if (live) {
-      s.ring_pg[(out + rank) & qm] = pg;
-      s.ring_st[(out + rank) & qm] = st;
-    }
+    // Every read of this chunk precedes the ranks' barrier. Writes go below
+    // base + kBmThreads, where the later chunks no longer read.
+    int32_t rank, unused_r, total, unused_t;
+    block_rank2(keep, false, rank, unused_r, total, unused_t, sh, buf);
+    if (keep) s.ring[(out + rank) & qm] = e;
     out += total;
-    __syncthreads();
   }
   c.tail = out;
 }
@@ -240,29 +324,23 @@ __device__ void ring_compact(const BmArgs& a, Ctrs& c, Shared& sh) {
 // Rebuilds the hash table from the cached pages (drops every tombstone).
 __device__ void tab_rebuild(const BmArgs& a, Ctrs& c) {
   const BmState& s = a.s;
-  for (int64_t i = threadIdx.x; i < s.C; i += kBmThreads) s.val[i] = kEmpty;
+  for (int64_t i = threadIdx.x; i < s.C; i += kBmThreads) *ent_page(s, i) = kEmpty;
   __syncthreads();
   for (int32_t p = threadIdx.x; p < s.P; p += kBmThreads)
-    if (s.flag[p] & 1) tab_insert(s, s.hash[p], p);
+    if (*rec_flag(s, p) & 1) tab_insert(s, *rec_hash(s, p), p);
   __syncthreads();
   c.tombs = 0;
 }
 
-// Probe results a thread keeps in registers for the pages it owns
-// (i = tid + j*kBmThreads); requests longer than kHeld*kBmThreads pages re-read
-// the rest from memory.
-constexpr int kHeld = 4;
-
-__device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
+__device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int64_t h0,
+                      const uint64_t (&hk)[kHeld], Ctrs& c, Shared& sh, int& buf, int par) {
   const BmState& s = a.s;
-  const int tid = threadIdx.x;
-  const int32_t n = a.ntok[r];
-  const int64_t h0 = a.hash_off[r];
-  const int64_t m = a.hash_off[r + 1] - h0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m = nhash;
   const int64_t n_pages = (n + 15) / 16;
   const bool cow = (n & 15) != 0;
   int32_t* row = a.tables + (int64_t)r * a.tstride;
-  if (n < 0 || m != n / 16 || n_pages > a.twidth) {
+  if (nhash < 0 || n_pages > a.twidth) {
     if (tid == 0) {
       a.status[r] = kStBad;
       a.hits[r] = 0;
@@ -273,41 +351,71 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
   }
   if (c.tombs > s.C / 4) tab_rebuild(a, c);
 
-  // 1. probe every page hash; k = first miss. Each lane keeps the page and its
-  //    current refcount for its first kHeld hashes.
-  if (tid == 0) {
-    sh.first_miss = (int32_t)m;
-    sh.count = 0;
-    sh.tomb_reused = 0;
-  }
-  __syncthreads();
-  int32_t held_pg[kHeld], held_ref[kHeld];
+  // 1. probe every page hash (the first kHeld*kBmThreads from registers); a
+  //    missing key remembers its insertion slot; evictable hits go into
+  //    per-wave ballots. The free-stack entries this request may take are
+  //    loaded meanwhile (one per thread).
+  const int64_t may_take = n_pages + (cow ? 1 : 0);
+  const int64_t pf_n = may_take < c.free_top ? may_take : c.free_top;
+  const int32_t pf_page = tid < pf_n ? s.free_list[c.free_top - 1 - tid] : -1;
+  int32_t held_pg[kHeld];
+  int64_t held_ins[kHeld];
+  int32_t held_ref[kHeld];
+  int32_t miss = INT_MAX;
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
+    const int64_t i = tid + (int64_t)j * kBmThreads;
     held_pg[j] = -1;
-    held_ref[j] = 0;
-  }
-  for (int64_t i = tid, j = 0; i < m; i += kBmThreads, ++j) {
-    const int32_t p = tab_find(s, a.hashes[h0 + i]);
-    row[i] = p;
-    if (p < 0) atomicMin(&sh.first_miss, (int32_t)i);
-    if (j < kHeld) {
+    held_ins[j] = -1;
+    held_ref[j] = 1;
+    if (i < m) {
+      const int32_t p = tab_find(s, hk[j], &held_ins[j]);
+      row[i] = p;
       held_pg[j] = p;
-      held_ref[j] = p >= 0 ? s.ref[p] : 0;
+      if (p >= 0)
+        held_ref[j] = *rec_ref(s, p);
+      else
+        miss = (int32_t)i < miss ? (int32_t)i : miss;
     }
   }
-  __syncthreads();
-  const int64_t k = sh.first_miss;
-
-  // 2. hits that are evictable now will be pinned: count them for the OOM check
-  {
-    int32_t cnt = 0;
-    for (int64_t i = tid, j = 0; i < k; i += kBmThreads, ++j)
-      cnt += (j < kHeld ? held_ref[j] : s.ref[row[i]]) == 0;
-    if (cnt) atomicAdd(&sh.count, cnt);
+  for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < m; i += kBmThreads) {
+    const int32_t p = tab_find(s, a.hashes[h0 + i]);
+    row[i] = p;
+    if (p < 0 && (int32_t)i < miss) miss = (int32_t)i;
   }
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    const uint64_t em = __ballot(held_pg[j] >= 0 && held_ref[j] == 0);
+    if (lane == 0) sh.evmask[j][wave] = em;
+  }
+  miss = wave_min(miss);
+  if (lane == 0 && miss != INT_MAX) atomicMin(&sh.first_miss[par], miss);
   __syncthreads();
-  const int64_t pinned = sh.count;
+  const int64_t k = sh.first_miss[par] < m ? sh.first_miss[par] : m;
+
+  // 2. hits that are evictable now get pinned: count them for the OOM check
+  //    (every thread adds up the ballots itself; hits past the held pages, if
+  //    any, through one more reduction)
+  int64_t pinned = 0;
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+#pragma unroll 4
+    for (int w = 0; w < kBmWaves; ++w) {
+      const int64_t first = (int64_t)j * kBmThreads + w * 64;
+      if (first >= k) break;
+      const uint64_t em = sh.evmask[j][w];
+      pinned += __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
+    }
+  }
+  if (k > (int64_t)kHeld * kBmThreads) {
+    int32_t cnt = 0;
+    for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
+      cnt += *rec_ref(s, row[i]) == 0;
+    cnt = wave_sum(cnt);
+    if (lane == 0 && cnt) atomicAdd(&sh.count[par], cnt);
+    __syncthreads();
+    pinned += sh.count[par];
+  }
   const int64_t take = n_pages - k + (cow ? 1 : 0);
   if (take > c.free_top + c.evictable - pinned) {
     if (tid == 0) {
@@ -315,33 +423,32 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
       a.hits[r] = 0;
       a.child_last[r] = a.cow_src[r] = a.cow_dst[r] = -1;
     }
-    __syncthreads();
     return;
   }
 
   // 3. pin the hits, for the parent and the forked child at once (+2)
-  for (int64_t i = tid, j = 0; i < k; i += kBmThreads, ++j) {
-    if (j < kHeld)
-      s.ref[held_pg[j]] = held_ref[j] + 2;
-    else
-      s.ref[row[i]] += 2;
-  }
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j)
+    if (tid + (int64_t)j * kBmThreads < k) *rec_ref(s, held_pg[j]) = held_ref[j] + 2;
+  for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
+    *rec_ref(s, row[i]) += 2;
   c.evictable -= pinned;
+  const int64_t from_free = take < c.free_top ? take : c.free_top;
+  if (pinned > 0 && from_free < take) __syncthreads();  // pins land before liveness checks
 
   // 4. take pages: the free stack's top first, then LRU victims in order. The
   //    first n_pages-k go to the table (held by parent and child: refcount 2,
   //    except a partial last page, which the child copies: 1), the last (if
   //    any) is the child's copy (refcount 1).
-  const int64_t from_free = take < c.free_top ? take : c.free_top;
   const int64_t table_new = n_pages - k;
   for (int64_t j = tid; j < from_free; j += kBmThreads) {
-    const int32_t p = s.free_list[c.free_top - 1 - j];
+    const int32_t p = j == tid ? pf_page : s.free_list[c.free_top - 1 - j];
     if (j < table_new) {
       row[k + j] = p;
-      s.ref[p] = (cow && k + j == n_pages - 1) ? 1 : 2;
+      *rec_ref(s, p) = (cow && k + j == n_pages - 1) ? 1 : 2;
     } else {
       a.cow_dst[r] = p;
-      s.ref[p] = 1;
+      *rec_ref(s, p) = 1;
     }
   }
   c.free_top -= from_free;
@@ -353,25 +460,28 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
       break;
     }
     const int64_t pos = c.head + tid;
-    bool live = false;
+    bool ok = false;
     int32_t pg = 0;
+    RecHead h{};
     if (pos < c.tail) {
-      pg = s.ring_pg[pos & qm];
-      live = ring_live(s, pg, s.ring_st[pos & qm]);
+      const uint64_t e = s.ring[pos & qm];
+      pg = (int32_t)(uint32_t)e;
+      h = rec_head(s, pg);
+      ok = live(h, (uint32_t)(e >> 32));
     }
-    int32_t total;
-    const int32_t rank = block_rank(live, total, sh);
+    int32_t rank, unused_r, total, unused_t;
+    block_rank2(ok, false, rank, unused_r, total, unused_t, sh, buf);
     const int64_t want = take - done;
-    if (live && rank < want) {
+    if (ok && rank < want) {
       const int64_t j = done + rank;
-      s.val[s.slot[pg]] = kTomb;  // the page's key leaves the table
-      s.flag[pg] &= ~1;
+      *ent_page(s, h.slot) = kTomb;  // the page's key leaves the table
+      *rec_flag(s, pg) = h.flag & ~1;
       if (j < table_new) {
         row[k + j] = pg;
-        s.ref[pg] = (cow && k + j == n_pages - 1) ? 1 : 2;
+        *rec_ref(s, pg) = (cow && k + j == n_pages - 1) ? 1 : 2;
       } else {
         a.cow_dst[r] = pg;
-        s.ref[pg] = 1;
+        *rec_ref(s, pg) = 1;
       }
       if (c.log_len + (j - from_free) < a.evict_cap)
         a.evict_log[c.log_len + (j - from_free)] = pg;
@@ -384,41 +494,61 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
     c.evictable -= got;
     c.tombs += got;
     done += got;
-    __syncthreads();
   }
   c.log_len += done - from_free;
+  const bool evicted = done > from_free;
 
   // 5. register the new full pages' hashes unless already present. A key the
-  //    probe did not find is still absent (only evictions ran since); a key
-  //    it found is present unless its page was just evicted. All presence
-  //    checks of a chunk finish before any of its inserts (barrier), so no
-  //    check reads a page another lane is registering.
-  for (int64_t base = 0; base < m; base += (int64_t)kHeld * kBmThreads) {
-    bool reg[kHeld];
+  //    probe did not find is still absent (only evictions ran since, and they
+  //    only remove keys); a key it found is present unless its page was just
+  //    evicted. All presence checks finish before any insert (barrier), so no
+  //    check reads a page another lane is registering, and every lane sees the
+  //    page ids other lanes wrote into the table row.
+  bool reg[kHeld];
 #pragma unroll
-    for (int j = 0; j < kHeld; ++j) {
-      const int64_t i = base + tid + (int64_t)j * kBmThreads;
-      reg[j] = false;
-      if (i < m && i >= k) {
-        const uint64_t h = a.hashes[h0 + i];
-        const int32_t seen = base == 0 ? held_pg[j] : tab_find(s, h);
-        reg[j] = !(seen >= 0 && (s.flag[seen] & 1) && s.hash[seen] == h);
-      }
+  for (int j = 0; j < kHeld; ++j) {
+    const int64_t i = tid + (int64_t)j * kBmThreads;
+    reg[j] = false;
+    if (i < m && i >= k) {
+      const int32_t seen = held_pg[j];
+      reg[j] = seen < 0 ||
+               (evicted && !((*rec_flag(s, seen) & 1) && *rec_hash(s, seen) == hk[j]));
+    }
+  }
+  __syncthreads();
+  int32_t reused = 0;
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    if (!reg[j]) continue;
+    const int64_t i = tid + (int64_t)j * kBmThreads;
+    const int32_t p = row[i];
+    *rec_hash(s, p) = hk[j];
+    *rec_flag(s, p) = 1;
+    reused += tab_insert(s, hk[j], p, held_pg[j] < 0 ? held_ins[j] : -1) == 1;
+  }
+  __syncthreads();
+  // pages past the held ones (requests longer than kHeld*kBmThreads pages)
+  for (int64_t base = (int64_t)kHeld * kBmThreads; base < m; base += kBmThreads) {
+    const int64_t i = base + tid;
+    bool rg = false;
+    uint64_t h = 0;
+    if (i < m && i >= k) {
+      h = a.hashes[h0 + i];
+      rg = tab_find(s, h) < 0;
     }
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kHeld; ++j) {
-      if (!reg[j]) continue;
-      const int64_t i = base + tid + (int64_t)j * kBmThreads;
-      const uint64_t h = a.hashes[h0 + i];
+    if (rg) {
       const int32_t p = row[i];
-      s.hash[p] = h;
-      s.flag[p] |= 1;
-      if (tab_insert(s, h, p) == 1) atomicAdd(&sh.tomb_reused, 1);
+      *rec_hash(s, p) = h;
+      *rec_flag(s, p) = 1;
+      reused += tab_insert(s, h, p) == 1;
     }
     __syncthreads();
   }
-  c.tombs -= sh.tomb_reused;
+  reused = wave_sum(reused);
+  if (lane == 0 && reused) atomicAdd(&sh.tomb_reused[par], reused);
+  __syncthreads();
+  c.tombs -= sh.tomb_reused[par];
 
   if (tid == 0) {
     a.hits[r] = (int32_t)k;
@@ -431,7 +561,6 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
       a.child_last[r] = n_pages ? row[n_pages - 1] : -1;
     }
   }
-  __syncthreads();
 }
 
 // Releases a forked request in one pass. Sequentially that is the child's
@@ -443,64 +572,76 @@ __device__ void admit(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
 // free stack; then every shared page loses both references at once, and the
 // parent's own partial last page (after a copy) loses one. Pages reach zero
 // in the same order as in the two sequential passes.
-__device__ void release(const BmArgs& a, int32_t r, Ctrs& c, Shared& sh) {
+__device__ void release(const BmArgs& a, int32_t r, int32_t n, Ctrs& c, Shared& sh, int& buf) {
   const BmState& s = a.s;
+  const int64_t n_pages = n < 0 ? 0 : (n + 15) / 16;
+  const bool cow = (n & 15) != 0;
+  const int32_t* row = a.tables + (int64_t)r * a.tstride;
+  // the first chunk's pages are loaded with the status, before it is known
+  const int64_t j0 = threadIdx.x;
+  const int32_t page0 = j0 < n_pages && n_pages <= a.twidth ? row[n_pages - 1 - j0] : 0;
   const int32_t st = a.status[r];
+  const int32_t child = a.child_last[r];
   if (st != kStOk) {  // an OOM request holds nothing; anything else is a caller error
     if (st != kStOom && threadIdx.x == 0) raise_err(a.err, MKV_DEVERR_BM);
     return;
   }
-  const int32_t n = a.ntok[r];
-  const int64_t n_pages = (n + 15) / 16;
-  const bool cow = (n & 15) != 0;
-  const int32_t* row = a.tables + (int64_t)r * a.tstride;
   const int64_t qm = s.Q - 1;
   if (cow) {  // the child's private copy: uncached, refcount 1 -> free stack
     if (threadIdx.x == 0) {
-      const int32_t p = a.child_last[r];
-      s.ref[p] = 0;
-      s.free_list[c.free_top] = p;
+      *rec_ref(s, child) = 0;
+      s.free_list[c.free_top] = child;
     }
     c.free_top += 1;
   }
-  if (c.tail - c.head + n_pages > s.Q) ring_compact(a, c, sh);
+  if (c.tail - c.head + n_pages > s.Q) ring_compact(a, c, sh, buf);
   for (int64_t base = 0; base < n_pages; base += kBmThreads) {
     const int64_t j = base + threadIdx.x;  // j-th page from the tail
     bool to_lru = false, to_free = false;
     int32_t page = 0;
     if (j < n_pages) {
       const int64_t i = n_pages - 1 - j;
-      page = row[i];
-      const int32_t drop = (cow && i == n_pages - 1) ? 1 : 2;
-      const int32_t left = s.ref[page] - drop;
-      s.ref[page] = left;
+      page = base == 0 ? page0 : row[i];
+      const RecHead h = rec_head(s, page);
+      const int32_t left = h.ref - ((cow && i == n_pages - 1) ? 1 : 2);
+      *rec_ref(s, page) = left;
       if (left == 0) {
-        to_lru = (s.flag[page] & 1) != 0;
+        to_lru = (h.flag & 1) != 0;
         to_free = !to_lru;
       }
     }
-    int32_t n_lru, n_free;
-    const int32_t rl = block_rank(to_lru, n_lru, sh);
-    const int32_t rf = block_rank(to_free, n_free, sh);
+    int32_t rl, rf, n_lru, n_free;
+    block_rank2(to_lru, to_free, rl, rf, n_lru, n_free, sh, buf);
     if (to_lru) {
       const uint32_t stamp = (uint32_t)(c.next_stamp + rl);
-      s.ring_pg[(c.tail + rl) & qm] = page;
-      s.ring_st[(c.tail + rl) & qm] = stamp;
-      s.stamp[page] = stamp;
+      s.ring[(c.tail + rl) & qm] = (uint32_t)page | (uint64_t)stamp << 32;
+      *rec_stamp(s, page) = stamp;
     }
     if (to_free) s.free_list[c.free_top + rf] = page;
     c.tail += n_lru;
     c.next_stamp += n_lru;
     c.evictable += n_lru;
     c.free_top += n_free;
-    __syncthreads();
   }
   if (threadIdx.x == 0) a.status[r] = kStReleased;
-  __syncthreads();
+}
+
+// Loads the page hashes this thread holds for op t of the staged chunk.
+__device__ __forceinline__ void fetch_hashes(const BmArgs& a, const OpMeta& om, int t,
+                                             uint64_t (&h)[kHeld]) {
+  const bool adm = om.op[t] >= 0;
+  const int64_t nh = om.nhash[t], h0 = om.h0[t];
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    const int64_t i = threadIdx.x + (int64_t)j * kBmThreads;
+    h[j] = adm && i < nh ? a.hashes[h0 + i] : 0;
+  }
 }
 
 __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   __shared__ Shared sh;
+  __shared__ OpMeta om;
+  int buf = 0;
   Ctrs c;
   c.free_top = a.s.ctr[kFreeTop];
   c.head = a.s.ctr[kHead];
@@ -509,17 +650,57 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   c.evictable = a.s.ctr[kEvictable];
   c.tombs = a.s.ctr[kTombs];
   c.log_len = a.s.ctr[kLogLen];
-  for (int32_t o = 0; o < a.num_ops; ++o) {
-    const int32_t op = a.ops[o];
-    const int32_t r = op >= 0 ? op : -(op + 1);
-    if (r >= a.num_requests) {
-      if (threadIdx.x == 0) raise_err(a.err, MKV_DEVERR_BM);
-    } else if (op >= 0) {
-      admit(a, r, c, sh);
-    } else {
-      release(a, r, c, sh);
+  if (threadIdx.x < 2) {
+    sh.first_miss[threadIdx.x] = INT_MAX;
+    sh.count[threadIdx.x] = 0;
+    sh.tomb_reused[threadIdx.x] = 0;
+  }
+  uint64_t cur[kHeld], nxt[kHeld] = {};
+  for (int32_t base = 0; base < a.num_ops; base += kOpChunk) {
+    const int cnt = a.num_ops - base < kOpChunk ? a.num_ops - base : kOpChunk;
+    for (int t = threadIdx.x; t < cnt; t += kBmThreads) {
+      const int32_t op = a.ops[base + t];
+      const int32_t r = op >= 0 ? op : -(op + 1);
+      int32_t n = 0, nh = -1;
+      int64_t h0 = 0;
+      if (r < a.num_requests) {
+        n = a.ntok[r];
+        if (op >= 0) {
+          h0 = a.hash_off[r];
+          const int64_t m = a.hash_off[r + 1] - h0;
+          nh = (n >= 0 && m == n / 16) ? (int32_t)m : -1;
+        }
+      }
+      om.op[t] = op;
+      om.ntok[t] = n;
+      om.nhash[t] = nh;
+      om.h0[t] = h0;
     }
-    __syncthreads();  // the op's writes are visible to the next op
+    __syncthreads();
+    fetch_hashes(a, om, 0, cur);
+    for (int t = 0; t < cnt; ++t) {
+      const int par = (base + t) & 1;
+      if (threadIdx.x == 0) {  // the previous op's set (its reads ended at its last barrier)
+        sh.first_miss[par ^ 1] = INT_MAX;
+        sh.count[par ^ 1] = 0;
+        sh.tomb_reused[par ^ 1] = 0;
+      }
+      // the next op's page hashes are loaded while this one runs
+      if (t + 1 < cnt) fetch_hashes(a, om, t + 1, nxt);
+      const int32_t op = om.op[t];
+      const int32_t r = op >= 0 ? op : -(op + 1);
+      if (r >= a.num_requests) {
+        if (threadIdx.x == 0) raise_err(a.err, MKV_DEVERR_BM);
+      } else if (op >= 0) {
+        admit(a, r, om.ntok[t], om.nhash[t], om.h0[t], cur, c, sh, buf, par);
+      } else {
+        release(a, r, om.ntok[t], c, sh, buf);
+      }
+      __syncthreads();  // the op's writes are visible to the next op
+#pragma unroll
+      for (int j = 0; j < kHeld; ++j) cur[j] = nxt[j];
+    }
+    __syncthreads();  // the staged metadata is rewritten by the next chunk
   }
   if (threadIdx.x == 0) {
     a.s.ctr[kFreeTop] = c.free_top;
@@ -535,13 +716,16 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
 __global__ __launch_bounds__(256) void bm_init_kernel(BmState s, const int32_t* free_order) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int64_t i = g; i < s.C; i += stride) s.val[i] = kEmpty;
+  for (int64_t i = g; i < s.C; i += stride) {
+    *ent_key(s, i) = 0;
+    *reinterpret_cast<uint64_t*>(ent_page(s, i)) = (uint32_t)kEmpty;  // page -1, unused 0
+  }
   for (int64_t p = g; p < s.P; p += stride) {
-    s.ref[p] = 0;
-    s.flag[p] = 0;
-    s.stamp[p] = 0;
+    *reinterpret_cast<u32x4*>(s.rec + p * kRecBytes) = u32x4{0u, 0u, 0u, 0xffffffffu};
+    *reinterpret_cast<u32x4*>(s.rec + p * kRecBytes + 16) = u32x4{0u, 0u, 0u, 0u};
     s.free_list[p] = free_order ? free_order[p] : (int32_t)p;
   }
+  for (int64_t q = g; q < s.Q; q += stride) s.ring[q] = 0;
   if (g < kNumCtr) s.ctr[g] = g == kFreeTop ? s.P : (g == kNextStamp ? 1 : 0);
 }
 
@@ -560,10 +744,8 @@ extern "C" int mkv_bm_layout(int32_t num_pages, int64_t* out) {
   MKV_REQUIRE(num_pages > 0 && num_pages <= (1 << 28) && out, MKV_E_INVALID,
               "mkv_bm_layout: bad arguments");
   const BmLayout l = bm_layout(num_pages);
-  const int64_t v[14] = {l.C,        l.Q,        l.off_ctr,   l.off_key,     l.off_val,
-                         l.off_ref,  l.off_flag, l.off_stamp, l.off_free,    l.off_hash,
-                         l.off_ring_pg, l.off_ring_st, l.off_slot, l.bytes};
-  for (int i = 0; i < 14; ++i) out[i] = v[i];
+  const int64_t v[8] = {l.C, l.Q, l.off_ctr, l.off_ent, l.off_rec, l.off_free, l.off_ring, l.bytes};
+  for (int i = 0; i < 8; ++i) out[i] = v[i];
   return MKV_OK;
 }
 

@@ -96,6 +96,24 @@ def test_larger_trace_with_ring_compaction():
     assert len(model.evicted) > 1000
 
 
+def test_long_requests_past_the_register_held_pages():
+    # up to 2600 pages per request: pages past the first 2048 of a request take
+    # the kernel's memory-resident path (probe, pin, register)
+    case("block manager: 5400-page pool, 14 requests of ~2300-2600 pages")
+    status, model = run(P=5400, n=14, batch=2, seed=11, n_templates=2, template_len=36000,
+                        suffix=(1, 5000), width=2600)
+    assert len(model.evicted) > 500
+
+
+def test_many_evictions_rebuild_the_table():
+    # 72 pages and a 1024-slot table: tombstones pass a quarter of the table
+    # many times over, so the table is rebuilt repeatedly
+    case("block manager: 72-page pool, 1500 requests, batches of 6")
+    status, model = run(P=72, n=1500, batch=6, seed=21, n_templates=40, template_len=128,
+                        suffix=(1, 120), width=32)
+    assert len(model.evicted) > 2000
+
+
 def test_release_of_unknown_request_is_flagged():
     case("block manager: release of a request never admitted")
     bm = BlockManager(64, 4, 8, DEV)
