@@ -5,61 +5,69 @@
 // [8, 128, 128] fp32 = 512 KiB and a conv state [2048, 4] bf16 = 16 KiB. Both
 // are moved as raw bytes. One launch serves up to two pools so a layer's
 // recurrent and conv states travel together. Work is cut into 16 KiB pieces
-// (256 threads x 4 x 16 bytes); a workgroup takes one piece, issuing its four
-// loads before its four stores.
+// (256 threads x 4 x 16 bytes): grid.x is the piece within an entry (pool 0's
+// pieces, then pool 1's), grid.y the entry, so nothing is decoded by
+// division; a workgroup issues its four loads before its four stores, both
+// non-temporal (each byte is moved once; on MI355X this streams faster than
+// a vendor device-to-device copy of the same bytes).
 #include "mkv_device.h"
 
 namespace mkv {
 namespace {
 
 constexpr int kUnroll = 4;
-constexpr int64_t kMaxGridWgs = 1 << 22;  // bigger jobs loop inside the grid
 constexpr int64_t kPiece = (int64_t)kThreads * 16 * kUnroll;  // 16 KiB
+constexpr unsigned kMaxGridY = 65535;                          // more entries loop in the grid
 
 struct StateArgs {
-  const uint8_t* pool[2];  // gather: source pools; scatter: destination pools
-  uint8_t* dense[2];       // gather: outputs;      scatter: inputs
-  int64_t bytes[2];
-  int64_t pieces_per_entry[2];
-  int64_t pieces0;  // number of pieces that belong to pool 0
-  int64_t total_pieces;
+  const uint8_t* pool0;  // gather: source pools; scatter: destination pools
+  const uint8_t* pool1;
+  uint8_t* dense0;       // gather: outputs;      scatter: inputs
+  uint8_t* dense1;
+  int64_t bytes0, bytes1;
+  uint32_t pieces0;  // pieces per pool-0 entry (grid.x below it is pool 0)
   int64_t pool_slots;
   const int32_t* slots;
+  int32_t n;
   int32_t* err;
 };
 
 template <bool GATHER>
 __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
-  for (int64_t w = blockIdx.x; w < a.total_pieces; w += gridDim.x) {
-    const int which = w < a.pieces0 ? 0 : 1;
-    const int64_t local = which == 0 ? w : w - a.pieces0;
-    const int64_t b = local / a.pieces_per_entry[which];
-    const int64_t piece = local - b * a.pieces_per_entry[which];
-    const int64_t bytes = a.bytes[which];
+  const bool second = blockIdx.x >= a.pieces0;
+  const int64_t piece = second ? blockIdx.x - a.pieces0 : blockIdx.x;
+  const int64_t bytes = second ? a.bytes1 : a.bytes0;
+  const uint8_t* pool = second ? a.pool1 : a.pool0;
+  uint8_t* dense = second ? a.dense1 : a.dense0;
+  const int64_t base = piece * kPiece;
+  const bool full = base + kPiece <= bytes;
+  for (int64_t b = blockIdx.y; b < a.n; b += gridDim.y) {
     const int32_t slot = a.slots[b];
     const bool ok = slot >= 0 && slot < a.pool_slots;
-    if (!ok && threadIdx.x == 0 && piece == 0 && which == 0) raise_err(a.err, MKV_DEVERR_STATE_SLOT);
+    if (!ok && threadIdx.x == 0 && piece == 0 && !second) raise_err(a.err, MKV_DEVERR_STATE_SLOT);
     if (!ok && !GATHER) continue;  // scatter: nothing to write for a bad slot
-    uint8_t* pool = const_cast<uint8_t*>(a.pool[which]);
-    uint8_t* entry = pool + (ok ? (int64_t)slot * bytes : 0);
-    uint8_t* dense = a.dense[which] + b * bytes;
-    const int64_t base = piece * kPiece;
+    uint8_t* entry = const_cast<uint8_t*>(pool) + (ok ? (int64_t)slot * bytes : 0) + base;
+    uint8_t* row = dense + b * bytes + base;
+    const uint8_t* src = GATHER ? entry : row;
+    uint8_t* dst = GATHER ? row : entry;
     u32x4 v[kUnroll];
+    if (full && ok) {  // straight-line: every load issued before any store
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t off = base + ((int64_t)u * kThreads + threadIdx.x) * 16;
+      for (int u = 0; u < kUnroll; ++u) v[u] = ld_nt(src + (u * kThreads + threadIdx.x) * 16);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) st_nt(dst + (u * kThreads + threadIdx.x) * 16, v[u]);
+      continue;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {  // an entry's last piece, or a bad slot (zeros)
+      const int64_t off = (u * kThreads + threadIdx.x) * 16;
       v[u] = u32x4{0u, 0u, 0u, 0u};
-      if (off < bytes && (ok || !GATHER)) v[u] = GATHER ? ld_nt(entry + off) : ld_nt(dense + off);
+      if (ok && base + off < bytes) v[u] = ld_nt(src + off);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t off = base + ((int64_t)u * kThreads + threadIdx.x) * 16;
-      if (off < bytes) {
-        if (GATHER)
-          st16(dense + off, v[u]);
-        else
-          st_nt(entry + off, v[u]);
-      }
+      const int64_t off = (u * kThreads + threadIdx.x) * 16;
+      if (base + off < bytes) st_nt(dst + off, v[u]);
     }
   }
 }
@@ -78,25 +86,24 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   MKV_REQUIRE(aligned16(pool0) && aligned16(dense0) && bytes0 % 16 == 0 &&
                   (!two || (aligned16(pool1) && aligned16(dense1) && bytes1 % 16 == 0)),
               MKV_E_ALIGN, "%s: pools, buffers and entry sizes must be 16-byte aligned", fn);
+  // a zero-byte entry still gets one (empty) piece: it reports bad slots
+  const int64_t p0 = bytes0 > 0 ? (bytes0 + kPiece - 1) / kPiece : 1;
+  const int64_t p1 = two ? (bytes1 > 0 ? (bytes1 + kPiece - 1) / kPiece : 1) : 0;
+  MKV_REQUIRE(p0 + p1 < (1ll << 31), MKV_E_UNSUPPORTED, "%s: entries too large", fn);
   StateArgs a{};
-  a.pool[0] = (const uint8_t*)pool0;
-  a.dense[0] = (uint8_t*)dense0;
-  a.bytes[0] = bytes0;
-  a.pieces_per_entry[0] = (bytes0 + kPiece - 1) / kPiece;
-  a.pool[1] = two ? (const uint8_t*)pool1 : (const uint8_t*)pool0;
-  a.dense[1] = two ? (uint8_t*)dense1 : (uint8_t*)dense0;
-  a.bytes[1] = two ? bytes1 : 0;
-  a.pieces_per_entry[1] = two ? (bytes1 + kPiece - 1) / kPiece : 0;
-  if (a.pieces_per_entry[0] == 0) a.pieces_per_entry[0] = 1;  // zero-byte entries: no-op pieces
-  if (two && a.pieces_per_entry[1] == 0) a.pieces_per_entry[1] = 1;
-  a.pieces0 = a.pieces_per_entry[0] * n;
-  a.total_pieces = a.pieces0 + a.pieces_per_entry[1] * n;
+  a.pool0 = (const uint8_t*)pool0;
+  a.dense0 = (uint8_t*)dense0;
+  a.bytes0 = bytes0;
+  a.pool1 = two ? (const uint8_t*)pool1 : (const uint8_t*)pool0;
+  a.dense1 = two ? (uint8_t*)dense1 : (uint8_t*)dense0;
+  a.bytes1 = two ? bytes1 : 0;
+  a.pieces0 = (uint32_t)p0;
   a.pool_slots = pool_slots;
   a.slots = slots;
+  a.n = n;
   a.err = err;
-  const int64_t wgs = a.total_pieces < kMaxGridWgs ? a.total_pieces : kMaxGridWgs;
-  hipLaunchKernelGGL((state_move_kernel<GATHER>), dim3((unsigned)wgs), dim3(kThreads), 0, stream,
-                     a);
+  const dim3 grid((unsigned)(p0 + p1), (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY);
+  hipLaunchKernelGGL((state_move_kernel<GATHER>), grid, dim3(kThreads), 0, stream, a);
   return check_launch(fn);
 }
 
