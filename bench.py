@@ -130,6 +130,20 @@ def counter_traffic() -> tuple[float | None, float | None]:
     return vals.get("traffic_bytes_per_gather_launch"), vals.get("traffic_to_algorithmic_ratio")
 
 
+def counter_ratios(name: str) -> dict[str, float]:
+    """Per-kernel HBM traffic / algorithmic-byte ratios ("ratio <kernel>: x"
+    lines) recorded in profiles/<name> from its FETCH_SIZE/WRITE_SIZE runs."""
+    out = {}
+    try:
+        for line in open(os.path.join(os.path.dirname(PMC_PROFILE), name)):
+            if line.startswith("ratio ") and ":" in line:
+                k, v = line[len("ratio "):].split(":", 1)
+                out[k.strip()] = float(v)
+    except OSError:
+        pass
+    return out
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -247,8 +261,12 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+            # HBM bytes per launch: the FETCH_SIZE/WRITE_SIZE runs' traffic-to-
+            # algorithmic ratio applied to this run's mean launch (the profiled
+            # launches had the same workload at its first steps' lengths)
+            "traffic": round(ratio * mean_gather_bytes) if ratio else None,
             "traffic_to_algorithmic": ratio,
+            "traffic_profiled_bytes_per_launch": traffic,
             "traffic_source": ("rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 (scales from a 1 GiB copy), "
                                "profiles/gather_decode_b256_hbm_counters.md"),
             "mean_launch_us": round(mean_gather_s * 1e6, 2),
@@ -274,10 +292,22 @@ def _pair(stream):
     return a, b
 
 
-def _kernel_roofline(name: str, nbytes: float, ms: float) -> dict:
+def _kernel_roofline(name: str, nbytes: float, ms: float, ratio: float | None = None) -> dict:
     gbs = nbytes / (ms / 1e3) / 1e9
-    return {"kernel": name, "algorithmic_bytes_per_launch": round(nbytes), "mean_launch_us":
-            round(ms * 1e3, 2), "achieved": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return {"kernel": name, "bound": "hbm", "algorithmic_bytes_per_launch": round(nbytes),
+            "mean_launch_us": round(ms * 1e3, 2), "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": round(ratio * nbytes) if ratio else None, "traffic_to_algorithmic": ratio}
+
+
+def _roofline_of(kernels: list[dict], profile: str) -> dict:
+    """The contract's roofline object for the kernel with the most time per
+    step (first in ``kernels`` by convention), plus every kernel's entry."""
+    top = dict(kernels[0])
+    top["traffic_source"] = (f"rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 (scales from a 1 GiB "
+                             f"copy), profiles/{profile}")
+    top["kernels"] = kernels
+    return top
 
 
 def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
@@ -369,6 +399,7 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     cache.check_errors()
+    ratios = counter_ratios("fp8_prefill_hbm_counters.md")
     append_bytes = T * (1024 + 512 + 8 + 8)
     gather_bytes = R * WIN * (520 + 1024) + R * (WIN // 16 + 1) * 4 + 8 * R
     step_bytes_ = L * (append_bytes + gather_bytes)
@@ -384,11 +415,12 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
                                 "scale, then dequant-gather of the last 8192 tokens; seed 103")},
         "appended_tokens_per_s": round(T / step_s, 1),
         "pct_of_hbm_peak": round(100 * step_bytes_ / step_s / 1e9 / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
-            _kernel_roofline("append_fp8_kernel (mkv_append_fp8)", append_bytes,
-                             _timed(recs, "append") / L),
+        "roofline": _roofline_of([
             _kernel_roofline("gather_dequant_kernel<1> (mkv_gather_dequant_fp8)", gather_bytes,
-                             _timed(recs, "gather") / L)]},
+                             _timed(recs, "gather") / L, ratios.get("gather_dequant_kernel")),
+            _kernel_roofline("append_fp8_kernel (mkv_append_fp8)", append_bytes,
+                             _timed(recs, "append") / L, ratios.get("append_fp8_kernel"))],
+            "fp8_prefill_hbm_counters.md"),
     }
     if with_cpu:
         from oracle import fp8 as ref
@@ -484,6 +516,7 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     cache.check_errors()
     entry = 8 * 128 * 128 * 4 + 2048 * 4 * 2
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
+    ratios = counter_ratios("gdn_state_hbm_counters.md")
     g_ms, s_ms = _timed(recs, "gather") / G, _timed(recs, "scatter") / G
     u_ms = _timed(recs, "update")
     state_s = G * (g_ms + s_ms) / 1e3
@@ -502,9 +535,12 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
         "state_move_ms_per_step": round(state_s * 1e3, 3),
         "synthetic_update_ms_per_step": round(u_ms, 3),
         "pct_of_hbm_peak": round(100 * per_step_state / state_s / 1e9 / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "kernels": [
-            _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms),
-            _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms)]},
+        "roofline": _roofline_of(sorted([
+            _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms,
+                             ratios.get("state_move_kernel<true>")),
+            _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms,
+                             ratios.get("state_move_kernel<false>"))],
+            key=lambda k: -k["mean_launch_us"]), "gdn_state_hbm_counters.md"),
     }
     if with_cpu:
         from oracle import state as ref
@@ -697,8 +733,8 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
              "GB_hashed_per_s": round(8 * int(cu_t[-1]) / (hash_ms / 1e3) / 1e9, 3)},
             {"kernel": "bm_step_kernel (mkv_bm_step)", "bound": "latency (one workgroup)",
              "us_per_request": round(step_ms * 1e3 / n_req, 3)},
-            dict(_kernel_roofline("copy_pages_kernel (mkv_copy_blocks)", cow_bytes / len(ops_dev),
-                                  cow_ms / len(ops_dev)), bound="hbm", peak=HBM_PEAK_GBS)]},
+            _kernel_roofline("copy_pages_kernel (mkv_copy_blocks)", cow_bytes / len(ops_dev),
+                             cow_ms / len(ops_dev))]},
     }
     if with_cpu:
         from oracle.blocks import BlockManagerModel

@@ -21,8 +21,9 @@ Pinning (what checks each function beyond its own restatement):
   sha.*                           FIPS 180-4 example vectors; per-page hashes vs
                                   hashing each prefix from scratch
   lru.PrefixCacheModel            scripted traces with hand-derived eviction order
-  lru.BlockManagerModel           invariants (refcounts = holders; free+used+cached = P;
+  blocks.BlockManagerModel        invariants (refcounts = holders; free+used+cached = P;
                                   no eviction of referenced pages) and an independent
-                                  timestamp-LRU brute force on small traces
+                                  timestamp-LRU brute force (blocks.TimestampLRUModel)
+                                  on small traces
   state.gather/scatter            round trip and index_select/index_copy_ identities
 """
