@@ -17,6 +17,7 @@ time (GB/s); ``roofline`` is the gather kernel's algorithmic bytes per launch
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -183,19 +184,22 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     kbuf = torch.empty(B * lpad_max * HEAD_DIM, dtype=torch.bfloat16, device=dev)
     vbuf = torch.empty_like(kbuf)
     stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
 
-    def one_step(i: int, events=None):
+    def one_step(i: int, rec=None, steps_rec=None):
+        step = stamps.span(stream) if steps_rec is not None else None
         slots = bt.decode_step()
         lpad = bt.padded_len()
         kout = kbuf[:B * lpad * HEAD_DIM].view(B, lpad, 1, HEAD_DIM)
         vout = vbuf[:B * lpad * HEAD_DIM].view(B, lpad, 1, HEAD_DIM)
         for l in range(LAYERS):
             cache.append(slots, kin[i, l], vin[i, l], layer=l)
-            if events is not None:
-                events[l][0].record(stream)
+            sp = stamps.span(stream) if rec is not None else None
             cache.gather(l, bt.tables, bt.seq_lens, out_len=lpad, out=(kout, vout))
-            if events is not None:
-                events[l][1].record(stream)
+            if rec is not None:
+                rec.append(("gather", sp.end(stream)))
+        if steps_rec is not None:
+            steps_rec.append(step.end(stream))
         return kout, vout
 
     log(f"warmup {warmup} steps")
@@ -211,18 +215,17 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
         all_bytes += a
         gather_bytes += g_
         useful += u
-    ev = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(LAYERS)]
-          for _ in range(steps)]
+    recs = [[] for _ in range(steps)]
+    step_spans: list = []
     log(f"timing {steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for j in range(steps):
-        out = one_step(warmup + j, ev[j])
+        out = one_step(warmup + j, recs[j], step_spans)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     cache.check_errors()
-    gather_ms = [e[0].elapsed_time(e[1]) for step in ev for e in step]
-    mean_gather_s = float(np.mean(gather_ms)) / 1e3
+    mean_gather_s = _timed(recs, "gather") / 1e3
     mean_gather_bytes = gather_bytes / steps
     lens_now = bt._lens.copy()
 
@@ -251,6 +254,7 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
             "ctx_sum_start": int(lens0.sum()), "ctx_max_start": int(lens0.max()),
         },
         "decode_step_us": round(step_s * 1e6, 1),
+        "step_time": _step_stats(step_spans),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "tokens_per_s": round(B / step_s, 1),
         "useful_GBps_without_padding_writes": round(useful / elapsed / 1e9, 2),
@@ -279,17 +283,81 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
-def _timed(events_per_step: list, label: str) -> float:
-    """Mean milliseconds of the (start, end) event pairs recorded under label."""
-    ms = [a.elapsed_time(b) for step in events_per_step for (lab, a, b) in step if lab == label]
+class Stamps:
+    """Timing events of the timed regions: HIP events created with
+    hipEventDisableSystemFence, recorded on torch's streams. A default event's
+    system-scope release (an L2 write-back) adds ~3 us to every launch it
+    brackets on MI355X; these agree with rocprof's kernel times within ~1 us.
+    Read after a synchronize."""
+    _NO_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self):
+        from muserve_amd import _lib
+        paths = _lib._hip_runtimes()
+        if len(paths) != 1:
+            raise RuntimeError(f"expected exactly one HIP runtime mapped, found {paths}")
+        hip = ctypes.CDLL(paths[0])
+        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self._hip = hip
+        self._events: list[ctypes.c_void_p] = []
+
+    def record(self, stream) -> ctypes.c_void_p:
+        ev = ctypes.c_void_p()
+        if self._hip.hipEventCreateWithFlags(ctypes.byref(ev), self._NO_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+        if self._hip.hipEventRecord(ev, ctypes.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+        self._events.append(ev)
+        return ev
+
+    def ms(self, a: ctypes.c_void_p, b: ctypes.c_void_p) -> float:
+        out = ctypes.c_float()
+        if self._hip.hipEventElapsedTime(ctypes.byref(out), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(out.value)
+
+    def span(self, stream) -> "Span":
+        return Span(self, stream)
+
+    def close(self) -> None:
+        for ev in self._events:
+            self._hip.hipEventDestroy(ev)
+        self._events.clear()
+
+
+class Span:
+    """A start event recorded now; end() records the stop event."""
+
+    def __init__(self, stamps: Stamps, stream):
+        self._s = stamps
+        self._a = stamps.record(stream)
+        self._b = None
+
+    def end(self, stream) -> "Span":
+        self._b = self._s.record(stream)
+        return self
+
+    def ms(self) -> float:
+        return self._s.ms(self._a, self._b)
+
+
+def _timed(recs: list, label: str) -> float:
+    """Mean milliseconds of the spans recorded under label (recs: per step,
+    lists of (label, Span))."""
+    ms = [sp.ms() for step in recs for (lab, sp) in step if lab == label]
     return float(np.mean(ms)) if ms else float("nan")
 
 
-def _pair(stream):
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    return a, b
+def _step_stats(spans: list) -> dict:
+    """Median / p10 / p90 of per-step times (ms)."""
+    ms = np.array([sp.ms() for sp in spans])
+    return {"median_ms": round(float(np.median(ms)), 4),
+            "p10_ms": round(float(np.percentile(ms, 10)), 4),
+            "p90_ms": round(float(np.percentile(ms, 90)), 4)}
 
 
 def _kernel_roofline(name: str, nbytes: float, ms: float, ratio: float | None = None) -> dict:
@@ -368,34 +436,36 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
     torch.cuda.synchronize()
     cache.check_errors()
     stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
 
     # A step appends the chunk to every layer, then dequant-gathers every
     # layer's window (each gather follows its own layer's append, as in a layer
     # loop). One event pair brackets each group of 15 launches, so the mean
     # launch time carries no per-launch event overhead.
-    def one_step(i: int, rec=None):
-        if rec is not None:
-            a, b = _pair(stream)
+    def one_step(i: int, rec=None, steps_rec=None):
+        step = stamps.span(stream) if steps_rec is not None else None
+        sp = stamps.span(stream) if rec is not None else None
         for l in range(L):
             cache.append(slots_dev[i], kin[i, l], vin[i, l], layer=l)
         if rec is not None:
-            b.record(stream)
-            rec.append(("append", a, b))
-            a, b = _pair(stream)
+            rec.append(("append", sp.end(stream)))
+            sp = stamps.span(stream)
         for l in range(L):
             cache.gather(l, bt, lens_dev[i], out_len=WIN, starts=starts_dev[i], out=(kbuf, vbuf),
                          cu_out=cu_out)
         if rec is not None:
-            b.record(stream)
-            rec.append(("gather", a, b))
+            rec.append(("gather", sp.end(stream)))
+        if steps_rec is not None:
+            steps_rec.append(step.end(stream))
 
     for i in range(warmup):
         one_step(i)
     torch.cuda.synchronize()
     recs = [[] for _ in range(steps)]
+    step_spans: list = []
     t0 = time.perf_counter()
     for j in range(steps):
-        one_step(warmup + j, recs[j])
+        one_step(warmup + j, recs[j], step_spans)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     cache.check_errors()
@@ -414,6 +484,7 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
                                 "contexts, 15 layers, 1 KV head x 256, e4m3fn + fp32 per-token "
                                 "scale, then dequant-gather of the last 8192 tokens; seed 103")},
         "appended_tokens_per_s": round(T / step_s, 1),
+        "step_time": _step_stats(step_spans),
         "pct_of_hbm_peak": round(100 * step_bytes_ / step_s / 1e9 / HBM_PEAK_GBS, 2),
         "roofline": _roofline_of([
             _kernel_roofline("gather_dequant_kernel<1> (mkv_gather_dequant_fp8)", gather_bytes,
@@ -442,13 +513,14 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
 
 
 def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
-    """Decode step of the hybrid stack: the 256 active requests' recurrent
-    [8,128,128] fp32 + conv [2048,4] bf16 states of all 45 GDN layers are
-    gathered from a 1024-slot pool (seeded permuted slots), updated (a
-    synthetic +1, timed apart) and scattered back; the 15 attention layers
-    append one decode token per request (the headline workload's appends)."""
+    """Decode step of the hybrid stack, 60 layers in model order: each GDN
+    layer gathers the 256 active requests' recurrent [8,128,128] fp32 + conv
+    [2048,4] bf16 states from a 1024-slot pool (seeded permuted slots),
+    updates them (a synthetic +1, timed apart) and scatters them back; each
+    attention layer (l % 4 == 3) appends one decode token per request (the
+    headline workload's appends)."""
     from muserve_amd.kv_cache import BlockTables, PagedKVCache, SequenceKVState, reserve_tokens
-    from muserve_amd.state_pool import StatePool
+    from muserve_amd.state_pool import StatePool, gdn_ordinal
 
     dev = torch.device("cuda:0")
     S, G = 1024, 45
@@ -470,46 +542,45 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     bt = BlockTables(cache, seqs, max_pages=int(-(-(int(ctx.max()) + total) // 16)))
     kin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
     vin = torch.randn(total, LAYERS, B, 1, HEAD_DIM, generator=gen, device=dev).bfloat16()
-    # the step's working set: every GDN layer's states of the batch, contiguous
-    sbuf = torch.empty((G, B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
-    cbuf = torch.empty((G, B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+    # the layer's working set: the batch's states, contiguous
+    sbuf = torch.empty((B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
+    cbuf = torch.empty((B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
     stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
 
-    # A decode step gathers the batch's states of all 45 GDN layers into the
-    # working set, updates them (a synthetic +1 stands in for the recurrence),
-    # and scatters them back, besides one KV append per attention layer. One
-    # event pair brackets each phase of 45 launches, so the mean launch time
-    # carries no per-launch event overhead.
-    def one_step(i: int, rec=None):
+    def one_step(i: int, rec=None, steps_rec=None):
+        step = stamps.span(stream) if steps_rec is not None else None
         kv_slots = bt.decode_step()
-        for a in range(LAYERS):
-            cache.append(kv_slots, kin[i, a], vin[i, a], layer=a)
-        ev = _pair(stream) if rec is not None else None
-        for g in range(G):
-            pool.gather(g, slots, out=(sbuf[g], cbuf[g]))
-        if rec is not None:
-            ev[1].record(stream)
-            rec.append(("gather",) + ev)
-            ev = _pair(stream)
-        sbuf.add_(1.0)
-        cbuf.add_(1.0)
-        if rec is not None:
-            ev[1].record(stream)
-            rec.append(("update",) + ev)
-            ev = _pair(stream)
-        for g in range(G):
-            pool.scatter(g, slots, sbuf[g], cbuf[g])
-        if rec is not None:
-            ev[1].record(stream)
-            rec.append(("scatter",) + ev)
+        for layer in range(60):
+            if layer % 4 == 3:
+                a = layer // 4
+                cache.append(kv_slots, kin[i, a], vin[i, a], layer=a)
+                continue
+            g = gdn_ordinal(layer)
+            sp = stamps.span(stream) if rec is not None else None
+            pool.gather(g, slots, out=(sbuf, cbuf))
+            if rec is not None:
+                rec.append(("gather", sp.end(stream)))
+                sp = stamps.span(stream)
+            sbuf.add_(1.0)
+            cbuf.add_(1.0)
+            if rec is not None:
+                rec.append(("update", sp.end(stream)))
+                sp = stamps.span(stream)
+            pool.scatter(g, slots, sbuf, cbuf)
+            if rec is not None:
+                rec.append(("scatter", sp.end(stream)))
+        if steps_rec is not None:
+            steps_rec.append(step.end(stream))
 
     for i in range(warmup):
         one_step(i)
     torch.cuda.synchronize()
     recs = [[] for _ in range(steps)]
+    step_spans: list = []
     t0 = time.perf_counter()
     for j in range(steps):
-        one_step(warmup + j, recs[j])
+        one_step(warmup + j, recs[j], step_spans)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     pool.check_errors()
@@ -517,8 +588,7 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     entry = 8 * 128 * 128 * 4 + 2048 * 4 * 2
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
     ratios = counter_ratios("gdn_state_hbm_counters.md")
-    g_ms, s_ms = _timed(recs, "gather") / G, _timed(recs, "scatter") / G
-    u_ms = _timed(recs, "update")
+    g_ms, s_ms, u_ms = _timed(recs, "gather"), _timed(recs, "scatter"), _timed(recs, "update")
     state_s = G * (g_ms + s_ms) / 1e3
     step_s = elapsed / steps
     per_step_state = 4 * G * B * entry
@@ -529,11 +599,12 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32+bf16",
         "data": "synthetic (seeded ~N(0,1) states, seeded permuted slots)",
         "config": {"workload": ("GDN state slots at decode: 45 layers x [8,128,128] fp32 + "
-                                "[2048,4] bf16, 1024-slot pool, batch 256: per decode step "
-                                "gather all layers -> +1 -> scatter all layers, plus decode "
-                                "appends on 15 attention layers; seed 105")},
+                                "[2048,4] bf16, 1024-slot pool, batch 256, 60 layers in model "
+                                "order: gather -> +1 -> scatter per GDN layer, decode append per "
+                                "attention layer; seed 105")},
         "state_move_ms_per_step": round(state_s * 1e3, 3),
-        "synthetic_update_ms_per_step": round(u_ms, 3),
+        "synthetic_update_ms_per_step": round(G * u_ms, 3),
+        "step_time": _step_stats(step_spans),
         "pct_of_hbm_peak": round(100 * per_step_state / state_s / 1e9 / HBM_PEAK_GBS, 2),
         "roofline": _roofline_of(sorted([
             _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms,
@@ -597,6 +668,15 @@ def run_plumbing(steps: int, warmup: int, with_cpu: bool) -> dict:
         one_step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    # per-step distribution from a second pass (recording events per step
+    # would add host work to this launch-bound loop)
+    stamps, spans = Stamps(), []
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(steps):
+        sp = stamps.span(stream)
+        one_step()
+        spans.append(sp.end(stream))
+    torch.cuda.synchronize()
     cache.check_errors()
     exact = bool(torch.equal(kout.view(torch.int16), k.view(torch.int16)) and
                  torch.equal(vout.view(torch.int16), v.view(torch.int16)))
@@ -609,6 +689,7 @@ def run_plumbing(steps: int, warmup: int, with_cpu: bool) -> dict:
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "plumbing: 1 layer, 512x16 pool, 8 prompts randint(1,513), seed 101",
                    "tokens": T},
+        "step_time": _step_stats(spans),
         "GBps": round(nbytes / step_s / 1e9, 2), "bit_exact_round_trip": exact,
     }
 
@@ -648,6 +729,7 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
     stream = torch.cuda.current_stream(dev)
 
     hash_stream = torch.cuda.Stream(dev)  # default priority, like every stream here
+    stamps = Stamps()
 
     def run_all(bm, rec=None):
         # Page hashing depends only on the prompts, and one lane walks one
@@ -656,32 +738,29 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
         # stream; the block manager (one workgroup) then processes the batches
         # in order, each step waiting for the hashes.
         with torch.cuda.stream(hash_stream):
-            ev = _pair(hash_stream) if rec is not None else None
+            sp = stamps.span(hash_stream) if rec is not None else None
             page_hashes_range(tokens, tok_off, page_off, 0, n_req, hashes, herr)
             if rec is not None:
-                ev[1].record(hash_stream)
-                rec.append(("hash",) + ev)
+                rec.append(("hash", sp.end(hash_stream)))
             ready = torch.cuda.Event()
             ready.record(hash_stream)
         stream.wait_event(ready)
         for b, ops in enumerate(ops_dev):
             first = b * batch
             cnt = min(batch, n_req - first)
-            ev = _pair(stream) if rec is not None else None
+            sp = stamps.span(stream) if rec is not None else None
             bm.step(ops, hashes, page_off, ntok)
             if rec is not None:
-                ev[1].record(stream)
-                rec.append(("step",) + ev)
-                ev = _pair(stream)
+                rec.append(("step", sp.end(stream)))
+                sp = stamps.span(stream)
             bm.copy_on_write(cache, first, first + cnt)
             if rec is not None:
-                ev[1].record(stream)
-                rec.append(("cow",) + ev)
+                rec.append(("cow", sp.end(stream)))
 
     for _ in range(warmup):  # whole-trace warm-ups on fresh managers
         run_all(BlockManager(P, n_req, width, dev, free_order=free))
     torch.cuda.synchronize()
-    best = None
+    trials = []  # (wall seconds, spans, manager) per whole-trace trial
     for _ in range(max(1, steps)):
         bm = BlockManager(P, n_req, width, dev, free_order=free, evict_log_capacity=1 << 20)
         rec = []
@@ -689,10 +768,9 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
         t0 = time.perf_counter()
         run_all(bm, rec)
         torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
-        if best is None or dt < best[0]:
-            best = (dt, rec, bm)
-    elapsed, rec, bm = best
+        trials.append((time.perf_counter() - t0, rec, bm))
+    walls = np.array([t[0] for t in trials])
+    elapsed, rec, bm = trials[int(np.argsort(walls)[len(walls) // 2])]  # the median trial
     bm.check_errors()
     herr.check("page hashes")
     cache.check_errors()
@@ -701,9 +779,9 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
     cow = int((bm.cow_src.cpu().numpy() >= 0).sum())
     ctr = bm.counters()
     n_pages = int(cu_p[-1])
-    hash_ms = sum(a.elapsed_time(b) for lab, a, b in rec if lab == "hash")
-    step_ms = sum(a.elapsed_time(b) for lab, a, b in rec if lab == "step")
-    cow_ms = sum(a.elapsed_time(b) for lab, a, b in rec if lab == "cow")
+    hash_ms = sum(sp.ms() for lab, sp in rec if lab == "hash")
+    step_ms = sum(sp.ms() for lab, sp in rec if lab == "step")
+    cow_ms = sum(sp.ms() for lab, sp in rec if lab == "cow")
     page_bytes = 16 * HEAD_DIM * 2
     cow_bytes = cow * 2 * LAYERS * 2 * page_bytes  # read + write, 15 layers x K,V
     us_req = elapsed / n_req * 1e6
@@ -718,6 +796,10 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
                                 "4096 random ids + 64..1024-token suffix, batches of 256, "
                                 "65536-page pool, 15 layers x 1 KV head x 256 bf16; seed 104")},
         "requests_per_s": round(n_req / elapsed, 1),
+        "step_time": {"median_ms": round(float(np.median(walls)) * 1e3, 3),
+                      "p10_ms": round(float(np.percentile(walls, 10)) * 1e3, 3),
+                      "p90_ms": round(float(np.percentile(walls, 90)) * 1e3, 3),
+                      "note": "a step is the whole 4096-request trace on a fresh manager"},
         "pages_hashed_per_s": round(n_pages / (hash_ms / 1e3), 1),
         "admitted": int(((status == 0) | (status == 3)).sum()), "oom": int((status == 1).sum()),
         "page_hit_rate": round(float(hits[status != 1].sum()) / max(1, n_pages), 4),
@@ -806,7 +888,7 @@ def main() -> int:
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
     if args.workload == "prefix" and steps == 1000:
-        steps, warmup = 3, 1  # a step is the whole 4096-request trace
+        steps, warmup = 5, 1  # a step is the whole 4096-request trace
     res = runner(steps, warmup, not args.no_cpu_baseline)
     print(json.dumps(res), flush=True)
     return 0

@@ -242,7 +242,7 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * writes 8 int64: table capacity C, ring capacity Q, then the byte offsets of
  * the counters (16 int64: free-stack top, ring head, ring tail, next stamp,
  * evictable pages, tombstones, eviction-log length), the table (C entries of
- * {u64 key, i32 page}), the page records (P x 32 bytes: i32 refcount, i32
+ * {u64 key, i32 page, i32 copy of the page's refcount}), the page records (P x 32 bytes: i32 refcount, i32
  * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
  * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), and the
  * total size.
@@ -284,6 +284,21 @@ int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_
                 int32_t* cow_src, int32_t* cow_dst, int32_t* status,
                 int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
                 void* stream);
+
+/*
+ * Read-only lookup in a block manager's table: for request r < num_requests
+ * with page hashes page_hashes[hash_offsets[r] .. hash_offsets[r+1]),
+ * pages[i] = the cached page holding hash i (or -1) for every one of them, and
+ * hits[r] = the number of leading hashes found — the shared prefix an admit
+ * issued now would get. Nothing changes (no LRU touch, no pin). Must not run
+ * concurrently with mkv_bm_step on the same state (issue both on one
+ * stream). A request with hash_offsets[r+1] < hash_offsets[r] gets hits 0
+ * and sets MKV_DEVERR_TABLE. Replaces the scan of PrefixCache.lookup
+ * (muserve/model/prefix_cache.py:46-79) without its move_to_end.
+ */
+int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_hashes,
+                   const int64_t* hash_offsets, int32_t num_requests, int32_t* pages,
+                   int32_t* hits, int32_t* err, void* stream);
 
 /* ---- self-test ------------------------------------------------------------ */
 

@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "mkv_bm_init": [_P, _I32, _P, _P],
     "mkv_bm_step": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P,
                     _I64, _P, _P],
+    "mkv_hash_probe": [_P, _I32, _P, _P, _I32, _P, _P, _P, _P],
 }
 
 _lock = threading.Lock()

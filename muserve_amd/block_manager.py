@@ -107,6 +107,24 @@ class BlockManager:
                   self.evict_log.data_ptr(), self.evict_log_capacity, self.errors.ptr(),
                   _lib.stream_of(self.device))
 
+    def probe(self, page_hashes: torch.Tensor, hash_offsets: torch.Tensor
+              ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Read-only lookup (no LRU touch, no pin) of the page hashes of
+        len(hash_offsets)-1 requests: (page id per hash or -1, leading hits per
+        request). Ordered after earlier steps on the same stream."""
+        hash_offsets = hash_offsets.to(device=self.device, dtype=torch.int64).contiguous()
+        page_hashes = page_hashes.to(device=self.device).contiguous()
+        if page_hashes.dtype != torch.int64:
+            raise TypeError("page_hashes must hold u64 bit patterns in an int64 tensor")
+        n = hash_offsets.numel() - 1
+        pages = torch.empty(page_hashes.numel(), dtype=torch.int32, device=self.device)
+        hits = torch.empty(max(n, 0), dtype=torch.int32, device=self.device)
+        if n > 0:
+            _lib.call("mkv_hash_probe", self.state.data_ptr(), self.num_pages,
+                      page_hashes.data_ptr(), hash_offsets.data_ptr(), n, pages.data_ptr(),
+                      hits.data_ptr(), self.errors.ptr(), _lib.stream_of(self.device))
+        return pages, hits
+
     def copy_on_write(self, cache, first: int = 0, last: int | None = None) -> None:
         """Copies every admitted request's shared partial page to its child's
         private page (requests first..last-1; pairs without a copy are -1)."""
@@ -144,7 +162,14 @@ class BlockManager:
             if flag[pg] & 1 and ref[pg] == 0 and int(stamp[pg]) == st:
                 lru.append(pg)
         cached = flag & 1
-        return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(),
+        # table entry: u64 key, i32 page, i32 copy of the page's refcount
+        ent = self._arr("ent", self.layout["C"] * 4, torch.int32).cpu().numpy().reshape(-1, 4)
+        cp = np.nonzero(cached)[0]
+        slot = rec[cp, 3]
+        table_ok = bool(np.all(ent[slot, 2] == cp) and np.all(ent[slot, 3] == ref[cp]) and
+                        np.all(ent.view(np.uint64).reshape(-1, 2)[slot, 0] == phash[cp]) and
+                        int(np.count_nonzero(ent[:, 2] >= 0)) == len(cp))
+        return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(), "table_ok": table_ok,
                 "cached": cached.tolist(),
                 "hash": [int(phash[p]) if cached[p] else None for p in range(P)],
                 "evictable": ctr[_EVICTABLE], "log_len": ctr[_LOG_LEN]}

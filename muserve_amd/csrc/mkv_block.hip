@@ -10,7 +10,8 @@
 //
 // A request costs a few dependent memory round trips, so the layout keeps
 // that chain short:
-//   * a table entry holds key and page id in 16 bytes: one load per probe step;
+//   * a table entry holds key, page id and (mirrored) the page's refcount in
+//     16 bytes: one load per probe step answers "cached, and evictable?";
 //   * a page's refcount, flags, LRU stamp and the table slot of its key are the
 //     first 16 bytes of its 32-byte record: one load tells whether the page is
 //     evictable and where its key lives;
@@ -27,8 +28,9 @@
 //   counters  free_top, ring head/tail, next stamp, #evictable, tombstones,
 //             eviction-log length
 //   table     ent[C] {u64 key, i32 page (-1 empty, -2 tombstone, -3 being
-//             written), i32 unused}: open addressing, linear probing; rebuilt
-//             when tombstones exceed C/4
+//             written), i32 the page's refcount (a copy of rec.ref, kept
+//             equal while the page is cached)}: open addressing, linear
+//             probing; rebuilt when tombstones exceed C/4
 //   pages     rec[P] {i32 ref, i32 flag (bit 0: cached), u32 stamp, i32 table
 //             slot of the page's key, u64 hash, u64 unused}
 //   free      stack free[P] (pop from the top, like PagedKVCache.alloc_pages)
@@ -50,7 +52,7 @@ constexpr int kBmWaves = kBmThreads / 64;
 constexpr int kOpChunk = 1024;  // ops whose request metadata is staged in LDS at once
 // Page hashes (and probe results) a thread keeps in registers: pages
 // tid + j*kBmThreads for j < kHeld. Longer requests re-read the rest.
-constexpr int kHeld = 2;
+constexpr int kHeld = 1;
 
 enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen, kNumCtr = 16 };
 enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
@@ -119,6 +121,11 @@ __device__ __forceinline__ int32_t* ent_page(const BmState& s, int64_t i) {
 }
 __device__ __forceinline__ uint64_t* ent_key(const BmState& s, int64_t i) {
   return reinterpret_cast<uint64_t*>(s.ent + i * kEntBytes);
+}
+// a cached page's refcount, mirrored in its table entry so that a probe
+// learns "found, and evictable?" from one load
+__device__ __forceinline__ int32_t* ent_ref(const BmState& s, int64_t i) {
+  return reinterpret_cast<int32_t*>(s.ent + i * kEntBytes + 12);
 }
 struct RecHead {
   int32_t ref, flag;
@@ -238,33 +245,36 @@ __device__ __forceinline__ void block_rank2(bool fa, bool fb, int32_t& ra, int32
   tb = ab;
 }
 
-// Page id under key h, or -1; *free_out (if given) receives the first empty or
-// tombstoned slot on h's probe path, where h would be inserted. Never runs
-// concurrently with a writer of the table.
-__device__ int32_t tab_find(const BmState& s, uint64_t h, int64_t* free_out = nullptr) {
+// A lookup's result: the page under the key (or -1), the refcount mirrored in
+// its entry, and the entry's slot — or, for a missing key, the first empty or
+// tombstoned slot on its probe path, where it would be inserted.
+struct Found {
+  int32_t page, ref, slot;
+};
+
+// Looks up key h. Never runs concurrently with a writer of the table.
+__device__ Found tab_find(const BmState& s, uint64_t h) {
   const int64_t mask = s.C - 1;
   int64_t i = slot_of(h) & mask;
   int64_t first_free = -1;
   for (int64_t n = 0; n < s.C; ++n) {
     const u32x4 e = *reinterpret_cast<const u32x4*>(s.ent + i * kEntBytes);
     const int32_t v = (int32_t)e.z;
-    if (v == kEmpty) {
-      if (free_out) *free_out = first_free >= 0 ? first_free : i;
-      return -1;
-    }
-    if (v >= 0 && ((uint64_t)e.y << 32 | e.x) == h) return v;
+    if (v == kEmpty) return Found{-1, 0, (int32_t)(first_free >= 0 ? first_free : i)};
+    if (v >= 0 && ((uint64_t)e.y << 32 | e.x) == h) return Found{v, (int32_t)e.w, (int32_t)i};
     if (v == kTomb && first_free < 0) first_free = i;
     i = (i + 1) & mask;
   }
-  if (free_out) *free_out = first_free;
-  return -1;
+  return Found{-1, 0, (int32_t)first_free};
 }
 
-// Claims slot i for (h, page) if it still holds `expect` (empty or tombstone).
+// Claims slot i for (h, page, refcount ref) if it still holds `expect` (empty
+// or tombstone).
 __device__ __forceinline__ bool tab_claim(const BmState& s, int64_t i, int32_t expect, uint64_t h,
-                                          int32_t page) {
+                                          int32_t page, int32_t ref) {
   if (atomicCAS(ent_page(s, i), expect, kBusy) != expect) return false;
   *ent_key(s, i) = h;
+  *ent_ref(s, i) = ref;
   *rec_slot(s, page) = (int32_t)i;
   __threadfence_block();
   __hip_atomic_store(ent_page(s, i), page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -276,17 +286,19 @@ __device__ __forceinline__ bool tab_claim(const BmState& s, int64_t i, int32_t e
 // 0 if it took an empty slot, -1 if the table was full (cannot happen: the
 // load stays below 1/2 because of the rebuild threshold). `hint` is a slot on
 // h's probe path at or before which nothing is free (from tab_find), or -1.
-__device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page, int64_t hint = -1) {
+__device__ int32_t tab_insert(const BmState& s, uint64_t h, int32_t page, int32_t ref,
+                              int64_t hint = -1) {
   const int64_t mask = s.C - 1;
   if (hint >= 0) {  // usually still free: one compare-and-swap
-    if (tab_claim(s, hint, kEmpty, h, page)) return 0;
-    if (tab_claim(s, hint, kTomb, h, page)) return 1;
+    if (tab_claim(s, hint, kEmpty, h, page, ref)) return 0;
+    if (tab_claim(s, hint, kTomb, h, page, ref)) return 1;
   }
   int64_t i = slot_of(h) & mask;
   for (int64_t n = 0; n < 2 * s.C; ++n) {
     const int32_t v =
         __hip_atomic_load(ent_page(s, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if ((v == kEmpty || v == kTomb) && tab_claim(s, i, v, h, page)) return v == kTomb ? 1 : 0;
+    if ((v == kEmpty || v == kTomb) && tab_claim(s, i, v, h, page, ref))
+      return v == kTomb ? 1 : 0;
     if (v == kEmpty || v == kTomb) continue;  // lost the race for this slot: look again
     i = (i + 1) & mask;
   }
@@ -327,9 +339,32 @@ __device__ void tab_rebuild(const BmArgs& a, Ctrs& c) {
   for (int64_t i = threadIdx.x; i < s.C; i += kBmThreads) *ent_page(s, i) = kEmpty;
   __syncthreads();
   for (int32_t p = threadIdx.x; p < s.P; p += kBmThreads)
-    if (*rec_flag(s, p) & 1) tab_insert(s, *rec_hash(s, p), p);
+    if (*rec_flag(s, p) & 1) tab_insert(s, *rec_hash(s, p), p, *rec_ref(s, p));
   __syncthreads();
   c.tombs = 0;
+}
+
+// A page taken for request r (from the free stack or by eviction): table index
+// i < n_pages gets refcount 2 (parent and child), except a partial last page
+// (1: the child copies it); otherwise it is the child's copy (refcount 1).
+// The taker of the table's last page or of the copy reports it.
+__device__ __forceinline__ void take_page(const BmArgs& a, int32_t r, int32_t p, int64_t i,
+                                          int64_t n_pages, bool in_table, bool cow, int32_t* row) {
+  if (in_table) {
+    row[i] = p;
+    const bool last = i == n_pages - 1;
+    *rec_ref(a.s, p) = (cow && last) ? 1 : 2;
+    if (last) {
+      if (cow)
+        a.cow_src[r] = p;
+      else
+        a.child_last[r] = p;
+    }
+  } else {
+    *rec_ref(a.s, p) = 1;
+    a.cow_dst[r] = p;
+    a.child_last[r] = p;
+  }
 }
 
 __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int64_t h0,
@@ -358,28 +393,27 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   const int64_t may_take = n_pages + (cow ? 1 : 0);
   const int64_t pf_n = may_take < c.free_top ? may_take : c.free_top;
   const int32_t pf_page = tid < pf_n ? s.free_list[c.free_top - 1 - tid] : -1;
-  int32_t held_pg[kHeld];
-  int64_t held_ins[kHeld];
-  int32_t held_ref[kHeld];
+  // per held page: the probe's page (or -1), the mirrored refcount, and the
+  // entry's slot (a hit) or the insertion slot (a miss)
+  int32_t held_pg[kHeld], held_ref[kHeld], held_slot[kHeld];
   int32_t miss = INT_MAX;
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
     const int64_t i = tid + (int64_t)j * kBmThreads;
     held_pg[j] = -1;
-    held_ins[j] = -1;
     held_ref[j] = 1;
+    held_slot[j] = -1;
     if (i < m) {
-      const int32_t p = tab_find(s, hk[j], &held_ins[j]);
-      row[i] = p;
-      held_pg[j] = p;
-      if (p >= 0)
-        held_ref[j] = *rec_ref(s, p);
-      else
-        miss = (int32_t)i < miss ? (int32_t)i : miss;
+      const Found f = tab_find(s, hk[j]);
+      row[i] = f.page;
+      held_pg[j] = f.page;
+      held_ref[j] = f.page >= 0 ? f.ref : 1;
+      held_slot[j] = f.slot;
+      if (f.page < 0 && (int32_t)i < miss) miss = (int32_t)i;
     }
   }
   for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < m; i += kBmThreads) {
-    const int32_t p = tab_find(s, a.hashes[h0 + i]);
+    const int32_t p = tab_find(s, a.hashes[h0 + i]).page;
     row[i] = p;
     if (p < 0 && (int32_t)i < miss) miss = (int32_t)i;
   }
@@ -396,17 +430,18 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   // 2. hits that are evictable now get pinned: count them for the OOM check
   //    (every thread adds up the ballots itself; hits past the held pages, if
   //    any, through one more reduction)
-  int64_t pinned = 0;
-#pragma unroll
-  for (int j = 0; j < kHeld; ++j) {
-#pragma unroll 4
-    for (int w = 0; w < kBmWaves; ++w) {
-      const int64_t first = (int64_t)j * kBmThreads + w * 64;
-      if (first >= k) break;
-      const uint64_t em = sh.evmask[j][w];
-      pinned += __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
+  //    (each lane of every wave takes one wave-ballot of the probe, so every
+  //    wave computes the same total)
+  static_assert(kHeld * kBmWaves <= 64, "one ballot per lane");
+  int32_t mine = 0;
+  if (lane < kHeld * kBmWaves) {
+    const int64_t first = (int64_t)(lane / kBmWaves) * kBmThreads + (lane % kBmWaves) * 64;
+    if (first < k) {
+      const uint64_t em = sh.evmask[lane / kBmWaves][lane % kBmWaves];
+      mine = __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
     }
   }
+  int64_t pinned = wave_sum(mine);
   if (k > (int64_t)kHeld * kBmThreads) {
     int32_t cnt = 0;
     for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
@@ -427,11 +462,24 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   }
 
   // 3. pin the hits, for the parent and the forked child at once (+2)
+  //    (the owner of the table's last page, when it is a hit, also reports it
+  //    as the child's last page: with a partial last page it is never a hit)
 #pragma unroll
-  for (int j = 0; j < kHeld; ++j)
-    if (tid + (int64_t)j * kBmThreads < k) *rec_ref(s, held_pg[j]) = held_ref[j] + 2;
-  for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
-    *rec_ref(s, row[i]) += 2;
+  for (int j = 0; j < kHeld; ++j) {
+    const int64_t i = tid + (int64_t)j * kBmThreads;
+    if (i < k) {
+      *rec_ref(s, held_pg[j]) = held_ref[j] + 2;
+      *ent_ref(s, held_slot[j]) = held_ref[j] + 2;
+      if (i == n_pages - 1) a.child_last[r] = held_pg[j];
+    }
+  }
+  for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads) {
+    const int32_t p = row[i];
+    const RecHead h = rec_head(s, p);
+    *rec_ref(s, p) = h.ref + 2;
+    *ent_ref(s, h.slot) = h.ref + 2;
+    if (i == n_pages - 1) a.child_last[r] = p;
+  }
   c.evictable -= pinned;
   const int64_t from_free = take < c.free_top ? take : c.free_top;
   if (pinned > 0 && from_free < take) __syncthreads();  // pins land before liveness checks
@@ -441,15 +489,10 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   //    except a partial last page, which the child copies: 1), the last (if
   //    any) is the child's copy (refcount 1).
   const int64_t table_new = n_pages - k;
+  //    Whoever takes the table's last page or the child's copy reports it.
   for (int64_t j = tid; j < from_free; j += kBmThreads) {
     const int32_t p = j == tid ? pf_page : s.free_list[c.free_top - 1 - j];
-    if (j < table_new) {
-      row[k + j] = p;
-      *rec_ref(s, p) = (cow && k + j == n_pages - 1) ? 1 : 2;
-    } else {
-      a.cow_dst[r] = p;
-      *rec_ref(s, p) = 1;
-    }
+    take_page(a, r, p, k + j, n_pages, table_new - j > 0, cow, row);
   }
   c.free_top -= from_free;
   int64_t done = from_free;
@@ -476,13 +519,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
       const int64_t j = done + rank;
       *ent_page(s, h.slot) = kTomb;  // the page's key leaves the table
       *rec_flag(s, pg) = h.flag & ~1;
-      if (j < table_new) {
-        row[k + j] = pg;
-        *rec_ref(s, pg) = (cow && k + j == n_pages - 1) ? 1 : 2;
-      } else {
-        a.cow_dst[r] = pg;
-        *rec_ref(s, pg) = 1;
-      }
+      take_page(a, r, pg, k + j, n_pages, j < table_new, cow, row);
       if (c.log_len + (j - from_free) < a.evict_cap)
         a.evict_log[c.log_len + (j - from_free)] = pg;
       if (rank == want - 1) sh.new_head = pos + 1;
@@ -524,7 +561,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     const int32_t p = row[i];
     *rec_hash(s, p) = hk[j];
     *rec_flag(s, p) = 1;
-    reused += tab_insert(s, hk[j], p, held_pg[j] < 0 ? held_ins[j] : -1) == 1;
+    reused += tab_insert(s, hk[j], p, 2, held_pg[j] < 0 ? held_slot[j] : -1) == 1;
   }
   __syncthreads();
   // pages past the held ones (requests longer than kHeld*kBmThreads pages)
@@ -534,14 +571,14 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     uint64_t h = 0;
     if (i < m && i >= k) {
       h = a.hashes[h0 + i];
-      rg = tab_find(s, h) < 0;
+      rg = tab_find(s, h).page < 0;
     }
     __syncthreads();
     if (rg) {
       const int32_t p = row[i];
       *rec_hash(s, p) = h;
       *rec_flag(s, p) = 1;
-      reused += tab_insert(s, h, p) == 1;
+      reused += tab_insert(s, h, p, 2) == 1;
     }
     __syncthreads();
   }
@@ -550,15 +587,12 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   __syncthreads();
   c.tombs -= sh.tomb_reused[par];
 
-  if (tid == 0) {
+  if (tid == 0) {  // the page-valued results were written by their owners
     a.hits[r] = (int32_t)k;
     a.status[r] = kStOk;
-    if (cow) {
-      a.cow_src[r] = row[n_pages - 1];
-      a.child_last[r] = a.cow_dst[r];
-    } else {
+    if (!cow) {
       a.cow_src[r] = a.cow_dst[r] = -1;
-      a.child_last[r] = n_pages ? row[n_pages - 1] : -1;
+      if (n_pages == 0) a.child_last[r] = -1;
     }
   }
 }
@@ -605,6 +639,7 @@ __device__ void release(const BmArgs& a, int32_t r, int32_t n, Ctrs& c, Shared& 
       const RecHead h = rec_head(s, page);
       const int32_t left = h.ref - ((cow && i == n_pages - 1) ? 1 : 2);
       *rec_ref(s, page) = left;
+      if (h.flag & 1) *ent_ref(s, h.slot) = left;
       if (left == 0) {
         to_lru = (h.flag & 1) != 0;
         to_free = !to_lru;
@@ -713,6 +748,37 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   }
 }
 
+// Read-only lookup (mkv_hash_probe): one workgroup per request probes its page
+// hashes 256 at a time; the first miss comes from an LDS minimum.
+constexpr int kProbeThreads = 256;
+
+__global__ __launch_bounds__(kProbeThreads) void probe_kernel(BmState s, const uint64_t* hashes,
+                                                              const int64_t* off, int32_t* pages,
+                                                              int32_t* hits, int32_t* err) {
+  __shared__ int32_t first_miss;
+  const int32_t r = blockIdx.x;
+  const int64_t h0 = off[r], m = off[r + 1] - h0;
+  if (threadIdx.x == 0) first_miss = INT_MAX;
+  __syncthreads();
+  if (m < 0) {
+    if (threadIdx.x == 0) {
+      hits[r] = 0;
+      raise_err(err, MKV_DEVERR_TABLE);
+    }
+    return;
+  }
+  int32_t miss = INT_MAX;
+  for (int64_t i = threadIdx.x; i < m; i += kProbeThreads) {
+    const int32_t p = tab_find(s, hashes[h0 + i]).page;
+    pages[h0 + i] = p;
+    if (p < 0 && (int32_t)i < miss) miss = (int32_t)i;
+  }
+  miss = wave_min(miss);
+  if ((threadIdx.x & 63) == 0 && miss != INT_MAX) atomicMin(&first_miss, miss);
+  __syncthreads();
+  if (threadIdx.x == 0) hits[r] = first_miss < m ? first_miss : (int32_t)m;
+}
+
 __global__ __launch_bounds__(256) void bm_init_kernel(BmState s, const int32_t* free_order) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -798,4 +864,21 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   a.err = err;
   hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, as_stream(stream), a);
   return check_launch("mkv_bm_step");
+}
+
+extern "C" int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_hashes,
+                              const int64_t* hash_offsets, int32_t num_requests, int32_t* pages,
+                              int32_t* hits, int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(num_pages > 0 && num_pages <= (1 << 28) && num_requests >= 0, MKV_E_INVALID,
+              "mkv_hash_probe: bad sizes");
+  if (num_requests == 0) return MKV_OK;
+  MKV_REQUIRE(state && page_hashes && hash_offsets && pages && hits && err, MKV_E_INVALID,
+              "mkv_hash_probe: null pointer");
+  MKV_REQUIRE(((uintptr_t)state & 255) == 0, MKV_E_ALIGN,
+              "mkv_hash_probe: state must be 256-byte aligned");
+  const BmState s = bm_state(const_cast<void*>(state), num_pages);
+  hipLaunchKernelGGL(probe_kernel, dim3((unsigned)num_requests), dim3(kProbeThreads), 0,
+                     as_stream(stream), s, page_hashes, hash_offsets, pages, hits, err);
+  return check_launch("mkv_hash_probe");
 }

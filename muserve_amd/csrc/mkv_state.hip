@@ -7,9 +7,10 @@
 // recurrent and conv states travel together. Work is cut into 16 KiB pieces
 // (256 threads x 4 x 16 bytes): grid.x is the piece within an entry (pool 0's
 // pieces, then pool 1's), grid.y the entry, so nothing is decoded by
-// division; a workgroup issues its four loads before its four stores, both
-// non-temporal (each byte is moved once; on MI355X this streams faster than
-// a vendor device-to-device copy of the same bytes).
+// division; a workgroup issues its four loads before its four stores. Loads
+// are non-temporal; a gather's output uses ordinary stores (the layer that
+// gathered it reads it next, often still from the MALL), a scatter's pool
+// writes non-temporal ones (the slot is not read again this step).
 #include "mkv_device.h"
 
 namespace mkv {
@@ -31,6 +32,14 @@ struct StateArgs {
   int32_t n;
   int32_t* err;
 };
+
+template <bool GATHER>
+__device__ __forceinline__ void store(uint8_t* p, u32x4 v) {
+  if (GATHER)
+    st16(p, v);
+  else
+    st_nt(p, v);
+}
 
 template <bool GATHER>
 __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
@@ -55,7 +64,7 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = ld_nt(src + (u * kThreads + threadIdx.x) * 16);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) st_nt(dst + (u * kThreads + threadIdx.x) * 16, v[u]);
+      for (int u = 0; u < kUnroll; ++u) store<GATHER>(dst + (u * kThreads + threadIdx.x) * 16, v[u]);
       continue;
     }
 #pragma unroll
@@ -67,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t off = (u * kThreads + threadIdx.x) * 16;
-      if (base + off < bytes) st_nt(dst + off, v[u]);
+      if (base + off < bytes) store<GATHER>(dst + off, v[u]);
     }
   }
 }

@@ -70,6 +70,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         assert tables[r, :npg].tolist() == w["table"], r
         assert (cl[r], cs[r], cd[r]) == (w["child_last"], w["cow_src"], w["cow_dst"]), r
     snap = bm.snapshot()
+    assert snap["table_ok"]  # entries = cached pages, with their keys and refcounts
     assert snap["free"] == model.free
     assert snap["lru"] == model.lru_order()
     assert snap["ref"] == model.ref
@@ -79,6 +80,17 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     if with_data:
         assert torch.equal(bits16(cache.cache), cpu.view(torch.int16))
         cache.check_errors()
+    # read-only probe of every request against the final table
+    pages, hit = bm.probe(hashes, off)
+    pages, hit = pages.cpu().tolist(), hit.cpu().tolist()
+    bm.check_errors()
+    for r in range(n):
+        h = [int(v) for v in hu[cu_pages[r]:cu_pages[r + 1]]]
+        want_pages = [model.table.get(x, -1) for x in h]
+        assert pages[cu_pages[r]:cu_pages[r + 1]] == want_pages, r
+        lead = next((i for i, p in enumerate(want_pages) if p < 0), len(h))
+        assert hit[r] == lead, r
+    assert bm.snapshot()["lru"] == snap["lru"]  # nothing moved
     return status, model
 
 
@@ -97,7 +109,7 @@ def test_larger_trace_with_ring_compaction():
 
 
 def test_long_requests_past_the_register_held_pages():
-    # up to 2600 pages per request: pages past the first 2048 of a request take
+    # up to 2600 pages per request: pages past the first 1024 of a request take
     # the kernel's memory-resident path (probe, pin, register)
     case("block manager: 5400-page pool, 14 requests of ~2300-2600 pages")
     status, model = run(P=5400, n=14, batch=2, seed=11, n_templates=2, template_len=36000,
