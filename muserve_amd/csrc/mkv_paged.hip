@@ -79,8 +79,8 @@ __global__ __launch_bounds__(kDataThreads) void gather_data_kernel(GatherArgs a)
   const int col = threadIdx.x % RC;
   const int rsub = threadIdx.x / RC;
   const uint8_t* plane = (t.is_v ? a.v_pool : a.k_pool) + (int64_t)t.layer * a.pool_layer_stride;
-  uint8_t* out = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
-                 t.out_row * ROW_BYTES + col * 16;
+  uint8_t* tile = (t.is_v ? a.v_out : a.k_out) + (int64_t)t.layer * a.out_layer_stride +
+                  t.out_row * ROW_BYTES;
   u32x4 v[CPT];
   if (t.full_data()) {
     // Straight-line: the waitcnt pass can overlap the stores (vmcnt counts
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kDataThreads) void gather_data_kernel(GatherArgs a)
       v[i] = ld_nt(plane + ((int64_t)t.page_of(p) * 16 + (p & 15)) * ROW_BYTES + col * 16);
     }
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) st_nt(out + (int64_t)(rsub + i * RSTEP) * ROW_BYTES, v[i]);
+    for (int i = 0; i < CPT; ++i) st_stream(tile, (rsub + i * RSTEP) * ROW_BYTES + col * 16, v[i]);
     return;
   }
   // Last data tile (or one with a bad page id): per-row guards.
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(kDataThreads) void gather_data_kernel(GatherArgs a)
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int r = rsub + i * RSTEP;
-    if (t.row0 + r < row_limit) st_nt(out + (int64_t)r * ROW_BYTES, v[i]);
+    if (t.row0 + r < row_limit) st_stream(tile, r * ROW_BYTES + col * 16, v[i]);
   }
 }
 

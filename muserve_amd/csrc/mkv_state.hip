@@ -10,7 +10,7 @@
 // division; a workgroup issues its four loads before its four stores. Loads
 // are non-temporal; a gather's output uses ordinary stores (the layer that
 // gathered it reads it next, often still from the MALL), a scatter's pool
-// writes non-temporal ones (the slot is not read again this step).
+// writes streaming ones (st_stream: the slot is not read again this step).
 #include "mkv_device.h"
 
 namespace mkv {
@@ -33,12 +33,13 @@ struct StateArgs {
   int32_t* err;
 };
 
+// base is the workgroup's piece (uniform), off the lane's offset in it
 template <bool GATHER>
-__device__ __forceinline__ void store(uint8_t* p, u32x4 v) {
+__device__ __forceinline__ void store(uint8_t* base, uint32_t off, u32x4 v) {
   if (GATHER)
-    st16(p, v);
+    st16(base + off, v);
   else
-    st_nt(p, v);
+    st_stream(base, off, v);
 }
 
 template <bool GATHER>
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = ld_nt(src + (u * kThreads + threadIdx.x) * 16);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) store<GATHER>(dst + (u * kThreads + threadIdx.x) * 16, v[u]);
+      for (int u = 0; u < kUnroll; ++u) store<GATHER>(dst, (u * kThreads + threadIdx.x) * 16, v[u]);
       continue;
     }
 #pragma unroll
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int64_t off = (u * kThreads + threadIdx.x) * 16;
-      if (base + off < bytes) store<GATHER>(dst + off, v[u]);
+      if (base + off < bytes) store<GATHER>(dst, (uint32_t)off, v[u]);
     }
   }
 }
