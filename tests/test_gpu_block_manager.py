@@ -17,7 +17,25 @@ from tests.gpu_util import DEV, bits16, case
 pytestmark = pytest.mark.gpu
 
 
-def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False):
+def interleaved_ops(n, batch):
+    """Per batch: admit the batch, then release the previous batch's requests
+    one at a time between them (single releases, not runs)."""
+    out = []
+    for b0 in range(0, n, batch):
+        prev = list(range(max(0, b0 - batch), b0))
+        cur = list(range(b0, min(n, b0 + batch)))
+        ops = []
+        for i, r in enumerate(cur):
+            ops.append(r)
+            if i < len(prev):
+                ops.append(-(prev[i] + 1))
+        ops += [-(r + 1) for r in prev[len(cur):]]
+        out.append(ops)
+    return out
+
+
+def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False,
+        ops_fn=bench.prefix_ops):
     reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
                                  template_len=template_len, suffix=suffix)
     lens = [len(x) for x in reqs]
@@ -38,7 +56,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     off = torch.from_numpy(cu_pages).to(DEV)
     ntok = torch.tensor(lens, dtype=torch.int32, device=DEV)
     want = {}
-    for ops in bench.prefix_ops(n, batch):
+    for ops in ops_fn(n, batch):
         bm.step(torch.tensor(ops, dtype=torch.int32), hashes, off, ntok)
         pairs = []
         for op in ops:
@@ -124,6 +142,47 @@ def test_many_evictions_rebuild_the_table():
     status, model = run(P=72, n=1500, batch=6, seed=21, n_templates=40, template_len=128,
                         suffix=(1, 120), width=32)
     assert len(model.evicted) > 2000
+
+
+def test_long_release_runs():
+    # batches of 100 requests of ~190-230 pages: runs of 100 releases dropping
+    # ~21,000 page references, in a pool small enough to evict thousands
+    case("block manager: 4000-page pool, 400 requests, batches of 100")
+    status, model = run(P=4000, n=400, batch=100, seed=9, n_templates=8, template_len=3000,
+                        suffix=(1, 600), width=240)
+    assert len(model.evicted) > 4000
+
+
+def test_single_releases_between_admits():
+    case("block manager: 72-page pool, 240 requests, releases between admits")
+    status, model = run(P=72, n=240, batch=6, seed=105, n_templates=6, template_len=128,
+                        suffix=(1, 120), width=32, ops_fn=interleaved_ops)
+    assert len(model.evicted) > 100
+
+
+def test_duplicate_release_is_flagged_once():
+    case("block manager: a request released twice in one step")
+    reqs = bench.prefix_requests(3, seed=3, n_templates=1, template_len=64, suffix=(5, 20))
+    lens = [len(x) for x in reqs]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    hashes, cu_pages = page_hashes(torch.from_numpy(np.concatenate(reqs)).to(DEV), cu)
+    off = torch.from_numpy(cu_pages).to(DEV)
+    ntok = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    free = list(range(64))
+    bm = BlockManager(64, 3, 8, DEV, free_order=free)
+    model = BlockManagerModel(64, free)
+    bm.step(torch.tensor([0, 1, 2], dtype=torch.int32), hashes, off, ntok)
+    hu = as_u64(hashes)
+    for r in range(3):
+        model.admit(r, [int(v) for v in hu[cu_pages[r]:cu_pages[r + 1]]], lens[r])
+    bm.step(torch.tensor([-1, -2, -1, -3], dtype=torch.int32), hashes, off, ntok)  # 0 twice
+    with pytest.raises(_lib.MkvDeviceError, match="block manager"):
+        bm.check_errors()
+    for r in (0, 1, 2):
+        model.release(r)
+    snap = bm.snapshot()
+    assert snap["table_ok"] and snap["ref"] == model.ref and snap["free"] == model.free
+    assert snap["lru"] == model.lru_order()
 
 
 def test_release_of_unknown_request_is_flagged():
