@@ -162,13 +162,12 @@ __global__ __launch_bounds__(kThreads) void decode_slots_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// page copies: one workgroup per (pair, plane).
+// page copies: one workgroup per (pair, plane) on a 2-D grid.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void copy_pages_kernel(
-    uint8_t* pool, int64_t plane_stride, int32_t num_planes, int64_t num_pages,
-    int64_t page_bytes, const int32_t* src, const int32_t* dst, int32_t* err) {
-  const int32_t i = blockIdx.x / num_planes;
-  const int32_t q = blockIdx.x - i * num_planes;
+    uint8_t* pool, int64_t plane_stride, int64_t num_pages, int64_t page_bytes,
+    const int32_t* src, const int32_t* dst, int32_t* err) {
+  const uint32_t i = blockIdx.x, q = blockIdx.y;  // pair, plane
   const int32_t s = src[i], d = dst[i];
   if (s < 0 || d < 0) return;  // a negative id marks "no copy" for this pair
   if (s >= num_pages || d >= num_pages) {
@@ -178,6 +177,17 @@ __global__ __launch_bounds__(kThreads) void copy_pages_kernel(
   const uint8_t* sp = pool + q * plane_stride + (int64_t)s * page_bytes;
   uint8_t* dp = pool + q * plane_stride + (int64_t)d * page_bytes;
   const int64_t chunks = page_bytes / 16;
+  const uint32_t o0 = threadIdx.x * 16, o1 = (threadIdx.x + kThreads) * 16;
+  if (chunks == 2 * kThreads) {  // an 8 KiB page (bf16, 1 head of 256): straight-line
+    const u32x4 v0 = ld_nt(sp + o0), v1 = ld_nt(sp + o1);
+    st_stream(dp, o0, v0);
+    st_stream(dp, o1, v1);
+    return;
+  }
+  if (chunks == kThreads) {  // a 4 KiB page (fp8, or bf16 rows of 128 values)
+    st_stream(dp, o0, ld_nt(sp + o0));
+    return;
+  }
   constexpr int U = 4;
   for (int64_t c0 = threadIdx.x; c0 < chunks; c0 += (int64_t)kThreads * U) {
     u32x4 v[U];
@@ -288,10 +298,9 @@ extern "C" int mkv_copy_blocks(void* pool, int64_t plane_stride, int32_t num_pla
   MKV_REQUIRE(aligned16(pool) && plane_stride % 16 == 0 && page_bytes > 0 && page_bytes % 16 == 0,
               MKV_E_ALIGN,
               "mkv_copy_blocks: pool, plane stride and page bytes must be 16-byte aligned");
-  MKV_REQUIRE((int64_t)n * num_planes < (1ll << 31), MKV_E_UNSUPPORTED,
-              "mkv_copy_blocks: too many pages for one call");
-  hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)(n * num_planes)), dim3(kThreads), 0,
-                     as_stream(stream), (uint8_t*)pool, plane_stride, num_planes, num_pages,
-                     page_bytes, src_pages, dst_pages, err);
+  MKV_REQUIRE(num_planes <= 65535, MKV_E_UNSUPPORTED, "mkv_copy_blocks: too many planes for one call");
+  hipLaunchKernelGGL(copy_pages_kernel, dim3((unsigned)n, (unsigned)num_planes), dim3(kThreads), 0,
+                     as_stream(stream), (uint8_t*)pool, plane_stride, num_pages, page_bytes,
+                     src_pages, dst_pages, err);
   return check_launch("mkv_copy_blocks");
 }
