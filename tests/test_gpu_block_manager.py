@@ -46,7 +46,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     for r in (0, n // 2, n - 1):  # the GPU hashes are the prefix keys
         assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r])
     free = np.random.default_rng(seed).permutation(P).tolist()
-    bm = BlockManager(P, n, width, DEV, free_order=free, evict_log_capacity=1 << 16)
+    bm = BlockManager(P, n, width, DEV, free_order=free, evict_log_capacity=1 << 20)
     model = BlockManagerModel(P, free)
     cache = cpu = None
     if with_data:

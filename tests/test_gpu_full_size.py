@@ -1,0 +1,144 @@
+"""Parity at the benchmark configurations' full sizes, through properties that
+do not depend on size: append -> gather round trips, oracle checks of sampled
+rows, gather/scatter identities, and the whole prefix-cache trace against the
+OrderedDict model."""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from muserve_amd.kv_cache import PagedKVCache, SequenceKVState, prefill_slot_mapping, reserve_tokens, slot_mapping_for
+from muserve_amd.state_pool import StatePool
+from oracle import fp8 as ref
+from tests.gpu_util import DEV, case
+from tests.test_gpu_block_manager import run as run_block_manager
+
+pytestmark = pytest.mark.gpu
+
+
+def _tables(seqs, width):
+    bt = torch.zeros(len(seqs), width, dtype=torch.int32)
+    for b, s in enumerate(seqs):
+        bt[b, :len(s.page_table)] = torch.tensor(s.page_table, dtype=torch.int32)
+    return bt.to(DEV)
+
+
+def test_decode_config_append_gather_round_trip():
+    case("full size: 256 sequences, lognormal lengths (seed 102), 15 layers, padded gather")
+    ctx = bench.context_lengths()
+    B, L = len(ctx), 15
+    cache = PagedKVCache(int(np.sum(-(-ctx // 16))) + 16, num_layers=L, dtype=torch.bfloat16,
+                         device=DEV, verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(102))
+    seqs = [SequenceKVState() for _ in range(B)]
+    slots = prefill_slot_mapping(cache, seqs, ctx.tolist())
+    T = int(ctx.sum())
+    bt = _tables(seqs, max(len(s.page_table) for s in seqs))
+    lens = torch.from_numpy(ctx.astype(np.int32)).to(DEV)
+    lpad = int(-(-int(ctx.max()) // 16) * 16)
+    # row of padded output [B*lpad] for every appended token, in append order
+    rows = np.concatenate([b * lpad + np.arange(n) for b, n in enumerate(ctx)])
+    rows = torch.from_numpy(rows).to(DEV)
+    gen = torch.Generator(device=DEV).manual_seed(102)
+    for layer in range(L):
+        k = torch.randn(T, 1, 256, generator=gen, device=DEV).bfloat16()
+        v = torch.randn(T, 1, 256, generator=gen, device=DEV).bfloat16()
+        cache.append(slots, k, v, layer=layer)
+        kd, vd = cache.gather(layer, bt, lens, out_len=lpad)
+        for got, src in ((kd, k), (vd, v)):
+            want = torch.zeros(B * lpad, 1, 256, dtype=torch.bfloat16, device=DEV)
+            want[rows] = src
+            assert torch.equal(got.reshape(B * lpad, 1, 256).view(torch.int16),
+                               want.view(torch.int16)), layer
+        del kd, vd
+    cache.check_errors()
+
+
+def test_fp8_config_append_and_window_sampled_against_oracle():
+    case("full size: fp8 pool of 262160 pages x 15 layers, 32 x 2048-token chunks into 128k contexts")
+    R, CHUNK, CTX, WIN, L = 32, 2048, 131072, 8192, 15
+    cache = PagedKVCache(R * CTX // 16 + 16, num_layers=L, dtype=torch.float8_e4m3fn, device=DEV,
+                         verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(103))
+    seqs = [SequenceKVState() for _ in range(R)]
+    prior = CTX - CHUNK
+    g = torch.Generator().manual_seed(103)
+    gen = torch.Generator(device=DEV).manual_seed(103)
+
+    def kv(t):
+        x = torch.randn(L, t, 1, 256, generator=gen, device=DEV)
+        boost = torch.rand(L, t, 1, 256, generator=gen, device=DEV) < 0.01
+        return torch.where(boost, x * 20.0, x).bfloat16()
+
+    # positions before the window's start are reserved (pages allocated) but
+    # never read; the window's prior tokens and the chunk are appended
+    fill = WIN - CHUNK
+    for s in seqs:
+        reserve_tokens(cache, s, prior - fill)
+    sl = torch.from_numpy(np.concatenate(
+        [slot_mapping_for(s, reserve_tokens(cache, s, fill), fill) for s in seqs])).to(DEV)
+    cache.append(sl, kv(len(sl)), kv(len(sl)))
+    chunk_slots = np.concatenate([slot_mapping_for(s, reserve_tokens(cache, s, CHUNK), CHUNK)
+                                  for s in seqs])
+    k, v = kv(R * CHUNK), kv(R * CHUNK)
+    cache.append(torch.from_numpy(chunk_slots).to(DEV), k, v)
+    cache.check_errors()
+    # sampled appended rows vs the oracle's quantiser (codes and scales, bit for bit)
+    pick = torch.randperm(R * CHUNK, generator=g)[:4096]
+    for layer in (0, L - 1):
+        for kvi, x in ((0, k), (1, v)):
+            q, sc = ref.quantize_rows(x[layer, pick].cpu())
+            slot = torch.from_numpy(chunk_slots)[pick]
+            got_q = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[slot.to(DEV)].cpu()
+            got_s = cache.scales[layer, kvi].reshape(-1, 1)[slot.to(DEV)].cpu()
+            assert torch.equal(got_q, q) and torch.equal(got_s.view(torch.int32), sc.view(torch.int32))
+    # dequant-gather of every request's last 8192 tokens, sampled against the oracle
+    bt = _tables(seqs, CTX // 16)
+    lens = torch.full((R,), CTX, dtype=torch.int32, device=DEV)
+    starts = lens - WIN
+    cu = torch.arange(R + 1, dtype=torch.int64, device=DEV) * WIN
+    out_rows = torch.randperm(R * WIN, generator=g)[:4096]
+    b_idx, i_idx = out_rows // WIN, out_rows % WIN
+    pos = CTX - WIN + i_idx
+    tables = bt.cpu().to(torch.int64)
+    slot = tables[b_idx, pos // 16] * 16 + pos % 16
+    for layer in (0, 7, L - 1):
+        kd, vd = cache.gather(layer, bt, lens, out_len=WIN, starts=starts, cu_out=cu)
+        for kvi, got in ((0, kd), (1, vd)):
+            codes = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[slot.to(DEV)].cpu()
+            scales = cache.scales[layer, kvi].reshape(-1, 1)[slot.to(DEV)].cpu()
+            want = ref.dequant_rows(codes, scales)
+            assert torch.equal(got[out_rows.to(DEV)].cpu().view(torch.int16), want.view(torch.int16))
+    cache.check_errors()
+
+
+def test_gdn_config_gather_scatter_identities():
+    case("full size: GDN pool 45 x 1024 slots x ([8,128,128] fp32 + [2048,4] bf16), batch 256")
+    S, G, B = 1024, 45, 256
+    pool = StatePool(num_layers=G, num_slots=S, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(105)
+    pool.state.normal_(generator=gen)
+    pool.conv.normal_(generator=gen)
+    slots = torch.randperm(S, generator=torch.Generator().manual_seed(105))[:B]
+    idx = slots.to(DEV)
+    s32 = idx.to(torch.int32)
+    for g in range(G):
+        before_s, before_c = pool.state[g].clone(), pool.conv[g].clone()
+        st, cv = pool.gather(g, s32)
+        assert torch.equal(st, before_s[idx]) and torch.equal(cv, before_c[idx]), g
+        pool.scatter(g, s32, st + 1.0, cv + 1.0)
+        want_s, want_c = before_s, before_c
+        want_s[idx] = st + 1.0
+        want_c[idx] = cv + 1.0
+        assert torch.equal(pool.state[g], want_s) and torch.equal(pool.conv[g], want_c), g
+    pool.check_errors()
+
+
+def test_prefix_config_full_trace_against_model():
+    # 4096 requests (Zipf(1.1) over 64 templates of 4096 ids + 64..1024-token
+    # suffixes), batches of 256, 65536 pages: every admit, table, hit count,
+    # copy-on-write pair, the 89k-entry eviction order and the final state
+    case("full size: prefix cache, 4096 requests, 65536 pages, batches of 256")
+    status, model = run_block_manager(P=65536, n=4096, batch=256, seed=104, n_templates=64,
+                                      template_len=4096, suffix=(64, 1024), width=320)
+    assert len(model.evicted) > 50000
