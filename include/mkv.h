@@ -239,15 +239,19 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * The state is one caller-owned device buffer of mkv_bm_state_bytes(P) bytes
  * (256-byte aligned), initialised by mkv_bm_init with the free stack
  * free_order[0..P) (popped from the end; NULL = 0..P-1). mkv_bm_layout
- * writes 8 int64: table capacity C, ring capacity Q, then the byte offsets of
+ * writes 10 int64: table capacity C, ring capacity Q, then the byte offsets of
  * the counters (16 int64: free-stack top, ring head, ring tail, next stamp,
  * evictable pages, tombstones, eviction-log length), the table (C entries of
  * {u64 key, i32 page, i32 copy of the page's refcount}), the page records (P x 32 bytes: i32 refcount, i32
  * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
- * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), and the
- * total size.
+ * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), the
+ * last-occurrence slots (P int32, -1 between steps) and the release-run
+ * scratch (about 13 MiB: counters, per-op offsets, page ids and bit arrays of
+ * up to 2^20 page references), and the total size.
  *
- * mkv_bm_step runs ops[0..num_ops) in order on one workgroup: op r >= 0
+ * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
+ * (a leading run of up to 1024 releases is retired by many-workgroup passes,
+ * the rest on one workgroup): op r >= 0
  * admits request r, op -(r+1) releases it (r < num_requests, the length of
  * the per-request arrays; hash_offsets has num_requests+1 entries, tables
  * num_requests rows). Request r has num_tokens[r]

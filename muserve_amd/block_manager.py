@@ -51,11 +51,13 @@ class BlockManager:
         nbytes = lib.mkv_bm_state_bytes(num_pages)
         if nbytes <= 0:
             raise ValueError(f"bad page count {num_pages}")
-        lay = (ctypes.c_int64 * 8)()
+        lay = (ctypes.c_int64 * 10)()
         _lib.call("mkv_bm_layout", num_pages, ctypes.addressof(lay))
         # table capacity, ring capacity, byte offsets of counters, table, page
-        # records, free stack, ring; total bytes
-        self.layout = dict(zip(("C", "Q", "ctr", "ent", "rec", "free", "ring", "bytes"), lay))
+        # records, free stack, ring, last-occurrence slots, release-run
+        # scratch; total bytes
+        self.layout = dict(zip(("C", "Q", "ctr", "ent", "rec", "free", "ring", "last", "run",
+                                "bytes"), lay))
         self.state = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         if self.state.data_ptr() % 256:
             raise RuntimeError("state buffer is not 256-byte aligned")
@@ -169,7 +171,10 @@ class BlockManager:
         table_ok = bool(np.all(ent[slot, 2] == cp) and np.all(ent[slot, 3] == ref[cp]) and
                         np.all(ent.view(np.uint64).reshape(-1, 2)[slot, 0] == phash[cp]) and
                         int(np.count_nonzero(ent[:, 2] >= 0)) == len(cp))
+        # the release-run scratch's last-occurrence slots are -1 between steps
+        last_ok = bool(np.all(self._arr("last", P, torch.int32).cpu().numpy() == -1))
         return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(), "table_ok": table_ok,
+                "last_ok": last_ok,
                 "cached": cached.tolist(),
                 "hash": [int(phash[p]) if cached[p] else None for p in range(P)],
                 "evictable": ctr[_EVICTABLE], "log_len": ctr[_LOG_LEN]}

@@ -60,9 +60,19 @@ enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
 constexpr int32_t kEmpty = -1, kTomb = -2, kBusy = -3;
 constexpr int64_t kEntBytes = 16, kRecBytes = 32;
 
+// A leading run of release ops is retired by multi-workgroup kernels before
+// the one-workgroup step runs the rest (see the run kernels below); its
+// scratch lives in the state buffer.
+constexpr int kRunMaxOps = 1024;               // releases retired in bulk per step
+constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
+constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
+enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunNumCtr = 16 };
+
 struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
-  int64_t off_ctr, off_ent, off_rec, off_free, off_ring, bytes;
+  int64_t off_ctr, off_ent, off_rec, off_free, off_ring, off_last, off_run, bytes;
+  // inside the run scratch at off_run
+  int64_t run_ctr, run_off, run_child, run_page, run_bits, run_wpre;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -86,6 +96,14 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.off_rec = take((int64_t)P * kRecBytes);
   l.off_free = take((int64_t)P * 4);
   l.off_ring = take(l.Q * 8);
+  l.off_last = take((int64_t)P * 4);
+  l.off_run = o;
+  l.run_ctr = take(kRunNumCtr * 8);
+  l.run_off = take((kRunMaxOps + 1) * 8);
+  l.run_child = take(kRunMaxOps * 4);
+  l.run_page = take(kRunMaxElems * 4);
+  l.run_bits = take(3 * kRunMaxWords * 4);
+  l.run_wpre = take(2 * kRunMaxWords * 4);
   l.bytes = o;
   return l;
 }
@@ -96,6 +114,13 @@ struct BmState {
   uint8_t* rec;  // P x 32 bytes
   int32_t* free_list;
   uint64_t* ring;
+  int32_t* last;       // run: a page's last position in the run (-1 between runs)
+  int64_t* run_ctr;    // run: RunCtr values
+  int64_t* run_off;    // run: element offset of each op of the run
+  int32_t* run_child;  // run: the op's child copy page, -1 none, -2 releases nothing
+  int32_t* run_page;   // run: page id of each element
+  uint32_t* run_bits;  // run: [3][kRunMaxWords] to the ring / free stack / last occurrence
+  uint32_t* run_wpre;  // run: [2][kRunMaxWords] exclusive prefix counts of the first two
   int64_t C, Q;
   int32_t P;
 };
@@ -109,6 +134,13 @@ inline BmState bm_state(void* base, int32_t P) {
   s.rec = b + l.off_rec;
   s.free_list = reinterpret_cast<int32_t*>(b + l.off_free);
   s.ring = reinterpret_cast<uint64_t*>(b + l.off_ring);
+  s.last = reinterpret_cast<int32_t*>(b + l.off_last);
+  s.run_ctr = reinterpret_cast<int64_t*>(b + l.run_ctr);
+  s.run_off = reinterpret_cast<int64_t*>(b + l.run_off);
+  s.run_child = reinterpret_cast<int32_t*>(b + l.run_child);
+  s.run_page = reinterpret_cast<int32_t*>(b + l.run_page);
+  s.run_bits = reinterpret_cast<uint32_t*>(b + l.run_bits);
+  s.run_wpre = reinterpret_cast<uint32_t*>(b + l.run_wpre);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -673,6 +705,347 @@ __device__ __forceinline__ void fetch_hashes(const BmArgs& a, const OpMeta& om, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Bulk release of the step's leading run of release ops, on many CUs.
+//
+// Sequentially, release j walks L_j = [its child's private copy (if any),
+// then its table from the last page], dropping references; a page that
+// reaches zero is pushed at that moment (LRU ring if cached, free stack
+// otherwise). Concatenate the walks into one list L. During a run references
+// only fall, so a page reaches zero exactly at its last occurrence in L, and
+// only if the run drops all of its references. One workgroup walking L is
+// bound by how many scattered cache lines one CU can touch, so the run is
+// retired by five launches before the step kernel runs the remaining ops:
+//   setup (1 workgroup): the run (leading valid releases, at most kRunMaxOps
+//     ops and kRunMaxElems references), each op's status, child copy and
+//     reference count, their prefix sums, room on the ring;
+//   drop (many): every element subtracts its references from its page's
+//     refcount and records its position as the page's last occurrence;
+//   mark (many): an element is a zero-crossing iff it is its page's last
+//     occurrence and the refcount is now 0 (bit arrays: to the ring / to the
+//     free stack); a cached page's final refcount is mirrored into its entry;
+//   scan (1 workgroup): prefix counts of the bit words, the counters, the
+//     requests' statuses;
+//   push (many): every crossing written at its place in L order; the
+//     last-occurrence slots reset to -1.
+// No kernel waits for another workgroup; the launches order the passes.
+// ---------------------------------------------------------------------------
+constexpr int kRunThreads = 256;
+constexpr int kRunGrid = 256;                  // workgroups of the many-CU passes
+constexpr int kRunUnroll = 4;
+constexpr int kRunChunk = kRunUnroll * kRunThreads;  // elements a workgroup takes at a time
+
+__device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
+  return op < 0 && -(op + 1) < a.num_requests;
+}
+
+__global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
+  __shared__ Shared sh;
+  __shared__ int32_t first_non;
+  __shared__ uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
+  __shared__ int64_t off[kRunMaxOps + 1];
+  __shared__ int64_t wave_tot[kBmWaves];
+  static_assert(kRunMaxOps <= kBmThreads, "one op per thread");
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int limit = a.num_ops < kRunMaxOps ? a.num_ops : kRunMaxOps;
+  if (tid == 0) first_non = limit;
+  for (int i = tid; i < 2 * kRunMaxOps; i += kBmThreads) {
+    key[i] = 0xffffffffu;
+    firsti[i] = 0xffffffffu;
+  }
+  __syncthreads();
+  const int32_t op = tid < limit ? a.ops[tid] : 0;
+  const int32_t r = -(op + 1);
+  int32_t st = kStBad, nt = 0;
+  if (tid < limit) {
+    // the run also ends at an admitted request whose token count no longer
+    // fits its table (a caller error the step kernel handles as before)
+    bool ok = valid_release(a, op);
+    if (ok) {
+      st = a.status[r];
+      nt = a.ntok[r];
+      ok = st != kStOk || (nt >= 0 && (nt + 15) / 16 <= a.twidth);
+    }
+    if (!ok) atomicMin(&first_non, tid);
+  }
+  __syncthreads();
+  int n = first_non;
+  if (n < 2) {
+    if (tid == 0) s.run_ctr[kRunOps] = 0;
+    return;
+  }
+  // a request released twice: the earliest op releases; sequentially a later
+  // one finds it released (a caller error) unless it got OOM (silent)
+  uint32_t slot = 0;
+  if (tid < n) {
+    slot = ((uint32_t)r * 2654435761u) & (2 * kRunMaxOps - 1);
+    for (;;) {  // at most n of 2 kRunMaxOps slots are taken
+      const uint32_t prev = atomicCAS(&key[slot], 0xffffffffu, (uint32_t)r);
+      if (prev == 0xffffffffu || prev == (uint32_t)r) break;
+      slot = (slot + 1) & (2 * kRunMaxOps - 1);
+    }
+    atomicMin(&firsti[slot], (uint32_t)tid);
+  }
+  __syncthreads();
+  int64_t cnt = 0;
+  int32_t child = -2;
+  if (tid < n) {
+    if (firsti[slot] == (uint32_t)tid && st == kStOk) {
+      const bool cow = (nt & 15) != 0;
+      child = cow ? a.child_last[r] : -1;
+      cnt = (nt + 15) / 16 + (cow ? 1 : 0);
+    } else if (st != kStOom) {
+      raise_err(a.err, MKV_DEVERR_BM);
+    }
+  }
+  // exclusive prefix sum of the counts
+  int64_t incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int64_t before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kBmWaves; ++w) {
+    before += w < wave ? wave_tot[w] : 0;
+    total += wave_tot[w];
+  }
+  if (tid < n) off[tid] = before + incl - cnt;
+  if (tid == 0) off[n] = total;
+  __syncthreads();
+  if (total > kRunMaxElems) {  // the longest prefix of ops that fits
+    int lo = 0, hi = n;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= kRunMaxElems) lo = mid; else hi = mid - 1;
+    }
+    n = lo;  // ops after it are the step kernel's (it repeats any error bit)
+  }
+  if (n < 2) {
+    if (tid == 0) s.run_ctr[kRunOps] = 0;
+    return;
+  }
+  // room on the ring for at most one push per distinct page
+  Ctrs c;
+  c.free_top = s.ctr[kFreeTop];
+  c.head = s.ctr[kHead];
+  c.tail = s.ctr[kTail];
+  c.next_stamp = s.ctr[kNextStamp];
+  c.evictable = s.ctr[kEvictable];
+  c.tombs = s.ctr[kTombs];
+  c.log_len = s.ctr[kLogLen];
+  const int64_t pushes = off[n] < s.P ? off[n] : s.P;
+  if (c.tail - c.head + pushes > s.Q) {
+    int buf = 0;
+    ring_compact(a, c, sh, buf);
+    if (tid == 0) s.ctr[kTail] = c.tail;
+  }
+  for (int j = tid; j <= n; j += kBmThreads) s.run_off[j] = off[j];
+  if (tid < n) s.run_child[tid] = child;
+  if (tid == 0) {
+    s.run_ctr[kRunOps] = n;
+    s.run_ctr[kRunTotal] = off[n];
+  }
+}
+
+// The run's per-op tables, staged in a pass workgroup's LDS.
+struct RunOps {
+  int64_t off[kRunMaxOps + 1];
+  int32_t child[kRunMaxOps];
+  int32_t req[kRunMaxOps];
+  int32_t np[kRunMaxOps];
+};
+
+__device__ __forceinline__ void run_stage(const BmArgs& a, int n, RunOps& ro) {
+  for (int j = threadIdx.x; j <= n; j += kRunThreads) ro.off[j] = a.s.run_off[j];
+  for (int j = threadIdx.x; j < n; j += kRunThreads) {
+    ro.child[j] = a.s.run_child[j];
+    const int32_t r = -(a.ops[j] + 1);
+    ro.req[j] = r;
+    ro.np[j] = (a.ntok[r] + 15) / 16;
+  }
+  __syncthreads();
+}
+
+// Element e of the run: its page and the references it drops. Its op is the
+// last one starting at or before e (ops without elements share offsets).
+__device__ __forceinline__ void run_elem(const BmArgs& a, const RunOps& ro, int n, int64_t e,
+                                         int32_t& page, int32_t& drop) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ro.off[mid] <= e) lo = mid; else hi = mid - 1;
+  }
+  const int j = lo;
+  const int32_t child = ro.child[j];
+  const int64_t np = ro.np[j];
+  const int64_t idx = e - ro.off[j] - (child >= 0 ? 1 : 0);
+  const int64_t i = idx < 0 ? 0 : np - 1 - idx;  // the child's element loads a valid entry
+  const int32_t tp = a.tables[(int64_t)ro.req[j] * a.tstride + i];
+  page = idx < 0 ? child : tp;
+  drop = idx < 0 ? 1 : ((child >= 0 && i == np - 1) ? 1 : 2);
+}
+
+__global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
+  __shared__ RunOps ro;
+  const BmState& s = a.s;
+  const int n = (int)s.run_ctr[kRunOps];
+  const int64_t total = s.run_ctr[kRunTotal];
+  if (n < 2 || (int64_t)blockIdx.x * kRunChunk >= total) return;
+  run_stage(a, n, ro);
+  for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
+       c0 += (int64_t)gridDim.x * kRunChunk) {
+    int32_t pg[kRunUnroll], dr[kRunUnroll];
+#pragma unroll
+    for (int u = 0; u < kRunUnroll; ++u) {
+      const int64_t e = c0 + u * kRunThreads + threadIdx.x;
+      run_elem(a, ro, n, e < total ? e : total - 1, pg[u], dr[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kRunUnroll; ++u) {
+      const int64_t e = c0 + u * kRunThreads + threadIdx.x;
+      if (e < total) {
+        s.run_page[e] = pg[u];
+        __hip_atomic_fetch_add(rec_ref(s, pg[u]), -dr[u], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_max(&s.last[pg[u]], (int32_t)e, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int n = (int)s.run_ctr[kRunOps];
+  const int64_t total = s.run_ctr[kRunTotal];
+  if (n < 2) return;
+  const int lane = threadIdx.x & 63;
+  for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
+       c0 += (int64_t)gridDim.x * kRunChunk) {
+    RecHead h[kRunUnroll];
+    int32_t lst[kRunUnroll];
+#pragma unroll
+    for (int u = 0; u < kRunUnroll; ++u) {
+      const int64_t e = c0 + u * kRunThreads + threadIdx.x;
+      const int32_t pg = s.run_page[e < total ? e : total - 1];
+      h[u] = rec_head(s, pg);
+      lst[u] = s.last[pg];
+    }
+#pragma unroll
+    for (int u = 0; u < kRunUnroll; ++u) {
+      const int64_t e = c0 + u * kRunThreads + threadIdx.x;  // a wave: 64 aligned elements
+      const bool is_last = e < total && lst[u] == (int32_t)e;
+      const bool zero = is_last && h[u].ref == 0;
+      const bool cached = (h[u].flag & 1) != 0;
+      if (is_last && cached) *ent_ref(s, h[u].slot) = h[u].ref;
+      const uint64_t ml = __ballot(is_last), mr = __ballot(zero && cached),
+                     mf = __ballot(zero && !cached);
+      if (lane == 0 && e < total) {
+        const int64_t w = e >> 5;
+        uint32_t* b = s.run_bits;
+        b[w] = (uint32_t)mr;
+        b[w + 1] = (uint32_t)(mr >> 32);
+        b[kRunMaxWords + w] = (uint32_t)mf;
+        b[kRunMaxWords + w + 1] = (uint32_t)(mf >> 32);
+        b[2 * kRunMaxWords + w] = (uint32_t)ml;
+        b[2 * kRunMaxWords + w + 1] = (uint32_t)(ml >> 32);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
+  __shared__ int64_t wave_tot[2][kBmWaves];
+  const BmState& s = a.s;
+  const int n = (int)s.run_ctr[kRunOps];
+  const int64_t total = s.run_ctr[kRunTotal];
+  if (n < 2) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nw = (total + 31) >> 5;
+  const int64_t per = (nw + kBmThreads - 1) / kBmThreads;  // words per thread
+  const int64_t w0 = tid * per, w1 = w0 + per < nw ? w0 + per : nw;
+  const uint32_t* bl = s.run_bits;
+  const uint32_t* bf = s.run_bits + kRunMaxWords;
+  int64_t cl = 0, cf = 0;
+  for (int64_t w = w0; w < w1; ++w) {
+    cl += __popc(bl[w]);
+    cf += __popc(bf[w]);
+  }
+  int64_t il = cl, jf = cf;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t ol = __shfl_up(il, d), of = __shfl_up(jf, d);
+    if (lane >= d) {
+      il += ol;
+      jf += of;
+    }
+  }
+  if (lane == 63) {
+    wave_tot[0][wave] = il;
+    wave_tot[1][wave] = jf;
+  }
+  __syncthreads();
+  int64_t pl = il - cl, pf = jf - cf, n_lru = 0, n_free = 0;
+#pragma unroll
+  for (int w = 0; w < kBmWaves; ++w) {
+    pl += w < wave ? wave_tot[0][w] : 0;
+    pf += w < wave ? wave_tot[1][w] : 0;
+    n_lru += wave_tot[0][w];
+    n_free += wave_tot[1][w];
+  }
+  for (int64_t w = w0; w < w1; ++w) {
+    s.run_wpre[w] = (uint32_t)pl;
+    s.run_wpre[kRunMaxWords + w] = (uint32_t)pf;
+    pl += __popc(bl[w]);
+    pf += __popc(bf[w]);
+  }
+  if (tid == 0) {
+    s.run_ctr[kRunTail] = s.ctr[kTail];
+    s.run_ctr[kRunStamp] = s.ctr[kNextStamp];
+    s.run_ctr[kRunFree] = s.ctr[kFreeTop];
+    s.ctr[kTail] += n_lru;
+    s.ctr[kNextStamp] += n_lru;
+    s.ctr[kEvictable] += n_lru;
+    s.ctr[kFreeTop] += n_free;
+  }
+  for (int j = tid; j < n; j += kBmThreads)
+    if (s.run_child[j] != -2) a.status[-(a.ops[j] + 1)] = kStReleased;
+}
+
+__global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int n = (int)s.run_ctr[kRunOps];
+  const int64_t total = s.run_ctr[kRunTotal];
+  if (n < 2) return;
+  const int64_t tail0 = s.run_ctr[kRunTail], stamp0 = s.run_ctr[kRunStamp];
+  const int64_t free0 = s.run_ctr[kRunFree], qm = s.Q - 1;
+  const uint32_t* b = s.run_bits;
+  for (int64_t e = (int64_t)blockIdx.x * kRunThreads + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * kRunThreads) {
+    const int64_t w = e >> 5;
+    const uint32_t bit = 1u << (e & 31), below = bit - 1u;
+    const uint32_t br = b[w], bf = b[kRunMaxWords + w], bl = b[2 * kRunMaxWords + w];
+    if (!((br | bf | bl) & bit)) continue;
+    const int32_t pg = s.run_page[e];
+    if (bl & bit) s.last[pg] = -1;
+    if (br & bit) {
+      const int64_t rank = s.run_wpre[w] + __popc(br & below);
+      const uint32_t stamp = (uint32_t)(stamp0 + rank);
+      s.ring[(tail0 + rank) & qm] = (uint32_t)pg | (uint64_t)stamp << 32;
+      *rec_stamp(s, pg) = stamp;
+    }
+    if (bf & bit) {
+      const int64_t rank = s.run_wpre[kRunMaxWords + w] + __popc(bf & below);
+      s.free_list[free0 + rank] = pg;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   __shared__ Shared sh;
   __shared__ OpMeta om;
@@ -691,7 +1064,9 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
     sh.tomb_reused[threadIdx.x] = 0;
   }
   uint64_t cur[kHeld], nxt[kHeld] = {};
-  for (int32_t base = 0; base < a.num_ops; base += kOpChunk) {
+  // the leading run of releases (if any) was retired by the run kernels
+  const int32_t start = (int32_t)a.s.run_ctr[kRunOps];
+  for (int32_t base = start; base < a.num_ops; base += kOpChunk) {
     const int cnt = a.num_ops - base < kOpChunk ? a.num_ops - base : kOpChunk;
     for (int t = threadIdx.x; t < cnt; t += kBmThreads) {
       const int32_t op = a.ops[base + t];
@@ -792,7 +1167,9 @@ __global__ __launch_bounds__(256) void bm_init_kernel(BmState s, const int32_t* 
     s.free_list[p] = free_order ? free_order[p] : (int32_t)p;
   }
   for (int64_t q = g; q < s.Q; q += stride) s.ring[q] = 0;
+  for (int64_t p = g; p < s.P; p += stride) s.last[p] = -1;
   if (g < kNumCtr) s.ctr[g] = g == kFreeTop ? s.P : (g == kNextStamp ? 1 : 0);
+  if (g < kRunNumCtr) s.run_ctr[g] = 0;
 }
 
 }  // namespace
@@ -810,8 +1187,9 @@ extern "C" int mkv_bm_layout(int32_t num_pages, int64_t* out) {
   MKV_REQUIRE(num_pages > 0 && num_pages <= (1 << 28) && out, MKV_E_INVALID,
               "mkv_bm_layout: bad arguments");
   const BmLayout l = bm_layout(num_pages);
-  const int64_t v[8] = {l.C, l.Q, l.off_ctr, l.off_ent, l.off_rec, l.off_free, l.off_ring, l.bytes};
-  for (int i = 0; i < 8; ++i) out[i] = v[i];
+  const int64_t v[10] = {l.C,        l.Q,        l.off_ctr,  l.off_ent, l.off_rec,
+                         l.off_free, l.off_ring, l.off_last, l.off_run, l.bytes};
+  for (int i = 0; i < 10; ++i) out[i] = v[i];
   return MKV_OK;
 }
 
@@ -862,7 +1240,13 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   a.evict_log = evict_log;
   a.evict_cap = evict_log_capacity;
   a.err = err;
-  hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, as_stream(stream), a);
+  const hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(run_setup_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+  hipLaunchKernelGGL(run_drop_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(run_scan_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+  hipLaunchKernelGGL(run_push_kernel, dim3(kRunGrid * kRunUnroll), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   return check_launch("mkv_bm_step");
 }
 

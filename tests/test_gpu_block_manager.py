@@ -34,6 +34,30 @@ def interleaved_ops(n, batch):
     return out
 
 
+def random_ops(seed):
+    """Random op streams: per step a leading run of 0..all releases of live
+    requests (random order), then new admits shuffled with more releases."""
+    def ops_fn(n, batch):
+        rng = np.random.default_rng(seed)
+        live, out, nxt = [], [], 0
+        while nxt < n or live:
+            rng.shuffle(live)
+            k = int(rng.integers(0, len(live) + 1))
+            lead, live = live[:k], live[k:]
+            m = int(rng.integers(0, len(live) + 1))
+            tail_rel, live = live[:m], live[m:]
+            new = list(range(nxt, min(n, nxt + int(rng.integers(1, 2 * batch)))))
+            nxt += len(new)
+            rest = new + [-(r + 1) for r in tail_rel]
+            rng.shuffle(rest)
+            ops = [-(r + 1) for r in lead] + rest
+            if ops:
+                out.append(ops)
+            live += new
+        return out
+    return ops_fn
+
+
 def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False,
         ops_fn=bench.prefix_ops):
     reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
@@ -67,9 +91,9 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
                     pairs.append((want[op]["cow_src"], want[op]["cow_dst"]))
             elif -op - 1 in model.reqs:
                 model.release(-op - 1)
-        if with_data:
-            first = min(o for o in ops if o >= 0)
-            bm.copy_on_write(cache, first, first + sum(1 for o in ops if o >= 0))
+        admits = [o for o in ops if o >= 0]  # consecutive request ids
+        if with_data and admits:
+            bm.copy_on_write(cache, min(admits), min(admits) + len(admits))
             for s, d in pairs:
                 cpu[:, :, d] = cpu[:, :, s]
     bm.check_errors()
@@ -89,6 +113,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         assert (cl[r], cs[r], cd[r]) == (w["child_last"], w["cow_src"], w["cow_dst"]), r
     snap = bm.snapshot()
     assert snap["table_ok"]  # entries = cached pages, with their keys and refcounts
+    assert snap["last_ok"] and snap["evictable"] == len(snap["lru"])
     assert snap["free"] == model.free
     assert snap["lru"] == model.lru_order()
     assert snap["ref"] == model.ref
@@ -153,6 +178,25 @@ def test_long_release_runs():
     assert len(model.evicted) > 4000
 
 
+def test_release_run_past_the_reference_limit():
+    # 1000 releases of ~1102 pages each drop ~1.1M references: the many-CU
+    # release run stops at the op boundary below 2^20 and the one-workgroup
+    # step kernel releases the rest
+    case("block manager: 5000-page pool, 2000 requests of ~1102 pages, batches of 1000")
+    status, model = run(P=5000, n=2000, batch=1000, seed=17, n_templates=1, template_len=17600,
+                        suffix=(1, 20), width=1102)
+    assert OOM not in status
+
+
+@pytest.mark.parametrize("seed", [31, 32, 33])
+def test_random_release_runs_and_interleavings(seed):
+    case(f"block manager: random op streams, 96-page pool, seed {seed}")
+    status, model = run(P=96, n=400, batch=8, seed=seed, n_templates=5, template_len=160,
+                        suffix=(1, 100), width=32, with_data=seed == 31,
+                        ops_fn=random_ops(seed))
+    assert len(model.evicted) > 100
+
+
 def test_single_releases_between_admits():
     case("block manager: 72-page pool, 240 requests, releases between admits")
     status, model = run(P=72, n=240, batch=6, seed=105, n_templates=6, template_len=128,
@@ -181,7 +225,8 @@ def test_duplicate_release_is_flagged_once():
     for r in (0, 1, 2):
         model.release(r)
     snap = bm.snapshot()
-    assert snap["table_ok"] and snap["ref"] == model.ref and snap["free"] == model.free
+    assert snap["table_ok"] and snap["last_ok"]
+    assert snap["ref"] == model.ref and snap["free"] == model.free
     assert snap["lru"] == model.lru_order()
 
 
@@ -192,3 +237,9 @@ def test_release_of_unknown_request_is_flagged():
     bm.step(torch.tensor([-(2 + 1)], dtype=torch.int32), z[:0], z, torch.zeros(4, dtype=torch.int32))
     with pytest.raises(_lib.MkvDeviceError, match="block manager"):
         bm.check_errors()
+    # (check_errors cleared the word) the same inside a leading run of releases
+    bm.step(torch.tensor([-(2 + 1), -(1 + 1)], dtype=torch.int32), z[:0], z,
+            torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(_lib.MkvDeviceError, match="block manager"):
+        bm.check_errors()
+    assert bm.snapshot()["last_ok"]
