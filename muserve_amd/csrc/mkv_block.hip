@@ -53,6 +53,7 @@ constexpr int kOpChunk = 1024;  // ops whose request metadata is staged in LDS a
 // Page hashes (and probe results) a thread keeps in registers: pages
 // tid + j*kBmThreads for j < kHeld. Longer requests re-read the rest.
 constexpr int kHeld = 1;
+constexpr int kSetSize = 2048;  // LDS set of the table slots an admit claims
 
 enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen, kNumCtr = 16 };
 enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
@@ -216,6 +217,14 @@ struct OpMeta {
   int64_t h0[kOpChunk];     // admits: index of the first page hash
 };
 
+// LDS of the step kernel's admits: the pages taken for table positions below
+// kBmThreads, and the table slots claimed by the current admit's inserts (a
+// set, open addressing, -1 empty; cleared when each op ends).
+struct AdmitLds {
+  int32_t new_pg[kBmThreads];
+  int32_t claims[kSetSize];
+};
+
 // Per-workgroup scratch.
 struct Shared {
   int32_t wave_sum[2][2][kBmWaves];  // block_rank2: [buffer][flag][wave]
@@ -230,6 +239,28 @@ struct Shared {
 };
 
 __device__ __forceinline__ uint32_t slot_of(uint64_t h) { return (uint32_t)(h ^ (h >> 29)); }
+
+// Values every lane holds alike but that come from LDS or a reduction: kept
+// in scalar registers (VGPRs are the step kernel's scarce resource).
+__device__ __forceinline__ int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)((uint64_t)hi << 32 | lo);
+}
+
+// Adds x >= 0 to an LDS set of kSetSize slots; false if it was already there
+// (or the set is full: callers add at most half of kSetSize values).
+__device__ __forceinline__ bool set_add(int32_t* set, int32_t x) {
+  uint32_t i = ((uint32_t)x * 2654435761u) >> 21;
+  static_assert(kSetSize == 1 << 11, "the hash takes 11 bits");
+  for (int n = 0; n < kSetSize; ++n, i = (i + 1) & (kSetSize - 1)) {
+    const int32_t prev = atomicCAS(&set[i], -1, x);
+    if (prev == -1) return true;
+    if (prev == x) return false;
+  }
+  return false;
+}
 
 __device__ __forceinline__ int32_t wave_min(int32_t v) {
 #pragma unroll
@@ -273,8 +304,8 @@ __device__ __forceinline__ void block_rank2(bool fa, bool fb, int32_t& ra, int32
   const uint64_t below = (1ull << lane) - 1ull;
   ra = ba + __popcll(ma & below);
   rb = bb + __popcll(mb & below);
-  ta = aa;
-  tb = ab;
+  ta = uni(aa);
+  tb = uni(ab);
 }
 
 // A lookup's result: the page under the key (or -1), the refcount mirrored in
@@ -282,6 +313,7 @@ __device__ __forceinline__ void block_rank2(bool fa, bool fb, int32_t& ra, int32
 // tombstoned slot on its probe path, where it would be inserted.
 struct Found {
   int32_t page, ref, slot;
+  bool tomb;  // a miss's insertion slot is a tombstone
 };
 
 // Looks up key h. Never runs concurrently with a writer of the table.
@@ -292,12 +324,13 @@ __device__ Found tab_find(const BmState& s, uint64_t h) {
   for (int64_t n = 0; n < s.C; ++n) {
     const u32x4 e = *reinterpret_cast<const u32x4*>(s.ent + i * kEntBytes);
     const int32_t v = (int32_t)e.z;
-    if (v == kEmpty) return Found{-1, 0, (int32_t)(first_free >= 0 ? first_free : i)};
-    if (v >= 0 && ((uint64_t)e.y << 32 | e.x) == h) return Found{v, (int32_t)e.w, (int32_t)i};
+    if (v == kEmpty)
+      return Found{-1, 0, (int32_t)(first_free >= 0 ? first_free : i), first_free >= 0};
+    if (v >= 0 && ((uint64_t)e.y << 32 | e.x) == h) return Found{v, (int32_t)e.w, (int32_t)i, false};
     if (v == kTomb && first_free < 0) first_free = i;
     i = (i + 1) & mask;
   }
-  return Found{-1, 0, (int32_t)first_free};
+  return Found{-1, 0, (int32_t)first_free, first_free >= 0};
 }
 
 // Claims slot i for (h, page, refcount ref) if it still holds `expect` (empty
@@ -379,11 +412,14 @@ __device__ void tab_rebuild(const BmArgs& a, Ctrs& c) {
 // A page taken for request r (from the free stack or by eviction): table index
 // i < n_pages gets refcount 2 (parent and child), except a partial last page
 // (1: the child copies it); otherwise it is the child's copy (refcount 1).
-// The taker of the table's last page or of the copy reports it.
+// The taker of the table's last page or of the copy reports it. Table pages
+// below kBmThreads are also recorded in new_pg (LDS).
 __device__ __forceinline__ void take_page(const BmArgs& a, int32_t r, int32_t p, int64_t i,
-                                          int64_t n_pages, bool in_table, bool cow, int32_t* row) {
+                                          int64_t n_pages, bool in_table, bool cow, int32_t* row,
+                                          int32_t* new_pg) {
   if (in_table) {
     row[i] = p;
+    if (i < kBmThreads) new_pg[i] = p;
     const bool last = i == n_pages - 1;
     *rec_ref(a.s, p) = (cow && last) ? 1 : 2;
     if (last) {
@@ -400,7 +436,8 @@ __device__ __forceinline__ void take_page(const BmArgs& a, int32_t r, int32_t p,
 }
 
 __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int64_t h0,
-                      const uint64_t (&hk)[kHeld], Ctrs& c, Shared& sh, int& buf, int par) {
+                      const uint64_t (&hk)[kHeld], Ctrs& c, Shared& sh, AdmitLds& al, int& buf,
+                      int par) {
   const BmState& s = a.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t m = nhash;
@@ -428,6 +465,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   // per held page: the probe's page (or -1), the mirrored refcount, and the
   // entry's slot (a hit) or the insertion slot (a miss)
   int32_t held_pg[kHeld], held_ref[kHeld], held_slot[kHeld];
+  bool held_tomb[kHeld];
   int32_t miss = INT_MAX;
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
@@ -435,12 +473,14 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     held_pg[j] = -1;
     held_ref[j] = 1;
     held_slot[j] = -1;
+    held_tomb[j] = false;
     if (i < m) {
       const Found f = tab_find(s, hk[j]);
       row[i] = f.page;
       held_pg[j] = f.page;
       held_ref[j] = f.page >= 0 ? f.ref : 1;
       held_slot[j] = f.slot;
+      held_tomb[j] = f.tomb;
       if (f.page < 0 && (int32_t)i < miss) miss = (int32_t)i;
     }
   }
@@ -457,7 +497,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   miss = wave_min(miss);
   if (lane == 0 && miss != INT_MAX) atomicMin(&sh.first_miss[par], miss);
   __syncthreads();
-  const int64_t k = sh.first_miss[par] < m ? sh.first_miss[par] : m;
+  const int64_t k = uni(sh.first_miss[par] < m ? sh.first_miss[par] : (int32_t)m);
 
   // 2. hits that are evictable now get pinned: count them for the OOM check
   //    (every thread adds up the ballots itself; hits past the held pages, if
@@ -473,7 +513,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
       mine = __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
     }
   }
-  int64_t pinned = wave_sum(mine);
+  int64_t pinned = uni(wave_sum(mine));
   if (k > (int64_t)kHeld * kBmThreads) {
     int32_t cnt = 0;
     for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
@@ -481,7 +521,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     cnt = wave_sum(cnt);
     if (lane == 0 && cnt) atomicAdd(&sh.count[par], cnt);
     __syncthreads();
-    pinned += sh.count[par];
+    pinned += uni(sh.count[par]);
   }
   const int64_t take = n_pages - k + (cow ? 1 : 0);
   if (take > c.free_top + c.evictable - pinned) {
@@ -524,7 +564,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   //    Whoever takes the table's last page or the child's copy reports it.
   for (int64_t j = tid; j < from_free; j += kBmThreads) {
     const int32_t p = j == tid ? pf_page : s.free_list[c.free_top - 1 - j];
-    take_page(a, r, p, k + j, n_pages, table_new - j > 0, cow, row);
+    take_page(a, r, p, k + j, n_pages, table_new - j > 0, cow, row, al.new_pg);
   }
   c.free_top -= from_free;
   int64_t done = from_free;
@@ -534,11 +574,17 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
       if (tid == 0) raise_err(a.err, MKV_DEVERR_BM);
       break;
     }
+    // Nearly every entry at the LRU's old end is live, so a window of the
+    // victims still wanted plus a little slack usually suffices: every entry
+    // examined costs a scattered record load.
+    const int64_t want = take - done;
+    const int64_t fit = (want + 16 + 63) / 64 * 64;
+    const int64_t win = fit < kBmThreads ? fit : kBmThreads;
     const int64_t pos = c.head + tid;
     bool ok = false;
     int32_t pg = 0;
     RecHead h{};
-    if (pos < c.tail) {
+    if (tid < win && pos < c.tail) {
       const uint64_t e = s.ring[pos & qm];
       pg = (int32_t)(uint32_t)e;
       h = rec_head(s, pg);
@@ -546,20 +592,18 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     }
     int32_t rank, unused_r, total, unused_t;
     block_rank2(ok, false, rank, unused_r, total, unused_t, sh, buf);
-    const int64_t want = take - done;
     if (ok && rank < want) {
       const int64_t j = done + rank;
       *ent_page(s, h.slot) = kTomb;  // the page's key leaves the table
       *rec_flag(s, pg) = h.flag & ~1;
-      take_page(a, r, pg, k + j, n_pages, j < table_new, cow, row);
+      take_page(a, r, pg, k + j, n_pages, j < table_new, cow, row, al.new_pg);
       if (c.log_len + (j - from_free) < a.evict_cap)
         a.evict_log[c.log_len + (j - from_free)] = pg;
       if (rank == want - 1) sh.new_head = pos + 1;
     }
     __syncthreads();
     const int64_t got = total < want ? total : want;
-    c.head = total >= want ? sh.new_head
-                           : (c.head + kBmThreads < c.tail ? c.head + kBmThreads : c.tail);
+    c.head = total >= want ? uni64(sh.new_head) : (c.head + win < c.tail ? c.head + win : c.tail);
     c.evictable -= got;
     c.tombs += got;
     done += got;
@@ -571,8 +615,11 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   //    probe did not find is still absent (only evictions ran since, and they
   //    only remove keys); a key it found is present unless its page was just
   //    evicted. All presence checks finish before any insert (barrier), so no
-  //    check reads a page another lane is registering, and every lane sees the
-  //    page ids other lanes wrote into the table row.
+  //    check reads a page another lane is registering; the pages taken are
+  //    read from LDS. A missing key goes to the insertion slot its probe found
+  //    (still empty or a tombstone), claimed in LDS so that one lane writes it
+  //    with plain stores; keys without a slot of their own are inserted after
+  //    a barrier, by compare-and-swap.
   bool reg[kHeld];
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
@@ -586,16 +633,32 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   }
   __syncthreads();
   int32_t reused = 0;
+  bool later[kHeld];
+  int32_t reg_pg[kHeld];
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
+    later[j] = false;
+    reg_pg[j] = 0;
     if (!reg[j]) continue;
     const int64_t i = tid + (int64_t)j * kBmThreads;
-    const int32_t p = row[i];
+    const int32_t p = i < kBmThreads ? al.new_pg[i] : row[i];
+    reg_pg[j] = p;
     *rec_hash(s, p) = hk[j];
     *rec_flag(s, p) = 1;
-    reused += tab_insert(s, hk[j], p, 2, held_pg[j] < 0 ? held_slot[j] : -1) == 1;
+    if (held_pg[j] < 0 && held_slot[j] >= 0 && set_add(al.claims, held_slot[j])) {
+      *reinterpret_cast<u32x4*>(s.ent + (int64_t)held_slot[j] * kEntBytes) =
+          u32x4{(uint32_t)hk[j], (uint32_t)(hk[j] >> 32), (uint32_t)p, 2u};
+      *rec_slot(s, p) = held_slot[j];
+      reused += held_tomb[j] ? 1 : 0;
+    } else {
+      later[j] = true;
+    }
   }
   __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j)
+    if (later[j]) reused += tab_insert(s, hk[j], reg_pg[j], 2) == 1;
+  if (m > (int64_t)kHeld * kBmThreads) __syncthreads();  // the inserts above are complete
   // pages past the held ones (requests longer than kHeld*kBmThreads pages)
   for (int64_t base = (int64_t)kHeld * kBmThreads; base < m; base += kBmThreads) {
     const int64_t i = base + tid;
@@ -617,7 +680,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   reused = wave_sum(reused);
   if (lane == 0 && reused) atomicAdd(&sh.tomb_reused[par], reused);
   __syncthreads();
-  c.tombs -= sh.tomb_reused[par];
+  c.tombs -= uni(sh.tomb_reused[par]);
 
   if (tid == 0) {  // the page-valued results were written by their owners
     a.hits[r] = (int32_t)k;
@@ -1049,6 +1112,7 @@ __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
 __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   __shared__ Shared sh;
   __shared__ OpMeta om;
+  __shared__ AdmitLds al;
   int buf = 0;
   Ctrs c;
   c.free_top = a.s.ctr[kFreeTop];
@@ -1063,6 +1127,7 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
     sh.count[threadIdx.x] = 0;
     sh.tomb_reused[threadIdx.x] = 0;
   }
+  for (int i = threadIdx.x; i < kSetSize; i += kBmThreads) al.claims[i] = -1;
   uint64_t cur[kHeld], nxt[kHeld] = {};
   // the leading run of releases (if any) was retired by the run kernels
   const int32_t start = (int32_t)a.s.run_ctr[kRunOps];
@@ -1097,15 +1162,16 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
       }
       // the next op's page hashes are loaded while this one runs
       if (t + 1 < cnt) fetch_hashes(a, om, t + 1, nxt);
-      const int32_t op = om.op[t];
+      const int32_t op = uni(om.op[t]);
       const int32_t r = op >= 0 ? op : -(op + 1);
       if (r >= a.num_requests) {
         if (threadIdx.x == 0) raise_err(a.err, MKV_DEVERR_BM);
       } else if (op >= 0) {
-        admit(a, r, om.ntok[t], om.nhash[t], om.h0[t], cur, c, sh, buf, par);
+        admit(a, r, uni(om.ntok[t]), uni(om.nhash[t]), uni64(om.h0[t]), cur, c, sh, al, buf, par);
       } else {
-        release(a, r, om.ntok[t], c, sh, buf);
+        release(a, r, uni(om.ntok[t]), c, sh, buf);
       }
+      for (int i = threadIdx.x; i < kSetSize; i += kBmThreads) al.claims[i] = -1;
       __syncthreads();  // the op's writes are visible to the next op
 #pragma unroll
       for (int j = 0; j < kHeld; ++j) cur[j] = nxt[j];
