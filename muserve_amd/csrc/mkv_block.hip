@@ -3,7 +3,7 @@
 //
 // Semantics (one request at a time, in op order): see mkv_bm_step in mkv.h.
 // Eviction order must equal a sequential OrderedDict model, so requests are
-// processed in order by a single 1024-thread workgroup and the parallelism is
+// processed in order by a single 512-thread workgroup and the parallelism is
 // inside a request: every page hash of a request is probed at once, pins and
 // refcount updates are one lane per page, and allocation / release positions
 // come from wavefront ballots + popcount prefix ranks.
@@ -20,7 +20,7 @@
 //     hashes are loaded while the current request runs, and the free-stack
 //     entries a request may take are loaded with its probe;
 //   * the probe remembers where a missing key would go, so registering it is
-//     one compare-and-swap;
+//     a plain store (the slot claimed in LDS);
 //   * the number of hits that leave the LRU comes from per-wave ballots kept
 //     in LDS, without another reduction.
 //
@@ -47,7 +47,10 @@
 namespace mkv {
 namespace {
 
-constexpr int kBmThreads = 1024;
+// 512 threads: a request's pages fit (up to 512 in registers), and every
+// wave runs the per-request bookkeeping, so more waves cost more than they
+// add (1024 and 256 threads measured slower).
+constexpr int kBmThreads = 512;
 constexpr int kBmWaves = kBmThreads / 64;
 constexpr int kOpChunk = 1024;  // ops whose request metadata is staged in LDS at once
 // Page hashes (and probe results) a thread keeps in registers: pages
@@ -221,7 +224,7 @@ struct OpMeta {
 // kBmThreads, and the table slots claimed by the current admit's inserts (a
 // set, open addressing, -1 empty; cleared when each op ends).
 struct AdmitLds {
-  int32_t new_pg[kBmThreads];
+  int32_t new_pg[kHeld * kBmThreads];
   int32_t claims[kSetSize];
 };
 
@@ -419,7 +422,7 @@ __device__ __forceinline__ void take_page(const BmArgs& a, int32_t r, int32_t p,
                                           int32_t* new_pg) {
   if (in_table) {
     row[i] = p;
-    if (i < kBmThreads) new_pg[i] = p;
+    if (i < kHeld * kBmThreads) new_pg[i] = p;
     const bool last = i == n_pages - 1;
     *rec_ref(a.s, p) = (cow && last) ? 1 : 2;
     if (last) {
@@ -641,7 +644,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     reg_pg[j] = 0;
     if (!reg[j]) continue;
     const int64_t i = tid + (int64_t)j * kBmThreads;
-    const int32_t p = i < kBmThreads ? al.new_pg[i] : row[i];
+    const int32_t p = i < kHeld * kBmThreads ? al.new_pg[i] : row[i];
     reg_pg[j] = p;
     *rec_hash(s, p) = hk[j];
     *rec_flag(s, p) = 1;
@@ -803,12 +806,13 @@ __device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
 }
 
 __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
+  constexpr int kOpt = kRunMaxOps / kBmThreads;  // consecutive ops per thread
+  static_assert(kOpt * kBmThreads == kRunMaxOps, "ops split evenly over the threads");
   __shared__ Shared sh;
   __shared__ int32_t first_non;
   __shared__ uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
   __shared__ int64_t off[kRunMaxOps + 1];
   __shared__ int64_t wave_tot[kBmWaves];
-  static_assert(kRunMaxOps <= kBmThreads, "one op per thread");
   const BmState& s = a.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int limit = a.num_ops < kRunMaxOps ? a.num_ops : kRunMaxOps;
@@ -818,19 +822,25 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     firsti[i] = 0xffffffffu;
   }
   __syncthreads();
-  const int32_t op = tid < limit ? a.ops[tid] : 0;
-  const int32_t r = -(op + 1);
-  int32_t st = kStBad, nt = 0;
-  if (tid < limit) {
-    // the run also ends at an admitted request whose token count no longer
-    // fits its table (a caller error the step kernel handles as before)
-    bool ok = valid_release(a, op);
-    if (ok) {
-      st = a.status[r];
-      nt = a.ntok[r];
-      ok = st != kStOk || (nt >= 0 && (nt + 15) / 16 <= a.twidth);
+  int32_t r[kOpt], st[kOpt], nt[kOpt];
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    const int32_t op = j < limit ? a.ops[j] : 0;
+    r[u] = -(op + 1);
+    st[u] = kStBad;
+    nt[u] = 0;
+    if (j < limit) {
+      // the run also ends at an admitted request whose token count no longer
+      // fits its table (a caller error the step kernel handles as before)
+      bool ok = valid_release(a, op);
+      if (ok) {
+        st[u] = a.status[r[u]];
+        nt[u] = a.ntok[r[u]];
+        ok = st[u] != kStOk || (nt[u] >= 0 && (nt[u] + 15) / 16 <= a.twidth);
+      }
+      if (!ok) atomicMin(&first_non, j);
     }
-    if (!ok) atomicMin(&first_non, tid);
   }
   __syncthreads();
   int n = first_non;
@@ -840,30 +850,43 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   }
   // a request released twice: the earliest op releases; sequentially a later
   // one finds it released (a caller error) unless it got OOM (silent)
-  uint32_t slot = 0;
-  if (tid < n) {
-    slot = ((uint32_t)r * 2654435761u) & (2 * kRunMaxOps - 1);
-    for (;;) {  // at most n of 2 kRunMaxOps slots are taken
-      const uint32_t prev = atomicCAS(&key[slot], 0xffffffffu, (uint32_t)r);
-      if (prev == 0xffffffffu || prev == (uint32_t)r) break;
-      slot = (slot + 1) & (2 * kRunMaxOps - 1);
+  uint32_t slot[kOpt];
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    slot[u] = 0;
+    if (j < n) {
+      uint32_t q = ((uint32_t)r[u] * 2654435761u) & (2 * kRunMaxOps - 1);
+      for (;;) {  // at most n of 2 kRunMaxOps slots are taken
+        const uint32_t prev = atomicCAS(&key[q], 0xffffffffu, (uint32_t)r[u]);
+        if (prev == 0xffffffffu || prev == (uint32_t)r[u]) break;
+        q = (q + 1) & (2 * kRunMaxOps - 1);
+      }
+      atomicMin(&firsti[q], (uint32_t)j);
+      slot[u] = q;
     }
-    atomicMin(&firsti[slot], (uint32_t)tid);
   }
   __syncthreads();
-  int64_t cnt = 0;
-  int32_t child = -2;
-  if (tid < n) {
-    if (firsti[slot] == (uint32_t)tid && st == kStOk) {
-      const bool cow = (nt & 15) != 0;
-      child = cow ? a.child_last[r] : -1;
-      cnt = (nt + 15) / 16 + (cow ? 1 : 0);
-    } else if (st != kStOom) {
-      raise_err(a.err, MKV_DEVERR_BM);
+  int64_t cnt[kOpt], mine = 0;
+  int32_t child[kOpt];
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    cnt[u] = 0;
+    child[u] = -2;
+    if (j < n) {
+      if (firsti[slot[u]] == (uint32_t)j && st[u] == kStOk) {
+        const bool cow = (nt[u] & 15) != 0;
+        child[u] = cow ? a.child_last[r[u]] : -1;
+        cnt[u] = (nt[u] + 15) / 16 + (cow ? 1 : 0);
+      } else if (st[u] != kStOom) {
+        raise_err(a.err, MKV_DEVERR_BM);
+      }
     }
+    mine += cnt[u];
   }
-  // exclusive prefix sum of the counts
-  int64_t incl = cnt;
+  // exclusive prefix sum of the counts (thread totals, then within a thread)
+  int64_t incl = mine;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int64_t o = __shfl_up(incl, d);
@@ -877,7 +900,13 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     before += w < wave ? wave_tot[w] : 0;
     total += wave_tot[w];
   }
-  if (tid < n) off[tid] = before + incl - cnt;
+  int64_t at = before + incl - mine;
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    if (j < n) off[j] = at;
+    at += cnt[u];
+  }
   if (tid == 0) off[n] = total;
   __syncthreads();
   if (total > kRunMaxElems) {  // the longest prefix of ops that fits
@@ -908,7 +937,11 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     if (tid == 0) s.ctr[kTail] = c.tail;
   }
   for (int j = tid; j <= n; j += kBmThreads) s.run_off[j] = off[j];
-  if (tid < n) s.run_child[tid] = child;
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    if (j < n) s.run_child[j] = child[u];
+  }
   if (tid == 0) {
     s.run_ctr[kRunOps] = n;
     s.run_ctr[kRunTotal] = off[n];
