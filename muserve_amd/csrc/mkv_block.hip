@@ -87,7 +87,11 @@ __host__ __device__ inline int64_t next_pow2(int64_t x) {
 
 __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   BmLayout l;
-  l.C = next_pow2(4 * (int64_t)P);
+  // 32 entries per page (at most 2^30, so slots stay int32; at least 4 per
+  // page): an admit waits for the longest probe chain among its hundreds of
+  // parallel lookups, so a sparse table pays (prefix trace: 22.9 ms of
+  // manager time at 4 entries per page, 18.5 at 16, 18.0 at 32, 17.7 at 64)
+  l.C = next_pow2(32 * (int64_t)P < (1LL << 30) ? 32 * (int64_t)P : (1LL << 30));
   l.Q = next_pow2(2 * (int64_t)P);
   int64_t o = 0;
   auto take = [&o](int64_t n) {
@@ -505,18 +509,17 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
   // 2. hits that are evictable now get pinned: count them for the OOM check
   //    (every thread adds up the ballots itself; hits past the held pages, if
   //    any, through one more reduction)
-  //    (each lane of every wave takes one wave-ballot of the probe, so every
-  //    wave computes the same total)
-  static_assert(kHeld * kBmWaves <= 64, "one ballot per lane");
-  int32_t mine = 0;
-  if (lane < kHeld * kBmWaves) {
-    const int64_t first = (int64_t)(lane / kBmWaves) * kBmThreads + (lane % kBmWaves) * 64;
+  //    (every lane reads all the wave ballots: LDS broadcasts)
+  int32_t pinned_held = 0;
+#pragma unroll
+  for (int w = 0; w < kHeld * kBmWaves; ++w) {
+    const int64_t first = (int64_t)(w / kBmWaves) * kBmThreads + (w % kBmWaves) * 64;
     if (first < k) {
-      const uint64_t em = sh.evmask[lane / kBmWaves][lane % kBmWaves];
-      mine = __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
+      const uint64_t em = sh.evmask[w / kBmWaves][w % kBmWaves];
+      pinned_held += __popcll(k - first >= 64 ? em : em & ((1ull << (k - first)) - 1ull));
     }
   }
-  int64_t pinned = uni(wave_sum(mine));
+  int64_t pinned = uni(pinned_held);
   if (k > (int64_t)kHeld * kBmThreads) {
     int32_t cnt = 0;
     for (int64_t i = tid + (int64_t)kHeld * kBmThreads; i < k; i += kBmThreads)
@@ -680,8 +683,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     }
     __syncthreads();
   }
-  reused = wave_sum(reused);
-  if (lane == 0 && reused) atomicAdd(&sh.tomb_reused[par], reused);
+  if (reused) atomicAdd(&sh.tomb_reused[par], reused);  // a few lanes: cheaper than a shuffle sum
   __syncthreads();
   c.tombs -= uni(sh.tomb_reused[par]);
 

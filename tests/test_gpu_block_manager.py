@@ -161,8 +161,8 @@ def test_long_requests_past_the_register_held_pages():
 
 
 def test_many_evictions_rebuild_the_table():
-    # 72 pages and a 1024-slot table: tombstones pass a quarter of the table
-    # many times over, so the table is rebuilt repeatedly
+    # 72 pages and a 4096-slot table: ~10,800 evictions leave tombstones past
+    # a quarter of the table many times over, so the table is rebuilt repeatedly
     case("block manager: 72-page pool, 1500 requests, batches of 6")
     status, model = run(P=72, n=1500, batch=6, seed=21, n_templates=40, template_len=128,
                         suffix=(1, 120), width=32)
