@@ -102,6 +102,16 @@ MKV_HD uint16_t f32_to_bf16_rne(float f) {
 // ---------------------------------------------------------------------------
 MKV_HD uint32_t rotr32(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
 
+// x ^ y ^ z. On gfx950 one v_bitop3_b32 (truth table 0x96); the compiler
+// otherwise emits two XORs for each of the 4 sigma functions of every round.
+MKV_HD uint32_t xor3(uint32_t x, uint32_t y, uint32_t z) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_bitop3_b32(x, y, z, 0x96);
+#else
+  return x ^ y ^ z;
+#endif
+}
+
 MKV_HD uint32_t bswap32(uint32_t x) {
   return (x >> 24) | ((x >> 8) & 0xff00u) | ((x << 8) & 0xff0000u) | (x << 24);
 }
@@ -142,14 +152,14 @@ MKV_HD void sha256_compress(Sha256& s, const uint32_t blk[16]) {
       wi = w[i];
     } else {
       const uint32_t w15 = w[(i - 15) & 15], w2 = w[(i - 2) & 15];
-      const uint32_t s0 = rotr32(w15, 7) ^ rotr32(w15, 18) ^ (w15 >> 3);
-      const uint32_t s1 = rotr32(w2, 17) ^ rotr32(w2, 19) ^ (w2 >> 10);
+      const uint32_t s0 = xor3(rotr32(w15, 7), rotr32(w15, 18), w15 >> 3);
+      const uint32_t s1 = xor3(rotr32(w2, 17), rotr32(w2, 19), w2 >> 10);
       wi = w[i & 15] = w[i & 15] + s0 + w[(i - 7) & 15] + s1;
     }
-    const uint32_t S1 = rotr32(e, 6) ^ rotr32(e, 11) ^ rotr32(e, 25);
+    const uint32_t S1 = xor3(rotr32(e, 6), rotr32(e, 11), rotr32(e, 25));
     const uint32_t ch = (e & f) ^ (~e & g);
     const uint32_t t1 = h + S1 + ch + kSha256K[i] + wi;
-    const uint32_t S0 = rotr32(a, 2) ^ rotr32(a, 13) ^ rotr32(a, 22);
+    const uint32_t S0 = xor3(rotr32(a, 2), rotr32(a, 13), rotr32(a, 22));
     const uint32_t maj = (a & b) ^ (a & c) ^ (b & c);
     const uint32_t t2 = S0 + maj;
     h = g; g = f; f = e; e = d + t1;
@@ -183,18 +193,18 @@ MKV_HD void sha256_compress2(Sha256& s1, const uint32_t blk1[16], Sha256& s2,
     } else {
       const uint32_t x15 = w1[(i - 15) & 15], x2 = w1[(i - 2) & 15];
       const uint32_t y15 = w2[(i - 15) & 15], y2 = w2[(i - 2) & 15];
-      wi1 = w1[i & 15] = w1[i & 15] + (rotr32(x15, 7) ^ rotr32(x15, 18) ^ (x15 >> 3)) +
-                         w1[(i - 7) & 15] + (rotr32(x2, 17) ^ rotr32(x2, 19) ^ (x2 >> 10));
-      wi2 = w2[i & 15] = w2[i & 15] + (rotr32(y15, 7) ^ rotr32(y15, 18) ^ (y15 >> 3)) +
-                         w2[(i - 7) & 15] + (rotr32(y2, 17) ^ rotr32(y2, 19) ^ (y2 >> 10));
+      wi1 = w1[i & 15] = w1[i & 15] + xor3(rotr32(x15, 7), rotr32(x15, 18), x15 >> 3) +
+                         w1[(i - 7) & 15] + xor3(rotr32(x2, 17), rotr32(x2, 19), x2 >> 10);
+      wi2 = w2[i & 15] = w2[i & 15] + xor3(rotr32(y15, 7), rotr32(y15, 18), y15 >> 3) +
+                         w2[(i - 7) & 15] + xor3(rotr32(y2, 17), rotr32(y2, 19), y2 >> 10);
     }
-    const uint32_t t1a = h1 + (rotr32(e1, 6) ^ rotr32(e1, 11) ^ rotr32(e1, 25)) +
+    const uint32_t t1a = h1 + xor3(rotr32(e1, 6), rotr32(e1, 11), rotr32(e1, 25)) +
                          ((e1 & f1) ^ (~e1 & g1)) + kSha256K[i] + wi1;
-    const uint32_t t1b = h2 + (rotr32(e2, 6) ^ rotr32(e2, 11) ^ rotr32(e2, 25)) +
+    const uint32_t t1b = h2 + xor3(rotr32(e2, 6), rotr32(e2, 11), rotr32(e2, 25)) +
                          ((e2 & f2) ^ (~e2 & g2)) + kSha256K[i] + wi2;
-    const uint32_t t2a = (rotr32(a1, 2) ^ rotr32(a1, 13) ^ rotr32(a1, 22)) +
+    const uint32_t t2a = xor3(rotr32(a1, 2), rotr32(a1, 13), rotr32(a1, 22)) +
                          ((a1 & b1) ^ (a1 & c1) ^ (b1 & c1));
-    const uint32_t t2b = (rotr32(a2, 2) ^ rotr32(a2, 13) ^ rotr32(a2, 22)) +
+    const uint32_t t2b = xor3(rotr32(a2, 2), rotr32(a2, 13), rotr32(a2, 22)) +
                          ((a2 & b2) ^ (a2 & c2) ^ (b2 & c2));
     h1 = g1; g1 = f1; f1 = e1; e1 = d1 + t1a; d1 = c1; c1 = b1; b1 = a1; a1 = t1a + t2a;
     h2 = g2; g2 = f2; f2 = e2; e2 = d2 + t1b; d2 = c2; c2 = b2; b2 = a2; a2 = t1b + t2b;
