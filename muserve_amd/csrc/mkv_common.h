@@ -169,52 +169,6 @@ MKV_HD void sha256_compress(Sha256& s, const uint32_t blk[16]) {
   s.h[4] += e; s.h[5] += f; s.h[6] += g; s.h[7] += h;
 }
 
-// Two independent compressions advanced round by round, so their dependency
-// chains interleave in one instruction stream (the GPU page hasher pairs a
-// page's finalisation with the next page's first block).
-MKV_HD void sha256_compress2(Sha256& s1, const uint32_t blk1[16], Sha256& s2,
-                             const uint32_t blk2[16]) {
-  uint32_t w1[16], w2[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    w1[i] = blk1[i];
-    w2[i] = blk2[i];
-  }
-  uint32_t a1 = s1.h[0], b1 = s1.h[1], c1 = s1.h[2], d1 = s1.h[3];
-  uint32_t e1 = s1.h[4], f1 = s1.h[5], g1 = s1.h[6], h1 = s1.h[7];
-  uint32_t a2 = s2.h[0], b2 = s2.h[1], c2 = s2.h[2], d2 = s2.h[3];
-  uint32_t e2 = s2.h[4], f2 = s2.h[5], g2 = s2.h[6], h2 = s2.h[7];
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    uint32_t wi1, wi2;
-    if (i < 16) {
-      wi1 = w1[i];
-      wi2 = w2[i];
-    } else {
-      const uint32_t x15 = w1[(i - 15) & 15], x2 = w1[(i - 2) & 15];
-      const uint32_t y15 = w2[(i - 15) & 15], y2 = w2[(i - 2) & 15];
-      wi1 = w1[i & 15] = w1[i & 15] + xor3(rotr32(x15, 7), rotr32(x15, 18), x15 >> 3) +
-                         w1[(i - 7) & 15] + xor3(rotr32(x2, 17), rotr32(x2, 19), x2 >> 10);
-      wi2 = w2[i & 15] = w2[i & 15] + xor3(rotr32(y15, 7), rotr32(y15, 18), y15 >> 3) +
-                         w2[(i - 7) & 15] + xor3(rotr32(y2, 17), rotr32(y2, 19), y2 >> 10);
-    }
-    const uint32_t t1a = h1 + xor3(rotr32(e1, 6), rotr32(e1, 11), rotr32(e1, 25)) +
-                         ((e1 & f1) ^ (~e1 & g1)) + kSha256K[i] + wi1;
-    const uint32_t t1b = h2 + xor3(rotr32(e2, 6), rotr32(e2, 11), rotr32(e2, 25)) +
-                         ((e2 & f2) ^ (~e2 & g2)) + kSha256K[i] + wi2;
-    const uint32_t t2a = xor3(rotr32(a1, 2), rotr32(a1, 13), rotr32(a1, 22)) +
-                         ((a1 & b1) ^ (a1 & c1) ^ (b1 & c1));
-    const uint32_t t2b = xor3(rotr32(a2, 2), rotr32(a2, 13), rotr32(a2, 22)) +
-                         ((a2 & b2) ^ (a2 & c2) ^ (b2 & c2));
-    h1 = g1; g1 = f1; f1 = e1; e1 = d1 + t1a; d1 = c1; c1 = b1; b1 = a1; a1 = t1a + t2a;
-    h2 = g2; g2 = f2; f2 = e2; e2 = d2 + t1b; d2 = c2; c2 = b2; b2 = a2; a2 = t1b + t2b;
-  }
-  s1.h[0] += a1; s1.h[1] += b1; s1.h[2] += c1; s1.h[3] += d1;
-  s1.h[4] += e1; s1.h[5] += f1; s1.h[6] += g1; s1.h[7] += h1;
-  s2.h[0] += a2; s2.h[1] += b2; s2.h[2] += c2; s2.h[3] += d2;
-  s2.h[4] += e2; s2.h[5] += f2; s2.h[6] += g2; s2.h[7] += h2;
-}
-
 // The padding block of a message of message_bytes bytes whose length is a
 // whole number of 64-byte blocks: 0x80, zeros, the 64-bit big-endian bit count.
 MKV_HD void sha256_pad_block(uint32_t pad[16], uint64_t message_bytes) {

@@ -82,32 +82,3 @@ extern "C" int64_t hc_check_div_by_recip(uint32_t a_lo, uint32_t a_hi, int64_t* 
   return bad;
 }
 
-// sha256_compress2 on random states/blocks vs two sha256_compress calls;
-// returns the number of differing states.
-extern "C" int64_t hc_check_compress2(int64_t n, uint64_t seed) {
-  uint64_t x = seed | 1;
-  auto rnd = [&x]() {
-    x ^= x << 13;
-    x ^= x >> 7;
-    x ^= x << 17;
-    return (uint32_t)x;
-  };
-  int64_t bad = 0;
-  for (int64_t i = 0; i < n; ++i) {
-    mkv::Sha256 a, b, c, d;
-    uint32_t w1[16], w2[16];
-    for (int k = 0; k < 8; ++k) {
-      a.h[k] = c.h[k] = rnd();
-      b.h[k] = d.h[k] = rnd();
-    }
-    for (int k = 0; k < 16; ++k) {
-      w1[k] = rnd();
-      w2[k] = rnd();
-    }
-    mkv::sha256_compress2(a, w1, b, w2);
-    mkv::sha256_compress(c, w1);
-    mkv::sha256_compress(d, w2);
-    for (int k = 0; k < 8; ++k) bad += (a.h[k] != c.h[k]) || (b.h[k] != d.h[k]);
-  }
-  return bad;
-}

@@ -41,11 +41,3 @@ def test_page_hash_is_prefix_cache_key():
     h = ref.page_hashes(ids)
     key = hashlib.sha256(ids[:32].tobytes()).hexdigest()[:16]  # prefix_cache.py:31-34
     assert h[1] == int(key, 16) and format(h[1], "016x") == key
-
-
-def test_paired_compression_equals_two_compressions():
-    import ctypes
-    fn = hostcheck().hc_check_compress2
-    fn.argtypes = [ctypes.c_int64, ctypes.c_uint64]
-    fn.restype = ctypes.c_int64
-    assert fn(20000, 12345) == 0
