@@ -245,9 +245,10 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * {u64 key, i32 page, i32 copy of the page's refcount}), the page records (P x 32 bytes: i32 refcount, i32
  * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
  * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), the
- * last-occurrence slots (P int32, -1 between steps) and the release-run
- * scratch (about 13 MiB: counters, per-op offsets, page ids and bit arrays of
- * up to 2^20 page references), and the total size.
+ * last-occurrence slots (P int32, -1 between steps), the scratch of the
+ * many-workgroup passes (4.6 MiB for a release run of up to 2^20 page
+ * references: counters, per-op offsets, page ids, bit arrays; plus 8.25 x Q
+ * bytes for compacting the ring), and the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
  * (a leading run of up to 1024 releases is retired by many-workgroup passes,

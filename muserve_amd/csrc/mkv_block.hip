@@ -70,13 +70,16 @@ constexpr int64_t kEntBytes = 16, kRecBytes = 32;
 constexpr int kRunMaxOps = 1024;               // releases retired in bulk per step
 constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
 constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
-enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunNumCtr = 16 };
+enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kRunSpan,
+              kRunNumCtr = 16 };
 
 struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
   int64_t off_ctr, off_ent, off_rec, off_free, off_ring, off_last, off_run, bytes;
   // inside the run scratch at off_run
   int64_t run_ctr, run_off, run_child, run_page, run_bits, run_wpre;
+  // ring compaction scratch: a copy of the ring span, live bits, their prefix counts
+  int64_t cmp_ring, cmp_bits, cmp_pre;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -112,6 +115,9 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.run_page = take(kRunMaxElems * 4);
   l.run_bits = take(3 * kRunMaxWords * 4);
   l.run_wpre = take(2 * kRunMaxWords * 4);
+  l.cmp_ring = take(l.Q * 8);
+  l.cmp_bits = take(l.Q / 32 * 4);
+  l.cmp_pre = take(l.Q / 32 * 4);
   l.bytes = o;
   return l;
 }
@@ -129,6 +135,9 @@ struct BmState {
   int32_t* run_page;   // run: page id of each element
   uint32_t* run_bits;  // run: [3][kRunMaxWords] to the ring / free stack / last occurrence
   uint32_t* run_wpre;  // run: [2][kRunMaxWords] exclusive prefix counts of the first two
+  uint64_t* cmp_ring;  // compaction: the ring span [head, tail) copied out
+  uint32_t* cmp_bits;  // compaction: live bit per copied entry
+  uint32_t* cmp_pre;   // compaction: live entries before each bit word
   int64_t C, Q;
   int32_t P;
 };
@@ -149,6 +158,9 @@ inline BmState bm_state(void* base, int32_t P) {
   s.run_page = reinterpret_cast<int32_t*>(b + l.run_page);
   s.run_bits = reinterpret_cast<uint32_t*>(b + l.run_bits);
   s.run_wpre = reinterpret_cast<uint32_t*>(b + l.run_wpre);
+  s.cmp_ring = reinterpret_cast<uint64_t*>(b + l.cmp_ring);
+  s.cmp_bits = reinterpret_cast<uint32_t*>(b + l.cmp_bits);
+  s.cmp_pre = reinterpret_cast<uint32_t*>(b + l.cmp_pre);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -803,6 +815,21 @@ constexpr int kRunGrid = 256;                  // workgroups of the many-CU pass
 constexpr int kRunUnroll = 4;
 constexpr int kRunChunk = kRunUnroll * kRunThreads;  // elements a workgroup takes at a time
 
+// The LRU ring is compacted (on many CUs, inside the run kernels) when more
+// than an eighth of its span is dead entries, and when a run's pushes might
+// not fit. Dead entries accumulate as admits pin cached pages, and a dense
+// ring lets an admit find its victims in one window. Live entries are
+// exactly the evictable pages, and a run leaves them live. One thread of the
+// setup kernel decides, on every path.
+constexpr int64_t kCompactMinDead = 1024;
+__device__ void decide_compaction(const BmState& s, int64_t run_refs) {
+  const int64_t span = s.ctr[kTail] - s.ctr[kHead], dead = span - s.ctr[kEvictable];
+  const int64_t pushes = run_refs < s.P ? run_refs : s.P;  // at most one per page
+  const bool pays = dead > kCompactMinDead && dead * 8 > span;
+  s.run_ctr[kRunCompact] = pays || span + pushes > s.Q;
+  s.run_ctr[kRunSpan] = span;
+}
+
 __device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
   return op < 0 && -(op + 1) < a.num_requests;
 }
@@ -810,7 +837,6 @@ __device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
 __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   constexpr int kOpt = kRunMaxOps / kBmThreads;  // consecutive ops per thread
   static_assert(kOpt * kBmThreads == kRunMaxOps, "ops split evenly over the threads");
-  __shared__ Shared sh;
   __shared__ int32_t first_non;
   __shared__ uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
   __shared__ int64_t off[kRunMaxOps + 1];
@@ -847,7 +873,10 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   __syncthreads();
   int n = first_non;
   if (n < 2) {
-    if (tid == 0) s.run_ctr[kRunOps] = 0;
+    if (tid == 0) {
+      s.run_ctr[kRunOps] = 0;
+      decide_compaction(s, 0);
+    }
     return;
   }
   // a request released twice: the earliest op releases; sequentially a later
@@ -920,23 +949,11 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     n = lo;  // ops after it are the step kernel's (it repeats any error bit)
   }
   if (n < 2) {
-    if (tid == 0) s.run_ctr[kRunOps] = 0;
+    if (tid == 0) {
+      s.run_ctr[kRunOps] = 0;
+      decide_compaction(s, 0);
+    }
     return;
-  }
-  // room on the ring for at most one push per distinct page
-  Ctrs c;
-  c.free_top = s.ctr[kFreeTop];
-  c.head = s.ctr[kHead];
-  c.tail = s.ctr[kTail];
-  c.next_stamp = s.ctr[kNextStamp];
-  c.evictable = s.ctr[kEvictable];
-  c.tombs = s.ctr[kTombs];
-  c.log_len = s.ctr[kLogLen];
-  const int64_t pushes = off[n] < s.P ? off[n] : s.P;
-  if (c.tail - c.head + pushes > s.Q) {
-    int buf = 0;
-    ring_compact(a, c, sh, buf);
-    if (tid == 0) s.ctr[kTail] = c.tail;
   }
   for (int j = tid; j <= n; j += kBmThreads) s.run_off[j] = off[j];
 #pragma unroll
@@ -947,6 +964,7 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   if (tid == 0) {
     s.run_ctr[kRunOps] = n;
     s.run_ctr[kRunTotal] = off[n];
+    decide_compaction(s, off[n]);
   }
 }
 
@@ -1020,8 +1038,7 @@ __global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
 __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
-  const int64_t total = s.run_ctr[kRunTotal];
-  if (n < 2) return;
+  const int64_t total = n < 2 ? 0 : s.run_ctr[kRunTotal];
   const int lane = threadIdx.x & 63;
   for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
        c0 += (int64_t)gridDim.x * kRunChunk) {
@@ -1055,71 +1072,127 @@ __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
       }
     }
   }
+  // Compaction: the ring span [head, tail) is copied out, with a bit per entry
+  // that stays live (an entry of a page this run pushes again does not).
+  if (s.run_ctr[kRunCompact] == 0) return;
+  const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
+  for (int64_t b0 = (int64_t)blockIdx.x * kRunThreads; b0 < span;
+       b0 += (int64_t)gridDim.x * kRunThreads) {
+    const int64_t i = b0 + threadIdx.x;  // a wave: 64 aligned entries
+    bool keep = false;
+    if (i < span) {
+      const uint64_t e = s.ring[(head + i) & qm];
+      const int32_t pg = (int32_t)(uint32_t)e;
+      s.cmp_ring[i] = e;
+      keep = live(rec_head(s, pg), (uint32_t)(e >> 32)) && (n < 2 || s.last[pg] < 0);
+    }
+    const uint64_t m = __ballot(keep);
+    if (lane == 0 && i < span) {
+      s.cmp_bits[i >> 5] = (uint32_t)m;
+      s.cmp_bits[(i >> 5) + 1] = (uint32_t)(m >> 32);
+    }
+  }
+}
+
+// Exclusive prefix counts of up to three bit arrays of nw words (per thread a
+// contiguous slice of words, then a wavefront scan and the waves' totals);
+// every thread gets the totals. NB bit arrays; pre[k][w] receives the count
+// of set bits before word w of array k.
+template <int NB>
+__device__ void scan_bits(const uint32_t* const (&bits)[NB], uint32_t* const (&pre)[NB], int64_t nw,
+                          int64_t (&tot)[NB], int64_t (&wave_tot)[NB][kBmWaves]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t per = (nw + kBmThreads - 1) / kBmThreads;  // words per thread
+  const int64_t w0 = tid * per, w1 = w0 + per < nw ? w0 + per : nw;
+  int64_t cnt[NB], incl[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    cnt[k] = 0;
+    for (int64_t w = w0; w < w1; ++w) cnt[k] += __popc(bits[k][w]);
+    incl[k] = cnt[k];
+  }
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int64_t o = __shfl_up(incl[k], d);
+      if (lane >= d) incl[k] += o;
+    }
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) wave_tot[k][wave] = incl[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    int64_t before = incl[k] - cnt[k];
+    tot[k] = 0;
+#pragma unroll
+    for (int w = 0; w < kBmWaves; ++w) {
+      before += w < wave ? wave_tot[k][w] : 0;
+      tot[k] += wave_tot[k][w];
+    }
+    for (int64_t w = w0; w < w1; ++w) {
+      pre[k][w] = (uint32_t)before;
+      before += __popc(bits[k][w]);
+    }
+  }
 }
 
 __global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
   __shared__ int64_t wave_tot[2][kBmWaves];
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
-  const int64_t total = s.run_ctr[kRunTotal];
-  if (n < 2) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t nw = (total + 31) >> 5;
-  const int64_t per = (nw + kBmThreads - 1) / kBmThreads;  // words per thread
-  const int64_t w0 = tid * per, w1 = w0 + per < nw ? w0 + per : nw;
-  const uint32_t* bl = s.run_bits;
-  const uint32_t* bf = s.run_bits + kRunMaxWords;
-  int64_t cl = 0, cf = 0;
-  for (int64_t w = w0; w < w1; ++w) {
-    cl += __popc(bl[w]);
-    cf += __popc(bf[w]);
+  const bool cmp = s.run_ctr[kRunCompact] != 0;
+  if (n < 2 && !cmp) return;
+  const int tid = threadIdx.x;
+  int64_t n_lru = 0, n_free = 0, n_kept = 0;
+  if (n >= 2) {
+    const uint32_t* const bits[2] = {s.run_bits, s.run_bits + kRunMaxWords};
+    uint32_t* const pre[2] = {s.run_wpre, s.run_wpre + kRunMaxWords};
+    int64_t tot[2];
+    scan_bits<2>(bits, pre, (s.run_ctr[kRunTotal] + 31) >> 5, tot, wave_tot);
+    n_lru = tot[0];
+    n_free = tot[1];
   }
-  int64_t il = cl, jf = cf;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int64_t ol = __shfl_up(il, d), of = __shfl_up(jf, d);
-    if (lane >= d) {
-      il += ol;
-      jf += of;
-    }
-  }
-  if (lane == 63) {
-    wave_tot[0][wave] = il;
-    wave_tot[1][wave] = jf;
-  }
-  __syncthreads();
-  int64_t pl = il - cl, pf = jf - cf, n_lru = 0, n_free = 0;
-#pragma unroll
-  for (int w = 0; w < kBmWaves; ++w) {
-    pl += w < wave ? wave_tot[0][w] : 0;
-    pf += w < wave ? wave_tot[1][w] : 0;
-    n_lru += wave_tot[0][w];
-    n_free += wave_tot[1][w];
-  }
-  for (int64_t w = w0; w < w1; ++w) {
-    s.run_wpre[w] = (uint32_t)pl;
-    s.run_wpre[kRunMaxWords + w] = (uint32_t)pf;
-    pl += __popc(bl[w]);
-    pf += __popc(bf[w]);
+  if (cmp) {
+    if (n >= 2) __syncthreads();  // wave_tot is reused
+    const uint32_t* const bits[1] = {s.cmp_bits};
+    uint32_t* const pre[1] = {s.cmp_pre};
+    int64_t tot[1];
+    int64_t(&wt)[1][kBmWaves] = reinterpret_cast<int64_t(&)[1][kBmWaves]>(wave_tot);
+    scan_bits<1>(bits, pre, (s.run_ctr[kRunSpan] + 31) >> 5, tot, wt);
+    n_kept = tot[0];
   }
   if (tid == 0) {
-    s.run_ctr[kRunTail] = s.ctr[kTail];
+    // pushes go after the kept entries (compacted from the head) or the tail
+    const int64_t base = cmp ? s.ctr[kHead] + n_kept : s.ctr[kTail];
+    s.run_ctr[kRunTail] = base;
     s.run_ctr[kRunStamp] = s.ctr[kNextStamp];
     s.run_ctr[kRunFree] = s.ctr[kFreeTop];
-    s.ctr[kTail] += n_lru;
+    s.ctr[kTail] = base + n_lru;
     s.ctr[kNextStamp] += n_lru;
     s.ctr[kEvictable] += n_lru;
     s.ctr[kFreeTop] += n_free;
   }
-  for (int j = tid; j < n; j += kBmThreads)
+  for (int j = tid; j < (n >= 2 ? n : 0); j += kBmThreads)
     if (s.run_child[j] != -2) a.status[-(a.ops[j] + 1)] = kStReleased;
 }
 
 __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
-  const int64_t total = s.run_ctr[kRunTotal];
-  if (n < 2) return;
+  const int64_t total = n < 2 ? 0 : s.run_ctr[kRunTotal];
+  if (s.run_ctr[kRunCompact] != 0) {  // the kept entries, from the head in order
+    const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
+    for (int64_t i = (int64_t)blockIdx.x * kRunThreads + threadIdx.x; i < span;
+         i += (int64_t)gridDim.x * kRunThreads) {
+      const uint32_t bits = s.cmp_bits[i >> 5], bit = 1u << (i & 31);
+      if (bits & bit)
+        s.ring[(head + s.cmp_pre[i >> 5] + __popc(bits & (bit - 1u))) & qm] = s.cmp_ring[i];
+    }
+  }
   const int64_t tail0 = s.run_ctr[kRunTail], stamp0 = s.run_ctr[kRunStamp];
   const int64_t free0 = s.run_ctr[kRunFree], qm = s.Q - 1;
   const uint32_t* b = s.run_bits;
