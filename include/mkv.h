@@ -305,6 +305,42 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
                    const int64_t* hash_offsets, int32_t num_requests, int32_t* pages,
                    int32_t* hits, int32_t* err, void* stream);
 
+/* ---- paged decode attention ----------------------------------------------- */
+
+/*
+ * Decode attention reading the paged pool directly. For sequence b < batch,
+ * with len = seq_lens[b] cached tokens in pages page_table[b][0..ceil(len/16)),
+ * and each query head h of KV head kv = h / G (G = num_q_heads / num_kv_heads):
+ *   out[b][h] = softmax_j(q[b][h] . k_j * softmax_scale) weighted sum of v_j,
+ *   over tokens j < len, k_j / v_j = k_cache / v_cache[page][j % 16][kv].
+ * Replaces the paged kernel wrapped by attn_decode (muserve/kernels/attention.py:
+ * 29-42: q [B,1,Hq,D], caches [P,16,Hkv,D], cache_seqlens, page_table), i.e.
+ * the math of muserve/model/qwen35_layer_v2.py:493-502 without gathering the
+ * padded K/V. Scores, softmax and accumulation are fp32; out is bf16 (RNE).
+ *   q, out:  [batch, num_q_heads, 256] bf16, contiguous (q[B,1,Hq,D] is too);
+ *   k_cache, v_cache: [num_pages, 16, num_kv_heads, 256] bf16 (one layer's
+ *            planes of the pool), 16-byte aligned;
+ *   page_table: [batch][table_stride] int32, table_width valid columns;
+ *   max_seq_len: an upper bound of seq_lens that sizes the launch (512-token
+ *            chunks per sequence); longer sequences are cut to it;
+ *   workspace: mkv_decode_attention_workspace_bytes(...) bytes (16-byte
+ *            aligned; none when max_seq_len <= 512) for the chunks' partial
+ *            softmax states, merged by a second kernel.
+ * head_dim must be 256 and G one of 1, 2, 4, 8 (MKV_E_UNSUPPORTED). A page id
+ * outside [0, num_pages) skips that page's tokens and sets MKV_DEVERR_PAGE; a
+ * length above 16*table_width or max_seq_len is cut to it and sets
+ * MKV_DEVERR_TABLE; a sequence of length 0 gets zeros.
+ */
+int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t num_kv_heads,
+                                             int32_t num_q_heads, int32_t max_seq_len);
+int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
+                              int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
+                              int32_t head_dim, const int32_t* page_table, int64_t table_stride,
+                              int32_t table_width, const int32_t* seq_lens, int32_t batch,
+                              int32_t max_seq_len, float softmax_scale, void* out,
+                              void* workspace, int64_t workspace_bytes, int32_t* err,
+                              void* stream);
+
 /* ---- self-test ------------------------------------------------------------ */
 
 /*

@@ -38,6 +38,7 @@ _DEVERR_TEXT = {
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
+_F32 = ctypes.c_float
 
 # name -> argtypes, in the order of include/mkv.h
 SIGNATURES: dict[str, list] = {
@@ -62,7 +63,11 @@ SIGNATURES: dict[str, list] = {
     "mkv_bm_step": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P,
                     _I64, _P, _P],
     "mkv_hash_probe": [_P, _I32, _P, _P, _I32, _P, _P, _P, _P],
+    "mkv_decode_attention_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
+                                  _I32, _F32, _P, _P, _I64, _P, _P],
 }
+_INT64_RESULT = {"mkv_bm_state_bytes", "mkv_decode_attention_workspace_bytes"}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -102,7 +107,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = (ctypes.c_char_p if name == "mkv_last_error" else
-                          ctypes.c_int64 if name == "mkv_bm_state_bytes" else ctypes.c_int)
+                          ctypes.c_int64 if name in _INT64_RESULT else ctypes.c_int)
         if lib.mkv_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH.name} ABI {lib.mkv_version()} != expected {ABI_VERSION}")
         runtimes = _hip_runtimes()

@@ -26,4 +26,9 @@ Pinning (what checks each function beyond its own restatement):
                                   timestamp-LRU brute force (blocks.TimestampLRUModel)
                                   on small traces
   state.gather/scatter            round trip and index_select/index_copy_ identities
+  attention.decode_attention      torch scaled_dot_product_attention (float64) on the
+                                  gathered K/V; closed forms (one token, constant V, equal
+                                  keys, one dominant key); invariance when the pool's
+                                  pages move; the reference's bf16 contiguous formula
+                                  (attention.reference_bf16) within bf16 rounding
 """

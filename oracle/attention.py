@@ -1,0 +1,76 @@
+"""Paged decode attention on the CPU (oracle; test infrastructure only).
+
+muserve's decode attention for one query token per sequence:
+  * the paged interface of attn_decode (muserve/kernels/attention.py:29-42):
+    q [B,1,Hq,D], k/v cache [P,16,Hkv,D], cache_seqlens [B] int32,
+    page_table [B,W] int32 (causal: a decode token sees every cached token);
+  * the math of the contiguous decode path (muserve/model/qwen35_layer_v2.py:
+    493-502): K/V repeated over the query-head group (repeat_interleave, so
+    query head h uses KV head h // G), scores = q k^T * scale, softmax over
+    the sequence, weighted sum of V.
+
+`decode_attention` evaluates that in float64 (numpy) from the pages the
+table names; `reference_bf16` runs the contiguous path as written, in torch
+bf16 on the CPU, on K/V gathered from the same pages.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+PAGE = 16
+
+
+def gather_kv(cache: np.ndarray, table_row: np.ndarray, length: int) -> np.ndarray:
+    """[P,16,Hkv,D] cache, one sequence's table row -> its first `length`
+    tokens as [length, Hkv, D] (muserve/kv_cache.py:149-158 page order)."""
+    pages = np.asarray(table_row[: -(-length // PAGE)], dtype=np.int64)
+    return cache[pages].reshape(-1, *cache.shape[2:])[:length]
+
+
+def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                     seq_lens: np.ndarray, page_table: np.ndarray, scale: float) -> np.ndarray:
+    """q [B,Hq,D], caches [P,16,Hkv,D] (any float dtype; computed in float64),
+    seq_lens [B], page_table [B,W] -> [B,Hq,D] float64. Length 0 -> zeros."""
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, D = q.shape
+    Hkv = k_cache.shape[2]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        n = int(seq_lens[b])
+        if n == 0:
+            continue
+        K = gather_kv(k_cache, page_table[b], n).astype(np.float64)  # [n, Hkv, D]
+        V = gather_kv(v_cache, page_table[b], n).astype(np.float64)
+        for h in range(Hq):
+            s = K[:, h // G] @ q[b, h] * scale
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ V[:, h // G]
+    return out
+
+
+def reference_bf16(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   seq_lens, page_table, scale: float) -> torch.Tensor:
+    """muserve/model/qwen35_layer_v2.py:493-502 per sequence, bf16 on the CPU:
+    q [B,Hq,D] bf16, caches [P,16,Hkv,D] bf16 -> [B,Hq,D] bf16."""
+    B, Hq, D = q.shape
+    Hkv = k_cache.shape[2]
+    G = Hq // Hkv
+    out = torch.zeros(B, Hq, D, dtype=torch.bfloat16)
+    for b in range(B):
+        n = int(seq_lens[b])
+        if n == 0:
+            continue
+        pages = torch.as_tensor(np.asarray(page_table[b][: -(-n // PAGE)], dtype=np.int64))
+        k_full = k_cache[pages].reshape(-1, Hkv, D)[:n].unsqueeze(0)  # [1, S, Hkv, D]
+        v_full = v_cache[pages].reshape(-1, Hkv, D)[:n].unsqueeze(0)
+        k_exp = k_full.repeat_interleave(G, dim=2)  # [1, S, Hq, D]
+        v_exp = v_full.repeat_interleave(G, dim=2)
+        q_4d = q[b].unsqueeze(0).unsqueeze(2)  # [1, Hq, 1, D]
+        k_4d = k_exp.permute(0, 2, 1, 3)  # [1, Hq, S, D]
+        scores = torch.matmul(q_4d, k_4d.transpose(-1, -2).contiguous()) * scale
+        weights = torch.softmax(scores, dim=-1)
+        v_4d = v_exp.permute(0, 2, 1, 3).contiguous()
+        out[b] = torch.matmul(weights, v_4d).squeeze(2)[0]
+    return out

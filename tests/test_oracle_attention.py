@@ -1,0 +1,101 @@
+"""The decode-attention oracle (oracle/attention.py) pinned against torch's
+scaled_dot_product_attention, closed forms, page placement and the
+reference's own bf16 formula (muserve/model/qwen35_layer_v2.py:493-502)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as att
+
+
+def make_case(rng, lens, Hq=4, Hkv=1, D=256, spare=3):
+    lens = np.asarray(lens)
+    pages = [-(-int(n) // 16) for n in lens]
+    P = sum(pages) + spare
+    perm = rng.permutation(P)
+    W = max(1, max(pages))
+    table = np.zeros((len(lens), W), dtype=np.int32)
+    at = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    k = rng.standard_normal((P, 16, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((P, 16, Hkv, D)).astype(np.float32)
+    q = rng.standard_normal((len(lens), Hq, D)).astype(np.float32)
+    return q, k, v, lens, table
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 1), (4, 2), (8, 1), (1, 1)])
+def test_matches_sdpa_float64(Hq, Hkv):
+    rng = np.random.default_rng(5)
+    q, k, v, lens, table = make_case(rng, [1, 17, 300, 40], Hq=Hq, Hkv=Hkv, D=64)
+    scale = 64 ** -0.5
+    got = att.decode_attention(q, k, v, lens, table, scale)
+    for b, n in enumerate(lens):
+        K = torch.from_numpy(att.gather_kv(k, table[b], n)).double()  # [n, Hkv, D]
+        V = torch.from_numpy(att.gather_kv(v, table[b], n)).double()
+        Kx = K.repeat_interleave(Hq // Hkv, dim=1).permute(1, 0, 2)  # [Hq, n, D]
+        Vx = V.repeat_interleave(Hq // Hkv, dim=1).permute(1, 0, 2)
+        Q = torch.from_numpy(q[b]).double().unsqueeze(1)  # [Hq, 1, D]
+        want = F.scaled_dot_product_attention(Q, Kx, Vx, scale=scale)[:, 0]
+        np.testing.assert_allclose(got[b], want.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(6)
+    q, k, v, lens, table = make_case(rng, [1, 50, 50, 50], Hq=4, Hkv=1, D=32)
+    # one token: its V row, whatever the scores
+    out = att.decode_attention(q, k, v, lens, table, 0.3)
+    np.testing.assert_allclose(out[0], np.repeat(v[table[0, 0], 0], 4, axis=0), rtol=1e-12)
+    # constant V over a sequence: that row
+    vc = v.copy()
+    for p in table[1, :4]:
+        vc[p] = vc[table[1, 0], 0]
+    out = att.decode_attention(q, k, vc, lens, table, 0.3)
+    np.testing.assert_allclose(out[1], np.repeat(vc[table[1, 0], 0], 4, axis=0), rtol=1e-12)
+    # equal keys: uniform weights, the mean of V
+    kc = k.copy()
+    for p in table[2, :4]:
+        kc[p] = kc[table[2, 0], 0]
+    out = att.decode_attention(q, kc, v, lens, table, 0.3)
+    mean = att.gather_kv(v, table[2], 50)[:, 0].astype(np.float64).mean(0)
+    np.testing.assert_allclose(out[2], np.tile(mean, (4, 1)), rtol=1e-10, atol=1e-12)
+    # one dominant key (token 7): its V row
+    kd = k.copy()
+    p7, r7 = table[3, 0], 7
+    kd[p7, r7, 0] = q[3, 0] * 1e3
+    out = att.decode_attention(q, kd, v, lens, table, 1.0)
+    np.testing.assert_allclose(out[3, 0], v[p7, r7, 0], rtol=1e-9, atol=1e-9)
+
+
+def test_page_placement_does_not_matter():
+    rng = np.random.default_rng(7)
+    q, k, v, lens, table = make_case(rng, [33, 70, 5], Hq=4, Hkv=2, D=32, spare=10)
+    P = k.shape[0]
+    perm = rng.permutation(P)  # page p moves to perm[p]
+    k2, v2 = np.empty_like(k), np.empty_like(v)
+    k2[perm], v2[perm] = k, v
+    a = att.decode_attention(q, k, v, lens, table, 0.2)
+    b = att.decode_attention(q, k2, v2, lens, perm[table].astype(np.int32), 0.2)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_zero_length_is_zero():
+    rng = np.random.default_rng(8)
+    q, k, v, lens, table = make_case(rng, [0, 3], D=16)
+    out = att.decode_attention(q, k, v, lens, table, 0.25)
+    assert not out[0].any() and out[1].any()
+
+
+def test_reference_bf16_formula_is_within_bf16_rounding():
+    # The reference computes scores, softmax and the weighted sum in bf16; the
+    # oracle in float64. They agree to bf16's few-ulp level.
+    rng = np.random.default_rng(9)
+    q, k, v, lens, table = make_case(rng, [1, 16, 100, 700], Hq=4, Hkv=1, D=256)
+    qb, kb, vb = (torch.from_numpy(x).bfloat16() for x in (q, k, v))
+    got = att.reference_bf16(qb, kb, vb, lens, table, 256 ** -0.5).double().numpy()
+    want = att.decode_attention(qb.float().numpy(), kb.float().numpy(), vb.float().numpy(),
+                                lens, table, 256 ** -0.5)
+    err = np.abs(got - want)
+    assert err.max() < 0.05 and np.median(err) < 0.005, (err.max(), np.median(err))
