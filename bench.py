@@ -838,6 +838,170 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
+Q_HEADS = 4  # query heads per rank over the one KV head (32 / TP 8)
+
+
+def attn_bytes(lens: np.ndarray) -> float:
+    """Algorithmic bytes of one decode-attention launch at lengths ``lens``:
+    every cached K and V row once, the table entries, q in, out."""
+    pages = -(-lens // 16)
+    return float(2 * ROW * lens.sum() + 4 * pages.sum() + 4 * B + 2 * B * Q_HEADS * ROW)
+
+
+def attn_cpu_baseline(cache, bt, q, lens_now: np.ndarray, gpu_out, n_seq: int = 16) -> dict:
+    """The reference's decode attention (muserve/model/qwen35_layer_v2.py:
+    493-502, restated in oracle.attention.reference_bf16: bf16 torch on the
+    CPU over K/V gathered from the pages) on the first n_seq sequences of the
+    last layer, timed on the host; also checks the GPU output of those
+    sequences against the float64 oracle (one bf16 ulp)."""
+    from oracle import attention as att
+
+    threads = torch.get_num_threads()
+    k = cache.cache[LAYERS - 1, 0].cpu()
+    v = cache.cache[LAYERS - 1, 1].cpu()
+    table = bt.tables.cpu().numpy()[:n_seq]
+    lens = lens_now[:n_seq]
+    qc = q[LAYERS - 1, :n_seq, 0].cpu()
+    t0 = time.perf_counter()
+    att.reference_bf16(qc, k, v, lens, table, HEAD_DIM ** -0.5)
+    dt = time.perf_counter() - t0
+    want = att.decode_attention(qc.float().numpy(), k.float().numpy(), v.float().numpy(), lens,
+                                table, HEAD_DIM ** -0.5)
+    got = gpu_out[:n_seq, 0].float().cpu().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -13))) - 7)
+    nbytes = 2 * ROW * float(lens.sum())
+    return {
+        "value": round(nbytes / dt / 1e9, 3),
+        "unit": "GB/s (K/V bytes attended)",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference decode attention (bf16 torch-CPU, {threads} threads) over the "
+                   f"first {n_seq} sequences of one layer ({int(lens.sum())} cached tokens): "
+                   f"{dt:.2f} s"),
+        "seconds": round(dt, 3),
+        "cpu_model": _cpu_model(),
+        "gpu_within_one_bf16_ulp_of_float64_on_sample": bool((np.abs(got - want) <= ulp).all()),
+    }
+
+
+def run_decode_attn(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Decode step with paged attention instead of the padded gather: per
+    layer, append the new token's K/V, then attn_decode for 4 query heads per
+    sequence reading the pool through the block tables (same pool, lengths
+    and seed as the default workload)."""
+    from muserve_amd.kernels import attention as A
+    from muserve_amd.kv_cache import BlockTables, PagedKVCache, SequenceKVState, reserve_tokens
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = context_lengths()
+    total_steps = warmup + steps
+    pages = int(np.sum(-(-(ctx + total_steps) // 16))) + 64
+    log(f"pool: {pages} pages x {LAYERS} layers (ctx sum {int(ctx.sum())}, max {int(ctx.max())})")
+    cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
+                         dtype=torch.bfloat16, device=dev, verbose=False)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    for l in range(LAYERS):
+        cache.cache[l].normal_(generator=gen)
+    cache.shuffle_free_list(torch.Generator().manual_seed(SEED))
+    seqs = [SequenceKVState() for _ in range(B)]
+    for s, n in zip(seqs, ctx):
+        reserve_tokens(cache, s, int(n))
+    width = int(-(-(int(ctx.max()) + total_steps) // 16))
+    bt = BlockTables(cache, seqs, max_pages=width)
+    kin = torch.empty(total_steps, LAYERS, B, 1, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vin = torch.empty_like(kin)
+    kin.normal_(generator=gen)
+    vin.normal_(generator=gen)
+    q = torch.empty(LAYERS, B, 1, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    q.normal_(generator=gen)
+    out = torch.empty(LAYERS, B, 1, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    max_len = int(ctx.max()) + total_steps
+    stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
+
+    def one_step(i: int, rec=None, steps_rec=None):
+        step = stamps.span(stream) if steps_rec is not None else None
+        slots = bt.decode_step()
+        for l in range(LAYERS):
+            cache.append(slots, kin[i, l], vin[i, l], layer=l)
+            kp, vp = cache.get_kv_by_layer(l)
+            sp = stamps.span(stream) if rec is not None else None
+            A.attn_decode(q[l], kp, vp, bt.seq_lens, bt.tables, max_seqlen=max_len, out=out[l])
+            if rec is not None:
+                rec.append(("attn", sp.end(stream)))
+        if steps_rec is not None:
+            steps_rec.append(step.end(stream))
+
+    log(f"warmup {warmup} steps")
+    for i in range(warmup):
+        one_step(i)
+    torch.cuda.synchronize()
+    cache.check_errors()
+    A.check_errors(dev)
+
+    lens0 = bt._lens.copy()
+    attn_total = step_total = 0.0
+    for j in range(steps):
+        ab = attn_bytes(lens0 + j + 1)
+        attn_total += ab
+        step_total += LAYERS * (ab + 2 * B * ROW + 2 * B * ROW + 8 * B)  # + the append
+    recs = [[] for _ in range(steps)]
+    step_spans: list = []
+    log(f"timing {steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(warmup + j, recs[j], step_spans)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    cache.check_errors()
+    A.check_errors(dev)
+    mean_attn_s = _timed(recs, "attn") / 1e3
+    mean_attn_bytes = attn_total / steps
+    ratio = counter_ratios("decode_attention_hbm_counters.md").get("attn")
+    step_s = elapsed / steps
+    value = step_total / elapsed / 1e9
+    achieved = mean_attn_bytes / mean_attn_s / 1e9
+    res = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) for KV append + paged decode attention; "
+                  "decode step µs @ batch 256",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (fp32 softmax and accumulation)",
+        "data": "synthetic (seeded ~N(0,1) q/K/V, seeded log-normal context lengths)",
+        "config": {
+            "workload": ("decode-step KV append + paged decode attention on one TP rank: 15 "
+                         "attention layers, batch 256, 4 query heads over 1 KV head x 256, bf16, "
+                         "16-token pages, ctx lognormal(median 4096, sigma 1.0, clip 1..32768), "
+                         "seed 102"),
+            "batch": B, "layers": LAYERS, "q_heads": Q_HEADS, "kv_heads": 1, "head_dim": HEAD_DIM,
+            "ctx_sum_start": int(lens0.sum()), "ctx_max_start": int(lens0.max()),
+        },
+        "decode_step_us": round(step_s * 1e6, 1),
+        "step_time": _step_stats(step_spans),
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(B / step_s, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mkv_decode_attention_bf16 = attn_chunk_kernel<4> + attn_merge_kernel<4>",
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": round(ratio * mean_attn_bytes) if ratio else None,
+            "traffic_to_algorithmic": ratio,
+            "traffic_source": ("rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 (scales from a 1 GiB "
+                               "copy), profiles/decode_attention_hbm_counters.md"),
+            "mean_launch_us": round(mean_attn_s * 1e6, 2),
+            "algorithmic_bytes_per_launch": round(mean_attn_bytes),
+            "flop_per_launch": round(4 * Q_HEADS * HEAD_DIM * float((lens0 + steps).sum())),
+        },
+    }
+    if with_cpu:
+        log("cpu baseline (reference decode attention on a sample)")
+        res["cpu_baseline"] = attn_cpu_baseline(cache, bt, q, bt._lens.copy(), out[LAYERS - 1])
+    return res
+
+
 def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
     """A plain device copy of known size (one 1 GiB state-pool entry through
     mkv_state_gather): the reference point for scaling rocprof's FETCH_SIZE and
@@ -868,7 +1032,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix"],
+                    choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
+                             "decode_attn"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -883,7 +1048,8 @@ def main() -> int:
         print(json.dumps(run_calibration()), flush=True)
         return 0
     runner = {"decode": run_decode, "fp8_prefill": run_fp8_prefill, "gdn_state": run_gdn_state,
-              "plumbing": run_plumbing, "prefix": run_prefix}[args.workload]
+              "plumbing": run_plumbing, "prefix": run_prefix,
+              "decode_attn": run_decode_attn}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window

@@ -321,12 +321,16 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
  *   k_cache, v_cache: [num_pages, 16, num_kv_heads, 256] bf16 (one layer's
  *            planes of the pool), 16-byte aligned;
  *   page_table: [batch][table_stride] int32, table_width valid columns;
- *   max_seq_len: an upper bound of seq_lens that sizes the launch (512-token
+ *   max_seq_len: an upper bound of seq_lens that sizes the launch (1024-token
  *            chunks per sequence); longer sequences are cut to it;
- *   workspace: mkv_decode_attention_workspace_bytes(...) bytes (16-byte
- *            aligned; none when max_seq_len <= 512) for the chunks' partial
- *            softmax states, merged by a second kernel.
- * head_dim must be 256 and G one of 1, 2, 4, 8 (MKV_E_UNSUPPORTED). A page id
+ *   workspace: mkv_decode_attention_workspace_bytes(...) bytes, 16-byte
+ *            aligned and zero-filled before its first use: it holds the work
+ *            counters (every call leaves them zero again) and, when
+ *            max_seq_len > 1024, the 1024-token chunks' partial softmax states
+ *            that a second kernel merges. Calls that share a workspace must
+ *            be ordered (one stream).
+ * head_dim must be 256, G one of 1, 2, 4, 8, batch * num_kv_heads at most
+ * 4096 and max_seq_len at most 2^24 (MKV_E_UNSUPPORTED). A page id
  * outside [0, num_pages) skips that page's tokens and sets MKV_DEVERR_PAGE; a
  * length above 16*table_width or max_seq_len is cut to it and sets
  * MKV_DEVERR_TABLE; a sequence of length 0 gets zeros.

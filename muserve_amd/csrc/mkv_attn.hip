@@ -8,7 +8,7 @@
 // path (muserve/model/qwen35_layer_v2.py:493-502), without the padded gather.
 //
 // Each K/V row is read once, 4 flop per byte at G = 4, so the bound is HBM.
-// A workgroup (4 waves) takes a 512-token chunk of one sequence and KV head;
+// A workgroup (4 waves) takes a 1024-token chunk of one sequence and KV head;
 // a wave takes one 16-token page at a time:
 //   * scores on MFMA (v_mfma_f32_16x16x32_bf16, 8 steps over head_dim 256):
 //     A = the K page, 16 contiguous bytes of a K row per lane loaded straight
@@ -22,7 +22,13 @@
 //     a V row is one coalesced 512-byte load per wave, with no transpose;
 //   * the waves' partial softmax states merge in LDS. A one-chunk sequence
 //     writes its normalised output; longer ones write (max, sum, unnormalised
-//     output) per chunk to the caller's workspace and a second kernel merges.
+//     output) per chunk to the caller's workspace and a second kernel merges
+//     them, one workgroup per (sequence, query head).
+// The chunks of all sequences form one list (sequence-major; every workgroup
+// computes the prefix of the chunk counts in LDS) that a grid of a few
+// workgroups per CU drains through an atomic counter: no workgroup is
+// launched for a chunk beyond its sequence's end, and the load balances
+// whatever the lengths. The last workgroup out resets the counter.
 #include <math.h>
 
 #include "mkv_device.h"
@@ -39,8 +45,9 @@ constexpr int kRowBytes = kHeadDim * 2;  // one bf16 K or V row of one KV head
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kPageTokens = 16;
-constexpr int kChunk = 512;  // tokens per workgroup
+constexpr int kChunk = 1024;  // tokens per work item (512 measured 3 % slower, 2048 4 %)
 constexpr int kChunkPages = kChunk / kPageTokens;
+constexpr int kMaxPairs = 4096;  // batch x KV heads whose chunk prefix fits in LDS
 
 struct AttnArgs {
   const uint8_t* q;  // [B, Hkv * G, 256] bf16
@@ -51,8 +58,9 @@ struct AttnArgs {
   uint8_t* out;          // [B, Hkv * G, 256] bf16
   float* part;           // [B, Hkv, chunks, G, 256] unnormalised chunk outputs
   float* ml;             // [B, Hkv, chunks, G, 2] chunk (max, sum), log2 units
+  int32_t* queue;        // [2]: next work item, workgroups done (zero between calls)
   int64_t num_pages, tstride;
-  int32_t twidth, hkv, chunks, max_len;
+  int32_t twidth, hkv, chunks, max_len, pairs;
   float scale_log2;  // softmax_scale * log2(e)
   int32_t* err;
 };
@@ -83,26 +91,21 @@ __device__ __forceinline__ int64_t attn_len(const AttnArgs& a, int64_t b, bool r
 }
 
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
-  static_assert(G >= 1 && G <= 8, "query heads per KV head");
-  __shared__ float p_lds[kAttnWaves][kPageTokens][16];  // [wave][token][head] probabilities
-  __shared__ float al_lds[kAttnWaves][16];              // [wave][head] rescale factor
-  __shared__ float m_w[kAttnWaves][G], l_w[kAttnWaves][G];
-  __shared__ __attribute__((aligned(16))) float o_w[kAttnWaves][G][kHeadDim];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t hk, int64_t c,
+                                           int64_t len, int64_t nch,
+                                           float (&p_lds)[kAttnWaves][kPageTokens][16],
+                                           float (&al_lds)[kAttnWaves][16],
+                                           float (&m_w)[kAttnWaves][G], float (&l_w)[kAttnWaves][G],
+                                           float (&o_w)[kAttnWaves][G][kHeadDim]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar page ids
   const int n = lane & 15, g = lane >> 4;
-  const int64_t b = blockIdx.y / a.hkv, hk = blockIdx.y % a.hkv;
-  const int c = blockIdx.x;
-  const int64_t len = attn_len(a, b, c == 0 && threadIdx.x == 0);
-  const int64_t nch = (len + kChunk - 1) / kChunk;
   uint8_t* out = a.out + (b * a.hkv + hk) * G * kRowBytes;
   if (len == 0) {  // nothing to attend to: zeros
-    if (c == 0)
-      for (int i = threadIdx.x; i < G * kRowBytes / 16; i += kAttnThreads)
-        st16(out + i * 16, u32x4{0u, 0u, 0u, 0u});
+    for (int i = threadIdx.x; i < G * kRowBytes / 16; i += kAttnThreads)
+      st16(out + i * 16, u32x4{0u, 0u, 0u, 0u});
     return;
   }
-  if (c >= nch) return;
 
   // the G query heads as the B operand, in the K rows' chunk order
   bf16x8 qb[8];
@@ -123,42 +126,64 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
   const int64_t pages = (len + kPageTokens - 1) / kPageTokens;
   const int64_t p_end = (c + 1) * (int64_t)kChunkPages < pages ? (c + 1) * (int64_t)kChunkPages : pages;
   const int32_t* trow = a.table + b * a.tstride;
-  for (int64_t p = c * (int64_t)kChunkPages + wave; p < p_end; p += kAttnWaves) {
-    const int32_t pid = ld_const(trow + p);
-    if (pid < 0 || pid >= a.num_pages) {  // wave-uniform: the page is skipped
-      if (lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
-      continue;
-    }
-    const int64_t base = ((int64_t)pid * kPageTokens * a.hkv + hk) * kRowBytes;
-    const uint8_t* kp = a.k + base + n * tok_stride;
-    const uint8_t* vp = a.v + base + lane * 8;
-    bf16x8 ka[8];
-    u32x2 vr[kPageTokens];
+  // This wave's pages are p0 + 4j: their ids in one load, lane j holding page
+  // j. A page id outside the pool is flagged and its tokens masked (page 0 is
+  // read in its place), so the loop below has no branches and the compiler's
+  // load counting stays exact.
+  static_assert(kChunkPages / kAttnWaves <= 32, "a wave's page validity fits a 32-bit mask");
+  const int64_t p0 = c * (int64_t)kChunkPages + wave;
+  const int np = p_end > p0 ? (int)((p_end - p0 + kAttnWaves - 1) / kAttnWaves) : 0;
+  const int32_t pid_raw = lane < np ? trow[p0 + (int64_t)kAttnWaves * lane] : 0;
+  const bool bad = lane < np && (pid_raw < 0 || pid_raw >= a.num_pages);
+  const uint32_t badmask = (uint32_t)__ballot(bad);
+  if (badmask && lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
+  const int32_t pid_v = bad ? 0 : pid_raw;
+  auto page_base = [&](int j) {
+    return ((int64_t)__builtin_amdgcn_readlane(pid_v, j) * kPageTokens * a.hkv + hk) * kRowBytes;
+  };
+  // Software pipeline: page j+1's K is loaded once the score MFMA has read
+  // page j's, and its V rows one by one as P V consumes page j's, into the
+  // same registers; the last page re-reads itself (cache hits).
+  bf16x8 ka[8];
+  u32x2 vr[kPageTokens];
+  if (np > 0) {
+    const int64_t base = page_base(0);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) ka[s] = __builtin_bit_cast(bf16x8, ld16(kp + (4 * s + g) * 16));
+    for (int s = 0; s < 8; ++s)
+      ka[s] = __builtin_bit_cast(bf16x8, ld16(a.k + base + n * tok_stride + (4 * s + g) * 16));
 #pragma unroll
     for (int t = 0; t < kPageTokens; ++t)
-      vr[t] = *reinterpret_cast<const u32x2*>(vp + t * tok_stride);
+      vr[t] = *reinterpret_cast<const u32x2*>(a.v + base + t * tok_stride + lane * 8);
+  }
+  for (int j = 0; j < np; ++j) {
+    const int64_t p = p0 + (int64_t)kAttnWaves * j;
+    const bool ok = ((badmask >> j) & 1u) == 0;
+    const int64_t nb = page_base(j + 1 < np ? j + 1 : j);
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], sc, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      ka[s] = __builtin_bit_cast(bf16x8, ld16(a.k + nb + n * tok_stride + (4 * s + g) * 16));
 
     // online softmax for head n over this page's tokens 4g .. 4g+3
     const int64_t tok0 = p * kPageTokens + 4 * g;
     float sv[4], pm = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sv[i] = tok0 + i < len ? sc[i] * a.scale_log2 : -INFINITY;
+      sv[i] = ok && tok0 + i < len ? sc[i] * a.scale_log2 : -INFINITY;
       pm = fmaxf(pm, sv[i]);
     }
     pm = fmaxf(pm, __shfl_xor(pm, 16));
     pm = fmaxf(pm, __shfl_xor(pm, 32));
-    const float m_new = fmaxf(m_run, pm);  // finite: a page holds at least one valid token
-    const float alpha = exp2_fast(m_run - m_new);
+    const float m_new = fmaxf(m_run, pm);
+    // -inf only while every page so far was masked: exponents then stay -inf
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_fast(m_run - m_ref);
     float pv[4], ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pv[i] = exp2_fast(sv[i] - m_new);
+      pv[i] = exp2_fast(sv[i] - m_ref);
       ps += pv[i];
     }
     ps += __shfl_xor(ps, 16);
@@ -173,12 +198,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     for (int h = 0; h < G; ++h) {
       const float al = al_lds[wave][h];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[h][j] *= al;
+      for (int jj = 0; jj < 4; ++jj) o[h][jj] *= al;
     }
 #pragma unroll
     for (int t = 0; t < kPageTokens; ++t) {
       const float v0 = bf16_lo(vr[t].x), v1 = bf16_hi(vr[t].x);
       const float v2 = bf16_lo(vr[t].y), v3 = bf16_hi(vr[t].y);
+      vr[t] = *reinterpret_cast<const u32x2*>(a.v + nb + t * tok_stride + lane * 8);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float pt = p_lds[wave][t][h];
@@ -226,42 +252,130 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
   }
 }
 
-// Merges the chunk states of sequences longer than one chunk.
+template <int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
+  static_assert(G >= 1 && G <= 8, "query heads per KV head");
+  __shared__ float p_lds[kAttnWaves][kPageTokens][16];  // [wave][token][head] probabilities
+  __shared__ float al_lds[kAttnWaves][16];              // [wave][head] rescale factor
+  __shared__ float m_w[kAttnWaves][G], l_w[kAttnWaves][G];
+  __shared__ __attribute__((aligned(16))) float o_w[kAttnWaves][G][kHeadDim];
+  __shared__ int32_t first[kMaxPairs + 1];  // first work item of each (sequence, KV head)
+  __shared__ int32_t wave_tot[kAttnWaves];
+  __shared__ int32_t item_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // chunk counts of all (sequence, KV head) pairs and their exclusive prefix,
+  // 256 pairs per round (one length load per thread and round)
+  int32_t total = 0;
+  for (int base = 0; base < a.pairs; base += kAttnThreads) {
+    const int pr = base + tid;
+    int32_t cnt = 0;
+    if (pr < a.pairs) {
+      const int64_t len = attn_len(a, pr / a.hkv, blockIdx.x == 0 && pr % a.hkv == 0);
+      cnt = (int32_t)(len == 0 ? 1 : (len + kChunk - 1) / kChunk);  // a zero-length pair zeroes its output
+    }
+    int32_t incl = cnt;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const int32_t o = __shfl_up(incl, dd);
+      if (lane >= dd) incl += o;
+    }
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int32_t at = total + incl - cnt, round = 0;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      at += w < wave ? wave_tot[w] : 0;
+      round += wave_tot[w];
+    }
+    if (pr < a.pairs) first[pr] = at;
+    total += round;
+    __syncthreads();  // wave_tot is rewritten by the next round
+  }
+  if (tid == 0) first[a.pairs] = total;
+  for (;;) {
+    __syncthreads();  // first[] written; the previous item's LDS reads done
+    if (tid == 0) item_sh = atomicAdd(a.queue, 1);
+    __syncthreads();
+    const int32_t item = item_sh;
+    if (item >= total || item < 0) break;  // uniform: every workgroup ends here
+    int lo = 0, hi = a.pairs - 1;  // the pair whose run of items holds `item`
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (first[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    const int64_t b = lo / a.hkv, hk = lo % a.hkv;
+    const int64_t len = attn_len(a, b, false);
+    attn_chunk<G>(a, b, hk, item - first[lo], len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w,
+                  l_w, o_w);
+  }
+  // the last workgroup out leaves the counters zero for the next call
+  if (tid == 0 && atomicAdd(a.queue + 1, 1) == (int)gridDim.x - 1) {
+    a.queue[0] = 0;
+    a.queue[1] = 0;
+  }
+}
+
+// Merges the chunk states of one (sequence, KV head, query head) of a
+// sequence longer than one chunk: the chunks' maximum by a block reduction,
+// then a thread per dim sums the rescaled partial rows (loads 8 chunks deep).
 template <int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
-  const int64_t b = blockIdx.x / a.hkv, hk = blockIdx.x % a.hkv;
+  __shared__ float red[kAttnWaves];
+  const int64_t pr = blockIdx.x / G;
+  const int h = blockIdx.x % G;
+  const int64_t b = pr / a.hkv;
   const int64_t len = attn_len(a, b, false);
   const int64_t nch = (len + kChunk - 1) / kChunk;
   if (nch <= 1) return;  // written by the chunk kernel
-  const int d = threadIdx.x;
-  uint8_t* out = a.out + (b * a.hkv + hk) * G * kRowBytes;
-  const int64_t at0 = (b * a.hkv + hk) * a.chunks * G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t at0 = pr * a.chunks * G + h;  // chunk c: at0 + c * G
+  float M = -INFINITY;
+  for (int64_t c = tid; c < nch; c += kAttnThreads) M = fmaxf(M, a.ml[(at0 + c * G) * 2]);
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float M = -INFINITY;
-    for (int64_t c = 0; c < nch; ++c) M = fmaxf(M, a.ml[(at0 + c * G + h) * 2]);
-    float O = 0.f, L = 0.f;
-    for (int64_t c = 0; c < nch; ++c) {
-      const int64_t at = at0 + c * G + h;
-      const float m = a.ml[at * 2];
-      const float f = m == -INFINITY ? 0.f : exp2_fast(m - M);
-      O += f * a.part[at * kHeadDim + d];
-      L += f * a.ml[at * 2 + 1];
-    }
-    reinterpret_cast<uint16_t*>(out + h * kRowBytes)[d] = f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, red[w]);
+  float O = 0.f, L = 0.f;
+#pragma unroll 8
+  for (int64_t c = 0; c < nch; ++c) {
+    const int64_t at = at0 + c * G;
+    const float m = ld_const(a.ml + at * 2);
+    const float f = m == -INFINITY ? 0.f : exp2_fast(m - M);
+    O += f * a.part[at * kHeadDim + tid];
+    L += f * ld_const(a.ml + at * 2 + 1);
   }
+  uint8_t* out = a.out + (pr * G + h) * kRowBytes;
+  reinterpret_cast<uint16_t*>(out)[tid] = f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
 }
 
 inline int64_t attn_chunks(int32_t max_seq_len) {
   return ((int64_t)max_seq_len + kChunk - 1) / kChunk;
 }
 
+// Workgroups of the chunk kernel: a few per CU drain the work list.
+int attn_grid() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev] * 4;
+}
+
 template <int G>
-void launch_attn(const AttnArgs& a, int64_t bh, hipStream_t st) {
-  hipLaunchKernelGGL(attn_chunk_kernel<G>, dim3((unsigned)(a.chunks > 0 ? a.chunks : 1), (unsigned)bh),
-                     dim3(kAttnThreads), 0, st, a);
+void launch_attn(const AttnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(attn_chunk_kernel<G>, dim3((unsigned)attn_grid()), dim3(kAttnThreads), 0, st,
+                     a);
   if (a.chunks > 1)
-    hipLaunchKernelGGL(attn_merge_kernel<G>, dim3((unsigned)bh), dim3(kAttnThreads), 0, st, a);
+    hipLaunchKernelGGL(attn_merge_kernel<G>, dim3((unsigned)(a.pairs * G)), dim3(kAttnThreads), 0,
+                       st, a);
 }
 
 }  // namespace
@@ -269,12 +383,13 @@ void launch_attn(const AttnArgs& a, int64_t bh, hipStream_t st) {
 
 using namespace mkv;
 
+constexpr int64_t kQueueBytes = 256;  // the work counters, at the workspace's start
+
 extern "C" int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t num_kv_heads,
                                                         int32_t num_q_heads, int32_t max_seq_len) {
   if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_seq_len < 0) return -1;
   const int64_t chunks = attn_chunks(max_seq_len);
-  if (chunks <= 1) return 0;
-  return (int64_t)batch * num_q_heads * chunks * (kHeadDim + 2) * 4;
+  return kQueueBytes + (chunks <= 1 ? 0 : (int64_t)batch * num_q_heads * chunks * (kHeadDim + 2) * 4);
 }
 
 extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
@@ -301,12 +416,13 @@ extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, con
               "mkv_decode_attention_bf16: null pointer");
   MKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
               MKV_E_ALIGN, "mkv_decode_attention_bf16: q, caches and out must be 16-byte aligned");
-  MKV_REQUIRE((int64_t)batch * num_kv_heads <= 65535, MKV_E_UNSUPPORTED,
-              "mkv_decode_attention_bf16: batch x KV heads above 65535");
+  MKV_REQUIRE((int64_t)batch * num_kv_heads <= kMaxPairs, MKV_E_UNSUPPORTED,
+              "mkv_decode_attention_bf16: batch x KV heads above %d", kMaxPairs);
+  MKV_REQUIRE(max_seq_len <= (1 << 24), MKV_E_UNSUPPORTED,
+              "mkv_decode_attention_bf16: max_seq_len above 2^24");
   const int64_t need = mkv_decode_attention_workspace_bytes(batch, num_kv_heads, num_q_heads,
                                                             max_seq_len);
-  MKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned16(workspace)),
-              MKV_E_INVALID,
+  MKV_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace), MKV_E_INVALID,
               "mkv_decode_attention_bf16: workspace of %lld bytes (16-byte aligned) required",
               (long long)need);
   AttnArgs a;
@@ -318,23 +434,24 @@ extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, con
   a.out = static_cast<uint8_t*>(out);
   const int64_t chunks = attn_chunks(max_seq_len);
   const int64_t part_floats = (int64_t)batch * num_q_heads * chunks * kHeadDim;
-  a.part = static_cast<float*>(workspace);
-  a.ml = need ? a.part + part_floats : nullptr;
+  a.queue = static_cast<int32_t*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kQueueBytes);
+  a.ml = a.part + part_floats;
   a.num_pages = num_pages;
   a.tstride = table_stride;
   a.twidth = table_width;
   a.hkv = num_kv_heads;
   a.chunks = (int32_t)chunks;
   a.max_len = max_seq_len;
+  a.pairs = (int32_t)((int64_t)batch * num_kv_heads);
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.err = err;
-  const int64_t bh = (int64_t)batch * num_kv_heads;
   const hipStream_t st = as_stream(stream);
   switch (G) {
-    case 1: launch_attn<1>(a, bh, st); break;
-    case 2: launch_attn<2>(a, bh, st); break;
-    case 4: launch_attn<4>(a, bh, st); break;
-    default: launch_attn<8>(a, bh, st); break;
+    case 1: launch_attn<1>(a, st); break;
+    case 2: launch_attn<2>(a, st); break;
+    case 4: launch_attn<4>(a, st); break;
+    default: launch_attn<8>(a, st); break;
   }
   return check_launch("mkv_decode_attention_bf16");
 }

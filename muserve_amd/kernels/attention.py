@@ -19,7 +19,7 @@ import torch
 from muserve_amd import _lib
 
 HEAD_DIM = 256
-CHUNK = 512  # tokens per workgroup of the kernel (sizes the workspace)
+CHUNK = 1024  # tokens per work item of the kernel (sizes the workspace)
 
 _errors: dict[torch.device, _lib.DeviceErrors] = {}
 _workspace: dict[torch.device, torch.Tensor] = {}
@@ -84,13 +84,14 @@ def attn_decode(
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     need = workspace_bytes(B, Hkv, Hq, max_seqlen)
     ws = _workspace.get(dev)
-    if need and (ws is None or ws.numel() < need):
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    if ws is None or ws.numel() < need:
+        # zero-filled once: the kernels keep its work counters at zero between calls
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         _workspace[dev] = ws
     # the workspace is reused by later calls on the stream: calls on one
     # device must be issued on one stream (or be ordered by the caller)
     _lib.call("mkv_decode_attention_bf16", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               P, Hkv, Hq, D, page_table.data_ptr(), page_table.stride(0), width,
               cache_seqlens.data_ptr(), B, max_seqlen, scale, out.data_ptr(),
-              _lib.ptr(ws) if need else None, need, _errword(dev).ptr(), _lib.stream_of(dev))
+              ws.data_ptr(), ws.numel(), _errword(dev).ptr(), _lib.stream_of(dev))
     return out

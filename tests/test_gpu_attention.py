@@ -6,8 +6,6 @@ rounds the result to bf16 once, so every output element is within one bf16
 ulp of the float64 result (ulp taken at |want|, floor 2^-20 near zero). The
 reference's own bf16 path (muserve/model/qwen35_layer_v2.py:493-502) is up to
 ~2 ulp off the same float64 result (tests/test_oracle_attention.py)."""
-import math
-
 import numpy as np
 import pytest
 import torch
@@ -62,7 +60,8 @@ def run(q, k, v, lens, table, max_seqlen=None, scale=None):
 
 @pytest.mark.parametrize("Hq,Hkv", [(4, 1), (1, 1), (2, 1), (8, 1), (4, 2), (8, 2)])
 def test_matches_oracle(Hq, Hkv):
-    lens = [1, 2, 15, 16, 17, 31, 33, 200, 511, 512, 513, 1000, 1024, 1500, 2049, 3000, 0, 7]
+    lens = [1, 2, 15, 16, 17, 31, 33, 200, 511, 512, 513, 1000, 1023, 1024, 1025, 1500, 2049, 3000,
+            4097, 0, 7]
     case(f"decode attention Hq={Hq} Hkv={Hkv} lens {lens}")
     q, k, v, lens, table = build(11 + Hq + 10 * Hkv, lens, Hq, Hkv)
     got, want = run(q, k, v, lens, table)
@@ -71,7 +70,7 @@ def test_matches_oracle(Hq, Hkv):
 
 def test_tight_bound_and_scale():
     lens = [300, 64, 511, 1]
-    case(f"decode attention, max_seqlen 512 (one chunk), scale 0.1, lens {lens}")
+    case(f"decode attention, max_seqlen 512 (no merge pass), scale 0.1, lens {lens}")
     q, k, v, lens, table = build(21, lens, 4, 1, width=100)
     got, want = run(q, k, v, lens, table, max_seqlen=512, scale=0.1)
     within_one_ulp(got, want)
