@@ -345,6 +345,26 @@ int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_
                               void* workspace, int64_t workspace_bytes, int32_t* err,
                               void* stream);
 
+/*
+ * The same over an fp8 pool, with the dequantisation fused: k_codes / v_codes
+ * are [num_pages, 16, num_kv_heads, 256] e4m3fn codes (16-byte aligned) and
+ * k_scales / v_scales the [num_pages, 16, num_kv_heads] fp32 scales that
+ * mkv_append_fp8 writes (4-byte aligned). A cached value is code * scale,
+ * exact in fp32 (gather_dequant's bf16 rounding is not applied): a token's
+ * score is scale_k * (q . codes) and its V weight p * scale_v. Same limits,
+ * workspace and error bits as mkv_decode_attention_bf16. Replaces the
+ * reference's decode read of the cache (muserve/kernels/attention.py:29-42,
+ * muserve/model/qwen35_layer_v2.py:493-502), which has no fp8 pool.
+ */
+int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_codes,
+                             const float* k_scales, const float* v_scales, int64_t num_pages,
+                             int32_t num_kv_heads, int32_t num_q_heads, int32_t head_dim,
+                             const int32_t* page_table, int64_t table_stride,
+                             int32_t table_width, const int32_t* seq_lens, int32_t batch,
+                             int32_t max_seq_len, float softmax_scale, void* out,
+                             void* workspace, int64_t workspace_bytes, int32_t* err,
+                             void* stream);
+
 /* ---- self-test ------------------------------------------------------------ */
 
 /*

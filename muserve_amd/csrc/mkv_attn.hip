@@ -31,6 +31,8 @@
 // whatever the lengths. The last workgroup out resets the counter.
 #include <math.h>
 
+#include <type_traits>
+
 #include "mkv_device.h"
 
 namespace mkv {
@@ -39,6 +41,7 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHeadDim = 256;
 constexpr int kRowBytes = kHeadDim * 2;  // one bf16 K or V row of one KV head
@@ -48,11 +51,17 @@ constexpr int kPageTokens = 16;
 constexpr int kChunk = 1024;  // tokens per work item (512 measured 3 % slower, 2048 4 %)
 constexpr int kChunkPages = kChunk / kPageTokens;
 constexpr int kMaxPairs = 4096;  // batch x KV heads whose chunk prefix fits in LDS
+constexpr int kPagesPerIter = 1;  // pages per wave iteration (2 measured 1.5 % slower on fp8)
+constexpr int kIterTokens = kPagesPerIter * kPageTokens;
+constexpr int kTailClasses = 32;  // length classes of the short chunks (32 tokens each)
+constexpr int kTailNone = 255;    // a pair without a short chunk
 
 struct AttnArgs {
   const uint8_t* q;  // [B, Hkv * G, 256] bf16
-  const uint8_t* k;  // [P, 16, Hkv, 256] bf16
+  const uint8_t* k;  // [P, 16, Hkv, 256] bf16, or e4m3fn codes
   const uint8_t* v;
+  const float* ks;   // fp8 caches: [P, 16, Hkv] fp32 scales of K and V
+  const float* vs;
   const int32_t* table;  // [B, tstride] int32
   const int32_t* lens;   // [B] int32
   uint8_t* out;          // [B, Hkv * G, 256] bf16
@@ -90,13 +99,31 @@ __device__ __forceinline__ int64_t attn_len(const AttnArgs& a, int64_t b, bool r
   return len;
 }
 
-template <int G>
+// Eight e4m3fn codes (little-endian bytes of lo, hi) as eight bf16: exact,
+// every e4m3fn value is a bf16 value.
+__device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
+  const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+  const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+  const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);
+  const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+  return bf16x8{(__bf16)a.x, (__bf16)a.y, (__bf16)b.x, (__bf16)b.y,
+                (__bf16)c.x, (__bf16)c.y, (__bf16)d.x, (__bf16)d.y};
+}
+
+// One 1024-token chunk of one (sequence, KV head). FP8: the caches hold
+// e4m3fn codes with an fp32 scale per (token, KV head); a token's score is
+// scale_k * (q . codes) and its V weight p * scale_v, so the codes convert
+// exactly to bf16 MFMA operands and no product is rounded before the fp32
+// accumulation.
+template <int G, bool FP8>
 __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t hk, int64_t c,
                                            int64_t len, int64_t nch,
-                                           float (&p_lds)[kAttnWaves][kPageTokens][16],
+                                           float (&p_lds)[kAttnWaves][kIterTokens][16],
                                            float (&al_lds)[kAttnWaves][16],
                                            float (&m_w)[kAttnWaves][G], float (&l_w)[kAttnWaves][G],
                                            float (&o_w)[kAttnWaves][G][kHeadDim]) {
+  constexpr int kCodeRow = FP8 ? kHeadDim : kRowBytes;  // bytes of one cached K or V row
+  constexpr int PPI = kPagesPerIter;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar page ids
   const int n = lane & 15, g = lane >> 4;
@@ -107,12 +134,17 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
     return;
   }
 
-  // the G query heads as the B operand, in the K rows' chunk order
+  // The G query heads as the B operand, in the K operand's dim order. Lane
+  // group g loads the 16-byte chunks 4r+g of a K row (a load instruction reads
+  // 64 contiguous bytes of each of the 16 rows): bf16, step s = r covers dims
+  // 8*(4s+g) .. +7; fp8, a chunk holds 16 codes, step s = 2r+h covers dims
+  // 16*(4r+g) + 8h .. +7, the q chunk 8r + 2g + h.
   bf16x8 qb[8];
   const uint8_t* qrow = a.q + ((b * a.hkv + hk) * G + (n < G ? n : 0)) * kRowBytes;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
-    const u32x4 w = n < G ? ld16(qrow + (4 * s + g) * 16) : u32x4{0u, 0u, 0u, 0u};
+    const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
+    const u32x4 w = n < G ? ld16(qrow + chunk * 16) : u32x4{0u, 0u, 0u, 0u};
     qb[s] = __builtin_bit_cast(bf16x8, w);
   }
   float m_run = -INFINITY, l_run = 0.f;  // head n
@@ -122,14 +154,14 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[h][j] = 0.f;
 
-  const int64_t tok_stride = (int64_t)a.hkv * kRowBytes;
+  const int64_t tok_stride = (int64_t)a.hkv * kCodeRow;
   const int64_t pages = (len + kPageTokens - 1) / kPageTokens;
   const int64_t p_end = (c + 1) * (int64_t)kChunkPages < pages ? (c + 1) * (int64_t)kChunkPages : pages;
   const int32_t* trow = a.table + b * a.tstride;
-  // This wave's pages are p0 + 4j: their ids in one load, lane j holding page
-  // j. A page id outside the pool is flagged and its tokens masked (page 0 is
-  // read in its place), so the loop below has no branches and the compiler's
-  // load counting stays exact.
+  // This wave's pages are p0 + 4q, q < np: their ids in one load, lane q
+  // holding page q. A page id outside the pool is flagged and its tokens
+  // masked (page 0 is read in its place), so the loop below has no branches
+  // and the compiler's load counting stays exact.
   static_assert(kChunkPages / kAttnWaves <= 32, "a wave's page validity fits a 32-bit mask");
   const int64_t p0 = c * (int64_t)kChunkPages + wave;
   const int np = p_end > p0 ? (int)((p_end - p0 + kAttnWaves - 1) / kAttnWaves) : 0;
@@ -138,41 +170,95 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   const uint32_t badmask = (uint32_t)__ballot(bad);
   if (badmask && lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
   const int32_t pid_v = bad ? 0 : pid_raw;
-  auto page_base = [&](int j) {
-    return ((int64_t)__builtin_amdgcn_readlane(pid_v, j) * kPageTokens * a.hkv + hk) * kRowBytes;
+  auto page_row = [&](int q) {  // page q's first (token, KV head) row; q >= np: page np-1
+    return (int64_t)__builtin_amdgcn_readlane(pid_v, q < np ? q : np - 1) * kPageTokens * a.hkv +
+           hk;
   };
-  // Software pipeline: page j+1's K is loaded once the score MFMA has read
-  // page j's, and its V rows one by one as P V consumes page j's, into the
-  // same registers; the last page re-reads itself (cache hits).
-  bf16x8 ka[8];
-  u32x2 vr[kPageTokens];
+  // Software pipeline over iterations of PPI pages: the next iteration's K
+  // (and scales) are loaded once the score MFMAs have read this one's, and its
+  // V rows one by one as P V consumes this one's, into the same registers.
+  // Past the wave's last page the loads repeat that page (cache hits) and the
+  // tokens are masked.
+  typedef typename std::conditional<FP8, u32x4, bf16x8>::type KReg;
+  typedef typename std::conditional<FP8, uint32_t, u32x2>::type VReg;
+  constexpr int kKRegs = FP8 ? 4 : 8;
+  KReg ka[PPI][kKRegs];
+  VReg vr[PPI][kPageTokens];
+  float sk[PPI][4], svs[PPI][4];  // fp8: scales of tokens 4g+i
+  auto load_k = [&](int u, int64_t row) {
+    const uint8_t* kp = a.k + row * kCodeRow + n * tok_stride;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ka[u][r] = ld16(kp + 16 * (4 * r + g));
+      // (one load and shuffles instead: 1 % faster, 18 more VGPRs)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sk[u][i] = a.ks[row + (int64_t)(4 * g + i) * a.hkv];
+        svs[u][i] = a.vs[row + (int64_t)(4 * g + i) * a.hkv];
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) ka[u][s] = __builtin_bit_cast(bf16x8, ld16(kp + (4 * s + g) * 16));
+    }
+  };
+  auto load_v = [&](int u, int64_t row, int t) {
+    const uint8_t* vp = a.v + row * kCodeRow + t * tok_stride;
+    if constexpr (FP8)
+      vr[u][t] = *reinterpret_cast<const uint32_t*>(vp + lane * 4);
+    else
+      vr[u][t] = *reinterpret_cast<const u32x2*>(vp + lane * 8);
+  };
   if (np > 0) {
-    const int64_t base = page_base(0);
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      ka[s] = __builtin_bit_cast(bf16x8, ld16(a.k + base + n * tok_stride + (4 * s + g) * 16));
+    for (int u = 0; u < PPI; ++u) {
+      const int64_t row = page_row(u);
+      load_k(u, row);
 #pragma unroll
-    for (int t = 0; t < kPageTokens; ++t)
-      vr[t] = *reinterpret_cast<const u32x2*>(a.v + base + t * tok_stride + lane * 8);
+      for (int t = 0; t < kPageTokens; ++t) load_v(u, row, t);
+    }
   }
-  for (int j = 0; j < np; ++j) {
-    const int64_t p = p0 + (int64_t)kAttnWaves * j;
-    const bool ok = ((badmask >> j) & 1u) == 0;
-    const int64_t nb = page_base(j + 1 < np ? j + 1 : j);
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+  for (int q0 = 0; q0 < np; q0 += PPI) {
+    int64_t nrow[PPI];
+    f32x4 sc[PPI];
+    float skj[PPI][4], svj[PPI][4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qb[s], sc, 0, 0, 0);
+    for (int u = 0; u < PPI; ++u) {
+      nrow[u] = page_row(q0 + PPI + u);
+      sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (FP8) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      ka[s] = __builtin_bit_cast(bf16x8, ld16(a.k + nb + n * tok_stride + (4 * s + g) * 16));
+        for (int r = 0; r < 4; ++r) {
+          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].x, ka[u][r].y),
+                                                          qb[2 * r], sc[u], 0, 0, 0);
+          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].z, ka[u][r].w),
+                                                          qb[2 * r + 1], sc[u], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          skj[u][i] = sk[u][i];
+          svj[u][i] = svs[u][i];
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[u][s], qb[s], sc[u], 0, 0, 0);
+      }
+      load_k(u, nrow[u]);
+    }
 
-    // online softmax for head n over this page's tokens 4g .. 4g+3
-    const int64_t tok0 = p * kPageTokens + 4 * g;
-    float sv[4], pm = -INFINITY;
+    // online softmax for head n over this iteration's tokens 16u + 4g + i
+    float sv[PPI][4], pm = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[i] = ok && tok0 + i < len ? sc[i] * a.scale_log2 : -INFINITY;
-      pm = fmaxf(pm, sv[i]);
+    for (int u = 0; u < PPI; ++u) {
+      const int q = q0 + u;
+      const bool ok = q < np && ((badmask >> q) & 1u) == 0;
+      const int64_t tok0 = (p0 + (int64_t)kAttnWaves * q) * kPageTokens + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float score = FP8 ? sc[u][i] * skj[u][i] : sc[u][i];
+        sv[u][i] = ok && tok0 + i < len ? score * a.scale_log2 : -INFINITY;
+        pm = fmaxf(pm, sv[u][i]);
+      }
     }
     pm = fmaxf(pm, __shfl_xor(pm, 16));
     pm = fmaxf(pm, __shfl_xor(pm, 32));
@@ -180,18 +266,19 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
     // -inf only while every page so far was masked: exponents then stay -inf
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = exp2_fast(m_run - m_ref);
-    float pv[4], ps = 0.f;
+    float ps = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pv[i] = exp2_fast(sv[i] - m_ref);
-      ps += pv[i];
-    }
+    for (int u = 0; u < PPI; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = exp2_fast(sv[u][i] - m_ref);
+        ps += pv;
+        p_lds[wave][16 * u + 4 * g + i][n] = FP8 ? pv * svj[u][i] : pv;
+      }
     ps += __shfl_xor(ps, 16);
     ps += __shfl_xor(ps, 32);
     l_run = l_run * alpha + ps;
     m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p_lds[wave][4 * g + i][n] = pv[i];
     if (g == 0) al_lds[wave][n] = alpha;
     wave_sync();
 #pragma unroll
@@ -201,20 +288,34 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
       for (int jj = 0; jj < 4; ++jj) o[h][jj] *= al;
     }
 #pragma unroll
-    for (int t = 0; t < kPageTokens; ++t) {
-      const float v0 = bf16_lo(vr[t].x), v1 = bf16_hi(vr[t].x);
-      const float v2 = bf16_lo(vr[t].y), v3 = bf16_hi(vr[t].y);
-      vr[t] = *reinterpret_cast<const u32x2*>(a.v + nb + t * tok_stride + lane * 8);
+    for (int u = 0; u < PPI; ++u)
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float pt = p_lds[wave][t][h];
-        o[h][0] += pt * v0;
-        o[h][1] += pt * v1;
-        o[h][2] += pt * v2;
-        o[h][3] += pt * v3;
+      for (int t = 0; t < kPageTokens; ++t) {
+        float v0, v1, v2, v3;
+        if constexpr (FP8) {
+          const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[u][t], false);
+          const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[u][t], true);
+          v0 = lo.x;
+          v1 = lo.y;
+          v2 = hi.x;
+          v3 = hi.y;
+        } else {
+          v0 = bf16_lo(vr[u][t].x);
+          v1 = bf16_hi(vr[u][t].x);
+          v2 = bf16_lo(vr[u][t].y);
+          v3 = bf16_hi(vr[u][t].y);
+        }
+        load_v(u, nrow[u], t);
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float pt = p_lds[wave][16 * u + t][h];
+          o[h][0] += pt * v0;
+          o[h][1] += pt * v1;
+          o[h][2] += pt * v2;
+          o[h][3] += pt * v3;
+        }
       }
-    }
-    wave_sync();  // the next page rewrites this wave's tiles
+    wave_sync();  // the next iteration rewrites this wave's tiles
   }
 
   // merge the waves' (max, sum, output) per head
@@ -252,26 +353,43 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   }
 }
 
-template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
+template <int G, bool FP8>
+// two workgroups per CU: without the bound the G = 8 kernels take 256 VGPRs
+// plus accumulation registers, one wave per SIMD
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
-  __shared__ float p_lds[kAttnWaves][kPageTokens][16];  // [wave][token][head] probabilities
+  __shared__ float p_lds[kAttnWaves][kIterTokens][16];  // [wave][token][head] probabilities
   __shared__ float al_lds[kAttnWaves][16];              // [wave][head] rescale factor
   __shared__ float m_w[kAttnWaves][G], l_w[kAttnWaves][G];
   __shared__ __attribute__((aligned(16))) float o_w[kAttnWaves][G][kHeadDim];
-  __shared__ int32_t first[kMaxPairs + 1];  // first work item of each (sequence, KV head)
+  // The work list, the same in every workgroup: first the full 1024-token
+  // chunks of all (sequence, KV head) pairs, pair-major, then each pair's
+  // last, shorter chunk (or the zeros of an empty pair) with the longest
+  // first, so that the short items fill the end of the launch.
+  __shared__ int32_t first[kMaxPairs + 1];  // first full-chunk item of each pair
+  __shared__ int32_t tail_pair[kMaxPairs];  // pairs with a short chunk, longest first
+  __shared__ uint8_t tail_key[kMaxPairs];   // its length class, or kTailNone
+  __shared__ int32_t class_at[kTailClasses];         // next free slot of each class
+  __shared__ int32_t class_wave[kAttnWaves][kTailClasses];
   __shared__ int32_t wave_tot[kAttnWaves];
   __shared__ int32_t item_sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // chunk counts of all (sequence, KV head) pairs and their exclusive prefix,
-  // 256 pairs per round (one length load per thread and round)
+  if (tid < kTailClasses) class_at[tid] = 0;
+  __syncthreads();
+  // pass 1, 256 pairs per round: full-chunk counts and their exclusive
+  // prefix, the short chunk's class and the class sizes
   int32_t total = 0;
   for (int base = 0; base < a.pairs; base += kAttnThreads) {
     const int pr = base + tid;
     int32_t cnt = 0;
     if (pr < a.pairs) {
       const int64_t len = attn_len(a, pr / a.hkv, blockIdx.x == 0 && pr % a.hkv == 0);
-      cnt = (int32_t)(len == 0 ? 1 : (len + kChunk - 1) / kChunk);  // a zero-length pair zeroes its output
+      cnt = (int32_t)(len / kChunk);
+      const int32_t rem = (int32_t)(len % kChunk);
+      const bool tail = rem != 0 || len == 0;  // an empty pair still zeroes its output
+      const int key = tail ? kTailClasses - 1 - rem / (kChunk / kTailClasses) : kTailNone;
+      tail_key[pr] = (uint8_t)key;
+      if (tail) atomicAdd(&class_at[key], 1);
     }
     int32_t incl = cnt;
 #pragma unroll
@@ -291,22 +409,75 @@ __global__ __launch_bounds__(kAttnThreads) void attn_chunk_kernel(AttnArgs a) {
     total += round;
     __syncthreads();  // wave_tot is rewritten by the next round
   }
-  if (tid == 0) first[a.pairs] = total;
+  const int32_t total_full = total;
+  // class sizes -> their first slots (exclusive scan of 32 counts in wave 0)
+  if (wave == 0) {
+    const int32_t n_c = lane < kTailClasses ? class_at[lane] : 0;
+    int32_t incl = n_c;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const int32_t o = __shfl_up(incl, dd);
+      if (lane >= dd) incl += o;
+    }
+    if (lane < kTailClasses) class_at[lane] = incl - n_c;
+    if (lane == 63) item_sh = incl;  // number of short chunks
+  }
+  __syncthreads();
+  const int32_t n_tail = __builtin_amdgcn_readfirstlane(item_sh);
+  // pass 2: each short chunk's slot, stable by pair index within its class
+  for (int base = 0; base < a.pairs; base += kAttnThreads) {
+    const int pr = base + tid;
+    const int key = pr < a.pairs ? tail_key[pr] : kTailNone;
+    int my_rank = 0;
+    for (int c = 0; c < kTailClasses; ++c) {
+      const uint64_t m = __ballot(key == c);
+      if (key == c) my_rank = __popcll(m & ((1ull << lane) - 1));
+      if (lane == 0) class_wave[wave][c] = __popcll(m);
+    }
+    __syncthreads();
+    if (key != kTailNone) {
+      int32_t slot = class_at[key] + my_rank;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) slot += w < wave ? class_wave[w][key] : 0;
+      tail_pair[slot] = pr;
+    }
+    __syncthreads();  // class_at and class_wave are updated below / rewritten next round
+    if (tid < kTailClasses) {
+      int32_t add = 0;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) add += class_wave[w][tid];
+      class_at[tid] += add;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) first[a.pairs] = total_full;
   for (;;) {
-    __syncthreads();  // first[] written; the previous item's LDS reads done
+    __syncthreads();  // the lists written; the previous item's LDS reads done
     if (tid == 0) item_sh = atomicAdd(a.queue, 1);
     __syncthreads();
-    const int32_t item = item_sh;
-    if (item >= total || item < 0) break;  // uniform: every workgroup ends here
-    int lo = 0, hi = a.pairs - 1;  // the pair whose run of items holds `item`
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (first[mid] <= item) lo = mid; else hi = mid - 1;
+    // work-item values are uniform: scalar registers (readfirstlane)
+    const int32_t item = __builtin_amdgcn_readfirstlane(item_sh);
+    if (item >= total_full + n_tail || item < 0) break;  // uniform: every workgroup ends here
+    int32_t pair, c;
+    if (item < total_full) {  // the last pair whose full chunks start at or before `item`
+      int lo = 0, hi = a.pairs - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (first[mid] <= item) lo = mid; else hi = mid - 1;
+      }
+      pair = lo;
+      c = item - first[lo];
+    } else {
+      pair = tail_pair[item - total_full];
+      c = -1;  // the pair's last chunk, index len / kChunk
     }
-    const int64_t b = lo / a.hkv, hk = lo % a.hkv;
+    pair = __builtin_amdgcn_readfirstlane(pair);
+    c = __builtin_amdgcn_readfirstlane(c);
+    const int64_t b = pair / a.hkv, hk = pair % a.hkv;
     const int64_t len = attn_len(a, b, false);
-    attn_chunk<G>(a, b, hk, item - first[lo], len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w,
-                  l_w, o_w);
+    if (c < 0) c = (int32_t)(len / kChunk);
+    attn_chunk<G, FP8>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w, l_w,
+                       o_w);
   }
   // the last workgroup out leaves the counters zero for the next call
   if (tid == 0 && atomicAdd(a.queue + 1, 1) == (int)gridDim.x - 1) {
@@ -369,10 +540,10 @@ int attn_grid() {
   return cus[dev] * 4;
 }
 
-template <int G>
+template <int G, bool FP8>
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(attn_chunk_kernel<G>, dim3((unsigned)attn_grid()), dim3(kAttnThreads), 0, st,
-                     a);
+  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8>), dim3((unsigned)attn_grid()), dim3(kAttnThreads), 0,
+                     st, a);
   if (a.chunks > 1)
     hipLaunchKernelGGL(attn_merge_kernel<G>, dim3((unsigned)(a.pairs * G)), dim3(kAttnThreads), 0,
                        st, a);
@@ -392,43 +563,48 @@ extern "C" int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t n
   return kQueueBytes + (chunks <= 1 ? 0 : (int64_t)batch * num_q_heads * chunks * (kHeadDim + 2) * 4);
 }
 
-extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
-                                         int64_t num_pages, int32_t num_kv_heads,
-                                         int32_t num_q_heads, int32_t head_dim,
-                                         const int32_t* page_table, int64_t table_stride,
-                                         int32_t table_width, const int32_t* seq_lens,
-                                         int32_t batch, int32_t max_seq_len, float softmax_scale,
-                                         void* out, void* workspace, int64_t workspace_bytes,
-                                         int32_t* err, void* stream) {
+namespace {
+
+// Shared by both entry points: `fn` names the caller in error messages; the
+// scale planes are null for bf16 caches.
+int decode_attention(const char* fn, bool fp8, const void* q, const void* k_cache,
+                     const void* v_cache, const float* k_scales, const float* v_scales,
+                     int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
+                     int32_t head_dim, const int32_t* page_table, int64_t table_stride,
+                     int32_t table_width, const int32_t* seq_lens, int32_t batch,
+                     int32_t max_seq_len, float softmax_scale, void* out, void* workspace,
+                     int64_t workspace_bytes, int32_t* err, void* stream) {
   clear_error();
   MKV_REQUIRE(batch >= 0 && num_pages > 0 && num_kv_heads > 0 && num_q_heads > 0 &&
                   table_width >= 0 && table_stride >= table_width && max_seq_len >= 0,
-              MKV_E_INVALID, "mkv_decode_attention_bf16: bad sizes");
-  MKV_REQUIRE(head_dim == kHeadDim, MKV_E_UNSUPPORTED,
-              "mkv_decode_attention_bf16: head_dim %d unsupported (256)", head_dim);
+              MKV_E_INVALID, "%s: bad sizes", fn);
+  MKV_REQUIRE(head_dim == kHeadDim, MKV_E_UNSUPPORTED, "%s: head_dim %d unsupported (256)", fn,
+              head_dim);
   const int32_t G = num_q_heads / num_kv_heads;
   MKV_REQUIRE(G * num_kv_heads == num_q_heads && (G == 1 || G == 2 || G == 4 || G == 8),
-              MKV_E_UNSUPPORTED,
-              "mkv_decode_attention_bf16: %d query heads per KV head unsupported (1, 2, 4, 8)",
+              MKV_E_UNSUPPORTED, "%s: %d query heads per KV head unsupported (1, 2, 4, 8)", fn,
               num_q_heads / num_kv_heads);
   if (batch == 0) return MKV_OK;
-  MKV_REQUIRE(q && k_cache && v_cache && page_table && seq_lens && out && err, MKV_E_INVALID,
-              "mkv_decode_attention_bf16: null pointer");
+  MKV_REQUIRE(q && k_cache && v_cache && page_table && seq_lens && out && err &&
+                  (!fp8 || (k_scales && v_scales)),
+              MKV_E_INVALID, "%s: null pointer", fn);
   MKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
-              MKV_E_ALIGN, "mkv_decode_attention_bf16: q, caches and out must be 16-byte aligned");
+              MKV_E_ALIGN, "%s: q, caches and out must be 16-byte aligned", fn);
+  MKV_REQUIRE(!fp8 || (aligned4(k_scales) && aligned4(v_scales)), MKV_E_ALIGN,
+              "%s: scale planes must be 4-byte aligned", fn);
   MKV_REQUIRE((int64_t)batch * num_kv_heads <= kMaxPairs, MKV_E_UNSUPPORTED,
-              "mkv_decode_attention_bf16: batch x KV heads above %d", kMaxPairs);
-  MKV_REQUIRE(max_seq_len <= (1 << 24), MKV_E_UNSUPPORTED,
-              "mkv_decode_attention_bf16: max_seq_len above 2^24");
+              "%s: batch x KV heads above %d", fn, kMaxPairs);
+  MKV_REQUIRE(max_seq_len <= (1 << 24), MKV_E_UNSUPPORTED, "%s: max_seq_len above 2^24", fn);
   const int64_t need = mkv_decode_attention_workspace_bytes(batch, num_kv_heads, num_q_heads,
                                                             max_seq_len);
   MKV_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace), MKV_E_INVALID,
-              "mkv_decode_attention_bf16: workspace of %lld bytes (16-byte aligned) required",
-              (long long)need);
+              "%s: workspace of %lld bytes (16-byte aligned) required", fn, (long long)need);
   AttnArgs a;
   a.q = static_cast<const uint8_t*>(q);
   a.k = static_cast<const uint8_t*>(k_cache);
   a.v = static_cast<const uint8_t*>(v_cache);
+  a.ks = k_scales;
+  a.vs = v_scales;
   a.table = page_table;
   a.lens = seq_lens;
   a.out = static_cast<uint8_t*>(out);
@@ -447,11 +623,51 @@ extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, con
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.err = err;
   const hipStream_t st = as_stream(stream);
-  switch (G) {
-    case 1: launch_attn<1>(a, st); break;
-    case 2: launch_attn<2>(a, st); break;
-    case 4: launch_attn<4>(a, st); break;
-    default: launch_attn<8>(a, st); break;
+  if (fp8) {
+    switch (G) {
+      case 1: launch_attn<1, true>(a, st); break;
+      case 2: launch_attn<2, true>(a, st); break;
+      case 4: launch_attn<4, true>(a, st); break;
+      default: launch_attn<8, true>(a, st); break;
+    }
+  } else {
+    switch (G) {
+      case 1: launch_attn<1, false>(a, st); break;
+      case 2: launch_attn<2, false>(a, st); break;
+      case 4: launch_attn<4, false>(a, st); break;
+      default: launch_attn<8, false>(a, st); break;
+    }
   }
-  return check_launch("mkv_decode_attention_bf16");
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
+                                         int64_t num_pages, int32_t num_kv_heads,
+                                         int32_t num_q_heads, int32_t head_dim,
+                                         const int32_t* page_table, int64_t table_stride,
+                                         int32_t table_width, const int32_t* seq_lens,
+                                         int32_t batch, int32_t max_seq_len, float softmax_scale,
+                                         void* out, void* workspace, int64_t workspace_bytes,
+                                         int32_t* err, void* stream) {
+  return decode_attention("mkv_decode_attention_bf16", false, q, k_cache, v_cache, nullptr,
+                          nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
+                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
+                          out, workspace, workspace_bytes, err, stream);
+}
+
+extern "C" int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_codes,
+                                        const float* k_scales, const float* v_scales,
+                                        int64_t num_pages, int32_t num_kv_heads,
+                                        int32_t num_q_heads, int32_t head_dim,
+                                        const int32_t* page_table, int64_t table_stride,
+                                        int32_t table_width, const int32_t* seq_lens,
+                                        int32_t batch, int32_t max_seq_len, float softmax_scale,
+                                        void* out, void* workspace, int64_t workspace_bytes,
+                                        int32_t* err, void* stream) {
+  return decode_attention("mkv_decode_attention_fp8", true, q, k_codes, v_codes, k_scales,
+                          v_scales, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
+                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
+                          out, workspace, workspace_bytes, err, stream);
 }

@@ -60,15 +60,49 @@ def attn_decode(
     """``max_seqlen`` bounds ``cache_seqlens`` (default: what the page table
     holds) and sizes the launch; a tighter bound launches fewer empty
     workgroups. ``out`` may be given to write in place."""
+    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
+        raise TypeError("attn_decode takes bf16 caches (attn_decode_fp8 reads fp8 ones)")
+    return _decode("mkv_decode_attention_bf16", q, k_cache, v_cache, None, None, cache_seqlens,
+                   page_table, softmax_scale, max_seqlen, out)
+
+
+def attn_decode_fp8(
+    q: torch.Tensor,                    # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16
+    k_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] e4m3fn
+    v_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] e4m3fn
+    k_scales: torch.Tensor,             # [num_pages, PAGE_SIZE, NUM_KV_HEADS] fp32
+    v_scales: torch.Tensor,             # [num_pages, PAGE_SIZE, NUM_KV_HEADS] fp32
+    cache_seqlens: torch.Tensor,
+    page_table: torch.Tensor | None,
+    softmax_scale: float | None = None,
+    *,
+    max_seqlen: int | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:                      # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16
+    """``attn_decode`` over an fp8 pool (codes plus one fp32 scale per token and
+    KV head, as ``PagedKVCache`` appends them), with the dequantisation fused:
+    a cached value is ``code * scale`` taken exactly (in fp32), not rounded to
+    bf16 first as ``gather``'s dequantisation does. Same arguments otherwise."""
+    if k_cache.dtype != torch.float8_e4m3fn or v_cache.dtype != torch.float8_e4m3fn:
+        raise TypeError("attn_decode_fp8 takes float8_e4m3fn caches")
+    for name, s in (("k_scales", k_scales), ("v_scales", v_scales)):
+        if s.dtype != torch.float32 or s.shape != k_cache.shape[:3] or not s.is_contiguous():
+            raise ValueError(f"{name} must be contiguous fp32 {tuple(k_cache.shape[:3])}")
+    return _decode("mkv_decode_attention_fp8", q, k_cache, v_cache, k_scales, v_scales,
+                   cache_seqlens, page_table, softmax_scale, max_seqlen, out)
+
+
+def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_table,
+            softmax_scale, max_seqlen, out):
     if page_table is None:
         raise ValueError("attn_decode reads the paged pool: page_table is required")
-    dev = _lib.require_gpu(q, k_cache, v_cache, cache_seqlens, page_table)
+    dev = _lib.require_gpu(q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_table)
     B, one, Hq, D = q.shape
     P, page, Hkv, Dk = k_cache.shape
     if one != 1 or page != 16 or D != HEAD_DIM or Dk != D or v_cache.shape != k_cache.shape:
         raise ValueError(f"unsupported shapes q {tuple(q.shape)}, cache {tuple(k_cache.shape)}")
-    if q.dtype != torch.bfloat16 or k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise TypeError("attn_decode takes bf16 q and caches")
+    if q.dtype != torch.bfloat16:
+        raise TypeError("attn_decode takes a bf16 query")
     if cache_seqlens.dtype != torch.int32 or page_table.dtype != torch.int32:
         raise TypeError("cache_seqlens and page_table must be int32")
     if not (q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()
@@ -90,7 +124,8 @@ def attn_decode(
         _workspace[dev] = ws
     # the workspace is reused by later calls on the stream: calls on one
     # device must be issued on one stream (or be ordered by the caller)
-    _lib.call("mkv_decode_attention_bf16", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+    scales = () if k_scales is None else (k_scales.data_ptr(), v_scales.data_ptr())
+    _lib.call(fn, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *scales,
               P, Hkv, Hq, D, page_table.data_ptr(), page_table.stride(0), width,
               cache_seqlens.data_ptr(), B, max_seqlen, scale, out.data_ptr(),
               ws.data_ptr(), ws.numel(), _errword(dev).ptr(), _lib.stream_of(dev))

@@ -12,13 +12,21 @@ muserve's decode attention for one query token per sequence:
 `decode_attention` evaluates that in float64 (numpy) from the pages the
 table names; `reference_bf16` runs the contiguous path as written, in torch
 bf16 on the CPU, on K/V gathered from the same pages.
+
+The reference has no fp8 pool. Over one, the fused decode reads a cached
+value as code * scale, taken exactly: `dequant_exact` gives those values
+(e4m3fn codes decoded by their OCP definition, fp8.e4m3fn_value) for
+`decode_attention` to attend over.
 """
 from __future__ import annotations
 
 import numpy as np
 import torch
 
+from oracle.fp8 import e4m3fn_value
+
 PAGE = 16
+_E4M3FN = np.array([e4m3fn_value(c) for c in range(256)])
 
 
 def gather_kv(cache: np.ndarray, table_row: np.ndarray, length: int) -> np.ndarray:
@@ -28,26 +36,49 @@ def gather_kv(cache: np.ndarray, table_row: np.ndarray, length: int) -> np.ndarr
     return cache[pages].reshape(-1, *cache.shape[2:])[:length]
 
 
+def dequant_exact(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """uint8 e4m3fn codes [..., D] and fp32 scales [...] -> float64
+    value(code) * scale [..., D], not rounded (fp8.dequant_rows rounds to bf16)."""
+    codes = np.asarray(codes, dtype=np.uint8)
+    return _E4M3FN[codes] * np.asarray(scales, dtype=np.float64)[..., None]
+
+
 def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
-                     seq_lens: np.ndarray, page_table: np.ndarray, scale: float) -> np.ndarray:
+                     seq_lens: np.ndarray, page_table: np.ndarray, scale: float,
+                     k_scales: np.ndarray | None = None,
+                     v_scales: np.ndarray | None = None, stats: bool = False):
     """q [B,Hq,D], caches [P,16,Hkv,D] (any float dtype; computed in float64),
-    seq_lens [B], page_table [B,W] -> [B,Hq,D] float64. Length 0 -> zeros."""
+    seq_lens [B], page_table [B,W] -> [B,Hq,D] float64. Length 0 -> zeros.
+    With k_scales / v_scales ([P,16,Hkv] fp32) the caches are uint8 e4m3fn
+    codes, read as dequant_exact values. stats=True also returns the attended
+    mass sum_j p_j |v_j| / sum_j p_j [B,Hq,D] and max_j |score_j| [B,Hq]
+    (what a float evaluation's rounding error scales with)."""
     q = np.asarray(q, dtype=np.float64)
     B, Hq, D = q.shape
     Hkv = k_cache.shape[2]
     G = Hq // Hkv
     out = np.zeros((B, Hq, D))
+    mass = np.zeros((B, Hq, D))
+    smax = np.zeros((B, Hq))
     for b in range(B):
         n = int(seq_lens[b])
         if n == 0:
             continue
-        K = gather_kv(k_cache, page_table[b], n).astype(np.float64)  # [n, Hkv, D]
-        V = gather_kv(v_cache, page_table[b], n).astype(np.float64)
+        K = gather_kv(k_cache, page_table[b], n)  # [n, Hkv, D]
+        V = gather_kv(v_cache, page_table[b], n)
+        if k_scales is not None:
+            K = dequant_exact(K, gather_kv(k_scales, page_table[b], n))
+            V = dequant_exact(V, gather_kv(v_scales, page_table[b], n))
+        K = K.astype(np.float64)
+        V = V.astype(np.float64)
         for h in range(Hq):
             s = K[:, h // G] @ q[b, h] * scale
             p = np.exp(s - s.max())
             out[b, h] = (p / p.sum()) @ V[:, h // G]
-    return out
+            if stats:
+                mass[b, h] = (p / p.sum()) @ np.abs(V[:, h // G])
+                smax[b, h] = np.abs(s).max()
+    return (out, mass, smax) if stats else out
 
 
 def reference_bf16(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

@@ -99,3 +99,41 @@ def test_reference_bf16_formula_is_within_bf16_rounding():
                                 lens, table, 256 ** -0.5)
     err = np.abs(got - want)
     assert err.max() < 0.05 and np.median(err) < 0.005, (err.max(), np.median(err))
+
+
+def test_dequant_exact_against_torch_and_bf16_dequant():
+    # every code, scales across 2^-20 .. 2^10: the values torch's e4m3fn decode
+    # times the fp32 scale gives (exact in float64), and bf16(value) is what
+    # fp8.dequant_rows writes
+    from oracle import fp8
+    codes = np.tile(np.arange(256, dtype=np.uint8), (31, 1))
+    codes[:, 0x7F] = codes[:, 0xFF] = 0  # leave out the NaN codes
+    scales = (2.0 ** np.linspace(-20, 10, 31)).astype(np.float32) * np.float32(1.37)
+    got = att.dequant_exact(codes, scales)
+    t_codes = torch.from_numpy(codes).view(torch.float8_e4m3fn)
+    want = t_codes.double() * torch.from_numpy(scales).double()[:, None]
+    np.testing.assert_array_equal(got, want.numpy())
+    bf = fp8.dequant_rows(torch.from_numpy(codes), torch.from_numpy(scales))
+    np.testing.assert_array_equal(torch.from_numpy(got).bfloat16().float().numpy(), bf.float().numpy())
+    assert got[3, 0x80] == 0.0 and np.signbit(got[3, 0x80])  # negative zero stays negative
+
+
+def test_fp8_attention_close_to_bf16_attention():
+    # quantising K/V per row (absmax / 448) moves the output by the fp8
+    # rounding only: a 3-bit mantissa, relative error 2^-4 per element at most
+    rng = np.random.default_rng(8)
+    q, k, v, lens, table = make_case(rng, [1, 40, 333], Hq=4, Hkv=1, D=256)
+    from oracle import fp8
+    kc, ks = fp8.quantize_rows(torch.from_numpy(k))
+    vc, vs = fp8.quantize_rows(torch.from_numpy(v))
+    kd = att.dequant_exact(kc.numpy(), ks.numpy())
+    vd = att.dequant_exact(vc.numpy(), vs.numpy())
+    assert np.abs(kd - k).max() <= np.abs(k).max() * 2.0 ** -4
+    exact = att.decode_attention(q, k, v, lens, table, 256 ** -0.5)
+    quant = att.decode_attention(q, kd, vd, lens, table, 256 ** -0.5)
+    # the codes-and-scales form dequantises the same way, sequence by sequence
+    np.testing.assert_array_equal(
+        att.decode_attention(q, kc.numpy(), vc.numpy(), lens, table, 256 ** -0.5,
+                             ks.numpy(), vs.numpy()), quant)
+    assert np.abs(quant - exact).max() < 0.1
+    assert np.abs(quant - exact).mean() < 0.01
