@@ -205,6 +205,40 @@ int mkv_state_scatter(void* pool0, int64_t entry_bytes0, const void* in0,
                       int64_t pool_slots, const int32_t* slots, int32_t n,
                       int32_t* err, void* stream);
 
+/* ---- host tier: layered block pack / unpack ------------------------------ */
+
+/*
+ * A layered pool holds num_planes planes, plane z starting at
+ * pool + z * plane_stride, each an array of pool_blocks blocks of block_bytes.
+ * Examples:
+ *   - a KV pool [L,2,P,16,H,D]: planes are the L x 2 K|V planes and blocks are
+ *     pages (block_bytes = 16*H*D*elem);
+ *   - its fp8 scales: 64-byte blocks;
+ *   - a GDN state pool: planes are layers and blocks are request slots.
+ * Pack copies blocks ids[0..n) of every plane into out, plane-major:
+ *   out[(z*n + i)*block_bytes ..] = plane z's block ids[i].
+ * Unpack is the inverse (ids unique within a call).
+ * out / in may be pinned host memory (hipHostMalloc, torch pin_memory): the
+ * kernel then reads or writes it across the host link directly, with no
+ * staging copy.
+ * Replaces PrefixCache._to_storage / _to_device
+ * (muserve/model/prefix_cache.py:36-44: tensor.cpu(), .to(device,
+ * non_blocking=True)) for state kept in this build's pools, and caches KV
+ * pages, which the reference does not.
+ * Requirements (otherwise MKV_E_INVALID / MKV_E_ALIGN):
+ *   - pool, out/in, block_bytes and plane_stride are 16-byte aligned;
+ *   - plane_stride >= pool_blocks * block_bytes when num_planes > 1;
+ *   - 1 <= num_planes <= 65535.
+ * An id outside [0, pool_blocks) sets MKV_DEVERR_STATE_SLOT. Pack writes
+ * zeros for it; unpack skips it.
+ */
+int mkv_pack_blocks(const void* pool, int64_t plane_stride, int32_t num_planes,
+                    int64_t block_bytes, int64_t pool_blocks, const int32_t* ids, int32_t n,
+                    void* out, int32_t* err, void* stream);
+int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                      int64_t block_bytes, int64_t pool_blocks, const int32_t* ids, int32_t n,
+                      const void* in, int32_t* err, void* stream);
+
 /* ---- prefix hashing ------------------------------------------------------ */
 
 /*

@@ -1,4 +1,5 @@
-// mkv_state.hip — GDN recurrent/conv state slot gather and scatter (gfx950).
+// mkv_state.hip — GDN recurrent/conv state slot gather and scatter, and the
+// layered block pack / unpack of the host tier (gfx950).
 //
 // A state pool is an array of fixed-size entries (one per request slot): for
 // the Qwen3.5 GDN layer of one tensor-parallel rank a recurrent state is
@@ -11,6 +12,13 @@
 // are non-temporal; a gather's output uses ordinary stores (the layer that
 // gathered it reads it next, often still from the MALL), a scatter's pool
 // writes streaming ones (st_stream: the slot is not read again this step).
+//
+// grid.z is the plane of a layered pool (a KV pool's [layer, K|V] planes, a
+// state pool's layers): plane z's entries start at pool + z * plane_stride and
+// its dense rows at dense + z * n * entry_bytes. Pack / unpack move the blocks
+// of every plane between the pool and one contiguous buffer, which may be
+// pinned host memory: the kernel's loads or stores then cross the host link
+// directly (no staging copy), at the link's rate.
 #include "mkv_device.h"
 
 namespace mkv {
@@ -27,6 +35,7 @@ struct StateArgs {
   uint8_t* dense1;
   int64_t bytes0, bytes1;
   uint32_t pieces0;  // pieces per pool-0 entry (grid.x below it is pool 0)
+  int64_t plane_stride;  // bytes between planes of pool 0 (grid.z); 0 with one plane
   int64_t pool_slots;
   const int32_t* slots;
   int32_t n;
@@ -51,10 +60,14 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
   uint8_t* dense = second ? a.dense1 : a.dense0;
   const int64_t base = piece * kPiece;
   const bool full = base + kPiece <= bytes;
+  const int64_t plane = blockIdx.z;  // pool 1 has one plane
+  pool += plane * a.plane_stride;
+  dense += plane * a.n * bytes;
   for (int64_t b = blockIdx.y; b < a.n; b += gridDim.y) {
     const int32_t slot = a.slots[b];
     const bool ok = slot >= 0 && slot < a.pool_slots;
-    if (!ok && threadIdx.x == 0 && piece == 0 && !second) raise_err(a.err, MKV_DEVERR_STATE_SLOT);
+    if (!ok && threadIdx.x == 0 && piece == 0 && !second && plane == 0)
+      raise_err(a.err, MKV_DEVERR_STATE_SLOT);
     if (!ok && !GATHER) continue;  // scatter: nothing to write for a bad slot
     uint8_t* entry = const_cast<uint8_t*>(pool) + (ok ? (int64_t)slot * bytes : 0) + base;
     uint8_t* row = dense + b * bytes + base;
@@ -85,10 +98,17 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 template <bool GATHER>
 int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* dense0,
                const void* pool1, int64_t bytes1, const void* dense1, int64_t pool_slots,
-               const int32_t* slots, int32_t n, int32_t* err, hipStream_t stream) {
+               const int32_t* slots, int32_t n, int32_t* err, hipStream_t stream,
+               int32_t planes = 1, int64_t plane_stride = 0) {
   clear_error();
-  MKV_REQUIRE(n >= 0 && pool_slots >= 0 && bytes0 >= 0 && bytes1 >= 0, MKV_E_INVALID,
-              "%s: negative size", fn);
+  MKV_REQUIRE(n >= 0 && pool_slots >= 0 && bytes0 >= 0 && bytes1 >= 0 && planes >= 1 &&
+                  plane_stride >= 0,
+              MKV_E_INVALID, "%s: negative size", fn);
+  MKV_REQUIRE(planes == 1 || (pool1 == nullptr && plane_stride % 16 == 0 &&
+                              plane_stride >= pool_slots * bytes0),
+              MKV_E_INVALID, "%s: planes must not overlap (plane_stride >= blocks x bytes)", fn);
+  MKV_REQUIRE(planes <= (int32_t)kMaxGridY, MKV_E_UNSUPPORTED, "%s: more than %u planes", fn,
+              kMaxGridY);
   if (n == 0) return MKV_OK;
   MKV_REQUIRE(slots && err && pool0 && dense0, MKV_E_INVALID, "%s: null pointer", fn);
   const bool two = pool1 != nullptr;
@@ -108,11 +128,13 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   a.dense1 = two ? (uint8_t*)dense1 : (uint8_t*)dense0;
   a.bytes1 = two ? bytes1 : 0;
   a.pieces0 = (uint32_t)p0;
+  a.plane_stride = plane_stride;
   a.pool_slots = pool_slots;
   a.slots = slots;
   a.n = n;
   a.err = err;
-  const dim3 grid((unsigned)(p0 + p1), (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY);
+  const dim3 grid((unsigned)(p0 + p1), (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY,
+                  (unsigned)planes);
   hipLaunchKernelGGL((state_move_kernel<GATHER>), grid, dim3(kThreads), 0, stream, a);
   return check_launch(fn);
 }
@@ -135,4 +157,20 @@ extern "C" int mkv_state_scatter(void* pool0, int64_t entry_bytes0, const void* 
                                  const int32_t* slots, int32_t n, int32_t* err, void* stream) {
   return state_move<false>("mkv_state_scatter", pool0, entry_bytes0, in0, pool1, entry_bytes1,
                            in1, pool_slots, slots, n, err, as_stream(stream));
+}
+
+extern "C" int mkv_pack_blocks(const void* pool, int64_t plane_stride, int32_t num_planes,
+                               int64_t block_bytes, int64_t pool_blocks, const int32_t* ids,
+                               int32_t n, void* out, int32_t* err, void* stream) {
+  return state_move<true>("mkv_pack_blocks", pool, block_bytes, out, nullptr, 0, nullptr,
+                          pool_blocks, ids, n, err, as_stream(stream), num_planes,
+                          num_planes > 1 ? plane_stride : 0);
+}
+
+extern "C" int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                                 int64_t block_bytes, int64_t pool_blocks, const int32_t* ids,
+                                 int32_t n, const void* in, int32_t* err, void* stream) {
+  return state_move<false>("mkv_unpack_blocks", pool, block_bytes, in, nullptr, 0, nullptr,
+                           pool_blocks, ids, n, err, as_stream(stream), num_planes,
+                           num_planes > 1 ? plane_stride : 0);
 }
