@@ -1059,6 +1059,152 @@ def run_decode_attn(steps: int, warmup: int, with_cpu: bool, fp8: bool = False) 
     return res
 
 
+HOST_LINK_PEAK_GBS = 64.0  # PCIe Gen5 x16, per direction (published)
+
+
+def run_offload(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Prefix-cache host tier (muserve/model/prefix_cache.py:36-44 replaced):
+    per step, store one 32K-token prefix entry of one rank into pinned host
+    memory, then restore it. The entry holds:
+    - the hidden state of every prefill token, [32768, 4096] bf16, as the
+      reference stores it;
+    - the 45 GDN states, [1, 8, 128, 128] fp32;
+    - the prefix's KV pages in all 15 attention layers (2048 pages, which the
+      reference does not keep).
+    The restore (lookup_kv) writes the KV into fresh pool pages. A second
+    restore without KV times the reference's content alone."""
+    from muserve_amd.kv_cache import PagedKVCache
+    from muserve_amd.model.prefix_cache import PrefixCache
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, hidden_size, n_gdn = 32768, 4096, 45
+    n_pages = T // 16
+    cache = PagedKVCache(2 * n_pages + 64, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
+                         dtype=torch.bfloat16, device=dev, verbose=False)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    cache.cache.normal_(generator=gen)
+    cache.shuffle_free_list(torch.Generator().manual_seed(SEED))
+    pages = cache.alloc_pages(n_pages)
+    hidden = torch.empty(T, hidden_size, dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+    states = [torch.empty(1, 8, 128, 128, device=dev).normal_(generator=gen)
+              for _ in range(n_gdn)]
+    dense_bytes = hidden.numel() * 2 + n_gdn * 8 * 128 * 128 * 4
+    kv_bytes = LAYERS * 2 * n_pages * 16 * HEAD_DIM * 2
+    entry_bytes = dense_bytes + kv_bytes
+    pc = PrefixCache(max_entries=2, host_bytes=2 * entry_bytes + (64 << 20))
+    ids_base = torch.arange(T + 16, dtype=torch.int64)
+    stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
+
+    def one_step(i: int, rec=None):
+        ids = ids_base + i * 1_000_003  # a new prefix each step: a full store
+        sp = stamps.span(stream) if rec is not None else None
+        pc.store(ids, T, hidden, states, kv=(cache, pages))
+        if rec is not None:
+            rec.append(("store", sp.end(stream)))
+            sp = stamps.span(stream)
+        hit = pc.lookup_kv(ids, dev, cache)
+        if rec is not None:
+            rec.append(("restore", sp.end(stream)))
+            sp = stamps.span(stream)
+        hit2 = pc.lookup(ids, dev)
+        if rec is not None:
+            rec.append(("restore_dense", sp.end(stream)))
+        assert hit is not None and hit2 is not None and len(hit[3]) == n_pages
+        cache.free_pages(hit[3])
+
+    log(f"entry: {entry_bytes / 2**20:.1f} MiB (hidden + states {dense_bytes / 2**20:.1f}, "
+        f"KV {kv_bytes / 2**20:.1f})")
+    for i in range(warmup):
+        one_step(i)
+    torch.cuda.synchronize()
+    recs = [[] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(warmup + j, recs[j])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    pc.sync()
+    cache.check_errors()
+    # the last restore equals the source (bit-exact)
+    ids = ids_base + (warmup + steps - 1) * 1_000_003
+    hit = pc.lookup_kv(ids, dev, cache)
+    torch.cuda.synchronize()
+    pc.sync()
+    exact = (torch.equal(hit[1], hidden) and all(torch.equal(a, b) for a, b in zip(hit[2], states))
+             and torch.equal(cache.cache[:, :, hit[3]], cache.cache[:, :, pages]))
+    cache.free_pages(hit[3])
+    # the link's own DMA rate on the same box: a contiguous pinned copy each way
+    host = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    devb = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dma = {}
+    for name, fn in (("d2h", lambda: host.copy_(devb, non_blocking=True)),
+                     ("h2d", lambda: devb.copy_(host, non_blocking=True))):
+        fn()
+        torch.cuda.synchronize()
+        sp = stamps.span(stream)
+        for _ in range(5):
+            fn()
+        sp.end(stream)
+        torch.cuda.synchronize()
+        dma[name] = 5 * host.numel() / (sp.ms() / 1e3) / 1e9
+    st_ms, rs_ms, rd_ms = (_timed(recs, "store"), _timed(recs, "restore"),
+                           _timed(recs, "restore_dense"))
+    value = 2 * entry_bytes / ((st_ms + rs_ms) / 1e3) / 1e9
+    res = {
+        "metric": ("host-tier store + restore GB/s across the host link for a 32K-token "
+                   "prefix-cache entry (hidden, 45 GDN states, 15 layers of KV pages)"),
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(elapsed / steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 + fp32 (bytes moved as is)",
+        "data": "synthetic (seeded ~N(0,1) hidden, states and KV; shuffled pool pages)",
+        "config": {"workload": (f"prefix-cache host tier, one rank: store then restore of a "
+                                f"{T}-token prefix entry: hidden [{T}, {hidden_size}] bf16, "
+                                f"{n_gdn} GDN states [1,8,128,128] fp32, KV of {LAYERS} layers "
+                                f"x {n_pages} pages (1 KV head x 256, bf16) restored into fresh "
+                                f"pages; pinned arena"),
+                   "entry_bytes": entry_bytes},
+        "store_ms": round(st_ms, 3), "restore_ms": round(rs_ms, 3),
+        "store_GBps": round(entry_bytes / st_ms / 1e6, 2),
+        "restore_GBps": round(entry_bytes / rs_ms / 1e6, 2),
+        "restore_hidden_and_states_ms": round(rd_ms, 3),
+        "restore_hidden_and_states_note": ("the reference's entry content alone; its docstring "
+                                           "claims ~25 ms per 32K prefix "
+                                           "(muserve/model/prefix_cache.py:4)"),
+        "restored_bit_exact": bool(exact),
+        "dma_ceiling_GBps": {k: round(v, 2) for k, v in dma.items()},
+        "roofline": {
+            "bound": "host link",
+            "kernel": ("mkv_pack_blocks / mkv_unpack_blocks (KV, zero-copy into pinned memory) "
+                       "+ hipMemcpyAsync (hidden, states)"),
+            "achieved": round(value, 2), "peak": HOST_LINK_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HOST_LINK_PEAK_GBS, 4), "traffic": None,
+            "frac_of_measured_dma": round(value / (0.5 * (dma["d2h"] + dma["h2d"])), 4),
+        },
+    }
+    if with_cpu:
+        # the reference's own path: tensor.cpu() into pageable memory, then
+        # .to(device, non_blocking=True) from it (prefix_cache.py:36-44), for
+        # the content it stores (hidden + states)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        stored = [t.cpu() for t in [hidden] + states]
+        t2 = time.perf_counter()
+        back = [t.to(dev, non_blocking=True) for t in stored]
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        assert all(torch.equal(a, b) for a, b in zip(back, [hidden] + states))
+        res["cpu_baseline"] = {
+            "value": round(2 * dense_bytes / (t3 - t1) / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"the reference's store / restore of hidden + {n_gdn} states "
+                       f"({dense_bytes / 2**20:.0f} MiB; pageable tensor.cpu(), then "
+                       f".to(device)): {1e3 * (t2 - t1):.1f} ms + {1e3 * (t3 - t2):.1f} ms"),
+        }
+    return res
+
+
 def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
     """A plain device copy of known size (one 1 GiB state-pool entry through
     mkv_state_gather): the reference point for scaling rocprof's FETCH_SIZE and
@@ -1090,7 +1236,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
-                             "decode_attn", "decode_attn_fp8"],
+                             "decode_attn", "decode_attn_fp8", "offload"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1107,12 +1253,15 @@ def main() -> int:
     runner = {"decode": run_decode, "fp8_prefill": run_fp8_prefill, "gdn_state": run_gdn_state,
               "plumbing": run_plumbing, "prefix": run_prefix,
               "decode_attn": run_decode_attn,
-              "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True)}[args.workload]
+              "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True),
+              "offload": run_offload}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
     if args.workload == "prefix" and steps == 1000:
         steps, warmup = 5, 1  # a step is the whole 4096-request trace
+    if args.workload == "offload" and steps == 1000:
+        steps, warmup = 10, 2  # a step moves ~1.5 GB across the host link
     # a garbage-collector pass in the timed loop stalls the host for tens of
     # ms, the stream drains and the event span around the launch absorbs the
     # pause: collect once, freeze what setup allocated and keep the collector

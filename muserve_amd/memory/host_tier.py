@@ -23,6 +23,7 @@ asynchronous (muserve/model/prefix_cache.py:36-44). Here:
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass
 
 import torch
@@ -147,6 +148,43 @@ class HostTier:
         self.arena = PinnedArena(nbytes)
         self.stream = torch.cuda.Stream(self.device)  # default priority
         self._errors = _lib.DeviceErrors(self.device)
+        self._batch = 0       # depth of open batches
+        self._batch_wait = False
+
+    @contextmanager
+    def batch(self, ordered: bool = True):
+        """Groups puts and gets: the copy stream waits for the current stream
+        once on entry, and (``ordered``, or if the batch restored anything) the
+        current stream waits for the copy stream once on exit, instead of a
+        pair of waits per transfer."""
+        if self._batch:
+            self._batch += 1
+            try:
+                yield self
+            finally:
+                self._batch -= 1
+            return
+        cur = torch.cuda.current_stream(self.device)
+        self.stream.wait_stream(cur)
+        self._batch, self._batch_wait = 1, ordered
+        try:
+            yield self
+        finally:
+            self._batch = 0
+            if self._batch_wait:
+                cur.wait_stream(self.stream)
+
+    def _begin(self) -> torch.cuda.Stream:
+        cur = torch.cuda.current_stream(self.device)
+        if not self._batch:
+            self.stream.wait_stream(cur)
+        return cur
+
+    def _end(self, cur: torch.cuda.Stream, wait: bool) -> None:
+        if self._batch:
+            self._batch_wait = self._batch_wait or wait
+        elif wait:
+            cur.wait_stream(self.stream)
 
     # ── dense tensors (DMA) ────────────────────────────────────────────────
 
@@ -164,25 +202,22 @@ class HostTier:
             if off is None:
                 return None
         src = t.detach().contiguous().view(-1).view(torch.uint8)
-        cur = torch.cuda.current_stream(self.device)
-        self.stream.wait_stream(cur)
+        cur = self._begin()
         with torch.cuda.stream(self.stream):
             self.arena.view(off, nbytes).copy_(src, non_blocking=True)
         src.record_stream(self.stream)
-        if ordered:
-            cur.wait_stream(self.stream)
+        self._end(cur, ordered)
         return HostTensor(off, nbytes, tuple(t.shape), t.dtype)
 
     def get_tensor(self, h: HostTensor) -> torch.Tensor:
         """A new device tensor with h's contents, ready on the current stream."""
-        cur = torch.cuda.current_stream(self.device)
         out = torch.empty(h.shape, dtype=h.dtype, device=self.device)
-        self.stream.wait_stream(cur)
+        cur = self._begin()
         with torch.cuda.stream(self.stream):
             out.view(-1).view(torch.uint8).copy_(self.arena.view(h.off, h.nbytes),
                                                   non_blocking=True)
         out.record_stream(self.stream)
-        cur.wait_stream(self.stream)
+        self._end(cur, True)
         return out
 
     # ── pool blocks (pack / unpack kernels across the host link) ──────────
@@ -205,14 +240,12 @@ class HostTier:
             off = self.arena.alloc(nbytes)
             if off is None:
                 return None
-        cur = torch.cuda.current_stream(self.device)
-        self.stream.wait_stream(cur)
+        cur = self._begin()
         _lib.call("mkv_pack_blocks", pool.data_ptr(), stride, planes, block_bytes, blocks,
                   ids.data_ptr(), n, self.arena.buf.data_ptr() + off, self._errors.ptr(),
                   self.stream.cuda_stream)
         ids.record_stream(self.stream)
-        if ordered:
-            cur.wait_stream(self.stream)
+        self._end(cur, ordered)
         return HostBlocks(off, nbytes, planes, n, block_bytes)
 
     def get_blocks(self, h: HostBlocks, pool: torch.Tensor, block_dims: int,
@@ -225,18 +258,21 @@ class HostTier:
             raise ValueError(f"pool / ids ({planes} planes, {ids.numel()} blocks of "
                              f"{block_bytes} B) do not match the stored blocks "
                              f"({h.planes}, {h.n}, {h.block_bytes})")
-        cur = torch.cuda.current_stream(self.device)
-        self.stream.wait_stream(cur)
+        cur = self._begin()
         _lib.call("mkv_unpack_blocks", pool.data_ptr(), stride, planes, block_bytes, blocks,
                   ids.data_ptr(), h.n, self.arena.buf.data_ptr() + h.off, self._errors.ptr(),
                   self.stream.cuda_stream)
         ids.record_stream(self.stream)
-        cur.wait_stream(self.stream)
+        self._end(cur, True)
 
     def _ids(self, ids) -> torch.Tensor:
+        """Block ids on the device, ready on the copy stream."""
         ids = torch.as_tensor(ids, dtype=torch.int32)
-        if ids.device != self.device:
-            ids = ids.to(self.device, non_blocking=True)
+        if ids.device != self.device:  # uploaded on the copy stream itself
+            with torch.cuda.stream(self.stream):
+                return ids.contiguous().to(self.device, non_blocking=True)
+        # device ids may come from the caller's stream after a batch began
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
         return ids.contiguous()
 
     # ── lifetime ────────────────────────────────────────────────────────────

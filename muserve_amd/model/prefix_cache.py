@@ -29,6 +29,7 @@ kept as the reference keeps them.
 """
 from __future__ import annotations
 
+import contextlib
 import hashlib
 from collections import OrderedDict
 from typing import Optional
@@ -116,10 +117,18 @@ class PrefixCache:
             return None
         self._cache.move_to_end(key)
         entry = self._cache[key]
-        hidden = self._to_device(entry["hidden"], device)
-        gdn_states = [self._to_device(s, device) if s is not None else None
-                      for s in entry["gdn_states"]]
+        with self._batch(entry):
+            hidden = self._to_device(entry["hidden"], device)
+            gdn_states = [self._to_device(s, device) if s is not None else None
+                          for s in entry["gdn_states"]]
         return entry["prefix_len"], hidden, gdn_states
+
+    def _batch(self, entry: dict):
+        """One copy-stream session for an entry's transfers (a no-op without
+        the host tier)."""
+        if self._tier is not None and "_range" in entry:
+            return self._tier.batch(ordered=True)
+        return contextlib.nullcontext()
 
     def lookup_kv(self, input_ids: torch.Tensor, device: torch.device, cache
                   ) -> Optional[tuple[int, torch.Tensor, list, Optional[list[int]]]]:
@@ -133,18 +142,20 @@ class PrefixCache:
         entry = self._cache[key]
         kv = entry.get("kv")
         pages = None
-        if kv is not None and kv["n"] == 0:
-            pages = []
-        elif kv is not None:
-            pages = cache.alloc_pages(kv["n"])  # (alloc_pages(0) would take every free page)
-            ids = torch.tensor(pages, dtype=torch.int32)
-            self._tier.get_blocks(kv["pages"], cache.cache, 3, ids)
-            if kv["scales"] is not None:
-                self._tier.get_blocks(kv["scales"], cache.scales, 2, ids)
+        if kv is not None:
+            # (alloc_pages(0) would take every free page)
+            pages = cache.alloc_pages(kv["n"]) if kv["n"] else []
         self._cache.move_to_end(key)
-        hidden = self._to_device(entry["hidden"], device)
-        gdn_states = [self._to_device(s, device) if s is not None else None
-                      for s in entry["gdn_states"]]
+        # page ids go up on the caller's stream, before the copy stream is busy
+        ids = torch.tensor(pages, dtype=torch.int32).to(device) if pages else None
+        with self._batch(entry):
+            if pages:
+                self._tier.get_blocks(kv["pages"], cache.cache, 3, ids)
+                if kv["scales"] is not None:
+                    self._tier.get_blocks(kv["scales"], cache.scales, 2, ids)
+            hidden = self._to_device(entry["hidden"], device)
+            gdn_states = [self._to_device(s, device) if s is not None else None
+                          for s in entry["gdn_states"]]
         return entry["prefix_len"], hidden, gdn_states, pages
 
     def store(self, input_ids: torch.Tensor, prefix_len: int, hidden: torch.Tensor,
@@ -187,6 +198,15 @@ class PrefixCache:
         off = self._reserve(total)
         if off is None:
             return  # larger than the whole arena: not cached
+        # page ids go up on the caller's stream, before the copy stream is busy
+        kv_ids = (torch.as_tensor(kv[1], dtype=torch.int32).to(self._tier.device)
+                  if kv is not None else None)
+        with self._tier.batch(ordered=not self.overlap_store):
+            self._store_parts(key, prefix_len, tensors, sizes, gdn_states, off, total, kv,
+                              kv_sizes, kv_ids)
+
+    def _store_parts(self, key, prefix_len, tensors, sizes, gdn_states, off, total, kv,
+                     kv_sizes, ids):
         at = off
         stored = []
         for t, sz in zip(tensors, sizes):
@@ -200,7 +220,8 @@ class PrefixCache:
             "_range": (off, total),
         }
         if kv is not None:
-            ids = torch.as_tensor(page_ids, dtype=torch.int32)
+            cache, page_ids = kv
+            n = len(page_ids)
             ordered = not self.overlap_store
             pages = self._tier.put_blocks(cache.cache, 3, ids, at, ordered)
             at += kv_sizes[0]
