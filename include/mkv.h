@@ -205,6 +205,31 @@ int mkv_state_scatter(void* pool0, int64_t entry_bytes0, const void* in0,
                       int64_t pool_slots, const int32_t* slots, int32_t n,
                       int32_t* err, void* stream);
 
+/*
+ * GDN decode conv in place on the conv-state pool of one layer, one token per
+ * request (the decode branch of _gdn_conv1d_apply,
+ * muserve/model/qwen35_layer_v2.py:163-201, :187-192):
+ *   - conv_pool is [pool_slots, channels, width] bf16: slot s holds the last
+ *     `width` inputs of each channel, oldest first (width 3 is the reference's
+ *     [C, K-1] state);
+ *   - for b < batch, with p = (state[c, width-3 .. width-1], x[b][c]):
+ *       out[b][c] = silu(sum_k weight[c][k] * p_k)   (fp32, rounded to bf16)
+ *       state[c] <- (state[c, 1 .. width-1], x[b][c])  (slot slots[b])
+ *   - x, out are [batch, channels] bf16; weight is [channels, 4] bf16 (the
+ *     conv1d.weight [C, 1, 4]).
+ * Each request has its own state. The reference's decode instead runs the
+ * batch through one state as if it were time, which is the same only at
+ * batch 1. Read once and written once per step, the slot needs no dense
+ * gather or scatter.
+ * Requirements: kernel_size 4, width 3 or 4, channels a multiple of 8,
+ * batch <= 65535 (MKV_E_UNSUPPORTED); pointers 16-byte aligned (MKV_E_ALIGN);
+ * slots unique. A slot outside [0, pool_slots) gives zeros and sets
+ * MKV_DEVERR_STATE_SLOT.
+ */
+int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t channels, int32_t width,
+                        const int32_t* slots, int32_t batch, const void* x, const void* weight,
+                        int32_t kernel_size, void* out, int32_t* err, void* stream);
+
 /* ---- host tier: layered block pack / unpack ------------------------------ */
 
 /*

@@ -139,6 +139,83 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   return check_launch(fn);
 }
 
+// ---------------------------------------------------------------------------
+// GDN decode conv (muserve/model/qwen35_layer_v2.py:163-201, decode branch
+// :187-192), per request slot and in place:
+//   out[b,c] = silu(sum_k w[c,k] p_k), p = (state[c, W-3 .. W-1], x[b,c]),
+//   state[c] <- (state[c, 1 .. W-1], x[b,c]),
+// fp32 arithmetic, bf16 in and out. A slot holds the last W (3 or 4) inputs of
+// each channel, oldest first, [C, W] bf16; the kernel width is 4. The slot is
+// read once and written once per step: no dense gather / scatter of the conv
+// state. A thread takes 8 channels (16-byte loads of x, out and the weights,
+// W 16-byte loads of the state); grid = (channel groups / 256, batch).
+// ---------------------------------------------------------------------------
+constexpr int kConvK = 4;
+
+struct ConvArgs {
+  uint8_t* pool;         // [pool_slots, C, W] bf16
+  const uint8_t* x;      // [B, C] bf16
+  const uint8_t* w;      // [C, 4] bf16
+  uint8_t* out;          // [B, C] bf16
+  const int32_t* slots;  // [B], unique
+  int64_t pool_slots;
+  int32_t channels, batch;
+  int32_t* err;
+};
+
+__device__ __forceinline__ uint32_t half16(const u32x4* v, int e) {  // bf16 element e
+  const uint32_t w = v[e >> 3][(e >> 1) & 3];
+  return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+template <int W>
+__global__ __launch_bounds__(kThreads) void conv_decode_kernel(ConvArgs a) {
+  static_assert(W >= kConvK - 1 && W <= 4, "conv state width");
+  const int64_t b = blockIdx.y;
+  const int32_t g = blockIdx.x * kThreads + threadIdx.x;  // group of 8 channels
+  if (g * 8 >= a.channels) return;
+  const int32_t slot = a.slots[b];
+  uint8_t* outp = a.out + (b * a.channels + g * 8) * 2;
+  if (slot < 0 || slot >= a.pool_slots) {  // nothing to convolve: zeros, the pool untouched
+    if (g == 0) raise_err(a.err, MKV_DEVERR_STATE_SLOT);
+    st16(outp, u32x4{0u, 0u, 0u, 0u});
+    return;
+  }
+  uint8_t* st = a.pool + ((int64_t)slot * a.channels + g * 8) * (W * 2);
+  u32x4 sv[W], wv[kConvK];
+#pragma unroll
+  for (int j = 0; j < W; ++j) sv[j] = ld16(st + 16 * j);
+  const u32x4 xv = ld16(a.x + (b * a.channels + g * 8) * 2);
+#pragma unroll
+  for (int j = 0; j < kConvK; ++j) wv[j] = ld16(a.w + ((int64_t)g * 8 * kConvK) * 2 + 16 * j);
+  uint32_t outw[4] = {0u, 0u, 0u, 0u};
+  uint32_t nsw[4 * W];
+#pragma unroll
+  for (int j = 0; j < 4 * W; ++j) nsw[j] = 0u;
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch) {
+    const uint32_t xb = half16(&xv, ch);
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < kConvK; ++k) {
+      const uint32_t pb = k < kConvK - 1 ? half16(sv, ch * W + (W - (kConvK - 1)) + k) : xb;
+      acc = fmaf(bits_f32(half16(wv, ch * kConvK + k) << 16), bits_f32(pb << 16), acc);
+    }
+    const float y = acc / (1.0f + expf(-acc));
+    outw[ch >> 1] |= (uint32_t)f32_to_bf16_rne(y) << (16 * (ch & 1));
+#pragma unroll
+    for (int j = 0; j < W; ++j) {  // shifted state: inputs 1 .. W-1, then x
+      const uint32_t v = j < W - 1 ? half16(sv, ch * W + j + 1) : xb;
+      const int e = ch * W + j;
+      nsw[e >> 1] |= v << (16 * (e & 1));
+    }
+  }
+  st16(outp, u32x4{outw[0], outw[1], outw[2], outw[3]});
+#pragma unroll
+  for (int j = 0; j < W; ++j)
+    st16(st + 16 * j, u32x4{nsw[4 * j], nsw[4 * j + 1], nsw[4 * j + 2], nsw[4 * j + 3]});
+}
+
 }  // namespace
 }  // namespace mkv
 
@@ -173,4 +250,39 @@ extern "C" int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_p
   return state_move<false>("mkv_unpack_blocks", pool, block_bytes, in, nullptr, 0, nullptr,
                            pool_blocks, ids, n, err, as_stream(stream), num_planes,
                            num_planes > 1 ? plane_stride : 0);
+}
+
+extern "C" int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t channels,
+                                   int32_t width, const int32_t* slots, int32_t batch,
+                                   const void* x, const void* weight, int32_t kernel_size,
+                                   void* out, int32_t* err, void* stream) {
+  clear_error();
+  const char* fn = "mkv_gdn_conv_decode";
+  MKV_REQUIRE(pool_slots >= 0 && channels > 0 && batch >= 0, MKV_E_INVALID, "%s: bad sizes", fn);
+  MKV_REQUIRE(kernel_size == kConvK && (width == 3 || width == 4), MKV_E_UNSUPPORTED,
+              "%s: kernel %d / state width %d unsupported (kernel 4, width 3 or 4)", fn,
+              kernel_size, width);
+  MKV_REQUIRE(channels % 8 == 0, MKV_E_UNSUPPORTED, "%s: channels must be a multiple of 8", fn);
+  if (batch == 0) return MKV_OK;
+  MKV_REQUIRE(conv_pool && slots && x && weight && out && err, MKV_E_INVALID, "%s: null pointer",
+              fn);
+  MKV_REQUIRE(aligned16(conv_pool) && aligned16(x) && aligned16(weight) && aligned16(out),
+              MKV_E_ALIGN, "%s: pool, x, weight and out must be 16-byte aligned", fn);
+  MKV_REQUIRE(batch <= 65535, MKV_E_UNSUPPORTED, "%s: batch above 65535", fn);
+  ConvArgs a;
+  a.pool = static_cast<uint8_t*>(conv_pool);
+  a.x = static_cast<const uint8_t*>(x);
+  a.w = static_cast<const uint8_t*>(weight);
+  a.out = static_cast<uint8_t*>(out);
+  a.slots = slots;
+  a.pool_slots = pool_slots;
+  a.channels = channels;
+  a.batch = batch;
+  a.err = err;
+  const dim3 grid((unsigned)((channels / 8 + kThreads - 1) / kThreads), (unsigned)batch);
+  if (width == 3)
+    hipLaunchKernelGGL(conv_decode_kernel<3>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(conv_decode_kernel<4>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  return check_launch(fn);
 }

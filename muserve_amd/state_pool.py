@@ -114,6 +114,38 @@ class StatePool:
                   cv.data_ptr() if use_conv else None, self.num_slots, slots.data_ptr(), n,
                   self._errors.ptr(), _lib.stream_of(self.device))
 
+    def conv_decode(self, layer: int, slots: torch.Tensor, x: torch.Tensor,
+                    weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The GDN decode conv of one token per request, in place on the conv
+        slots (muserve/model/qwen35_layer_v2.py:163-201, decode branch): x
+        [B, C] bf16 (one token's mixed_qkv per request), weight [C, 1, 4] or
+        [C, 4] bf16 (conv1d.weight) -> silu(conv) [B, C] bf16. Each slot's
+        last inputs shift by one with x appended. Slots must be unique. Each
+        request has its own state (the reference's decode shares one across
+        the batch)."""
+        if self.conv is None:
+            raise RuntimeError("this pool keeps no conv states")
+        slots = self._check(slots)
+        if not 0 <= layer < self.num_layers:
+            raise IndexError(f"GDN layer {layer} out of range (pool has {self.num_layers})")
+        C, W = self.conv.shape[2], self.conv.shape[3]
+        B = slots.numel()
+        w = weight.reshape(weight.shape[0], -1)
+        if x.shape != (B, C) or x.dtype != torch.bfloat16 or self.conv.dtype != torch.bfloat16:
+            raise ValueError(f"x must be bf16 [{B}, {C}] and the conv pool bf16")
+        if w.shape[0] != C or w.dtype != torch.bfloat16:
+            raise ValueError(f"weight must be bf16 [{C}, 1, K]")
+        x, w = x.contiguous(), w.contiguous()
+        if out is None:
+            out = torch.empty_like(x)
+        elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("out must be a contiguous tensor shaped like x")
+        _lib.require_gpu(slots, x, w, out, self.conv)
+        _lib.call("mkv_gdn_conv_decode", self.conv[layer].data_ptr(), self.num_slots, C, W,
+                  slots.data_ptr(), B, x.data_ptr(), w.data_ptr(), w.shape[1], out.data_ptr(),
+                  self._errors.ptr(), _lib.stream_of(self.device))
+        return out
+
     def check_errors(self) -> None:
         if self._errors is not None:
             self._errors.check("StatePool")

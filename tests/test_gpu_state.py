@@ -1,4 +1,9 @@
-"""GPU parity of GDN state-pool slot gather/scatter vs index_select/index_copy_."""
+"""GPU parity of GDN state-pool slot gather/scatter vs index_select/index_copy_,
+and of the in-place decode conv (StatePool.conv_decode) vs the float64 oracle:
+the shifted state bit-exact, the output within one bf16 ulp plus the fp32
+evaluation term 2^-20 x sum_k |w_k p_k| (which matters only where the
+output cancels to near zero)."""
+import numpy as np
 import pytest
 import torch
 
@@ -48,3 +53,46 @@ def test_bad_slot_is_reported():
     with pytest.raises(_lib.MkvDeviceError, match="state-pool slot"):
         pool.check_errors()
     assert st[1].abs().sum().item() == 0 and cv[1].float().abs().sum().item() == 0
+
+
+@pytest.mark.parametrize("channels,width", [(2048, 4), (1536, 3)])
+def test_conv_decode_in_place(channels, width):
+    case(f"GDN decode conv in place, {channels} channels, state width {width}")
+    g = torch.Generator().manual_seed(channels + width)
+    S, B = 96, 40
+    pool = StatePool(num_layers=2, num_slots=S, conv_shape=(channels, width), device=DEV)
+    cv_cpu = torch.randn(pool.conv.shape, generator=g).bfloat16()
+    pool.conv.copy_(cv_cpu.to(DEV))
+    slots = torch.randperm(S, generator=g)[:B].to(torch.int32)
+    x = torch.randn(B, channels, generator=g).bfloat16()
+    w = (0.6 * torch.randn(channels, 1, 4, generator=g)).bfloat16()
+    for step in range(3):  # consecutive steps chain through the slots
+        xs = (x * (step + 1)).bfloat16()
+        out = pool.conv_decode(1, slots.to(DEV), xs.to(DEV), w.to(DEV))
+        torch.cuda.synchronize()
+        pool.check_errors()
+        p = torch.cat([cv_cpu[1, slots.long(), :, width - 3:].double(),
+                       xs.double().unsqueeze(2)], dim=2)
+        mass = (w.view(channels, 4).double().unsqueeze(0) * p).abs().sum(2).numpy()
+        want = ref.conv_decode(cv_cpu[1], slots, xs, w.view(channels, 4))
+        err = (out.cpu().double() - want).abs().numpy()
+        mag = np.maximum(np.abs(want.numpy()), 2.0 ** -126)
+        tol = 2.0 ** (np.floor(np.log2(mag)) - 7) + 2.0 ** -20 * mass
+        assert (err <= tol).all(), f"step {step}: worst {err.max()}"
+        assert torch.equal(pool.conv.cpu(), cv_cpu), f"step {step}: state differs"
+
+
+def test_conv_decode_bad_slot():
+    case("GDN decode conv, slot outside the pool")
+    pool = StatePool(num_layers=1, num_slots=8, device=DEV)
+    pool.conv.normal_()
+    before = pool.conv.clone()
+    x = torch.randn(2, 2048, device=DEV).bfloat16()
+    w = torch.randn(2048, 1, 4, device=DEV).bfloat16()
+    out = pool.conv_decode(0, torch.tensor([3, 8], device=DEV), x, w)
+    with pytest.raises(_lib.MkvDeviceError, match="state-pool slot out of range"):
+        pool.check_errors()
+    assert torch.count_nonzero(out[1]) == 0
+    assert torch.equal(pool.conv[0, 3, :, :3], before[0, 3, :, 1:])
+    keep = [i for i in range(8) if i != 3]
+    assert torch.equal(pool.conv[0, keep], before[0, keep])
