@@ -513,13 +513,17 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
     return res
 
 
-def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
+def run_gdn_state(steps: int, warmup: int, with_cpu: bool, fused_conv: bool = False) -> dict:
     """Decode step of the hybrid stack, 60 layers in model order: each GDN
     layer gathers the 256 active requests' recurrent [8,128,128] fp32 + conv
     [2048,4] bf16 states from a 1024-slot pool (seeded permuted slots),
     updates them (a synthetic +1, timed apart) and scatters them back; each
     attention layer (l % 4 == 3) appends one decode token per request (the
-    headline workload's appends)."""
+    headline workload's appends). fused_conv: the conv states are not
+    gathered; each GDN layer runs the decode conv in place on them
+    (StatePool.conv_decode: one token's mixed_qkv per request in, silu(conv)
+    out, state shifted), and only the recurrent states are gathered, updated
+    and scattered."""
     from muserve_amd.kv_cache import BlockTables, PagedKVCache, SequenceKVState, reserve_tokens
     from muserve_amd.state_pool import StatePool, gdn_ordinal
 
@@ -546,6 +550,11 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     # the layer's working set: the batch's states, contiguous
     sbuf = torch.empty((B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
     cbuf = torch.empty((B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+    C = pool.conv.shape[2]
+    if fused_conv:  # a ring of 4 steps of per-request conv inputs, the layers' weights
+        xin = torch.randn(4, G, B, C, generator=gen, device=dev).bfloat16()
+        wconv = (0.5 * torch.randn(G, C, 1, 4, generator=gen, device=dev)).bfloat16()
+        cout = torch.empty(B, C, dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
     stamps = Stamps()
 
@@ -559,16 +568,21 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
                 continue
             g = gdn_ordinal(layer)
             sp = stamps.span(stream) if rec is not None else None
-            pool.gather(g, slots, out=(sbuf, cbuf))
+            if fused_conv:  # recurrent gather + conv in place, one launch
+                pool.decode_gather(g, slots, xin[i % 4, g], wconv[g], state_out=sbuf,
+                                   conv_out=cout)
+            else:
+                pool.gather(g, slots, out=(sbuf, cbuf))
             if rec is not None:
                 rec.append(("gather", sp.end(stream)))
                 sp = stamps.span(stream)
             sbuf.add_(1.0)
-            cbuf.add_(1.0)
+            if not fused_conv:
+                cbuf.add_(1.0)
             if rec is not None:
                 rec.append(("update", sp.end(stream)))
                 sp = stamps.span(stream)
-            pool.scatter(g, slots, sbuf, cbuf)
+            pool.scatter(g, slots, sbuf, None if fused_conv else cbuf)
             if rec is not None:
                 rec.append(("scatter", sp.end(stream)))
         if steps_rec is not None:
@@ -586,34 +600,47 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool) -> dict:
     elapsed = time.perf_counter() - t0
     pool.check_errors()
     cache.check_errors()
-    entry = 8 * 128 * 128 * 4 + 2048 * 4 * 2
+    rec_bytes = 8 * 128 * 128 * 4
+    entry = rec_bytes + (0 if fused_conv else 2048 * 4 * 2)
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
+    # in-place conv: the slot read and written, x in, out, the weights, the slots
+    conv_bytes = 2 * B * C * 4 * 2 + 2 * B * C * 2 + C * 4 * 2 + 4 * B
     ratios = counter_ratios("gdn_state_hbm_counters.md")
     g_ms, s_ms, u_ms = _timed(recs, "gather"), _timed(recs, "scatter"), _timed(recs, "update")
     state_s = G * (g_ms + s_ms) / 1e3
     step_s = elapsed / steps
-    per_step_state = 4 * G * B * entry
+    per_step_state = 4 * G * B * entry + (G * conv_bytes if fused_conv else 0)
+    kernels = [
+        _kernel_roofline("gdn_decode_gather_kernel<4> (mkv_gdn_decode_gather)" if fused_conv
+                         else "state_move_kernel<true> (mkv_state_gather)",
+                         move_bytes + (conv_bytes if fused_conv else 0), g_ms,
+                         None if fused_conv else ratios.get("state_move_kernel<true>")),
+        _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms,
+                         None if fused_conv else ratios.get("state_move_kernel<false>"))]
     res = {
-        "metric": "achieved HBM GB/s (% of 8 TB/s) for GDN state slot gather+scatter",
+        "metric": ("achieved HBM GB/s (% of 8 TB/s) for GDN decode-step state traffic: "
+                   "recurrent slot gather+scatter, conv in place" if fused_conv else
+                   "achieved HBM GB/s (% of 8 TB/s) for GDN state slot gather+scatter"),
         "value": round(per_step_state / state_s / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32+bf16",
         "data": "synthetic (seeded ~N(0,1) states, seeded permuted slots)",
-        "config": {"workload": ("GDN state slots at decode: 45 layers x [8,128,128] fp32 + "
-                                "[2048,4] bf16, 1024-slot pool, batch 256, 60 layers in model "
-                                "order: gather -> +1 -> scatter per GDN layer, decode append per "
-                                "attention layer; seed 105")},
+        "config": {"workload": (
+            "GDN state slots at decode: 45 layers x [8,128,128] fp32 + [2048,4] bf16, "
+            "1024-slot pool, batch 256, 60 layers in model order: "
+            + ("recurrent gather -> +1 -> scatter and the decode conv (kernel 4) in place on the "
+               "conv slots per GDN layer" if fused_conv else
+               "gather -> +1 -> scatter per GDN layer")
+            + ", decode append per attention layer; seed 105")},
         "state_move_ms_per_step": round(state_s * 1e3, 3),
         "synthetic_update_ms_per_step": round(G * u_ms, 3),
         "step_time": _step_stats(step_spans),
         "pct_of_hbm_peak": round(100 * per_step_state / state_s / 1e9 / HBM_PEAK_GBS, 2),
-        "roofline": _roofline_of(sorted([
-            _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, g_ms,
-                             ratios.get("state_move_kernel<true>")),
-            _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms,
-                             ratios.get("state_move_kernel<false>"))],
-            key=lambda k: -k["mean_launch_us"]), "gdn_state_hbm_counters.md"),
+        "roofline": _roofline_of(sorted(kernels, key=lambda k: -k["mean_launch_us"]),
+                                 "gdn_state_hbm_counters.md"),
     }
+    if fused_conv:
+        res["conv_bytes_per_layer"] = conv_bytes
     if with_cpu:
         from oracle import state as ref
         n = 32
@@ -1236,7 +1263,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
-                             "decode_attn", "decode_attn_fp8", "offload"],
+                             "decode_attn", "decode_attn_fp8", "offload", "gdn_decode"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1254,7 +1281,8 @@ def main() -> int:
               "plumbing": run_plumbing, "prefix": run_prefix,
               "decode_attn": run_decode_attn,
               "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True),
-              "offload": run_offload}[args.workload]
+              "offload": run_offload,
+              "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True)}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window

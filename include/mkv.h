@@ -230,6 +230,21 @@ int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t channels, i
                         const int32_t* slots, int32_t batch, const void* x, const void* weight,
                         int32_t kernel_size, void* out, int32_t* err, void* stream);
 
+/*
+ * One GDN layer's decode-step state reads in one launch: mkv_state_gather of
+ * the batch's recurrent states (state_pool: one layer's [pool_slots,
+ * state_bytes] entries -> state_out [batch, state_bytes]) and
+ * mkv_gdn_conv_decode on the conv slots (conv_pool [pool_slots, channels,
+ * width] -> conv_out [batch, channels]), both indexed by slots. The same
+ * results as the two calls, one launch instead of two. Same requirements as
+ * each (state_bytes a multiple of 16).
+ */
+int mkv_gdn_decode_gather(const void* state_pool, int64_t state_bytes, void* state_out,
+                          void* conv_pool, int32_t channels, int32_t width, int64_t pool_slots,
+                          const int32_t* slots, int32_t batch, const void* x,
+                          const void* weight, int32_t kernel_size, void* conv_out,
+                          int32_t* err, void* stream);
+
 /* ---- host tier: layered block pack / unpack ------------------------------ */
 
 /*

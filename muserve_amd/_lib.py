@@ -56,6 +56,8 @@ SIGNATURES: dict[str, list] = {
     "mkv_state_gather": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
     "mkv_state_scatter": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I32, _P, _P],
     "mkv_gdn_conv_decode": [_P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _P],
+    "mkv_gdn_decode_gather": [_P, _I64, _P, _P, _I32, _I32, _I64, _P, _I32, _P, _P, _I32, _P,
+                              _P, _P],
     "mkv_pack_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P, _P],
     "mkv_unpack_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P, _P],
     "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],

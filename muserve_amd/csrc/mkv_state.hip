@@ -51,10 +51,11 @@ __device__ __forceinline__ void store(uint8_t* base, uint32_t off, u32x4 v) {
     st_stream(base, off, v);
 }
 
+// One workgroup's piece `bx` (grid.x) of every entry it covers.
 template <bool GATHER>
-__global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
-  const bool second = blockIdx.x >= a.pieces0;
-  const int64_t piece = second ? blockIdx.x - a.pieces0 : blockIdx.x;
+__device__ __forceinline__ void move_piece(const StateArgs& a, uint32_t bx) {
+  const bool second = bx >= a.pieces0;
+  const int64_t piece = second ? bx - a.pieces0 : bx;
   const int64_t bytes = second ? a.bytes1 : a.bytes0;
   const uint8_t* pool = second ? a.pool1 : a.pool0;
   uint8_t* dense = second ? a.dense1 : a.dense0;
@@ -96,11 +97,17 @@ __global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
 }
 
 template <bool GATHER>
-int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* dense0,
+__global__ __launch_bounds__(kThreads) void state_move_kernel(StateArgs a) {
+  move_piece<GATHER>(a, blockIdx.x);
+}
+
+constexpr int kEmpty = 1;  // argument check passed, nothing to launch
+
+// Checks a move's arguments and fills `a`; `pieces` = grid.x.
+int state_args(const char* fn, const void* pool0, int64_t bytes0, const void* dense0,
                const void* pool1, int64_t bytes1, const void* dense1, int64_t pool_slots,
-               const int32_t* slots, int32_t n, int32_t* err, hipStream_t stream,
-               int32_t planes = 1, int64_t plane_stride = 0) {
-  clear_error();
+               const int32_t* slots, int32_t n, int32_t* err, int32_t planes,
+               int64_t plane_stride, StateArgs& a, int64_t& pieces) {
   MKV_REQUIRE(n >= 0 && pool_slots >= 0 && bytes0 >= 0 && bytes1 >= 0 && planes >= 1 &&
                   plane_stride >= 0,
               MKV_E_INVALID, "%s: negative size", fn);
@@ -109,7 +116,7 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
               MKV_E_INVALID, "%s: planes must not overlap (plane_stride >= blocks x bytes)", fn);
   MKV_REQUIRE(planes <= (int32_t)kMaxGridY, MKV_E_UNSUPPORTED, "%s: more than %u planes", fn,
               kMaxGridY);
-  if (n == 0) return MKV_OK;
+  if (n == 0) return kEmpty;
   MKV_REQUIRE(slots && err && pool0 && dense0, MKV_E_INVALID, "%s: null pointer", fn);
   const bool two = pool1 != nullptr;
   MKV_REQUIRE(!two || dense1, MKV_E_INVALID, "%s: pool1 given without its dense buffer", fn);
@@ -120,7 +127,6 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   const int64_t p0 = bytes0 > 0 ? (bytes0 + kPiece - 1) / kPiece : 1;
   const int64_t p1 = two ? (bytes1 > 0 ? (bytes1 + kPiece - 1) / kPiece : 1) : 0;
   MKV_REQUIRE(p0 + p1 < (1ll << 31), MKV_E_UNSUPPORTED, "%s: entries too large", fn);
-  StateArgs a{};
   a.pool0 = (const uint8_t*)pool0;
   a.dense0 = (uint8_t*)dense0;
   a.bytes0 = bytes0;
@@ -133,7 +139,22 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
   a.slots = slots;
   a.n = n;
   a.err = err;
-  const dim3 grid((unsigned)(p0 + p1), (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY,
+  pieces = p0 + p1;
+  return MKV_OK;
+}
+
+template <bool GATHER>
+int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* dense0,
+               const void* pool1, int64_t bytes1, const void* dense1, int64_t pool_slots,
+               const int32_t* slots, int32_t n, int32_t* err, hipStream_t stream,
+               int32_t planes = 1, int64_t plane_stride = 0) {
+  clear_error();
+  StateArgs a{};
+  int64_t pieces = 0;
+  const int rc = state_args(fn, pool0, bytes0, dense0, pool1, bytes1, dense1, pool_slots, slots,
+                            n, err, planes, plane_stride, a, pieces);
+  if (rc != MKV_OK) return rc == kEmpty ? MKV_OK : rc;
+  const dim3 grid((unsigned)pieces, (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY,
                   (unsigned)planes);
   hipLaunchKernelGGL((state_move_kernel<GATHER>), grid, dim3(kThreads), 0, stream, a);
   return check_launch(fn);
@@ -168,11 +189,11 @@ __device__ __forceinline__ uint32_t half16(const u32x4* v, int e) {  // bf16 ele
   return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
+// Channel groups of workgroup `bx` for request b.
 template <int W>
-__global__ __launch_bounds__(kThreads) void conv_decode_kernel(ConvArgs a) {
+__device__ __forceinline__ void conv_row(const ConvArgs& a, uint32_t bx, int64_t b) {
   static_assert(W >= kConvK - 1 && W <= 4, "conv state width");
-  const int64_t b = blockIdx.y;
-  const int32_t g = blockIdx.x * kThreads + threadIdx.x;  // group of 8 channels
+  const int32_t g = bx * kThreads + threadIdx.x;  // group of 8 channels
   if (g * 8 >= a.channels) return;
   const int32_t slot = a.slots[b];
   uint8_t* outp = a.out + (b * a.channels + g * 8) * 2;
@@ -216,6 +237,22 @@ __global__ __launch_bounds__(kThreads) void conv_decode_kernel(ConvArgs a) {
     st16(st + 16 * j, u32x4{nsw[4 * j], nsw[4 * j + 1], nsw[4 * j + 2], nsw[4 * j + 3]});
 }
 
+template <int W>
+__global__ __launch_bounds__(kThreads) void conv_decode_kernel(ConvArgs a) {
+  conv_row<W>(a, blockIdx.x, blockIdx.y);
+}
+
+// The decode step's state reads of one GDN layer in one launch: workgroups
+// below s.pieces0 gather the batch's recurrent states (move_piece), the rest
+// run the conv in place on the conv slots (conv_row); grid.y is the request.
+template <int W>
+__global__ __launch_bounds__(kThreads) void gdn_decode_gather_kernel(StateArgs s, ConvArgs c) {
+  if (blockIdx.x < s.pieces0)
+    move_piece<true>(s, blockIdx.x);
+  else
+    conv_row<W>(c, blockIdx.x - s.pieces0, blockIdx.y);
+}
+
 }  // namespace
 }  // namespace mkv
 
@@ -252,24 +289,24 @@ extern "C" int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_p
                            num_planes > 1 ? plane_stride : 0);
 }
 
-extern "C" int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t channels,
-                                   int32_t width, const int32_t* slots, int32_t batch,
-                                   const void* x, const void* weight, int32_t kernel_size,
-                                   void* out, int32_t* err, void* stream) {
-  clear_error();
-  const char* fn = "mkv_gdn_conv_decode";
+namespace mkv {
+namespace {
+
+// Checks a decode conv's arguments and fills `a`.
+int conv_args(const char* fn, void* conv_pool, int64_t pool_slots, int32_t channels,
+              int32_t width, const int32_t* slots, int32_t batch, const void* x,
+              const void* weight, int32_t kernel_size, void* out, int32_t* err, ConvArgs& a) {
   MKV_REQUIRE(pool_slots >= 0 && channels > 0 && batch >= 0, MKV_E_INVALID, "%s: bad sizes", fn);
   MKV_REQUIRE(kernel_size == kConvK && (width == 3 || width == 4), MKV_E_UNSUPPORTED,
               "%s: kernel %d / state width %d unsupported (kernel 4, width 3 or 4)", fn,
               kernel_size, width);
   MKV_REQUIRE(channels % 8 == 0, MKV_E_UNSUPPORTED, "%s: channels must be a multiple of 8", fn);
-  if (batch == 0) return MKV_OK;
+  if (batch == 0) return kEmpty;
   MKV_REQUIRE(conv_pool && slots && x && weight && out && err, MKV_E_INVALID, "%s: null pointer",
               fn);
   MKV_REQUIRE(aligned16(conv_pool) && aligned16(x) && aligned16(weight) && aligned16(out),
               MKV_E_ALIGN, "%s: pool, x, weight and out must be 16-byte aligned", fn);
   MKV_REQUIRE(batch <= 65535, MKV_E_UNSUPPORTED, "%s: batch above 65535", fn);
-  ConvArgs a;
   a.pool = static_cast<uint8_t*>(conv_pool);
   a.x = static_cast<const uint8_t*>(x);
   a.w = static_cast<const uint8_t*>(weight);
@@ -279,10 +316,56 @@ extern "C" int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t 
   a.channels = channels;
   a.batch = batch;
   a.err = err;
-  const dim3 grid((unsigned)((channels / 8 + kThreads - 1) / kThreads), (unsigned)batch);
+  return MKV_OK;
+}
+
+int64_t conv_groups(int32_t channels) { return (channels / 8 + kThreads - 1) / kThreads; }
+
+}  // namespace
+}  // namespace mkv
+
+extern "C" int mkv_gdn_conv_decode(void* conv_pool, int64_t pool_slots, int32_t channels,
+                                   int32_t width, const int32_t* slots, int32_t batch,
+                                   const void* x, const void* weight, int32_t kernel_size,
+                                   void* out, int32_t* err, void* stream) {
+  clear_error();
+  const char* fn = "mkv_gdn_conv_decode";
+  ConvArgs a{};
+  const int rc = conv_args(fn, conv_pool, pool_slots, channels, width, slots, batch, x, weight,
+                           kernel_size, out, err, a);
+  if (rc != MKV_OK) return rc == kEmpty ? MKV_OK : rc;
+  const dim3 grid((unsigned)conv_groups(channels), (unsigned)batch);
   if (width == 3)
     hipLaunchKernelGGL(conv_decode_kernel<3>, grid, dim3(kThreads), 0, as_stream(stream), a);
   else
     hipLaunchKernelGGL(conv_decode_kernel<4>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  return check_launch(fn);
+}
+
+extern "C" int mkv_gdn_decode_gather(const void* state_pool, int64_t state_bytes,
+                                     void* state_out, void* conv_pool, int32_t channels,
+                                     int32_t width, int64_t pool_slots, const int32_t* slots,
+                                     int32_t batch, const void* x, const void* weight,
+                                     int32_t kernel_size, void* conv_out, int32_t* err,
+                                     void* stream) {
+  clear_error();
+  const char* fn = "mkv_gdn_decode_gather";
+  StateArgs s{};
+  int64_t pieces = 0;
+  const int rs = state_args(fn, state_pool, state_bytes, state_out, nullptr, 0, nullptr,
+                            pool_slots, slots, batch, err, 1, 0, s, pieces);
+  if (rs < 0) return rs;
+  ConvArgs c{};
+  const int rc = conv_args(fn, conv_pool, pool_slots, channels, width, slots, batch, x, weight,
+                           kernel_size, conv_out, err, c);
+  if (rc < 0) return rc;
+  if (rs == kEmpty || rc == kEmpty) return MKV_OK;  // batch 0
+  const dim3 grid((unsigned)(pieces + conv_groups(channels)), (unsigned)batch);
+  if (width == 3)
+    hipLaunchKernelGGL(gdn_decode_gather_kernel<3>, grid, dim3(kThreads), 0, as_stream(stream), s,
+                       c);
+  else
+    hipLaunchKernelGGL(gdn_decode_gather_kernel<4>, grid, dim3(kThreads), 0, as_stream(stream), s,
+                       c);
   return check_launch(fn);
 }

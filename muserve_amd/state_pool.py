@@ -114,15 +114,30 @@ class StatePool:
                   cv.data_ptr() if use_conv else None, self.num_slots, slots.data_ptr(), n,
                   self._errors.ptr(), _lib.stream_of(self.device))
 
-    def conv_decode(self, layer: int, slots: torch.Tensor, x: torch.Tensor,
-                    weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-        """The GDN decode conv of one token per request, in place on the conv
-        slots (muserve/model/qwen35_layer_v2.py:163-201, decode branch): x
-        [B, C] bf16 (one token's mixed_qkv per request), weight [C, 1, 4] or
-        [C, 4] bf16 (conv1d.weight) -> silu(conv) [B, C] bf16. Each slot's
-        last inputs shift by one with x appended. Slots must be unique. Each
-        request has its own state (the reference's decode shares one across
-        the batch)."""
+    def decode_gather(self, layer: int, slots: torch.Tensor, x: torch.Tensor,
+                      weight: torch.Tensor, state_out: torch.Tensor | None = None,
+                      conv_out: torch.Tensor | None = None):
+        """A GDN layer's decode-step state reads in one launch: the batch's
+        recurrent states gathered (as ``gather``, without the conv states) and
+        the decode conv run in place on the conv slots (as ``conv_decode``).
+        Returns (states [B, ...], silu(conv) [B, C])."""
+        slots, C, W, w, x, conv_out = self._conv_args(layer, slots, x, weight, conv_out)
+        B = slots.numel()
+        if state_out is None:
+            state_out = torch.empty((B, *self.state.shape[2:]), dtype=self.state.dtype,
+                                    device=self.device)
+        elif (state_out.dtype != self.state.dtype or not state_out.is_contiguous()
+              or state_out.numel() != B * self.state[0, 0].numel()):
+            raise ValueError("state_out has the wrong dtype, size or layout")
+        _lib.require_gpu(state_out)
+        _lib.call("mkv_gdn_decode_gather", self.state[layer].data_ptr(),
+                  self._entry_bytes(self.state), state_out.data_ptr(), self.conv[layer].data_ptr(),
+                  C, W, self.num_slots, slots.data_ptr(), B, x.data_ptr(), w.data_ptr(),
+                  w.shape[1], conv_out.data_ptr(), self._errors.ptr(),
+                  _lib.stream_of(self.device))
+        return state_out, conv_out
+
+    def _conv_args(self, layer, slots, x, weight, out):
         if self.conv is None:
             raise RuntimeError("this pool keeps no conv states")
         slots = self._check(slots)
@@ -141,6 +156,19 @@ class StatePool:
         elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError("out must be a contiguous tensor shaped like x")
         _lib.require_gpu(slots, x, w, out, self.conv)
+        return slots, C, W, w, x, out
+
+    def conv_decode(self, layer: int, slots: torch.Tensor, x: torch.Tensor,
+                    weight: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The GDN decode conv of one token per request, in place on the conv
+        slots (muserve/model/qwen35_layer_v2.py:163-201, decode branch): x
+        [B, C] bf16 (one token's mixed_qkv per request), weight [C, 1, 4] or
+        [C, 4] bf16 (conv1d.weight) -> silu(conv) [B, C] bf16. Each slot's
+        last inputs shift by one with x appended. Slots must be unique. Each
+        request has its own state (the reference's decode shares one across
+        the batch)."""
+        slots, C, W, w, x, out = self._conv_args(layer, slots, x, weight, out)
+        B = slots.numel()
         _lib.call("mkv_gdn_conv_decode", self.conv[layer].data_ptr(), self.num_slots, C, W,
                   slots.data_ptr(), B, x.data_ptr(), w.data_ptr(), w.shape[1], out.data_ptr(),
                   self._errors.ptr(), _lib.stream_of(self.device))

@@ -96,3 +96,28 @@ def test_conv_decode_bad_slot():
     assert torch.equal(pool.conv[0, 3, :, :3], before[0, 3, :, 1:])
     keep = [i for i in range(8) if i != 3]
     assert torch.equal(pool.conv[0, keep], before[0, keep])
+
+
+@pytest.mark.parametrize("width", [4, 3])
+def test_decode_gather_equals_gather_plus_conv(width):
+    case(f"GDN decode gather (recurrent gather + conv in one launch), width {width}")
+    g = torch.Generator().manual_seed(40 + width)
+    S, B, C = 64, 24, 2048 if width == 4 else 1536
+    a = StatePool(num_layers=2, num_slots=S, conv_shape=(C, width), device=DEV)
+    a.state.copy_(torch.randn(a.state.shape, generator=g).to(DEV))
+    a.conv.copy_(torch.randn(a.conv.shape, generator=g).bfloat16().to(DEV))
+    b = StatePool(num_layers=2, num_slots=S, conv_shape=(C, width), device=DEV)
+    b.state.copy_(a.state)
+    b.conv.copy_(a.conv)
+    slots = torch.randperm(S, generator=g)[:B].to(torch.int32).to(DEV)
+    x = torch.randn(B, C, generator=g).bfloat16().to(DEV)
+    w = torch.randn(C, 1, 4, generator=g).bfloat16().to(DEV)
+    st, out = a.decode_gather(1, slots, x, w)
+    st2, _ = b.gather(1, slots, out=(torch.empty_like(st), None))
+    out2 = b.conv_decode(1, slots, x, w)
+    torch.cuda.synchronize()
+    a.check_errors()
+    b.check_errors()
+    assert torch.equal(st, st2) and torch.equal(st.cpu(), a.state[1, slots.long()].cpu())
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(a.conv, b.conv) and torch.equal(a.state, b.state)
