@@ -1086,6 +1086,225 @@ def run_decode_attn(steps: int, warmup: int, with_cpu: bool, fp8: bool = False) 
     return res
 
 
+SCHED_SEED = 106
+SCHED_BATCH = 256          # muserve/config.py:32-33 MAX_RUNNING_REQUESTS / MAX_DECODE_BATCH
+SCHED_MAX_PROMPT = 8192
+SCHED_MAX_NEW = 512
+
+
+def sched_requests(n: int, seed: int = SCHED_SEED) -> tuple[np.ndarray, np.ndarray]:
+    """Prompt lengths lognormal(median 1024, sigma 1) clipped to [16, 8192];
+    output lengths uniform in [32, 512]."""
+    rng = np.random.default_rng(seed)
+    prompts = np.clip(np.round(rng.lognormal(np.log(1024.0), 1.0, n)), 16,
+                      SCHED_MAX_PROMPT).astype(np.int64)
+    return prompts, rng.integers(32, SCHED_MAX_NEW + 1, n)
+
+
+def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Continuous-batching serving steps on one TP rank, driven by the
+    scheduler's step plan: a backlog of requests, at most 256 running, a
+    4096-token chunked-prefill budget per step (muserve/config.py:33,40).
+    Per step: plan_step (one upload + one mkv_step_plan launch: slot mapping,
+    positions, cu_seqlens, per-entry block tables), then per attention layer
+    the append of every scheduled token's K/V through the slot mapping and
+    paged decode attention (4 query heads) for the decode entries through the
+    plan's tables; complete_step retires requests at their output length.
+    The warmup fills the batch; the timed steps run with it full."""
+    from muserve_amd.kernels import attention as A
+    from muserve_amd.kv_cache import PagedKVCache
+    from muserve_amd.scheduler import ContinuousBatchScheduler, InferenceRequest
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    max_seq = SCHED_MAX_PROMPT + SCHED_MAX_NEW
+    width = -(-max_seq // 16)
+    pages = SCHED_BATCH * width + 64  # every running request can reach max_seq: no OOM
+    n_req = 4096
+    prompts, outs = sched_requests(n_req)
+    cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
+                         dtype=torch.bfloat16, device=dev, verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(SCHED_SEED))
+    free0 = list(cache._free_pages)
+    chunk = 4096
+    s = ContinuousBatchScheduler(max_batch_size=SCHED_BATCH, max_seq_len=max_seq, kv_cache=cache,
+                                 chunked_prefill_size=chunk)
+    for i in range(n_req):
+        s.add_request(InferenceRequest(request_id=str(i), input_ids=[0] * int(prompts[i]),
+                                       max_new_tokens=int(outs[i])))
+    gen = torch.Generator(device=dev).manual_seed(SCHED_SEED)
+    max_t = SCHED_BATCH + chunk
+    kin = torch.empty(LAYERS, max_t * HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    vin = torch.empty_like(kin)
+    kin.normal_(generator=gen)
+    vin.normal_(generator=gen)
+    q = torch.empty(LAYERS, SCHED_BATCH, 1, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    q.normal_(generator=gen)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
+    log(f"pool: {pages} pages x {LAYERS} layers; {n_req} queued requests "
+        f"(prompt median {int(np.median(prompts))}, max {int(prompts.max())})")
+
+    first_slots = []  # slot mappings of the first steps, checked against the oracle
+
+    def one_step(rec=None, host=None, info=None):
+        t0 = time.perf_counter()
+        plan = s.plan_host()
+        if host is not None:
+            host.append(time.perf_counter() - t0)
+        sp = stamps.span(stream) if rec is not None else None
+        s.launch_plan(plan)
+        if rec is not None:
+            rec.append(("plan", sp.end(stream)))
+        T, nd = plan.num_tokens, plan.num_decode
+        if len(first_slots) < 8:
+            first_slots.append(plan.slot_mapping.cpu().tolist())
+        # the decode half's lengths after this step's append (host copy of
+        # what the kernel writes), for the byte count
+        ent = plan.upload[:8 * nd].reshape(nd, 8)
+        lens = ent[:, 1] + ent[:, 2]
+        for l in range(LAYERS):
+            sp = stamps.span(stream) if rec is not None else None
+            cache.append(plan.slot_mapping, kin[l, :T * HEAD_DIM].view(T, 1, HEAD_DIM),
+                         vin[l, :T * HEAD_DIM].view(T, 1, HEAD_DIM), layer=l)
+            if rec is not None:
+                rec.append(("append", sp.end(stream)))
+            if nd:
+                kp, vp = cache.get_kv_by_layer(l)
+                sp = stamps.span(stream) if rec is not None else None
+                A.attn_decode(q[l, :nd], kp, vp, plan.seq_lens[:nd], plan.block_tables[:nd],
+                              out=out[l, :nd])
+                if rec is not None:
+                    rec.append(("attn", sp.end(stream)))
+        if info is not None:
+            info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1]))
+        s.complete_step(plan)
+
+    log(f"warmup {warmup} steps")
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    cache.check_errors()
+    s.check_errors()
+    A.check_errors(dev)
+    recs = [[] for _ in range(steps)]
+    host: list[float] = []
+    info: list = []
+    log(f"timing {steps} steps ({s.num_running} running, {s.num_prefilling} prefilling, "
+        f"{s.num_waiting} waiting)")
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(recs[j], host, info)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    cache.check_errors()
+    s.check_errors()
+    A.check_errors(dev)
+    tokens = sum(t for t, _, _, _, _ in info)
+    decode_tokens = sum(nd for _, nd, _, _, _ in info)
+    attn_b = append_b = 0.0
+    for T, nd, _, lens, w in info:
+        if nd:
+            ln = lens.astype(np.int64)
+            attn_b += LAYERS * float(2 * ROW * ln.sum() + 4 * (-(-ln // 16)).sum() + 4 * nd
+                                     + 2 * nd * Q_HEADS * ROW)
+        append_b += LAYERS * float(4 * T * ROW + 8 * T)
+    attn_launches = LAYERS * sum(1 for _, nd, _, _, _ in info if nd)
+    attn_ms = _timed(recs, "attn")
+    plan_ms = _timed(recs, "plan")
+    append_ms = _timed(recs, "append")
+    step_s = elapsed / steps
+    value = (attn_b + append_b) / elapsed / 1e9
+    achieved = attn_b / attn_launches / (attn_ms / 1e3) / 1e9
+    ratio = counter_ratios("sched_serving_kernel_trace.md").get("attn")
+    res = {
+        "metric": ("achieved HBM GB/s (% of 8 TB/s) of continuous-batching serving steps "
+                   "(scheduler step plan + KV append + paged decode attention); step µs"),
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (fp32 softmax and accumulation)",
+        "data": ("synthetic (seeded ~N(0,1) q/K/V; seeded lognormal prompt lengths, uniform "
+                 "output lengths; a sampled token is a placeholder)"),
+        "config": {
+            "workload": ("continuous-batching serving on one TP rank: 4096 queued requests, "
+                         "prompts lognormal(median 1024, sigma 1, clip 16..8192), outputs "
+                         "uniform 32..512 tokens, at most 256 running, 4096-token chunked "
+                         "prefill budget per step; 15 attention layers, 1 KV head x 256, bf16 "
+                         "pool of 16-token pages, 4 query heads; seed 106"),
+            "max_batch": SCHED_BATCH, "chunked_prefill_size": chunk, "layers": LAYERS,
+            "kv_heads": 1, "head_dim": HEAD_DIM, "q_heads": Q_HEADS, "pool_pages": pages,
+        },
+        "tokens_per_s": round(tokens / elapsed, 1),
+        "decode_tokens_per_s": round(decode_tokens / elapsed, 1),
+        "prefill_tokens_per_s": round((tokens - decode_tokens) / elapsed, 1),
+        "mean_entries": {"decode": round(decode_tokens / steps, 1),
+                         "prefill_chunks": round(sum(p for _, _, p, _, _ in info) / steps, 2),
+                         "tokens": round(tokens / steps, 1)},
+        "plan_device_us": round(plan_ms * 1e3, 2),
+        "plan_device_note": "upload of the step records + the mkv_step_plan launch (events)",
+        "plan_host_us": round(float(np.mean(host)) * 1e6, 1),
+        "plan_host_us_p90": round(float(np.percentile(host, 90)) * 1e6, 1),
+        "append_us_per_layer": round(append_ms * 1e3, 2),
+        "attn_us_per_layer": round(attn_ms * 1e3, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mkv_decode_attention_bf16 = attn_chunk_kernel<4, false> + attn_merge_kernel<4>",
+            "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": round(ratio * attn_b / attn_launches) if ratio else None,
+            "traffic_to_algorithmic": ratio,
+            "traffic_source": ("rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 of the same kernel in "
+                               "this workload, profiles/sched_serving_kernel_trace.md"),
+            "mean_launch_us": round(attn_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": round(attn_b / attn_launches),
+        },
+    }
+    if with_cpu:
+        log("cpu baseline (scheduler oracle: per-token page bookkeeping of the same trace)")
+        res["cpu_baseline"] = sched_cpu_baseline(prompts, outs, pages, free0, chunk, max_seq,
+                                                 first_slots, warmup, steps)
+    return res
+
+
+def sched_cpu_baseline(prompts, outs, pages, free0, chunk, max_seq, first_slots, warmup: int,
+                       steps: int, budget_s: float = 20.0) -> dict:
+    """The scheduler oracle (per-token SequenceKVState bookkeeping with
+    alloc_pages(1), muserve/kv_cache.py:133-158, and per-entry page-table
+    lists) planning the same trace from its start: the warmup steps, then
+    the timed steps (as many as fit in budget_s seconds of host time); its
+    first steps' slot mappings are compared with the GPU's."""
+    from oracle import paged as pg
+    from oracle import sched as S
+
+    m = S.ChunkedSchedulerModel(SCHED_BATCH, chunk, pg.PoolModel(pages, free0), max_seq)
+    for i, (n, g) in enumerate(zip(prompts, outs)):
+        m.add(S.Req(str(i), int(n), int(g)))
+    same = True
+    t_all = t_timed = 0.0
+    n = tokens = timed = 0
+    while n < warmup + steps and t_all < budget_s:
+        t0 = time.perf_counter()
+        out = m.step()
+        dt = time.perf_counter() - t0
+        t_all += dt
+        if n < len(first_slots):
+            same = same and out["slots"] == first_slots[n]
+        if n >= warmup:
+            t_timed += dt
+            tokens += len(out["slots"])
+            timed += 1
+        n += 1
+        m.complete()
+    return {"value": round(t_timed / timed * 1e6, 1) if timed else None,
+            "unit": "us per step (plan only)", "cores": 1, "kind": "port",
+            "sample": (f"scheduler oracle (pure Python, 1 thread) planning the same trace: "
+                       f"{warmup} warmup steps, then {timed} of the timed steps "
+                       f"({tokens} tokens): {t_timed:.1f} s of {t_all:.1f} s"),
+            "gpu_matches_cpu_on_first_steps": bool(same),
+            "steps_compared": min(n, len(first_slots))}
+
+
 HOST_LINK_PEAK_GBS = 64.0  # PCIe Gen5 x16, per direction (published)
 
 
@@ -1263,7 +1482,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
-                             "decode_attn", "decode_attn_fp8", "offload", "gdn_decode"],
+                             "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
+                             "sched"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1282,7 +1502,8 @@ def main() -> int:
               "decode_attn": run_decode_attn,
               "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True),
               "offload": run_offload,
-              "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True)}[args.workload]
+              "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True),
+              "sched": run_sched}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
@@ -1290,6 +1511,8 @@ def main() -> int:
         steps, warmup = 5, 1  # a step is the whole 4096-request trace
     if args.workload == "offload" and steps == 1000:
         steps, warmup = 10, 2  # a step moves ~1.5 GB across the host link
+    if args.workload == "sched" and (steps, warmup) == (1000, 20):
+        steps, warmup = 500, 300  # the warmup fills the 256-request batch
     # a garbage-collector pass in the timed loop stalls the host for tens of
     # ms, the stream drains and the event span around the launch absorbs the
     # pause: collect once, freeze what setup allocated and keep the collector

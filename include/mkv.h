@@ -124,6 +124,57 @@ int mkv_decode_slots(int32_t* seq_lens, int32_t* block_tables,
                      int64_t num_pages, int64_t* slot_out, int32_t* err,
                      void* stream);
 
+/*
+ * One batch entry of a scheduler step: `count` new tokens of the request whose
+ * persistent block-table row is `row`, at positions [start, start+count).
+ * The row holds `held` pages before the step; the step appends `new_pages`
+ * pages taken from new_pages[page_off ...]. The entry's tokens occupy
+ * [tok_off, tok_off+count) of the step's token arrays.
+ */
+typedef struct MkvStepEntry {
+  int32_t row;
+  int32_t start;
+  int32_t count;
+  int32_t held;
+  int32_t new_pages;
+  int32_t page_off;
+  int32_t tok_off;
+  int32_t reserved; /* 0 */
+} MkvStepEntry;
+
+/*
+ * Scheduler step plan, on the device, for a batch mixing decode tokens and
+ * chunked-prefill chunks. For entry i < num_entries (rows unique within a call;
+ * token offsets tiling [0, num_tokens) in entry order):
+ *   block_tables[row][held + j] = new_pages[page_off + j]      j < new_pages
+ *   for t < count, pos = start + t:
+ *     pos_out[tok_off + t]  = pos
+ *     slot_out[tok_off + t] = page(pos/16)*16 + pos%16
+ *   step_tables[i][j] = page j of the row (j < held+new_pages), else 0
+ *   step_lens[i] = start + count;  rows_out[i] = row;  cu_seqlens[i] = tok_off
+ *   cu_seqlens[num_entries] = num_tokens
+ * step_tables may be NULL (no per-step table). An entry whose pages do not
+ * cover start+count, whose row or page range is outside the tables, or whose
+ * offsets do not tile sets MKV_DEVERR_TABLE and writes slot -1 for its tokens
+ * (when its offsets are consistent), length 0, row -1 and a zero step-table
+ * row; a page id outside [0, num_pages) sets MKV_DEVERR_PAGE and slot -1.
+ * Table strides are in int32 elements.
+ *
+ * Replaces the per-request SequenceKVState bookkeeping of
+ * muserve/kv_cache.py:133-158 (needs_new_page, current_page, last_page_slot,
+ * to_page_table_tensor) and the positions/cu_seqlens tensors built per
+ * request in muserve/inference_loop.py:100-101,121, for a whole step of the
+ * continuous-batching scheduler (muserve/scheduler.py:73-98) with chunked
+ * prefill (muserve/config.py:40 CHUNKED_PREFILL_SIZE) in one launch.
+ */
+int mkv_step_plan(int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                  int32_t num_rows, const MkvStepEntry* entries, int32_t num_entries,
+                  const int32_t* new_pages, int32_t num_new_pages, int64_t num_pages,
+                  int64_t* slot_out, int64_t* pos_out, int64_t num_tokens,
+                  int32_t* step_tables, int64_t step_stride, int32_t step_width,
+                  int32_t* step_lens, int32_t* rows_out, int64_t* cu_seqlens,
+                  int32_t* err, void* stream);
+
 /* ---- fp8 e4m3fn quantize-on-append / dequant-gather --------------------- */
 
 /*

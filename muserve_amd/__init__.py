@@ -11,6 +11,9 @@ Drop-in modules with the reference's class names and signatures:
 * ``muserve_amd.state_pool``      -> ``StatePool`` for GDN recurrent/conv states
 * ``muserve_amd.block_manager``   -> ``BlockManager`` (refcounts, copy-on-write,
                                      prefix-hash table, LRU eviction)
+* ``muserve_amd.scheduler``       -> ``ContinuousBatchScheduler``,
+                                     ``InferenceRequest`` (muserve/scheduler.py),
+                                     plus the paged step plan (chunked prefill)
 
 All device work runs in hand-written gfx950 HIP kernels in libmuserve_kv.so
 (C ABI: include/mkv.h), reached through ``muserve_amd._lib``. There is no CPU

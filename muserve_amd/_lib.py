@@ -48,6 +48,8 @@ SIGNATURES: dict[str, list] = {
     "mkv_gather_bf16": [_P, _P, _I64, _I64, _P, _I64, _I32, _P, _P, _I32, _I64, _P, _P, _P,
                         _I64, _I32, _I32, _P, _P],
     "mkv_decode_slots": [_P, _P, _I64, _I32, _P, _I32, _I64, _P, _P, _P],
+    "mkv_step_plan": [_P, _I64, _I32, _I32, _P, _I32, _P, _I32, _I64, _P, _P, _I64, _P, _I64, _I32,
+                      _P, _P, _P, _P, _P],
     "mkv_append_fp8": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I32,
                        _I32, _I32, _P, _P],
     "mkv_gather_dequant_fp8": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _I32,

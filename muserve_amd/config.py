@@ -23,3 +23,6 @@ KV_DTYPE = "float16"     # muserve/config.py:37
 # Attention layers of the 60-layer hybrid stack (every fourth layer),
 # muserve/memory/kv_cache.py:20.
 ATTN_LAYER_INDICES = [3, 7, 11, 15, 19, 23, 27, 31, 35, 39, 43, 47, 51, 55, 59]
+
+MAX_SEQ_LEN = 262144            # muserve/config.py:10
+CHUNKED_PREFILL_SIZE = 4096     # muserve/config.py:40

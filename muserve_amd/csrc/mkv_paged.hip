@@ -162,6 +162,106 @@ __global__ __launch_bounds__(kThreads) void decode_slots_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// scheduler step plan: one workgroup per batch entry (a decode token or a
+// prefill chunk). Nothing an entry reads is written by another entry (rows are
+// unique per step), and an entry's own new pages are taken from new_pages
+// rather than read back from the table it writes, so no barrier is needed.
+// ---------------------------------------------------------------------------
+struct StepPlanArgs {
+  int32_t* tables;  // persistent [num_rows, stride] rows
+  int64_t stride;
+  int32_t width;
+  int32_t num_rows;
+  const MkvStepEntry* entries;
+  int32_t num_entries;
+  const int32_t* new_pages;
+  int32_t num_new_pages;
+  int64_t num_pages;
+  int64_t* slot_out;
+  int64_t* pos_out;
+  int64_t num_tokens;
+  int32_t* step_tables;  // [num_entries, step_stride], may be null
+  int64_t step_stride;
+  int32_t step_width;
+  int32_t* step_lens;
+  int32_t* rows_out;
+  int64_t* cu_seqlens;
+  int32_t* err;
+};
+
+__global__ __launch_bounds__(kThreads) void step_plan_kernel(StepPlanArgs a) {
+  const int32_t i = blockIdx.x;
+  const MkvStepEntry e = a.entries[i];
+  const int64_t next = (i + 1 < a.num_entries) ? (int64_t)a.entries[i + 1].tok_off : a.num_tokens;
+  // Token offsets must tile [0, num_tokens) in entry order; otherwise this
+  // entry's output range is unknown and nothing of it is written.
+  const bool offsets_ok = e.count >= 0 && e.tok_off >= 0 && (i > 0 || e.tok_off == 0) &&
+                          (int64_t)e.tok_off + e.count == next && next <= a.num_tokens;
+  const int64_t pages = (int64_t)e.held + e.new_pages;
+  const bool ok = offsets_ok && e.row >= 0 && e.row < a.num_rows && e.start >= 0 &&
+                  e.held >= 0 && e.new_pages >= 0 && pages <= a.width &&
+                  (int64_t)e.start + e.count <= pages * 16 && e.page_off >= 0 &&
+                  (int64_t)e.page_off + e.new_pages <= a.num_new_pages &&
+                  (!a.step_tables || pages <= a.step_width);
+  if (!ok) {
+    if (threadIdx.x == 0) {
+      raise_err(a.err, MKV_DEVERR_TABLE);
+      a.step_lens[i] = 0;
+      a.rows_out[i] = -1;
+      if (offsets_ok) a.cu_seqlens[i] = e.tok_off;
+    }
+    if (offsets_ok)
+      for (int32_t t = threadIdx.x; t < e.count; t += kThreads) {
+        a.slot_out[e.tok_off + t] = -1;
+        a.pos_out[e.tok_off + t] = (int64_t)e.start + t;
+      }
+    if (a.step_tables)
+      for (int32_t j = threadIdx.x; j < a.step_width; j += kThreads)
+        a.step_tables[(int64_t)i * a.step_stride + j] = 0;
+    return;
+  }
+  int32_t* row = a.tables + (int64_t)e.row * a.stride;
+  const int32_t* fresh = a.new_pages + e.page_off;
+  auto page_at = [&](int32_t j) -> int32_t {  // page j of the row after this step
+    const int32_t p = j < e.held ? row[j] : fresh[j - e.held];
+    return (p >= 0 && p < a.num_pages) ? p : -1;
+  };
+  int32_t bad = 0;
+  for (int32_t j = threadIdx.x; j < e.new_pages; j += kThreads) {
+    const int32_t p = fresh[j];
+    if (p < 0 || p >= a.num_pages) bad = MKV_DEVERR_PAGE;
+    row[e.held + j] = (p >= 0 && p < a.num_pages) ? p : -1;
+  }
+  for (int32_t t = threadIdx.x; t < e.count; t += kThreads) {
+    const int64_t pos = (int64_t)e.start + t;
+    const int32_t p = page_at((int32_t)(pos >> 4));
+    if (p < 0) bad = MKV_DEVERR_PAGE;
+    a.slot_out[e.tok_off + t] = p < 0 ? -1 : (int64_t)p * 16 + (pos & 15);
+    a.pos_out[e.tok_off + t] = pos;
+  }
+  if (a.step_tables) {
+    // the reference's page-table tensor: the row's pages, then zeros
+    // (muserve/kv_cache.py:149-158)
+    int32_t* out = a.step_tables + (int64_t)i * a.step_stride;
+    for (int32_t j = threadIdx.x; j < a.step_width; j += kThreads) {
+      int32_t p = 0;
+      if (j < pages) {
+        p = page_at(j);
+        if (p < 0) bad = MKV_DEVERR_PAGE;
+      }
+      out[j] = p;
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.step_lens[i] = e.start + e.count;
+    a.rows_out[i] = e.row;
+    a.cu_seqlens[i] = e.tok_off;
+    if (i + 1 == a.num_entries) a.cu_seqlens[i + 1] = (int64_t)e.tok_off + e.count;
+  }
+  if (bad) raise_err(a.err, bad);
+}
+
+// ---------------------------------------------------------------------------
 // page copies: one workgroup per (pair, plane) on a 2-D grid.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void copy_pages_kernel(
@@ -284,6 +384,34 @@ extern "C" int mkv_decode_slots(int32_t* seq_lens, int32_t* block_tables, int64_
                      dim3(kThreads), 0, as_stream(stream), seq_lens, block_tables, table_stride,
                      table_width, new_pages, batch, num_pages, slot_out, err);
   return check_launch("mkv_decode_slots");
+}
+
+extern "C" int mkv_step_plan(int32_t* block_tables, int64_t table_stride, int32_t table_width,
+                             int32_t num_rows, const MkvStepEntry* entries, int32_t num_entries,
+                             const int32_t* new_pages, int32_t num_new_pages, int64_t num_pages,
+                             int64_t* slot_out, int64_t* pos_out, int64_t num_tokens,
+                             int32_t* step_tables, int64_t step_stride, int32_t step_width,
+                             int32_t* step_lens, int32_t* rows_out, int64_t* cu_seqlens,
+                             int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(num_entries >= 0 && num_rows >= 0 && table_width >= 0 && num_new_pages >= 0 &&
+                  num_tokens >= 0 && step_width >= 0 && num_pages >= 0,
+              MKV_E_INVALID, "mkv_step_plan: negative size");
+  if (num_entries == 0) return MKV_OK;
+  MKV_REQUIRE(block_tables && entries && slot_out && pos_out && step_lens && rows_out &&
+                  cu_seqlens && err && (new_pages || num_new_pages == 0),
+              MKV_E_INVALID, "mkv_step_plan: null pointer");
+  MKV_REQUIRE(table_width <= table_stride && (!step_tables || step_width <= step_stride),
+              MKV_E_INVALID, "mkv_step_plan: table width exceeds its row stride");
+  MKV_REQUIRE(aligned4(entries), MKV_E_ALIGN, "mkv_step_plan: entries must be 4-byte aligned");
+  MKV_REQUIRE(num_tokens < ((int64_t)1 << 31), MKV_E_UNSUPPORTED,
+              "mkv_step_plan: more than 2^31-1 tokens in one step");
+  StepPlanArgs a{block_tables, table_stride, table_width, num_rows, entries, num_entries,
+                 new_pages, num_new_pages, num_pages, slot_out, pos_out, num_tokens,
+                 step_tables, step_stride, step_width, step_lens, rows_out, cu_seqlens, err};
+  hipLaunchKernelGGL(step_plan_kernel, dim3((unsigned)num_entries), dim3(kThreads), 0,
+                     as_stream(stream), a);
+  return check_launch("mkv_step_plan");
 }
 
 extern "C" int mkv_copy_blocks(void* pool, int64_t plane_stride, int32_t num_planes,

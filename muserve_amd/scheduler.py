@@ -1,0 +1,424 @@
+"""Continuous-batching scheduler driving the paged KV pool — drop-in for
+muserve/scheduler.py.
+
+``ContinuousBatchScheduler`` keeps the reference's class, request type and
+methods (muserve/scheduler.py:22-123): ``add_request``, ``schedule_step``
+(decode every running request, admit waiting ones while running + admitted <
+max_batch_size), ``finish_prefill``, ``finish_request`` and the counters, with
+the same semantics.
+
+Attached to a ``PagedKVCache`` it also plans whole steps for the pool:
+
+* ``plan_step()`` decodes every running request (one token each) and spends a
+  prefill budget of ``chunked_prefill_size`` tokens (muserve/config.py:40) on
+  requests being prefilled, oldest first, then on newly admitted ones. A
+  request takes as many prompt tokens as the budget and the free pages allow;
+  the first request that gets none ends the step's prefill. Pages come from
+  the pool's LIFO free list in the order repeated ``alloc_pages(1)`` calls
+  would give them (decode entries first, then the chunks). An admitted
+  request takes the smallest free batch row, which is also its GDN state slot.
+* One ``mkv_step_plan`` launch then writes the step's slot mapping, positions,
+  cu_seqlens, per-entry block tables (``to_page_table_tensor`` layout:
+  pages, then zeros), sequence lengths and rows on the device. The host only
+  uploads one small record per entry plus the new page ids; no per-token work
+  runs on the host.
+* ``complete_step(plan, tokens)`` applies the sampled tokens: a decode entry
+  appends its token; a chunk that finished its prompt appends the first token
+  and joins the running batch (``finish_prefill``); a request finishes at
+  ``max_new_tokens``, on ``eos_token_id``, or when its next decode would pass
+  ``max_seq_len`` (``finish_request``). Its pages and row are freed at the
+  next ``plan_step``.
+
+Entries are ordered decode tokens first (running order), then prefill chunks,
+so ``plan.block_tables[:plan.num_decode]`` and ``plan.seq_lens[:plan.num_decode]``
+are what ``attn_decode`` reads for the decode half. A plan's device tensors
+are rewritten by the next ``plan_step``: work that reads them must be issued
+on the same stream before then (stream order does the rest).
+"""
+from __future__ import annotations
+
+import heapq
+import threading
+import time
+from collections import deque
+from dataclasses import dataclass, field
+from enum import Enum
+from typing import Optional
+
+import numpy as np
+import torch
+
+from muserve_amd import _lib
+from muserve_amd.config import CHUNKED_PREFILL_SIZE, KV_PAGE_SIZE
+from muserve_amd.kv_cache import PagedKVCache, SequenceKVState
+from muserve_amd.memory.kv_cache import KVCache
+
+_ENTRY_INTS = 8  # MkvStepEntry: row, start, count, held, new_pages, page_off, tok_off, reserved
+
+
+class RequestState(Enum):
+    WAITING = "waiting"
+    PREFILLING = "prefilling"
+    DECODING = "decoding"
+    FINISHED = "finished"
+
+
+@dataclass
+class InferenceRequest:
+    """muserve/scheduler.py:29-51, plus the paged-pool bookkeeping."""
+    request_id: str
+    input_ids: list[int]
+    max_new_tokens: int = 256
+    temperature: float = 0.0
+    state: RequestState = RequestState.WAITING
+    generated_tokens: list[int] = field(default_factory=list)
+    gdn_states: Optional[list] = None
+    kv_cache: Optional[KVCache] = None
+    created_at: float = field(default_factory=time.time)
+    first_token_at: Optional[float] = None
+    finished_at: Optional[float] = None
+    # paged pool: the sequence's pages and length, its batch row (also its
+    # GDN state slot) and how much of the prompt is in the cache
+    seq: Optional[SequenceKVState] = None
+    row: int = -1
+    num_prefilled: int = 0
+
+    @property
+    def total_len(self) -> int:
+        return len(self.input_ids) + len(self.generated_tokens)
+
+    @property
+    def is_done(self) -> bool:
+        return self.state == RequestState.FINISHED
+
+
+@dataclass
+class StepPlan:
+    """One scheduled step. Host lists describe the entries; the tensors are
+    device views written by ``mkv_step_plan`` (valid until the next plan)."""
+    decode: list[InferenceRequest]
+    prefill: list[tuple[InferenceRequest, int, int]]  # (request, start, count)
+    num_tokens: int
+    upload: np.ndarray                  # what the kernel read: entries, then new pages
+    slot_mapping: torch.Tensor          # [num_tokens] int64
+    positions: torch.Tensor             # [num_tokens] int64
+    cu_seqlens: torch.Tensor            # [num_entries + 1] int64
+    block_tables: torch.Tensor          # [num_entries, width] int32
+    seq_lens: torch.Tensor              # [num_entries] int32, after the step
+    rows: torch.Tensor                  # [num_entries] int32 batch rows / GDN state slots
+
+    @property
+    def num_decode(self) -> int:
+        return len(self.decode)
+
+    @property
+    def num_entries(self) -> int:
+        return len(self.decode) + len(self.prefill)
+
+    @property
+    def entries(self) -> list[InferenceRequest]:
+        return self.decode + [r for r, _, _ in self.prefill]
+
+
+class ContinuousBatchScheduler:
+    """Continuous batching scheduler (muserve/scheduler.py:54-123) with a paged
+    step planner when a ``PagedKVCache`` is attached."""
+
+    _RING = 4  # pinned upload buffers in flight
+
+    def __init__(self, max_batch_size: int = 8, max_seq_len: int = 32768,
+                 device: torch.device = None, *, kv_cache: PagedKVCache | None = None,
+                 chunked_prefill_size: int = CHUNKED_PREFILL_SIZE,
+                 eos_token_id: int | None = None):
+        self.max_batch_size = max_batch_size
+        self.max_seq_len = max_seq_len
+        self.device = device
+
+        self.waiting_queue: deque[InferenceRequest] = deque()
+        self.running_batch: list[InferenceRequest] = []
+        self.lock = threading.Lock()
+
+        self.kv_cache = kv_cache
+        self.chunked_prefill_size = chunked_prefill_size
+        self.eos_token_id = eos_token_id
+        self.prefilling: list[InferenceRequest] = []
+        self._free_rows = list(range(max_batch_size))
+        self.width = -(-max_seq_len // KV_PAGE_SIZE)  # pages per row
+        self._last: StepPlan | None = None
+        self._dev = None
+        if kv_cache is not None:
+            if chunked_prefill_size <= 0:
+                raise ValueError("chunked_prefill_size must be positive")
+            if kv_cache.device.type == "cuda":
+                self._alloc_device(kv_cache.device)
+
+    # ── reference protocol (muserve/scheduler.py:69-123) ────────────────────
+
+    def add_request(self, request: InferenceRequest):
+        if self.kv_cache is not None:
+            n = len(request.input_ids)
+            if n == 0:
+                raise ValueError(f"request {request.request_id}: empty prompt")
+            if n > self.max_seq_len:
+                raise ValueError(f"request {request.request_id}: prompt of {n} tokens exceeds "
+                                 f"max_seq_len {self.max_seq_len}")
+        with self.lock:
+            self.waiting_queue.append(request)
+
+    def schedule_step(self) -> tuple[list[InferenceRequest], list[InferenceRequest]]:
+        """(prefill_requests, decode_requests): drop finished requests, decode
+        every running one, admit waiting ones while the batch has room."""
+        with self.lock:
+            self.running_batch = [r for r in self.running_batch if not r.is_done]
+            decode_requests = list(self.running_batch)
+            prefill_requests = []
+            while (self.waiting_queue
+                   and len(self.running_batch) + len(prefill_requests) < self.max_batch_size):
+                req = self.waiting_queue.popleft()
+                req.state = RequestState.PREFILLING
+                prefill_requests.append(req)
+            return prefill_requests, decode_requests
+
+    def finish_prefill(self, requests: list[InferenceRequest]):
+        with self.lock:
+            for req in requests:
+                req.state = RequestState.DECODING
+                req.first_token_at = time.time()
+                self.running_batch.append(req)
+
+    def finish_request(self, request: InferenceRequest):
+        request.state = RequestState.FINISHED
+        request.finished_at = time.time()
+
+    @property
+    def num_waiting(self) -> int:
+        return len(self.waiting_queue)
+
+    @property
+    def num_running(self) -> int:
+        return len(self.running_batch)
+
+    @property
+    def num_prefilling(self) -> int:
+        return len(self.prefilling)
+
+    @property
+    def is_idle(self) -> bool:
+        return self.num_waiting == 0 and self.num_running == 0 and self.num_prefilling == 0
+
+    # ── paged step planning ─────────────────────────────────────────────────
+
+    def _alloc_device(self, dev: torch.device) -> None:
+        B = self.max_batch_size
+        max_tokens = B + self.chunked_prefill_size
+        # decode takes at most one page per request; the chunks at most the
+        # budget's pages plus one partial page per chunk
+        self._max_new_pages = 2 * B + -(-self.chunked_prefill_size // KV_PAGE_SIZE) + 1
+        upload_ints = B * _ENTRY_INTS + self._max_new_pages
+        i32 = dict(dtype=torch.int32, device=dev)
+        i64 = dict(dtype=torch.int64, device=dev)
+        self._dev = dict(
+            tables=torch.zeros(B, self.width, **i32),
+            upload=torch.empty(upload_ints, **i32),
+            slots=torch.empty(max_tokens, **i64),
+            positions=torch.empty(max_tokens, **i64),
+            cu=torch.zeros(B + 1, **i64),
+            step_tables=torch.zeros(B, self.width, **i32),
+            step_lens=torch.zeros(B, **i32),
+            rows=torch.zeros(B, **i32),
+            errors=_lib.DeviceErrors(dev),
+        )
+        self._pinned = [torch.empty(upload_ints, dtype=torch.int32, pin_memory=True)
+                        for _ in range(self._RING)]
+        self._events = [None] * self._RING
+        self._ring = 0
+
+    def _retire(self, lst: list[InferenceRequest]) -> list[InferenceRequest]:
+        keep = []
+        for r in lst:
+            if r.is_done:
+                if r.seq is not None:
+                    self.kv_cache.free_pages(r.seq.page_table)
+                    r.seq.page_table = []
+                if r.row >= 0:
+                    heapq.heappush(self._free_rows, r.row)
+                    r.row = -1
+            else:
+                keep.append(r)
+        return keep
+
+    def plan_host(self) -> StepPlan | None:
+        """The host half of ``plan_step``: scheduling decisions, page
+        allocation and the upload record (``plan.upload``); device tensors are
+        left unset. Returns None when nothing is scheduled."""
+        if self.kv_cache is None:
+            raise RuntimeError("plan_step needs a PagedKVCache (kv_cache=...)")
+        if self._last is not None:
+            raise RuntimeError("complete_step the previous plan before planning another")
+        cache = self.kv_cache
+        P = KV_PAGE_SIZE
+        with self.lock:
+            self.running_batch = self._retire(self.running_batch)
+            self.prefilling = self._retire(self.prefilling)
+            rec = []  # (request, start, count, held, new)
+            need_decode = 0
+            for r in self.running_batch:
+                seq = r.seq
+                start = seq.seq_len
+                held = len(seq.page_table)
+                new = (start + P) // P - held   # pages to cover start + 1 tokens
+                rec.append((r, start, 1, held, new))
+                need_decode += new
+            free = cache.num_free_pages - need_decode
+            if free < 0:
+                cache.alloc_pages(need_decode)  # raises the reference's OOM error
+            budget = self.chunked_prefill_size
+            prefill: list[tuple[InferenceRequest, int, int]] = []
+
+            def take(r: InferenceRequest) -> int:
+                nonlocal free, budget
+                start = r.seq.seq_len
+                held = len(r.seq.page_table)
+                room = held * P - start + free * P
+                n = min(len(r.input_ids) - r.num_prefilled, budget, room)
+                if n <= 0:
+                    return 0
+                new = -(-(start + n) // P) - held
+                free -= new
+                budget -= n
+                rec.append((r, start, n, held, new))
+                prefill.append((r, start, n))
+                return n
+
+            stopped = False
+            for r in self.prefilling:
+                if budget == 0:
+                    break
+                if take(r) == 0:
+                    stopped = True
+                    break
+            while (not stopped and budget > 0 and self.waiting_queue
+                   and len(self.running_batch) + len(self.prefilling) < self.max_batch_size):
+                r = self.waiting_queue[0]
+                if r.seq is None:
+                    r.seq = SequenceKVState(max_pages=self.width)
+                if take(r) == 0:
+                    break
+                self.waiting_queue.popleft()
+                r.state = RequestState.PREFILLING
+                r.row = heapq.heappop(self._free_rows)
+                self.prefilling.append(r)
+            if not rec:
+                return None
+
+            total_new = sum(e[4] for e in rec)
+            pages = cache.alloc_pages(total_new)[::-1] if total_new else []
+            n = len(rec)
+            flat = []
+            page_off = tok_off = 0
+            for r, start, count, held, new in rec:
+                flat += (r.row, start, count, held, new, page_off, tok_off, 0)
+                if new:
+                    r.seq.page_table += pages[page_off:page_off + new]
+                page_off += new
+                tok_off += count
+                r.seq.seq_len = start + count
+            for r, _, count in prefill:
+                r.num_prefilled += count
+            up = np.array(flat + pages, dtype=np.int32)
+            decode = [e[0] for e in rec[:len(self.running_batch)]]
+            plan = StepPlan(decode=decode, prefill=prefill, num_tokens=tok_off, upload=up,
+                            slot_mapping=None, positions=None, cu_seqlens=None,
+                            block_tables=None, seq_lens=None, rows=None)
+            self._last = plan
+            return plan
+
+    def plan_step(self) -> StepPlan | None:
+        """Schedules one step and writes its device tensors (one upload, one
+        launch, on the current stream of the cache's device)."""
+        if self.kv_cache is not None and self._dev is None:
+            raise RuntimeError(
+                f"plan_step runs its kernel on a ROCm GPU; the cache is on {self.kv_cache.device}")
+        plan = self.plan_host()
+        if plan is None:
+            return None
+        return self.launch_plan(plan)
+
+    def launch_plan(self, plan: StepPlan) -> StepPlan:
+        """The device half of ``plan_step``: uploads ``plan.upload`` and runs
+        mkv_step_plan, filling the plan's device tensors."""
+        if self._dev is None:
+            raise RuntimeError("launch_plan needs the scheduler's pool on a ROCm GPU")
+        if plan is not self._last or plan.slot_mapping is not None:
+            raise RuntimeError("launch_plan takes the plan plan_host just returned, once")
+        d = self._dev
+        dev = self.kv_cache.device
+        up = plan.upload
+        n = plan.num_entries
+        i = self._ring
+        self._ring = (i + 1) % self._RING
+        if self._events[i] is not None:
+            self._events[i].synchronize()
+        staging = self._pinned[i]
+        staging.numpy()[:up.size] = up
+        d["upload"][:up.size].copy_(staging[:up.size], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(dev))
+        self._events[i] = ev
+        # per-step table width: the longest entry's pages (16-entry granules)
+        npages = plan.upload[:n * _ENTRY_INTS].reshape(n, _ENTRY_INTS)
+        width = int((npages[:, 3] + npages[:, 4]).max())
+        width = min(self.width, -(-width // 16) * 16)
+        base = d["upload"].data_ptr()
+        _lib.call("mkv_step_plan", d["tables"].data_ptr(), d["tables"].stride(0), self.width,
+                  self.max_batch_size, base, n, base + 4 * n * _ENTRY_INTS,
+                  up.size - n * _ENTRY_INTS, self.kv_cache.num_pages, d["slots"].data_ptr(),
+                  d["positions"].data_ptr(), plan.num_tokens, d["step_tables"].data_ptr(),
+                  d["step_tables"].stride(0), width, d["step_lens"].data_ptr(),
+                  d["rows"].data_ptr(), d["cu"].data_ptr(), d["errors"].ptr(),
+                  _lib.stream_of(dev))
+        T = plan.num_tokens
+        plan.slot_mapping = d["slots"][:T]
+        plan.positions = d["positions"][:T]
+        plan.cu_seqlens = d["cu"][:n + 1]
+        plan.block_tables = d["step_tables"][:n, :width]
+        plan.seq_lens = d["step_lens"][:n]
+        plan.rows = d["rows"][:n]
+        return plan
+
+    def complete_step(self, plan: StepPlan, next_tokens=None) -> list[InferenceRequest]:
+        """Applies one sampled token per entry (decode entries, then chunks;
+        a chunk that did not finish its prompt ignores its token). Returns the
+        requests that finished."""
+        if plan is not self._last:
+            raise RuntimeError("complete_step takes the last plan, once")
+        self._last = None
+        toks = [0] * plan.num_entries if next_tokens is None else list(next_tokens)
+        if len(toks) != plan.num_entries:
+            raise ValueError(f"{len(toks)} tokens for {plan.num_entries} entries")
+        done = []
+        now = time.time()
+        eos, max_len = self.eos_token_id, self.max_seq_len
+        nd = len(plan.decode)
+        with self.lock:
+            for i, r in enumerate(plan.decode + [r for r, _, _ in plan.prefill]):
+                if i >= nd:
+                    if r.num_prefilled < len(r.input_ids):
+                        continue
+                    r.state = RequestState.DECODING
+                    r.first_token_at = now
+                    self.prefilling.remove(r)
+                    self.running_batch.append(r)
+                tok = int(toks[i])
+                gen = r.generated_tokens
+                gen.append(tok)
+                if (len(gen) >= r.max_new_tokens or tok == eos or r.seq.seq_len >= max_len):
+                    r.state = RequestState.FINISHED
+                    r.finished_at = now
+                    done.append(r)
+        return done
+
+    def check_errors(self) -> None:
+        """Synchronises and raises MkvDeviceError if a step plan was malformed."""
+        if self._dev is not None:
+            self._dev["errors"].check("ContinuousBatchScheduler")
