@@ -330,6 +330,20 @@ int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
                       int64_t block_bytes, int64_t pool_blocks, const int32_t* ids, int32_t n,
                       const void* in, int32_t* err, void* stream);
 
+/*
+ * Zero-fill of blocks ids[0..n) in every plane of a layered pool (the layout
+ * of mkv_pack_blocks): a GDN state pool's planes are its layers and its blocks
+ * request slots, so one call gives a newly admitted request zero recurrent
+ * (or conv) states in every layer. Replaces the zero initial states the
+ * reference builds per request (_init_gdn_states / _init_conv_states,
+ * muserve/model/qwen35_model.py:28-49) for slots reused across requests.
+ * Requirements as for mkv_pack_blocks; an id outside [0, pool_blocks) sets
+ * MKV_DEVERR_STATE_SLOT and is skipped. Ids must be unique within a call.
+ */
+int mkv_zero_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                    int64_t block_bytes, int64_t pool_blocks, const int32_t* ids, int32_t n,
+                    int32_t* err, void* stream);
+
 /* ---- prefix hashing ------------------------------------------------------ */
 
 /*

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
                               _P, _P],
     "mkv_pack_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P, _P],
     "mkv_unpack_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P, _P],
+    "mkv_zero_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P],
     "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],
     "mkv_check_conversions": [_P, _P],
     "mkv_bm_state_bytes": [_I32],

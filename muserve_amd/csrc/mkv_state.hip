@@ -161,6 +161,40 @@ int state_move(const char* fn, const void* pool0, int64_t bytes0, const void* de
 }
 
 // ---------------------------------------------------------------------------
+// Block zero-fill of a layered pool: a new request's GDN state slots start as
+// zeros in every layer. Same grid as the moves (piece, block, plane); every
+// store is a streaming zero store.
+// ---------------------------------------------------------------------------
+struct ZeroArgs {
+  uint8_t* pool;
+  int64_t bytes;
+  int64_t plane_stride;
+  int64_t pool_blocks;
+  const int32_t* ids;
+  int32_t n;
+  int32_t* err;
+};
+
+__global__ __launch_bounds__(kThreads) void zero_blocks_kernel(ZeroArgs a) {
+  const int64_t base = (int64_t)blockIdx.x * kPiece;
+  uint8_t* plane = a.pool + (int64_t)blockIdx.z * a.plane_stride;
+  for (int64_t b = blockIdx.y; b < a.n; b += gridDim.y) {
+    const int32_t id = a.ids[b];
+    if (id < 0 || id >= a.pool_blocks) {
+      if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.z == 0)
+        raise_err(a.err, MKV_DEVERR_STATE_SLOT);
+      continue;
+    }
+    uint8_t* blk = plane + (int64_t)id * a.bytes + base;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t off = (u * kThreads + threadIdx.x) * 16;
+      if (base + off < a.bytes) st_stream(blk, (uint32_t)off, u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // GDN decode conv (muserve/model/qwen35_layer_v2.py:163-201, decode branch
 // :187-192), per request slot and in place:
 //   out[b,c] = silu(sum_k w[c,k] p_k), p = (state[c, W-3 .. W-1], x[b,c]),
@@ -287,6 +321,32 @@ extern "C" int mkv_unpack_blocks(void* pool, int64_t plane_stride, int32_t num_p
   return state_move<false>("mkv_unpack_blocks", pool, block_bytes, in, nullptr, 0, nullptr,
                            pool_blocks, ids, n, err, as_stream(stream), num_planes,
                            num_planes > 1 ? plane_stride : 0);
+}
+
+extern "C" int mkv_zero_blocks(void* pool, int64_t plane_stride, int32_t num_planes,
+                               int64_t block_bytes, int64_t pool_blocks, const int32_t* ids,
+                               int32_t n, int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(n >= 0 && pool_blocks >= 0 && block_bytes >= 0 && plane_stride >= 0 &&
+                  num_planes >= 1,
+              MKV_E_INVALID, "mkv_zero_blocks: negative size");
+  MKV_REQUIRE(num_planes <= (int32_t)kMaxGridY, MKV_E_UNSUPPORTED,
+              "mkv_zero_blocks: more than %u planes", kMaxGridY);
+  MKV_REQUIRE(num_planes == 1 || plane_stride >= pool_blocks * block_bytes, MKV_E_INVALID,
+              "mkv_zero_blocks: planes must not overlap (plane_stride >= blocks x bytes)");
+  if (n == 0 || block_bytes == 0) return MKV_OK;
+  MKV_REQUIRE(pool && ids && err, MKV_E_INVALID, "mkv_zero_blocks: null pointer");
+  MKV_REQUIRE(aligned16(pool) && block_bytes % 16 == 0 &&
+                  (num_planes == 1 || plane_stride % 16 == 0),
+              MKV_E_ALIGN, "mkv_zero_blocks: pool, block bytes and plane stride must be 16-byte aligned");
+  const int64_t pieces = (block_bytes + kPiece - 1) / kPiece;
+  MKV_REQUIRE(pieces < (1ll << 31), MKV_E_UNSUPPORTED, "mkv_zero_blocks: blocks too large");
+  ZeroArgs a{(uint8_t*)pool, block_bytes, num_planes > 1 ? plane_stride : 0, pool_blocks, ids, n,
+             err};
+  const dim3 grid((unsigned)pieces, (unsigned)n < kMaxGridY ? (unsigned)n : kMaxGridY,
+                  (unsigned)num_planes);
+  hipLaunchKernelGGL(zero_blocks_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+  return check_launch("mkv_zero_blocks");
 }
 
 namespace mkv {

@@ -16,7 +16,9 @@ Attached to a ``PagedKVCache`` it also plans whole steps for the pool:
   the first request that gets none ends the step's prefill. Pages come from
   the pool's LIFO free list in the order repeated ``alloc_pages(1)`` calls
   would give them (decode entries first, then the chunks). An admitted
-  request takes the smallest free batch row, which is also its GDN state slot.
+  request takes the smallest free batch row, which is also its GDN state slot
+  (with ``state_pool=``, ``launch_plan`` zeroes an admitted request's slots in
+  every layer).
 * One ``mkv_step_plan`` launch then writes the step's slot mapping, positions,
   cu_seqlens, per-entry block tables (``to_page_table_tensor`` layout:
   pages, then zeros), sequence lengths and rows on the device. The host only
@@ -106,6 +108,7 @@ class StepPlan:
     block_tables: torch.Tensor          # [num_entries, width] int32
     seq_lens: torch.Tensor              # [num_entries] int32, after the step
     rows: torch.Tensor                  # [num_entries] int32 batch rows / GDN state slots
+    admitted: list[InferenceRequest] = field(default_factory=list)  # the last prefill entries
 
     @property
     def num_decode(self) -> int:
@@ -129,7 +132,7 @@ class ContinuousBatchScheduler:
     def __init__(self, max_batch_size: int = 8, max_seq_len: int = 32768,
                  device: torch.device = None, *, kv_cache: PagedKVCache | None = None,
                  chunked_prefill_size: int = CHUNKED_PREFILL_SIZE,
-                 eos_token_id: int | None = None):
+                 eos_token_id: int | None = None, state_pool=None):
         self.max_batch_size = max_batch_size
         self.max_seq_len = max_seq_len
         self.device = device
@@ -146,6 +149,12 @@ class ContinuousBatchScheduler:
         self.width = -(-max_seq_len // KV_PAGE_SIZE)  # pages per row
         self._last: StepPlan | None = None
         self._dev = None
+        # GDN state pool indexed by batch row: an admitted request's slots are
+        # zeroed in every layer by launch_plan
+        if state_pool is not None and state_pool.num_slots < max_batch_size:
+            raise ValueError(f"state pool has {state_pool.num_slots} slots for "
+                             f"{max_batch_size} batch rows")
+        self.state_pool = state_pool
         if kv_cache is not None:
             if chunked_prefill_size <= 0:
                 raise ValueError("chunked_prefill_size must be positive")
@@ -297,6 +306,7 @@ class ContinuousBatchScheduler:
                 if take(r) == 0:
                     stopped = True
                     break
+            admitted = []
             while (not stopped and budget > 0 and self.waiting_queue
                    and len(self.running_batch) + len(self.prefilling) < self.max_batch_size):
                 r = self.waiting_queue[0]
@@ -308,6 +318,7 @@ class ContinuousBatchScheduler:
                 r.state = RequestState.PREFILLING
                 r.row = heapq.heappop(self._free_rows)
                 self.prefilling.append(r)
+                admitted.append(r)
             if not rec:
                 return None
 
@@ -329,7 +340,7 @@ class ContinuousBatchScheduler:
             decode = [e[0] for e in rec[:len(self.running_batch)]]
             plan = StepPlan(decode=decode, prefill=prefill, num_tokens=tok_off, upload=up,
                             slot_mapping=None, positions=None, cu_seqlens=None,
-                            block_tables=None, seq_lens=None, rows=None)
+                            block_tables=None, seq_lens=None, rows=None, admitted=admitted)
             self._last = plan
             return plan
 
@@ -384,6 +395,9 @@ class ContinuousBatchScheduler:
         plan.block_tables = d["step_tables"][:n, :width]
         plan.seq_lens = d["step_lens"][:n]
         plan.rows = d["rows"][:n]
+        if self.state_pool is not None and plan.admitted:
+            # the admitted requests are the last prefill entries
+            self.state_pool.reset(plan.rows[n - len(plan.admitted):])
         return plan
 
     def complete_step(self, plan: StepPlan, next_tokens=None) -> list[InferenceRequest]:

@@ -72,6 +72,24 @@ class StatePool:
             slots = slots.to(device=self.device, dtype=torch.int32)
         return slots.contiguous()
 
+    def reset(self, slots) -> None:
+        """Zeroes the recurrent and conv states of ``slots`` in every layer, the
+        zero initial states a new request starts from (``_init_gdn_states`` /
+        ``_init_conv_states``, muserve/model/qwen35_model.py:28-49), for slots
+        reused across requests. Slots must be unique; one launch per pool."""
+        if not isinstance(slots, torch.Tensor):
+            slots = torch.as_tensor(list(slots), dtype=torch.int32)
+        slots = self._check(slots)
+        n = slots.numel()
+        if n == 0:
+            return
+        for pool in (self.state, self.conv):
+            if pool is None:
+                continue
+            _lib.call("mkv_zero_blocks", pool.data_ptr(), pool.stride(0) * pool.element_size(),
+                      self.num_layers, self._entry_bytes(pool), self.num_slots, slots.data_ptr(),
+                      n, self._errors.ptr(), _lib.stream_of(self.device))
+
     def gather(self, layer: int, slots: torch.Tensor,
                out: tuple[torch.Tensor, torch.Tensor | None] | None = None):
         """(state[layer, slots], conv[layer, slots]) as contiguous [n, ...] buffers."""

@@ -17,6 +17,15 @@ def scatter(pool: torch.Tensor, layer: int, slots: torch.Tensor, x: torch.Tensor
     pool[layer].index_copy_(0, slots.to(torch.int64), x)
 
 
+def reset(pool: torch.Tensor, slots) -> None:
+    """A new request's states: zeros in every layer of a pool [layers, slots,
+    ...] (the torch.zeros of _init_gdn_states / _init_conv_states,
+    muserve/model/qwen35_model.py:28-49). Slots outside the pool are skipped."""
+    for s in [int(x) for x in slots]:
+        if 0 <= s < pool.shape[1]:
+            pool[:, s] = 0
+
+
 def pack_blocks(pool: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
     """Host-tier pack of a layered pool [planes, blocks, ...]: every plane's
     blocks ids, plane-major -> [planes, n, ...]. An id outside the pool gives

@@ -50,6 +50,9 @@ int main() {
                                                              N, 4, N, E, N));
   expect_rejected("pack_blocks", mkv_pack_blocks(N, 0, 1, 8192, 4, nullptr, 1, N, E, N));
   expect_rejected("unpack_blocks", mkv_unpack_blocks(N, 0, 1, 8192, 4, nullptr, 1, N, E, N));
+  expect_rejected("zero_blocks", mkv_zero_blocks(N, 0, 1, 8192, 4, nullptr, 1, E, N));
+  expect_rejected("zero_blocks overlap", mkv_zero_blocks(N, 16, 2, 8192, 4, nullptr, 1, E, N));
+  expect_ok("zero_blocks empty", mkv_zero_blocks(N, 0, 1, 8192, 4, nullptr, 0, E, N));
   expect_rejected("block_hash", mkv_block_hash_sha256(N, nullptr, nullptr, 1, 8, nullptr, E, N));
   expect_rejected("bm_init", mkv_bm_init(N, 16, nullptr, N));
   expect_rejected("bm_step", mkv_bm_step(N, 16, nullptr, 1, 1, nullptr, nullptr, nullptr, nullptr, 4,

@@ -186,3 +186,40 @@ def test_malformed_entries_raise_without_faulting():
     torch.cuda.synchronize()
     assert err.item() == _lib.DEVERR_TABLE
     assert slots[:10].cpu().tolist() == [7] * 6 + [96, 97, 98, 99]
+
+
+def test_admitted_requests_get_zeroed_state_slots():
+    """With a state pool attached, each step zeroes the GDN state slots (in
+    every layer) of exactly the requests it admits: their rows."""
+    case("scheduler admissions zero their GDN state slots")
+    from muserve_amd.state_pool import StatePool
+    rng = np.random.default_rng(5)
+    batch = 6
+    cache = PagedKVCache(256, num_layers=1, dtype=torch.bfloat16, device=DEV, verbose=False)
+    pool = StatePool(num_layers=3, num_slots=batch + 2, state_shape=(2, 16, 16),
+                     conv_shape=(64, 4), device=DEV)
+    s = ContinuousBatchScheduler(max_batch_size=batch, max_seq_len=512, kv_cache=cache,
+                                 chunked_prefill_size=96, state_pool=pool)
+    for i in range(14):
+        s.add_request(req(i, int(rng.integers(1, 120)), int(rng.integers(1, 6))))
+    admitted_total = 0
+    while True:
+        pool.state.fill_(7.0)  # every slot dirty before the step
+        pool.conv.fill_(3.0)
+        plan = s.plan_step()
+        if plan is None:
+            break
+        torch.cuda.synchronize()
+        rows = {r.row for r in plan.admitted}
+        assert rows == set(plan.rows.cpu().tolist()[plan.num_entries - len(plan.admitted):])
+        st, cv = pool.state.cpu(), pool.conv.cpu().float()
+        for slot in range(pool.num_slots):
+            want = 0.0 if slot in rows else None
+            if want is None:
+                assert (st[:, slot] == 7.0).all() and (cv[:, slot] == 3.0).all()
+            else:
+                assert (st[:, slot] == 0).all() and (cv[:, slot] == 0).all()
+        admitted_total += len(rows)
+        s.complete_step(plan)
+    pool.check_errors()
+    assert admitted_total == 14

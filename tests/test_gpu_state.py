@@ -55,6 +55,36 @@ def test_bad_slot_is_reported():
     assert st[1].abs().sum().item() == 0 and cv[1].float().abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("layers,slots_n", [(3, 64), (45, 8)])
+def test_reset_zeroes_only_the_given_slots(layers, slots_n):
+    """StatePool.reset vs the oracle's zero initial states: the given slots of
+    every layer of both pools become zeros, every other byte is unchanged, an
+    out-of-pool slot is flagged and skipped."""
+    case(f"state pool reset, {layers} layers x {slots_n} slots")
+    g = torch.Generator().manual_seed(layers)
+    pool = StatePool(num_layers=layers, num_slots=slots_n, device=DEV)
+    st_cpu = torch.randn(pool.state.shape, generator=g)
+    cv_cpu = torch.randn(pool.conv.shape, generator=g).bfloat16()
+    pool.state.copy_(st_cpu.to(DEV))
+    pool.conv.copy_(cv_cpu.to(DEV))
+    slots = torch.randperm(slots_n, generator=g)[:max(1, slots_n // 3)].to(torch.int32)
+    pool.reset(slots.to(DEV))
+    torch.cuda.synchronize()
+    pool.check_errors()
+    ref.reset(st_cpu, slots)
+    ref.reset(cv_cpu, slots)
+    assert torch.equal(pool.state.cpu().view(torch.int32), st_cpu.view(torch.int32))
+    assert torch.equal(pool.conv.cpu().view(torch.int16), cv_cpu.view(torch.int16))
+    pool.reset([])  # nothing to do
+    pool.reset([slots_n - 1, slots_n + 5])
+    with pytest.raises(_lib.MkvDeviceError, match="state-pool slot"):
+        pool.check_errors()
+    ref.reset(st_cpu, [slots_n - 1, slots_n + 5])
+    ref.reset(cv_cpu, [slots_n - 1, slots_n + 5])
+    assert torch.equal(pool.state.cpu().view(torch.int32), st_cpu.view(torch.int32))
+    assert torch.equal(pool.conv.cpu().view(torch.int16), cv_cpu.view(torch.int16))
+
+
 @pytest.mark.parametrize("channels,width", [(2048, 4), (1536, 3)])
 def test_conv_decode_in_place(channels, width):
     case(f"GDN decode conv in place, {channels} channels, state width {width}")
