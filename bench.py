@@ -1101,7 +1101,8 @@ def sched_requests(n: int, seed: int = SCHED_SEED) -> tuple[np.ndarray, np.ndarr
     return prompts, rng.integers(32, SCHED_MAX_NEW + 1, n)
 
 
-def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
+def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
+              hybrid: bool = False) -> dict:
     """Continuous-batching serving steps on one TP rank, driven by the
     scheduler's step plan: a backlog of requests, at most 256 running, a
     4096-token chunked-prefill budget per step (muserve/config.py:33,40).
@@ -1110,10 +1111,18 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
     the append of every scheduled token's K/V through the slot mapping and
     paged decode attention (4 query heads) for the decode entries through the
     plan's tables; complete_step retires requests at their output length.
-    The warmup fills the batch; the timed steps run with it full."""
+    The warmup fills the batch; the timed steps run with it full.
+    fp8: an e4m3fn pool (quantise on append, dequantise inside attention).
+    hybrid: the 60-layer stack in model order; each of the 45 GDN layers moves
+    the scheduled requests' state slots (a request's batch row is its slot,
+    zeroed at admission): decode entries through the fused recurrent gather +
+    in-place decode conv, prefill entries through a gather of both states,
+    then a scatter of the recurrent states back (the GDN recurrence itself is
+    model math and is not run)."""
     from muserve_amd.kernels import attention as A
     from muserve_amd.kv_cache import PagedKVCache
     from muserve_amd.scheduler import ContinuousBatchScheduler, InferenceRequest
+    from muserve_amd.state_pool import StatePool, gdn_ordinal
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -1122,17 +1131,23 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
     pages = SCHED_BATCH * width + 64  # every running request can reach max_seq: no OOM
     n_req = 4096
     prompts, outs = sched_requests(n_req)
+    kv_dtype = torch.float8_e4m3fn if fp8 else torch.bfloat16
     cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
-                         dtype=torch.bfloat16, device=dev, verbose=False)
+                         dtype=kv_dtype, device=dev, verbose=False)
     cache.shuffle_free_list(torch.Generator().manual_seed(SCHED_SEED))
     free0 = list(cache._free_pages)
     chunk = 4096
+    gen = torch.Generator(device=dev).manual_seed(SCHED_SEED)
+    pool = None
+    if hybrid:
+        pool = StatePool(num_layers=45, num_slots=SCHED_BATCH, device=dev)
+        pool.state.normal_(generator=gen)
+        pool.conv.normal_(generator=gen)
     s = ContinuousBatchScheduler(max_batch_size=SCHED_BATCH, max_seq_len=max_seq, kv_cache=cache,
-                                 chunked_prefill_size=chunk)
+                                 chunked_prefill_size=chunk, state_pool=pool)
     for i in range(n_req):
         s.add_request(InferenceRequest(request_id=str(i), input_ids=[0] * int(prompts[i]),
                                        max_new_tokens=int(outs[i])))
-    gen = torch.Generator(device=dev).manual_seed(SCHED_SEED)
     max_t = SCHED_BATCH + chunk
     kin = torch.empty(LAYERS, max_t * HEAD_DIM, dtype=torch.bfloat16, device=dev)
     vin = torch.empty_like(kin)
@@ -1141,12 +1156,22 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
     q = torch.empty(LAYERS, SCHED_BATCH, 1, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
     q.normal_(generator=gen)
     out = torch.empty_like(q)
+    if hybrid:
+        C = pool.conv.shape[2]
+        xin = torch.randn(45, SCHED_BATCH, C, generator=gen, device=dev).bfloat16()
+        wconv = (0.5 * torch.randn(45, C, 1, 4, generator=gen, device=dev)).bfloat16()
+        sbuf = torch.empty((SCHED_BATCH, *pool.state.shape[2:]), dtype=pool.state.dtype,
+                           device=dev)
+        cbuf = torch.empty((SCHED_BATCH, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+        cout = torch.empty(SCHED_BATCH, C, dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
     stamps = Stamps()
-    log(f"pool: {pages} pages x {LAYERS} layers; {n_req} queued requests "
-        f"(prompt median {int(np.median(prompts))}, max {int(prompts.max())})")
+    log(f"pool: {pages} pages x {LAYERS} layers ({kv_dtype}); {n_req} queued requests "
+        f"(prompt median {int(np.median(prompts))}, max {int(prompts.max())})"
+        + ("; 45 GDN layers x 256 state slots" if hybrid else ""))
 
     first_slots = []  # slot mappings of the first steps, checked against the oracle
+    layer_order = list(range(60)) if hybrid else [4 * l + 3 for l in range(LAYERS)]
 
     def one_step(rec=None, host=None, info=None):
         t0 = time.perf_counter()
@@ -1157,14 +1182,27 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
         s.launch_plan(plan)
         if rec is not None:
             rec.append(("plan", sp.end(stream)))
-        T, nd = plan.num_tokens, plan.num_decode
+        T, nd, n = plan.num_tokens, plan.num_decode, plan.num_entries
         if len(first_slots) < 8:
             first_slots.append(plan.slot_mapping.cpu().tolist())
         # the decode half's lengths after this step's append (host copy of
         # what the kernel writes), for the byte count
         ent = plan.upload[:8 * nd].reshape(nd, 8)
         lens = ent[:, 1] + ent[:, 2]
-        for l in range(LAYERS):
+        for layer in layer_order:
+            if layer % 4 != 3:  # a GDN layer: the scheduled requests' state slots
+                g = gdn_ordinal(layer)
+                sp = stamps.span(stream) if rec is not None else None
+                if nd:
+                    pool.decode_gather(g, plan.rows[:nd], xin[g, :nd], wconv[g],
+                                       state_out=sbuf[:nd], conv_out=cout[:nd])
+                if n > nd:
+                    pool.gather(g, plan.rows[nd:], out=(sbuf[nd:n], cbuf[nd:n]))
+                pool.scatter(g, plan.rows, sbuf[:n])
+                if rec is not None:
+                    rec.append(("gdn", sp.end(stream)))
+                continue
+            l = layer // 4
             sp = stamps.span(stream) if rec is not None else None
             cache.append(plan.slot_mapping, kin[l, :T * HEAD_DIM].view(T, 1, HEAD_DIM),
                          vin[l, :T * HEAD_DIM].view(T, 1, HEAD_DIM), layer=l)
@@ -1173,12 +1211,16 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
             if nd:
                 kp, vp = cache.get_kv_by_layer(l)
                 sp = stamps.span(stream) if rec is not None else None
-                A.attn_decode(q[l, :nd], kp, vp, plan.seq_lens[:nd], plan.block_tables[:nd],
-                              out=out[l, :nd])
+                if fp8:
+                    A.attn_decode_fp8(q[l, :nd], kp, vp, cache.scales[l, 0], cache.scales[l, 1],
+                                      plan.seq_lens[:nd], plan.block_tables[:nd], out=out[l, :nd])
+                else:
+                    A.attn_decode(q[l, :nd], kp, vp, plan.seq_lens[:nd], plan.block_tables[:nd],
+                                  out=out[l, :nd])
                 if rec is not None:
                     rec.append(("attn", sp.end(stream)))
         if info is not None:
-            info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1]))
+            info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1], n))
         s.complete_step(plan)
 
     log(f"warmup {warmup} steps")
@@ -1188,58 +1230,87 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
     cache.check_errors()
     s.check_errors()
     A.check_errors(dev)
+    if pool is not None:
+        pool.check_errors()
     recs = [[] for _ in range(steps)]
     host: list[float] = []
     info: list = []
     log(f"timing {steps} steps ({s.num_running} running, {s.num_prefilling} prefilling, "
         f"{s.num_waiting} waiting)")
+    step_spans: list = []
     t0 = time.perf_counter()
     for j in range(steps):
+        step = stamps.span(stream)
         one_step(recs[j], host, info)
+        step_spans.append(step.end(stream))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     cache.check_errors()
     s.check_errors()
     A.check_errors(dev)
-    tokens = sum(t for t, _, _, _, _ in info)
-    decode_tokens = sum(nd for _, nd, _, _, _ in info)
-    attn_b = append_b = 0.0
-    for T, nd, _, lens, w in info:
+    if pool is not None:
+        pool.check_errors()
+    tokens = sum(x[0] for x in info)
+    decode_tokens = sum(x[1] for x in info)
+    row_kv = HEAD_DIM + 4 if fp8 else ROW  # bytes of one cached K or V row
+    attn_b = append_b = gdn_b = 0.0
+    st_b = pool.state[0, 0].numel() * 4 if hybrid else 0
+    cv_b = pool.conv[0, 0].numel() * 2 if hybrid else 0
+    for T, nd, _, lens, w, n in info:
         if nd:
             ln = lens.astype(np.int64)
-            attn_b += LAYERS * float(2 * ROW * ln.sum() + 4 * (-(-ln // 16)).sum() + 4 * nd
+            attn_b += LAYERS * float(2 * row_kv * ln.sum() + 4 * (-(-ln // 16)).sum() + 4 * nd
                                      + 2 * nd * Q_HEADS * ROW)
-        append_b += LAYERS * float(4 * T * ROW + 8 * T)
-    attn_launches = LAYERS * sum(1 for _, nd, _, _, _ in info if nd)
+        append_b += LAYERS * float(2 * T * ROW + 2 * T * row_kv + 8 * T)
+        if hybrid:  # decode: state gather + conv in place (+ x, out); prefill: both gathered;
+            # then every entry's state scattered back
+            C = pool.conv.shape[2]
+            gdn_b += 45 * float(nd * (2 * st_b + 2 * cv_b + 4 * C + 8)
+                                + (n - nd) * (2 * st_b + 2 * cv_b + 4) + n * (2 * st_b + 4))
+    attn_launches = LAYERS * sum(1 for x in info if x[1])
     attn_ms = _timed(recs, "attn")
     plan_ms = _timed(recs, "plan")
     append_ms = _timed(recs, "append")
     step_s = elapsed / steps
-    value = (attn_b + append_b) / elapsed / 1e9
+    value = (attn_b + append_b + gdn_b) / elapsed / 1e9
     achieved = attn_b / attn_launches / (attn_ms / 1e3) / 1e9
-    ratio = counter_ratios("sched_serving_kernel_trace.md").get("attn")
+    ratio = None if hybrid else counter_ratios("sched_serving_kernel_trace.md").get(
+        "attn_fp8" if fp8 else "attn")
+    kernel = ("mkv_decode_attention_fp8 = attn_chunk_kernel<4, true> + attn_merge_kernel<4>"
+              if fp8 else
+              "mkv_decode_attention_bf16 = attn_chunk_kernel<4, false> + attn_merge_kernel<4>")
     res = {
         "metric": ("achieved HBM GB/s (% of 8 TB/s) of continuous-batching serving steps "
-                   "(scheduler step plan + KV append + paged decode attention); step µs"),
+                   "(scheduler step plan + KV append + paged decode attention"
+                   + (" + GDN state slot moves" if hybrid else "") + "); step µs"),
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16 (fp32 softmax and accumulation)",
+        "vs_baseline": None,
+        "dtype": ("fp8 e4m3fn KV with fp32 scales, bf16 q/out (fp32 softmax and accumulation)"
+                  if fp8 else "bf16 (fp32 softmax and accumulation)")
+                 + ("; fp32 recurrent / bf16 conv GDN states" if hybrid else ""),
         "data": ("synthetic (seeded ~N(0,1) q/K/V; seeded lognormal prompt lengths, uniform "
                  "output lengths; a sampled token is a placeholder)"),
         "config": {
             "workload": ("continuous-batching serving on one TP rank: 4096 queued requests, "
                          "prompts lognormal(median 1024, sigma 1, clip 16..8192), outputs "
                          "uniform 32..512 tokens, at most 256 running, 4096-token chunked "
-                         "prefill budget per step; 15 attention layers, 1 KV head x 256, bf16 "
-                         "pool of 16-token pages, 4 query heads; seed 106"),
+                         "prefill budget per step; 15 attention layers, 1 KV head x 256, "
+                         + ("fp8 e4m3fn" if fp8 else "bf16") + " pool of 16-token pages, "
+                         "4 query heads"
+                         + ("; 60 layers in model order with 45 GDN layers' state slots "
+                            "([8,128,128] fp32 + [2048,4] bf16 per request)" if hybrid else "")
+                         + "; seed 106"),
             "max_batch": SCHED_BATCH, "chunked_prefill_size": chunk, "layers": LAYERS,
             "kv_heads": 1, "head_dim": HEAD_DIM, "q_heads": Q_HEADS, "pool_pages": pages,
+            "gdn_layers": 45 if hybrid else 0,
         },
+        "step_time": _step_stats(step_spans),
         "tokens_per_s": round(tokens / elapsed, 1),
         "decode_tokens_per_s": round(decode_tokens / elapsed, 1),
         "prefill_tokens_per_s": round((tokens - decode_tokens) / elapsed, 1),
         "mean_entries": {"decode": round(decode_tokens / steps, 1),
-                         "prefill_chunks": round(sum(p for _, _, p, _, _ in info) / steps, 2),
+                         "prefill_chunks": round(sum(x[2] for x in info) / steps, 2),
                          "tokens": round(tokens / steps, 1)},
         "plan_device_us": round(plan_ms * 1e3, 2),
         "plan_device_note": "upload of the step records + the mkv_step_plan launch (events)",
@@ -1248,18 +1319,22 @@ def run_sched(steps: int, warmup: int, with_cpu: bool) -> dict:
         "append_us_per_layer": round(append_ms * 1e3, 2),
         "attn_us_per_layer": round(attn_ms * 1e3, 2),
         "roofline": {
-            "bound": "hbm",
-            "kernel": "mkv_decode_attention_bf16 = attn_chunk_kernel<4, false> + attn_merge_kernel<4>",
+            "bound": "hbm", "kernel": kernel,
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": round(ratio * attn_b / attn_launches) if ratio else None,
             "traffic_to_algorithmic": ratio,
             "traffic_source": ("rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 of the same kernel in "
-                               "this workload, profiles/sched_serving_kernel_trace.md"),
+                               "this workload, profiles/sched_serving_kernel_trace.md"
+                               if ratio else None),
             "mean_launch_us": round(attn_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": round(attn_b / attn_launches),
         },
     }
+    if hybrid:
+        gdn_ms = _timed(recs, "gdn")
+        res["gdn_us_per_layer"] = round(gdn_ms * 1e3, 2)
+        res["gdn_GBps"] = round(gdn_b / steps / 45 / (gdn_ms / 1e3) / 1e9, 2)
     if with_cpu:
         log("cpu baseline (scheduler oracle: per-token page bookkeeping of the same trace)")
         res["cpu_baseline"] = sched_cpu_baseline(prompts, outs, pages, free0, chunk, max_seq,
@@ -1483,7 +1558,7 @@ def main() -> int:
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
-                             "sched"],
+                             "sched", "sched_fp8", "sched_hybrid"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1503,7 +1578,9 @@ def main() -> int:
               "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True),
               "offload": run_offload,
               "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True),
-              "sched": run_sched}[args.workload]
+              "sched": run_sched,
+              "sched_fp8": lambda *a: run_sched(*a, fp8=True),
+              "sched_hybrid": lambda *a: run_sched(*a, hybrid=True)}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
@@ -1511,7 +1588,7 @@ def main() -> int:
         steps, warmup = 5, 1  # a step is the whole 4096-request trace
     if args.workload == "offload" and steps == 1000:
         steps, warmup = 10, 2  # a step moves ~1.5 GB across the host link
-    if args.workload == "sched" and (steps, warmup) == (1000, 20):
+    if args.workload.startswith("sched") and (steps, warmup) == (1000, 20):
         steps, warmup = 500, 300  # the warmup fills the 256-request batch
     # a garbage-collector pass in the timed loop stalls the host for tens of
     # ms, the stream drains and the event span around the launch absorbs the
