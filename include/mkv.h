@@ -507,6 +507,35 @@ int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_c
 /* ---- self-test ------------------------------------------------------------ */
 
 /*
+ * Varlen prefill attention, causal or not: the math of attn_prefill
+ * (muserve/kernels/attention.py:6-25, flash_attn_varlen_func) for 4 query
+ * heads per KV head and head_dim 256, bf16 in and out, fp32 softmax and
+ * accumulation, probabilities rounded to bf16 for the P V product.
+ * Sequence b's queries are rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) of q
+ * [num_q_tokens, num_q_heads, 256]; its keys are either
+ *   contiguous (page_table NULL): rows [cu_seqlens_k[b], cu_seqlens_k[b+1])
+ *     of k/v [kv_units, num_kv_heads, 256], or
+ *   paged: the first seq_lens_k[b] tokens of block table row b over a pool
+ *     [kv_units pages, 16, num_kv_heads, 256] (chunked prefill: the chunk's
+ *     own K/V appended first, so a query also sees the cached prefix).
+ * Query t of a sequence with nq queries and nk keys sits at position
+ * nk - nq + t (the bottom-right alignment of flash-attention's causal mask)
+ * and, when causal, attends to positions 0 .. nk - nq + t; query head h reads
+ * KV head h / 4. A query that sees no key gets zeros. max_seqlen_q bounds nq
+ * (it sizes the grid). Bad query or key offsets, a sequence longer than its
+ * table or than max_seqlen_q set MKV_DEVERR_TABLE; a page id outside the pool
+ * sets MKV_DEVERR_PAGE and reads zeros.
+ */
+int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v, int64_t kv_units,
+                               int32_t num_kv_heads, int32_t num_q_heads, int32_t head_dim,
+                               const int32_t* page_table, int64_t table_stride,
+                               int32_t table_width, const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, const int32_t* seq_lens_k,
+                               int32_t batch, int64_t num_q_tokens, int32_t max_seqlen_q,
+                               float softmax_scale, int32_t causal, void* out, int32_t* err,
+                               void* stream);
+
+/*
  * On-device check of what the fp8 kernels rely on. Adds into counts[7]
  * (device uint64, caller-zeroed): [0] v_cvt_pk_fp8_f32 results that differ
  * from RNE e4m3fn (|x| <= 448, or not NaN for NaN), [1] v_cvt_pk_bf16_f32

@@ -1,0 +1,287 @@
+// mkv_prefill.hip — varlen prefill attention (gfx950, MFMA): the math of
+// attn_prefill (muserve/kernels/attention.py:6-25, flash_attn_varlen_func)
+// over contiguous K/V, and the same over the paged pool for chunked prefill
+// (a chunk's queries attend to the sequence's cached prefix and to
+// themselves).
+//
+// Sequence b has nq queries and nk keys; query t sits at position nk - nq + t
+// (causal masking aligned to the bottom-right corner) and, when causal,
+// attends to positions 0 .. nk - nq + t. Query head h reads KV head h / 4.
+//
+// A workgroup (4 waves) takes 16 query tokens of one sequence and KV head;
+// wave w holds query head 4*hk + w, so the 4 waves share every K/V tile
+// through LDS. Per 32-token KV tile:
+//   * the tile is staged in LDS: K rows as they are, V transposed (dim-major),
+//     so both products read their MFMA operands as 16-byte LDS loads;
+//   * S = Q K^T on MFMA (v_mfma_f32_16x16x32_bf16): A = 16 query rows x 32
+//     dims held in registers for the whole loop, B = 16 K rows; 8 steps over
+//     head_dim 256 for each 16-token half;
+//   * online softmax in fp32 on the 4 rows x 2 tokens a lane holds (exp2,
+//     log2(e) folded into the scale), reductions over the 16 lanes of a row;
+//   * P goes through a per-wave LDS tile to become the A operand (16 rows x
+//     32 tokens, bf16); O += P V on MFMA, 16 blocks of 16 dims.
+// The output is O / l, rounded to bf16 once.
+#include <math.h>
+
+#include "mkv_device.h"
+
+namespace mkv {
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+constexpr int kPD = 256;           // head_dim
+constexpr int kPRow = kPD * 2;     // bytes of one bf16 row
+constexpr int kPThreads = 256;     // 4 waves
+constexpr int kPG = 4;             // query heads per KV head (one per wave)
+constexpr int kQTok = 16;          // query tokens per workgroup
+constexpr int kKvTile = 32;        // KV tokens per step
+constexpr int kKStride = kPD + 8;  // bf16 per staged K row (padded against bank conflicts)
+constexpr int kVtStride = kKvTile + 8;  // bf16 per transposed V row
+constexpr int kPStride = kKvTile + 8;   // bf16 per P row
+
+struct PrefillArgs {
+  const uint8_t* q;      // [Tq, Hq, 256] bf16
+  const uint8_t* k;      // paged [P, 16, Hkv, 256] or contiguous [Tk, Hkv, 256] bf16
+  const uint8_t* v;
+  const int32_t* table;  // paged: [B, tstride] page ids; null: contiguous
+  int64_t tstride;
+  int32_t twidth;
+  int64_t kv_units;      // pages (paged) or token rows (contiguous)
+  const int32_t* cu_q;   // [B + 1]
+  const int32_t* cu_k;   // contiguous: [B + 1]
+  const int32_t* lens_k; // paged: [B]
+  int64_t num_q;         // query rows Tq
+  int32_t max_q;         // the launch's bound on a sequence's queries
+  uint8_t* out;          // [Tq, Hq, 256] bf16
+  int32_t hkv;
+  int32_t causal;
+  float scale_log2;
+  int32_t* err;
+};
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return f32_to_bf16_rne(x); }
+
+__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKvTile][kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kPD][kVtStride];
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPThreads / 64][kQTok][kPStride];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.y, hk = blockIdx.z;
+  const int32_t qs = a.cu_q[b];
+  const int32_t nq_raw = a.cu_q[b + 1] - qs;
+  // query offsets outside the buffer, or more queries than the launch covers:
+  // flagged; nothing of the sequence (or nothing past the bound) is touched
+  const bool q_ok = qs >= 0 && nq_raw >= 0 && (int64_t)qs + nq_raw <= a.num_q;
+  if ((!q_ok || nq_raw > a.max_q) && tid == 0 && blockIdx.x == 0 && blockIdx.z == 0)
+    raise_err(a.err, MKV_DEVERR_TABLE);
+  const int32_t nq = q_ok ? (nq_raw < a.max_q ? nq_raw : a.max_q) : 0;
+  const int32_t q0 = (int32_t)blockIdx.x * kQTok;
+  if (q0 >= nq) return;  // uniform
+  const int64_t hq = (int64_t)a.hkv * kPG;
+  const int64_t h = hk * kPG + wave;  // this wave's query head
+
+  // the sequence's keys: a length checked against what the table (or the
+  // buffer) holds; a bad one is flagged and clamped
+  int64_t nk, kbase = 0;
+  bool bad = false;
+  if (a.table) {
+    nk = a.lens_k[b];
+    const int64_t cap = (int64_t)a.twidth * 16;
+    if (nk < 0 || nk > cap) {
+      bad = true;
+      nk = nk < 0 ? 0 : cap;
+    }
+  } else {
+    kbase = a.cu_k[b];
+    nk = (int64_t)a.cu_k[b + 1] - kbase;
+    if (kbase < 0 || nk < 0 || kbase + nk > a.kv_units) {
+      bad = true;
+      nk = 0;
+    }
+  }
+  if (bad && tid == 0 && blockIdx.x == 0) raise_err(a.err, MKV_DEVERR_TABLE);
+  const int64_t shift = nk - nq;  // query t sits at position shift + t
+  const int32_t last_q = (q0 + kQTok < nq ? q0 + kQTok : nq) - 1;
+  int64_t kv_end = a.causal ? shift + last_q + 1 : nk;
+  if (kv_end > nk) kv_end = nk;
+
+  // Q as the A operand: row n = query token q0 + n, dims 32 s + 8 g .. +7
+  bf16x8 qa[8];
+  {
+    const bool ok = q0 + n < nq;
+    const uint8_t* row = a.q + (((int64_t)qs + q0 + n) * hq + h) * kPRow;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qa[s] = __builtin_bit_cast(bf16x8, ok ? ld16(row + (32 * s + 8 * g) * 2)
+                                            : u32x4{0u, 0u, 0u, 0u});
+  }
+  // this lane's C rows 4 g + i: query positions, running max and sum
+  float m_run[4], l_run[4];
+  int64_t qpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+    qpos[i] = shift + q0 + 4 * g + i;
+  }
+  f32x4 o[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int32_t* trow = a.table ? a.table + b * a.tstride : nullptr;
+
+  for (int64_t kv0 = 0; kv0 < kv_end; kv0 += kKvTile) {
+    // stage K (row-major) and V (transposed) of tokens kv0 .. kv0+31; a
+    // token past the keys, or on a page outside the pool, is zeros
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + kPThreads * u;  // 16-byte chunk: token r, dims 8 col .. +7
+      const int r = c >> 5, col = c & 31;
+      const int64_t tok = kv0 + r;
+      u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+      if (tok < nk) {
+        int64_t rowi;
+        bool ok = true;
+        if (trow) {
+          const int32_t page = trow[tok >> 4];
+          ok = page >= 0 && page < a.kv_units;
+          if (!ok && col == 0) raise_err(a.err, MKV_DEVERR_PAGE);
+          rowi = ((int64_t)(ok ? page : 0) * 16 + (tok & 15)) * a.hkv + hk;
+        } else {
+          rowi = (kbase + tok) * a.hkv + hk;
+        }
+        if (ok) {
+          kv = ld16(a.k + rowi * kPRow + col * 16);
+          vv = ld16(a.v + rowi * kPRow + col * 16);
+        }
+      }
+      *reinterpret_cast<u32x4*>(&k_lds[r][col * 8]) = kv;
+      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vt_lds[col * 8 + 2 * j][r] = (uint16_t)(w4[j] & 0xffffu);
+        vt_lds[col * 8 + 2 * j + 1][r] = (uint16_t)(w4[j] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // S = Q K^T for the two 16-token halves: lane holds rows 4 g + i, token n
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&k_lds[n][32 * s + 8 * g]);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&k_lds[16 + n][32 * s + 8 * g]);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], k0, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], k1, s1, 0, 0, 0);
+    }
+    const int64_t t0 = kv0 + n, t1 = kv0 + 16 + n;
+    float alpha[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok0 = t0 < nk && (!a.causal || t0 <= qpos[i]);
+      const bool ok1 = t1 < nk && (!a.causal || t1 <= qpos[i]);
+      const float v0 = ok0 ? s0[i] * a.scale_log2 : -INFINITY;
+      const float v1 = ok1 ? s1[i] * a.scale_log2 : -INFINITY;
+      float mx = fmaxf(v0, v1);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float m_new = fmaxf(m_run[i], mx);
+      const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing seen yet
+      alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - m_ref);
+      const float p0 = __builtin_amdgcn_exp2f(v0 - m_ref);
+      const float p1 = __builtin_amdgcn_exp2f(v1 - m_ref);
+      float ps = p0 + p1;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off);
+      l_run[i] = l_run[i] * alpha[i] + ps;
+      m_run[i] = m_new;
+      p_lds[wave][4 * g + i][n] = bf16_bits(p0);
+      p_lds[wave][4 * g + i][16 + n] = bf16_bits(p1);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O += P V: A = P (row n, tokens 8 g .. +7), B = V^T block (dim 16 j + n)
+    const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&p_lds[wave][n][8 * g]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&vt_lds[16 * j + n][8 * g]);
+      o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[j], 0, 0, 0);
+    }
+    __syncthreads();  // the tiles are rewritten by the next step
+  }
+
+  // out[token q0 + 4 g + i][h][16 j + n] = O / l (zeros for a row that saw nothing)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t t = q0 + 4 * g + i;
+    if (t >= nq) continue;
+    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out + (((int64_t)qs + t) * hq + h) * kPRow);
+    const float L = l_run[i];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) orow[16 * j + n] = bf16_bits(L > 0.f ? o[j][i] / L : 0.f);
+  }
+}
+
+}  // namespace
+}  // namespace mkv
+
+using namespace mkv;
+
+extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v,
+                                          int64_t kv_units, int32_t num_kv_heads,
+                                          int32_t num_q_heads, int32_t head_dim,
+                                          const int32_t* page_table, int64_t table_stride,
+                                          int32_t table_width, const int32_t* cu_seqlens_q,
+                                          const int32_t* cu_seqlens_k, const int32_t* seq_lens_k,
+                                          int32_t batch, int64_t num_q_tokens, int32_t max_seqlen_q,
+                                          float softmax_scale, int32_t causal, void* out,
+                                          int32_t* err, void* stream) {
+  clear_error();
+  MKV_REQUIRE(batch >= 0 && kv_units >= 0 && num_kv_heads > 0 && num_q_heads > 0 &&
+                  max_seqlen_q >= 0 && num_q_tokens >= 0 && table_width >= 0 &&
+                  table_stride >= table_width,
+              MKV_E_INVALID, "mkv_prefill_attention_bf16: bad sizes");
+  MKV_REQUIRE(head_dim == kPD, MKV_E_UNSUPPORTED,
+              "mkv_prefill_attention_bf16: head_dim %d unsupported (256)", head_dim);
+  MKV_REQUIRE(num_q_heads == kPG * num_kv_heads, MKV_E_UNSUPPORTED,
+              "mkv_prefill_attention_bf16: %d query heads per KV head unsupported (4)",
+              num_q_heads / num_kv_heads);
+  MKV_REQUIRE(num_kv_heads <= 65535 && batch <= 65535, MKV_E_UNSUPPORTED,
+              "mkv_prefill_attention_bf16: batch or KV heads above 65535");
+  if (batch == 0 || max_seqlen_q == 0) return MKV_OK;
+  MKV_REQUIRE(q && k && v && cu_seqlens_q && out && err &&
+                  (page_table ? seq_lens_k != nullptr : cu_seqlens_k != nullptr),
+              MKV_E_INVALID, "mkv_prefill_attention_bf16: null pointer");
+  MKV_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), MKV_E_ALIGN,
+              "mkv_prefill_attention_bf16: q, k, v and out must be 16-byte aligned");
+  PrefillArgs a;
+  a.q = static_cast<const uint8_t*>(q);
+  a.k = static_cast<const uint8_t*>(k);
+  a.v = static_cast<const uint8_t*>(v);
+  a.table = page_table;
+  a.tstride = table_stride;
+  a.twidth = table_width;
+  a.kv_units = kv_units;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.lens_k = seq_lens_k;
+  a.num_q = num_q_tokens;
+  a.max_q = max_seqlen_q;
+  a.out = static_cast<uint8_t*>(out);
+  a.hkv = num_kv_heads;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.err = err;
+  const dim3 grid((unsigned)((max_seqlen_q + kQTok - 1) / kQTok), (unsigned)batch,
+                  (unsigned)num_kv_heads);
+  hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPThreads), 0, as_stream(stream), a);
+  return check_launch("mkv_prefill_attention_bf16");
+}

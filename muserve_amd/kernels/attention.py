@@ -1,4 +1,5 @@
-"""Paged decode attention over the KV pool (muserve/kernels/attention.py).
+"""Attention over the KV pool (muserve/kernels/attention.py): paged decode,
+and varlen prefill over contiguous K/V or over the pool.
 
 ``attn_decode`` keeps the reference wrapper's signature and meaning
 (muserve/kernels/attention.py:29-42): one query token per sequence attends to
@@ -44,6 +45,96 @@ def workspace_bytes(batch: int, num_kv_heads: int, num_q_heads: int, max_seqlen:
     if n < 0:
         raise ValueError("bad attention shape")
     return n
+
+
+def attn_prefill(
+    q: torch.Tensor,            # [total_tokens, NUM_Q_HEADS, HEAD_DIM] bf16
+    k: torch.Tensor,            # [total_tokens, NUM_KV_HEADS, HEAD_DIM] bf16
+    v: torch.Tensor,            # [total_tokens, NUM_KV_HEADS, HEAD_DIM] bf16
+    cu_seqlens_q: torch.Tensor, # [num_seqs + 1] int32
+    cu_seqlens_k: torch.Tensor, # [num_seqs + 1] int32
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float | None = None,
+    causal: bool = True,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:              # [total_tokens, NUM_Q_HEADS, HEAD_DIM] bf16
+    """Varlen prefill attention (muserve/kernels/attention.py:6-25, the
+    reference's flash_attn_varlen_func): sequence b's queries are rows
+    cu_seqlens_q[b]..cu_seqlens_q[b+1] of q, its keys the same rows range of
+    cu_seqlens_k in k/v; with causal masking aligned to the bottom-right
+    corner (query t of nq sees keys 0 .. nk - nq + t). 4 query heads per KV
+    head, head_dim 256; fp32 softmax and accumulation, probabilities rounded
+    to bf16 for the P V product, one bf16 rounding of the output."""
+    return _prefill(q, k, v, None, cu_seqlens_q, cu_seqlens_k, None, max_seqlen_q, softmax_scale,
+                    causal, out)
+
+
+def attn_prefill_paged(
+    q: torch.Tensor,              # [total_tokens, NUM_Q_HEADS, HEAD_DIM] bf16
+    k_cache: torch.Tensor,        # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] bf16
+    v_cache: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,   # [num_seqs + 1] int32/int64: the step's query rows
+    cache_seqlens: torch.Tensor,  # [num_seqs] int32: keys per sequence, the chunk included
+    page_table: torch.Tensor,     # [num_seqs, max_pages] int32
+    max_seqlen_q: int,
+    softmax_scale: float | None = None,
+    causal: bool = True,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """attn_prefill over the paged pool, for chunked prefill: a chunk's
+    queries (its K/V appended to the pool first) attend to the sequence's
+    cached prefix and to themselves, read through the block table — the
+    prefill counterpart of attn_decode. With a scheduler plan, the prefill
+    entries are plan.cu_seqlens / plan.seq_lens / plan.block_tables past the
+    decode entries."""
+    if page_table is None:
+        raise ValueError("attn_prefill_paged reads the paged pool: page_table is required")
+    return _prefill(q, k_cache, v_cache, page_table, cu_seqlens_q, None, cache_seqlens,
+                    max_seqlen_q, softmax_scale, causal, out)
+
+
+def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scale, causal, out):
+    dev = _lib.require_gpu(q, k, v, page_table, cu_q, cu_k, lens_k)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("attn_prefill takes bf16 q, k and v")
+    Tq, Hq, D = q.shape
+    Hkv = k.shape[-2]
+    if D != HEAD_DIM or k.shape[-1] != D or v.shape != k.shape or Hq != 4 * Hkv:
+        raise ValueError(f"unsupported shapes q {tuple(q.shape)}, k {tuple(k.shape)} "
+                         "(head_dim 256, 4 query heads per KV head)")
+    if page_table is not None and (k.dim() != 4 or k.shape[1] != 16):
+        raise ValueError("the paged pool must be [num_pages, 16, kv_heads, 256]")
+    if page_table is None and k.dim() != 3:
+        raise ValueError("contiguous k/v must be [total_tokens, kv_heads, 256]")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("q, k and v must be contiguous")
+    cu_q = cu_q.to(device=dev, dtype=torch.int32).contiguous()
+    batch = cu_q.numel() - 1
+    if cu_k is not None:
+        cu_k = cu_k.to(device=dev, dtype=torch.int32).contiguous()
+        if cu_k.numel() != batch + 1:
+            raise ValueError("cu_seqlens_k must have as many entries as cu_seqlens_q")
+    if lens_k is not None:
+        if lens_k.dtype != torch.int32 or page_table.dtype != torch.int32:
+            raise TypeError("cache_seqlens and page_table must be int32")
+        if lens_k.numel() != batch or page_table.shape[0] < batch or page_table.stride(1) != 1:
+            raise ValueError("cache_seqlens / page_table rows do not match cu_seqlens_q")
+        lens_k = lens_k.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    units = k.shape[0]
+    _lib.call("mkv_prefill_attention_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), units, Hkv,
+              Hq, D, _lib.ptr(page_table), page_table.stride(0) if page_table is not None else 0,
+              page_table.shape[1] if page_table is not None else 0, cu_q.data_ptr(),
+              _lib.ptr(cu_k), _lib.ptr(lens_k), batch, Tq, int(max_seqlen_q), scale,
+              1 if causal else 0, out.data_ptr(), _errword(dev).ptr(), _lib.stream_of(dev))
+    return out
 
 
 def attn_decode(

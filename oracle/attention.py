@@ -81,6 +81,50 @@ def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
     return (out, mass, smax) if stats else out
 
 
+def prefill_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_q, scale: float,
+                      causal: bool = True, cu_k=None, lens_k=None, page_table=None,
+                      stats: bool = False):
+    """Varlen prefill attention in float64: the math of attn_prefill
+    (muserve/kernels/attention.py:6-25, flash_attn_varlen_func with causal
+    masking aligned to the bottom-right corner, as flash-attention defines it
+    for nk != nq), with query head h reading KV head h // G.
+    q [Tq,Hq,D]; contiguous k/v [Tk,Hkv,D] with cu_k, or a paged pool
+    [P,16,Hkv,D] with page_table [B,W] and lens_k [B]. Sequence b's query
+    token t sits at position nk - nq + t and, when causal, attends to
+    positions 0..that position; a token that sees nothing gets zeros.
+    -> out [Tq,Hq,D] (and, with stats, the attended mass sum p|v| / sum p)."""
+    q = np.asarray(q, dtype=np.float64)
+    Tq, Hq, D = q.shape
+    Hkv = k.shape[-2]
+    G = Hq // Hkv
+    out = np.zeros((Tq, Hq, D))
+    mass = np.zeros((Tq, Hq, D))
+    for b in range(len(cu_q) - 1):
+        q0, q1 = int(cu_q[b]), int(cu_q[b + 1])
+        nq = q1 - q0
+        if page_table is not None:
+            nk = int(lens_k[b])
+            K = gather_kv(k, page_table[b], nk).astype(np.float64)
+            V = gather_kv(v, page_table[b], nk).astype(np.float64)
+        else:
+            k0, k1 = int(cu_k[b]), int(cu_k[b + 1])
+            nk = k1 - k0
+            K = np.asarray(k[k0:k1], dtype=np.float64)
+            V = np.asarray(v[k0:k1], dtype=np.float64)
+        for t in range(nq):
+            last = nk - nq + t if causal else nk - 1
+            if last < 0 or nk == 0:
+                continue
+            for h in range(Hq):
+                s = K[:last + 1, h // G] @ q[q0 + t, h] * scale
+                p = np.exp(s - s.max())
+                w = p / p.sum()
+                out[q0 + t, h] = w @ V[:last + 1, h // G]
+                if stats:
+                    mass[q0 + t, h] = w @ np.abs(V[:last + 1, h // G])
+    return (out, mass) if stats else out
+
+
 def reference_bf16(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                    seq_lens, page_table, scale: float) -> torch.Tensor:
     """muserve/model/qwen35_layer_v2.py:493-502 per sequence, bf16 on the CPU:

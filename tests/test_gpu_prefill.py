@@ -1,0 +1,174 @@
+"""GPU parity of the varlen prefill attention (attn_prefill over contiguous
+K/V, attn_prefill_paged over the pool) vs the float64 oracle.
+
+Tolerance, per output element: one bf16 ulp of the float64 value plus
+2^-8 x the attended mass sum_j p_j |v_j| / sum_j p_j. The second term covers
+the probabilities' rounding to bf16 for the P V product (relative 2^-9 each,
+as in flash attention's bf16 path) with a factor of 2 for the fp32
+evaluation."""
+import numpy as np
+import pytest
+import torch
+
+from muserve_amd import _lib
+from muserve_amd.kernels import attention as A
+from muserve_amd.kv_cache import PagedKVCache
+from muserve_amd.scheduler import ContinuousBatchScheduler, InferenceRequest
+from oracle import attention as att
+from tests.gpu_util import DEV, case
+
+pytestmark = pytest.mark.gpu
+
+
+def within(got: torch.Tensor, want) -> None:
+    want, mass = want
+    got = got.float().cpu().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    tol = ulp + 2.0 ** -8 * mass
+    err = np.abs(got - want)
+    bad = err > tol
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements out of tolerance; worst "
+                           f"{err[bad].max()} at {np.argwhere(bad)[0]}")
+
+
+def seqs(lens, seed):
+    g = torch.Generator().manual_seed(seed)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    return g, cu
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_contiguous_varlen_matches_oracle(causal):
+    lens = [1, 5, 15, 16, 17, 31, 33, 64, 100, 257, 600]
+    case(f"attn_prefill contiguous varlen causal={causal} lens {lens}")
+    g, cu = seqs(lens, 31 + causal)
+    T = int(cu[-1])
+    q = torch.randn(T, 4, 256, generator=g).bfloat16()
+    k = torch.randn(T, 1, 256, generator=g).bfloat16()
+    v = torch.randn(T, 1, 256, generator=g).bfloat16()
+    out = A.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), max(lens),
+                         max(lens), causal=causal)
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.prefill_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                 cu.numpy(), 256 ** -0.5, causal, cu_k=cu.numpy(), stats=True)
+    within(out, want)
+
+
+def test_contiguous_with_prefix_two_kv_heads_and_scale():
+    """nk > nq (a prefix before the queries), 2 KV heads (8 query heads), a
+    softmax scale of 0.1, and a sequence with more queries than keys."""
+    lq = [7, 40, 3, 129]
+    lk = [20, 40, 1, 300]
+    case(f"attn_prefill with prefix: nq {lq}, nk {lk}, 2 KV heads")
+    g = torch.Generator().manual_seed(35)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(lq)]), dtype=torch.int32)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lk)]), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), 8, 256, generator=g).bfloat16()
+    k = torch.randn(int(cu_k[-1]), 2, 256, generator=g).bfloat16()
+    v = torch.randn(int(cu_k[-1]), 2, 256, generator=g).bfloat16()
+    out = A.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), cu_q.to(DEV), cu_k.to(DEV), max(lq),
+                         max(lk), softmax_scale=0.1)
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.prefill_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                 cu_q.numpy(), 0.1, True, cu_k=cu_k.numpy(), stats=True)
+    within(out, want)
+    assert not out[int(cu_q[2]):int(cu_q[2]) + 2].float().abs().sum().item()  # saw nothing
+
+
+def test_paged_chunks_match_oracle():
+    """Chunked prefill over the pool: each sequence has a cached prefix and a
+    chunk (appended first); queries are the chunk's tokens."""
+    prefix = [0, 3, 16, 100, 1000]
+    chunk = [17, 1, 32, 64, 300]
+    case(f"attn_prefill_paged prefix {prefix} chunk {chunk}")
+    g = torch.Generator().manual_seed(36)
+    P = 256
+    kc = torch.randn(P, 16, 1, 256, generator=g).bfloat16()
+    vc = torch.randn(P, 16, 1, 256, generator=g).bfloat16()
+    perm = torch.randperm(P, generator=g)
+    lens = [p + c for p, c in zip(prefix, chunk)]
+    width = max(-(-n // 16) for n in lens)
+    table = torch.zeros(len(lens), width, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(lens):
+        m = -(-n // 16)
+        table[b, :m] = perm[at:at + m].to(torch.int32)
+        at += m
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(chunk)]), dtype=torch.int32)
+    q = torch.randn(int(cu_q[-1]), 4, 256, generator=g).bfloat16()
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
+    out = A.attn_prefill_paged(q.to(DEV), kc.to(DEV), vc.to(DEV), cu_q.to(DEV), seq_lens.to(DEV),
+                               table.to(DEV), max(chunk))
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.prefill_attention(q.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                 cu_q.numpy(), 256 ** -0.5, True, lens_k=seq_lens.numpy(),
+                                 page_table=table.numpy(), stats=True)
+    within(out, want)
+
+
+def test_scheduler_prefill_entries_through_the_pool():
+    """A scheduler step's prefill entries: their tokens' K/V appended through
+    plan.slot_mapping, then attn_prefill_paged on plan.cu_seqlens /
+    plan.seq_lens / plan.block_tables past the decode entries."""
+    case("scheduler prefill chunks -> append -> attn_prefill_paged")
+    rng = np.random.default_rng(7)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    cache = PagedKVCache(1024, num_layers=1, dtype=torch.bfloat16, device=DEV, verbose=False)
+    cache._free_pages = rng.permutation(1024).tolist()
+    s = ContinuousBatchScheduler(max_batch_size=6, max_seq_len=2048, kv_cache=cache,
+                                 chunked_prefill_size=300)
+    for i in range(8):
+        s.add_request(InferenceRequest(request_id=str(i), input_ids=[0] * int(rng.integers(20, 700)),
+                                       max_new_tokens=int(rng.integers(2, 6))))
+    checked = 0
+    for _ in range(12):
+        plan = s.plan_step()
+        if plan is None:
+            break
+        T, nd, n = plan.num_tokens, plan.num_decode, plan.num_entries
+        k = torch.randn(T, 1, 256, device=DEV, generator=g).bfloat16()
+        v = torch.randn(T, 1, 256, device=DEV, generator=g).bfloat16()
+        cache.append(plan.slot_mapping, k, v, layer=0)
+        if n > nd:
+            cu = plan.cu_seqlens[nd:] - plan.cu_seqlens[nd]
+            t0 = int(plan.cu_seqlens[nd].item())
+            q = torch.randn(T - t0, 4, 256, device=DEV, generator=g).bfloat16()
+            width = plan.block_tables.shape[1]
+            out = A.attn_prefill_paged(q, *cache.get_kv_by_layer(0), cu, plan.seq_lens[nd:],
+                                       plan.block_tables[nd:], max(c for _, _, c in plan.prefill))
+            torch.cuda.synchronize()
+            A.check_errors(DEV)
+            kc, vc = cache.get_kv_by_layer(0)
+            want = att.prefill_attention(q.float().cpu().numpy(), kc.float().cpu().numpy(),
+                                         vc.float().cpu().numpy(), cu.cpu().numpy(), 256 ** -0.5,
+                                         True, lens_k=plan.seq_lens[nd:].cpu().numpy(),
+                                         page_table=plan.block_tables[nd:].cpu().numpy(),
+                                         stats=True)
+            within(out, want)
+            assert width >= 1
+            checked += 1
+        s.complete_step(plan)
+    s.check_errors()
+    assert checked >= 3
+
+
+def test_bad_page_and_bad_offsets_are_flagged():
+    case("attn_prefill_paged bad page id; attn_prefill offsets past the buffer")
+    g = torch.Generator().manual_seed(37)
+    kc = torch.randn(8, 16, 1, 256, generator=g).bfloat16().to(DEV)
+    vc = torch.randn(8, 16, 1, 256, generator=g).bfloat16().to(DEV)
+    q = torch.randn(20, 4, 256, generator=g).bfloat16().to(DEV)
+    table = torch.tensor([[1, 99]], dtype=torch.int32, device=DEV)
+    cu = torch.tensor([0, 20], dtype=torch.int32, device=DEV)
+    A.attn_prefill_paged(q, kc, vc, cu, torch.tensor([30], dtype=torch.int32, device=DEV), table,
+                         20)
+    with pytest.raises(_lib.MkvDeviceError, match="page id"):
+        A.check_errors(DEV)
+    k = torch.randn(20, 1, 256, generator=g).bfloat16().to(DEV)
+    cu_k = torch.tensor([0, 25], dtype=torch.int32, device=DEV)  # past the 20 key rows
+    A.attn_prefill(q, k, k.clone(), cu, cu_k, 20, 25)
+    with pytest.raises(_lib.MkvDeviceError, match="table"):
+        A.check_errors(DEV)

@@ -137,3 +137,68 @@ def test_fp8_attention_close_to_bf16_attention():
                              ks.numpy(), vs.numpy()), quant)
     assert np.abs(quant - exact).max() < 0.1
     assert np.abs(quant - exact).mean() < 0.01
+
+
+def _sdpa_varlen(q, k, v, cu_q, cu_k, scale, causal):
+    """torch's float64 SDPA per sequence, with the causal mask written out
+    bottom-right aligned (query t of nq sees keys 0 .. nk - nq + t)."""
+    out = torch.zeros(q.shape, dtype=torch.float64)
+    Hq, Hkv = q.shape[1], k.shape[1]
+    for b in range(len(cu_q) - 1):
+        q0, q1, k0, k1 = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        nq, nk = q1 - q0, k1 - k0
+        qq = torch.as_tensor(q[q0:q1]).double().permute(1, 0, 2)            # [Hq, nq, D]
+        kk = torch.as_tensor(k[k0:k1]).double().repeat_interleave(Hq // Hkv, 1).permute(1, 0, 2)
+        vv = torch.as_tensor(v[k0:k1]).double().repeat_interleave(Hq // Hkv, 1).permute(1, 0, 2)
+        mask = None
+        if causal:
+            pos = torch.arange(nq).unsqueeze(1) + (nk - nq)
+            mask = torch.arange(nk).unsqueeze(0) <= pos
+            live = mask.any(1)
+        o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask, scale=scale)
+        if causal:
+            o[:, ~live] = 0
+        out[q0:q1] = o.permute(1, 0, 2)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_matches_sdpa_float64(causal):
+    g = torch.Generator().manual_seed(21)
+    lens_q = [1, 5, 16, 33, 70]
+    lens_k = [1, 9, 16, 40, 70]   # a cached prefix where nk > nq
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)])
+    cu_k = np.concatenate([[0], np.cumsum(lens_k)])
+    q = torch.randn(int(cu_q[-1]), 4, 32, generator=g).double().numpy()
+    k = torch.randn(int(cu_k[-1]), 1, 32, generator=g).double().numpy()
+    v = torch.randn(int(cu_k[-1]), 1, 32, generator=g).double().numpy()
+    got = att.prefill_attention(q, k, v, cu_q, 0.3, causal, cu_k=cu_k)
+    want = _sdpa_varlen(q, k, v, cu_q, cu_k, 0.3, causal)
+    assert np.abs(got - want).max() < 1e-12
+
+
+def test_prefill_closed_forms_and_paged_equals_contiguous():
+    g = torch.Generator().manual_seed(22)
+    # one key: every query returns its V row; constant V: the output is V
+    q = torch.randn(3, 4, 16, generator=g).numpy()
+    k = torch.randn(3, 1, 16, generator=g).numpy()
+    v = np.tile(torch.randn(1, 1, 16, generator=g).numpy(), (3, 1, 1))
+    out = att.prefill_attention(q, k, v, [0, 3], 1.0, True, cu_k=[0, 3])
+    assert np.allclose(out, np.broadcast_to(v[:1], out.shape), atol=1e-12)
+    out1 = att.prefill_attention(q[:1], k[:1], v[:1], [0, 1], 1.0, True, cu_k=[0, 1])
+    assert np.allclose(out1[0], np.broadcast_to(v[0], (4, 16)))
+    # more queries than keys: the first queries see nothing
+    out2 = att.prefill_attention(q, k[:1], v[:1], [0, 3], 1.0, True, cu_k=[0, 1])
+    assert not out2[:2].any() and np.allclose(out2[2], np.broadcast_to(v[0], (4, 16)))
+    # the paged form of the same keys gives the same result
+    P = 8
+    kc = torch.randn(P, 16, 1, 16, generator=g).numpy()
+    vc = torch.randn(P, 16, 1, 16, generator=g).numpy()
+    table = np.array([[5, 2, 7]], dtype=np.int32)
+    n = 40
+    kk = kc[table[0]].reshape(-1, 1, 16)[:n]
+    vv = vc[table[0]].reshape(-1, 1, 16)[:n]
+    qq = torch.randn(12, 4, 16, generator=g).numpy()
+    a = att.prefill_attention(qq, kc, vc, [0, 12], 0.25, True, lens_k=[n], page_table=table)
+    b = att.prefill_attention(qq, kk, vv, [0, 12], 0.25, True, cu_k=[0, n])
+    assert np.array_equal(a, b)
