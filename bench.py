@@ -1156,6 +1156,10 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     q = torch.empty(LAYERS, SCHED_BATCH, 1, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
     q.normal_(generator=gen)
     out = torch.empty_like(q)
+    # the prefill chunks' queries (bf16 pools: their attention over the pool)
+    qp = torch.empty(chunk * Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=dev).normal_(
+        generator=gen)
+    outp = torch.empty_like(qp)
     if hybrid:
         C = pool.conv.shape[2]
         xin = torch.randn(45, SCHED_BATCH, C, generator=gen, device=dev).bfloat16()
@@ -1189,6 +1193,9 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         # what the kernel writes), for the byte count
         ent = plan.upload[:8 * nd].reshape(nd, 8)
         lens = ent[:, 1] + ent[:, 2]
+        if n > nd and not fp8:
+            cu_pre = plan.cu_seqlens[nd:] - nd  # decode entries hold one token each
+            max_chunk = max(c for _, _, c in plan.prefill)
         for layer in layer_order:
             if layer % 4 != 3:  # a GDN layer: the scheduled requests' state slots
                 g = gdn_ordinal(layer)
@@ -1219,8 +1226,19 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                                   out=out[l, :nd])
                 if rec is not None:
                     rec.append(("attn", sp.end(stream)))
+            if n > nd and not fp8:  # the prefill chunks attend to their prefix and themselves
+                kp, vp = cache.get_kv_by_layer(l)
+                tp = T - nd
+                sp = stamps.span(stream) if rec is not None else None
+                A.attn_prefill_paged(qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM), kp,
+                                     vp, cu_pre, plan.seq_lens[nd:], plan.block_tables[nd:],
+                                     max_chunk, out=outp[:tp * Q_HEADS * HEAD_DIM].view(
+                                         tp, Q_HEADS, HEAD_DIM))
+                if rec is not None:
+                    rec.append(("prefill_attn", sp.end(stream)))
         if info is not None:
-            info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1], n))
+            info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1], n,
+                         [(st, c) for _, st, c in plan.prefill]))
         s.complete_step(plan)
 
     log(f"warmup {warmup} steps")
@@ -1256,7 +1274,7 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     attn_b = append_b = gdn_b = 0.0
     st_b = pool.state[0, 0].numel() * 4 if hybrid else 0
     cv_b = pool.conv[0, 0].numel() * 2 if hybrid else 0
-    for T, nd, _, lens, w, n in info:
+    for T, nd, _, lens, w, n, _pre in info:
         if nd:
             ln = lens.astype(np.int64)
             attn_b += LAYERS * float(2 * row_kv * ln.sum() + 4 * (-(-ln // 16)).sum() + 4 * nd
@@ -1268,6 +1286,10 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             gdn_b += 45 * float(nd * (2 * st_b + 2 * cv_b + 4 * C + 8)
                                 + (n - nd) * (2 * st_b + 2 * cv_b + 4) + n * (2 * st_b + 4))
     attn_launches = LAYERS * sum(1 for x in info if x[1])
+    # prefill attention: 4 x D flops per (query head, visible key) pair x 4 heads
+    pre_pairs = sum(c * st + c * (c + 1) // 2 for x in info for st, c in x[6])
+    pre_flops = LAYERS * 4.0 * HEAD_DIM * Q_HEADS * pre_pairs
+    pre_ms = _timed(recs, "prefill_attn")
     attn_ms = _timed(recs, "attn")
     plan_ms = _timed(recs, "plan")
     append_ms = _timed(recs, "append")
@@ -1282,6 +1304,7 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     res = {
         "metric": ("achieved HBM GB/s (% of 8 TB/s) of continuous-batching serving steps "
                    "(scheduler step plan + KV append + paged decode attention"
+                   + ("" if fp8 else " + paged prefill attention")
                    + (" + GDN state slot moves" if hybrid else "") + "); step µs"),
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak",
@@ -1331,6 +1354,10 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             "algorithmic_bytes_per_launch": round(attn_b / attn_launches),
         },
     }
+    if not fp8 and pre_pairs:
+        n_pre = LAYERS * sum(1 for x in info if x[6])
+        res["prefill_attn_us_per_layer"] = round(pre_ms * 1e3, 2)
+        res["prefill_attn_TFLOPs"] = round(pre_flops / n_pre / (pre_ms / 1e3) / 1e12, 2)
     if hybrid:
         gdn_ms = _timed(recs, "gdn")
         res["gdn_us_per_layer"] = round(gdn_ms * 1e3, 2)
@@ -1378,6 +1405,103 @@ def sched_cpu_baseline(prompts, outs, pages, free0, chunk, max_seq, first_slots,
                        f"({tokens} tokens): {t_timed:.1f} s of {t_all:.1f} s"),
             "gpu_matches_cpu_on_first_steps": bool(same),
             "steps_compared": min(n, len(first_slots))}
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (no sparsity)
+
+
+def run_prefill_attn(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Varlen causal prefill attention (attn_prefill, the reference's
+    flash_attn_varlen_func interface): 8 prompts of 4096 tokens, 4 query heads
+    over 1 KV head of 256, bf16, 15 attention layers per step (each layer its
+    own q/k/v). MFMA-bound: the roofline is the bf16 dense peak."""
+    from muserve_amd.kernels import attention as A
+    from oracle import attention as att
+
+    dev = torch.device("cuda:0")
+    nseq, L = 8, 4096
+    T = nseq * L
+    gen = torch.Generator(device=dev).manual_seed(107)
+    q = torch.empty(LAYERS, T, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev).normal_(
+        generator=gen)
+    k = torch.empty(LAYERS, T, 1, HEAD_DIM, dtype=torch.bfloat16, device=dev).normal_(
+        generator=gen)
+    v = torch.empty_like(k).normal_(generator=gen)
+    out = torch.empty(T, Q_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+    cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
+    pairs = nseq * L * (L + 1) // 2
+    flops = 4.0 * HEAD_DIM * Q_HEADS * pairs  # QK^T and PV, 2 flop per multiply-add each
+    stream = torch.cuda.current_stream(dev)
+    stamps = Stamps()
+
+    def one_step(rec=None):
+        for l in range(LAYERS):
+            sp = stamps.span(stream) if rec is not None else None
+            A.attn_prefill(q[l], k[l], v[l], cu, cu, L, L, out=out)
+            if rec is not None:
+                rec.append(("attn", sp.end(stream)))
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    A.check_errors(dev)
+    recs = [[] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for j in range(steps):
+        one_step(recs[j])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    A.check_errors(dev)
+    ms = _timed(recs, "attn")
+    achieved = flops / (ms / 1e3) / 1e12
+    step_s = elapsed / steps
+    # the last layer's output on the first 64 tokens of sequence 0 (causal: they
+    # depend on its first 64 keys only) against the float64 oracle
+    n = 64
+    want, mass = att.prefill_attention(q[LAYERS - 1, :n].float().cpu().numpy(),
+                                       k[LAYERS - 1, :n].float().cpu().numpy(),
+                                       v[LAYERS - 1, :n].float().cpu().numpy(), [0, n],
+                                       HEAD_DIM ** -0.5, True, cu_k=[0, n], stats=True)
+    got = out[:n].float().cpu().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    sample_ok = bool((np.abs(got - want) <= ulp + 2.0 ** -8 * mass).all())
+    res = {
+        "metric": "varlen causal prefill attention TFLOP/s (bf16 MFMA)",
+        "value": round(achieved, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (fp32 softmax and accumulation, bf16 probabilities for P V)",
+        "data": "synthetic (seeded ~N(0,1) q/K/V)",
+        "config": {"workload": ("varlen causal prefill attention: 8 prompts x 4096 tokens, 4 query "
+                                "heads over 1 KV head x 256, bf16, 15 attention layers; seed 107"),
+                   "sequences": nseq, "tokens": L, "layers": LAYERS},
+        "attention_us_per_layer": round(ms * 1e3, 2),
+        "gpu_matches_oracle_on_sample": sample_ok,
+        "roofline": {"bound": "mfma", "kernel": "prefill_attn_kernel (mkv_prefill_attention_bf16)",
+                     "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "mean_launch_us": round(ms * 1e3, 2),
+                     "flop_per_launch": flops,
+                     "flop_note": "4 x head_dim x query heads per visible (query, key) pair"},
+    }
+    if with_cpu:
+        import torch.nn.functional as F
+        m = 1024
+        qc = q[0, :m].float().cpu().permute(1, 0, 2).contiguous()
+        kc = k[0, :m].float().cpu().repeat_interleave(Q_HEADS, 1).permute(1, 0, 2).contiguous()
+        vc = v[0, :m].float().cpu().repeat_interleave(Q_HEADS, 1).permute(1, 0, 2).contiguous()
+        reps = 0
+        t1 = time.perf_counter()
+        while time.perf_counter() - t1 < 10.0 and reps < 200:
+            F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
+            reps += 1
+        dt = (time.perf_counter() - t1) / reps
+        res["cpu_baseline"] = {
+            "value": round(4.0 * HEAD_DIM * Q_HEADS * (m * (m + 1) // 2) / dt / 1e12, 4),
+            "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"torch CPU scaled_dot_product_attention (fp32, causal) on one "
+                       f"{m}-token sequence, {reps} runs: {dt * 1e3:.1f} ms each")}
+    return res
 
 
 HOST_LINK_PEAK_GBS = 64.0  # PCIe Gen5 x16, per direction (published)
@@ -1558,7 +1682,7 @@ def main() -> int:
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
-                             "sched", "sched_fp8", "sched_hybrid"],
+                             "sched", "sched_fp8", "sched_hybrid", "prefill_attn"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1580,7 +1704,8 @@ def main() -> int:
               "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True),
               "sched": run_sched,
               "sched_fp8": lambda *a: run_sched(*a, fp8=True),
-              "sched_hybrid": lambda *a: run_sched(*a, hybrid=True)}[args.workload]
+              "sched_hybrid": lambda *a: run_sched(*a, hybrid=True),
+              "prefill_attn": run_prefill_attn}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
@@ -1588,6 +1713,8 @@ def main() -> int:
         steps, warmup = 5, 1  # a step is the whole 4096-request trace
     if args.workload == "offload" and steps == 1000:
         steps, warmup = 10, 2  # a step moves ~1.5 GB across the host link
+    if args.workload == "prefill_attn" and (steps, warmup) == (1000, 20):
+        steps, warmup = 20, 3
     if args.workload.startswith("sched") and (steps, warmup) == (1000, 20):
         steps, warmup = 500, 300  # the warmup fills the 256-request batch
     # a garbage-collector pass in the timed loop stalls the host for tens of

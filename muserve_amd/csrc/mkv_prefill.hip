@@ -8,16 +8,21 @@
 // (causal masking aligned to the bottom-right corner) and, when causal,
 // attends to positions 0 .. nk - nq + t. Query head h reads KV head h / 4.
 //
-// A workgroup (4 waves) takes 16 query tokens of one sequence and KV head;
-// wave w holds query head 4*hk + w, so the 4 waves share every K/V tile
-// through LDS. Per 32-token KV tile:
-//   * the tile is staged in LDS: K rows as they are, V transposed (dim-major),
-//     so both products read their MFMA operands as 16-byte LDS loads;
+// A workgroup (8 waves) takes 32 query tokens of one sequence and KV head;
+// wave w holds query head 4*hk + w % 4 for tokens 16 (w / 4) .. +15, so the 8
+// waves share every K/V tile through LDS. The next tile's global loads are
+// issued before the current tile is computed (held in registers, stored to LDS
+// after it). Per 32-token KV tile:
+//   * the tile is staged in LDS, K and V both as token rows (16-byte
+//     stores); the S product reads K operands as 16-byte LDS loads, the P V
+//     product reads V operands with gfx950's transposing LDS load
+//     (ds_read_b64_tr_b16), so V is never transposed by hand;
 //   * S = Q K^T on MFMA (v_mfma_f32_16x16x32_bf16): A = 16 query rows x 32
 //     dims held in registers for the whole loop, B = 16 K rows; 8 steps over
 //     head_dim 256 for each 16-token half;
 //   * online softmax in fp32 on the 4 rows x 2 tokens a lane holds (exp2,
-//     log2(e) folded into the scale), reductions over the 16 lanes of a row;
+//     log2(e) folded into the scale), reductions over the 16 lanes of a row
+//     by DPP moves;
 //   * P goes through a per-wave LDS tile to become the A operand (16 rows x
 //     32 tokens, bf16); O += P V on MFMA, 16 blocks of 16 dims.
 // The output is O / l, rounded to bf16 once.
@@ -30,16 +35,29 @@ namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j names an 8-byte
+// row R_j of 4 bf16; lane i receives R_{4e + i/4}[i % 4] as element e (a
+// layout probed on the device). Lane j of the group naming
+// V[t0 + j/4][d0 + 4 (j % 4) ..] therefore hands lane i the 4 values
+// V[t0 .. t0+3][d0 + i]: a column of 4 tokens, the MFMA B-operand order.
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
 
 constexpr int kPD = 256;           // head_dim
 constexpr int kPRow = kPD * 2;     // bytes of one bf16 row
-constexpr int kPThreads = 256;     // 4 waves
-constexpr int kPG = 4;             // query heads per KV head (one per wave)
-constexpr int kQTok = 16;          // query tokens per workgroup
+constexpr int kPThreads = 512;     // 8 waves
+constexpr int kPWaves = kPThreads / 64;
+constexpr int kPG = 4;             // query heads per KV head
+constexpr int kQTok = 32;          // query tokens per workgroup (16 per wave)
 constexpr int kKvTile = 32;        // KV tokens per step
-constexpr int kKStride = kPD + 8;  // bf16 per staged K row (padded against bank conflicts)
-constexpr int kVtStride = kKvTile + 8;  // bf16 per transposed V row
+constexpr int kKStride = kPD + 8;   // bf16 per staged K row (padded against bank conflicts)
+constexpr int kVStride = kPD + 16;  // bf16 per staged V row
 constexpr int kPStride = kKvTile + 8;   // bf16 per P row
+constexpr int kStage = kKvTile * kPRow / 16 / kPThreads;  // 16-byte K (and V) chunks per thread
 
 struct PrefillArgs {
   const uint8_t* q;      // [Tq, Hq, 256] bf16
@@ -63,10 +81,34 @@ struct PrefillArgs {
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) { return f32_to_bf16_rne(x); }
 
+// All-reduce over the 16 lanes of a row with DPP moves (VALU, no LDS round
+// trip): swap neighbours, swap pairs, mirror within 8, mirror within 16.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141; // row_half_mirror
+constexpr int kMirror = 0x140;     // row_mirror
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<kQuadSwap1>(x));
+  x = fmaxf(x, dpp<kQuadSwap2>(x));
+  x = fmaxf(x, dpp<kHalfMirror>(x));
+  return fmaxf(x, dpp<kMirror>(x));
+}
+__device__ __forceinline__ float row_sum16(float x) {
+  x += dpp<kQuadSwap1>(x);
+  x += dpp<kQuadSwap2>(x);
+  x += dpp<kHalfMirror>(x);
+  return x + dpp<kMirror>(x);
+}
+
 __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKvTile][kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kPD][kVtStride];
-  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPThreads / 64][kQTok][kPStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kKvTile][kVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPWaves][16][kPStride];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -79,10 +121,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   if ((!q_ok || nq_raw > a.max_q) && tid == 0 && blockIdx.x == 0 && blockIdx.z == 0)
     raise_err(a.err, MKV_DEVERR_TABLE);
   const int32_t nq = q_ok ? (nq_raw < a.max_q ? nq_raw : a.max_q) : 0;
-  const int32_t q0 = (int32_t)blockIdx.x * kQTok;
-  if (q0 >= nq) return;  // uniform
+  const int32_t qt = (int32_t)blockIdx.x * kQTok;  // the workgroup's first query
+  if (qt >= nq) return;  // uniform
   const int64_t hq = (int64_t)a.hkv * kPG;
-  const int64_t h = hk * kPG + wave;  // this wave's query head
+  const int64_t h = hk * kPG + (wave & 3);  // this wave's query head
+  const int32_t q0 = qt + 16 * (wave >> 2);  // this wave's first query
 
   // the sequence's keys: a length checked against what the table (or the
   // buffer) holds; a bad one is flagged and clamped
@@ -105,7 +148,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   }
   if (bad && tid == 0 && blockIdx.x == 0) raise_err(a.err, MKV_DEVERR_TABLE);
   const int64_t shift = nk - nq;  // query t sits at position shift + t
-  const int32_t last_q = (q0 + kQTok < nq ? q0 + kQTok : nq) - 1;
+  const int32_t last_q = (qt + kQTok < nq ? qt + kQTok : nq) - 1;  // the workgroup's last
   int64_t kv_end = a.causal ? shift + last_q + 1 : nk;
   if (kv_end > nk) kv_end = nk;
 
@@ -133,15 +176,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   for (int j = 0; j < 16; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int32_t* trow = a.table ? a.table + b * a.tstride : nullptr;
 
-  for (int64_t kv0 = 0; kv0 < kv_end; kv0 += kKvTile) {
-    // stage K (row-major) and V (transposed) of tokens kv0 .. kv0+31; a
-    // token past the keys, or on a page outside the pool, is zeros
+  // K and V of tokens kv0 .. kv0+31 into registers: this thread's 16-byte
+  // chunks c = tid + kPThreads u (token c / 32, dims 8 (c % 32) ..); a token
+  // past the keys, or on a page outside the pool, is zeros
+  u32x4 kreg[kStage], vreg[kStage];
+  auto fetch = [&](int64_t kv0) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + kPThreads * u;  // 16-byte chunk: token r, dims 8 col .. +7
+    for (int u = 0; u < kStage; ++u) {
+      const int c = tid + kPThreads * u;
       const int r = c >> 5, col = c & 31;
       const int64_t tok = kv0 + r;
-      u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+      kreg[u] = vreg[u] = u32x4{0u, 0u, 0u, 0u};
       if (tok < nk) {
         int64_t rowi;
         bool ok = true;
@@ -154,19 +199,22 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
           rowi = (kbase + tok) * a.hkv + hk;
         }
         if (ok) {
-          kv = ld16(a.k + rowi * kPRow + col * 16);
-          vv = ld16(a.v + rowi * kPRow + col * 16);
+          kreg[u] = ld16(a.k + rowi * kPRow + col * 16);
+          vreg[u] = ld16(a.v + rowi * kPRow + col * 16);
         }
       }
-      *reinterpret_cast<u32x4*>(&k_lds[r][col * 8]) = kv;
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+    }
+  };
+  if (kv_end > 0) fetch(0);
+  for (int64_t kv0 = 0; kv0 < kv_end; kv0 += kKvTile) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vt_lds[col * 8 + 2 * j][r] = (uint16_t)(w4[j] & 0xffffu);
-        vt_lds[col * 8 + 2 * j + 1][r] = (uint16_t)(w4[j] >> 16);
-      }
+    for (int u = 0; u < kStage; ++u) {
+      const int c = tid + kPThreads * u;
+      *reinterpret_cast<u32x4*>(&k_lds[c >> 5][(c & 31) * 8]) = kreg[u];
+      *reinterpret_cast<u32x4*>(&v_lds[c >> 5][(c & 31) * 8]) = vreg[u];
     }
     __syncthreads();
+    if (kv0 + kKvTile < kv_end) fetch(kv0 + kKvTile);  // in flight while this tile computes
 
     // S = Q K^T for the two 16-token halves: lane holds rows 4 g + i, token n
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -185,34 +233,40 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       const bool ok1 = t1 < nk && (!a.causal || t1 <= qpos[i]);
       const float v0 = ok0 ? s0[i] * a.scale_log2 : -INFINITY;
       const float v1 = ok1 ? s1[i] * a.scale_log2 : -INFINITY;
-      float mx = fmaxf(v0, v1);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float mx = row_max16(fmaxf(v0, v1));
       const float m_new = fmaxf(m_run[i], mx);
       const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing seen yet
       alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - m_ref);
       const float p0 = __builtin_amdgcn_exp2f(v0 - m_ref);
       const float p1 = __builtin_amdgcn_exp2f(v1 - m_ref);
-      float ps = p0 + p1;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off);
+      const float ps = row_sum16(p0 + p1);
       l_run[i] = l_run[i] * alpha[i] + ps;
       m_run[i] = m_new;
       p_lds[wave][4 * g + i][n] = bf16_bits(p0);
       p_lds[wave][4 * g + i][16 + n] = bf16_bits(p1);
     }
+    // rescale only when some row's maximum moved (uniform branch)
+    const bool moved = alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f;
+    if (__builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+      for (int j = 0; j < 16; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
+        for (int i = 0; i < 4; ++i) o[j][i] *= alpha[i];
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // O += P V: A = P (row n, tokens 8 g .. +7), B = V^T block (dim 16 j + n)
+    // O += P V: A = P (row n, tokens 8 g .. +7), B = V (tokens 8 g .. +7,
+    // dim 16 j + n) by two transposing loads of 4 tokens each
     const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&p_lds[wave][n][8 * g]);
+    const uint16_t* vbase = &v_lds[8 * g + (n >> 2)][4 * (n & 3)];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const bf16x8 vb = *reinterpret_cast<const bf16x8*>(&vt_lds[16 * j + n][8 * g]);
+      const s16x4 lo = lds_read_tr16(vbase + 16 * j);
+      const s16x4 hi = lds_read_tr16(vbase + 4 * kVStride + 16 * j);
+      const bf16x8 vb = __builtin_bit_cast(
+          bf16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y,
+                                                                 hi.z, hi.w});
       o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[j], 0, 0, 0);
     }
     __syncthreads();  // the tiles are rewritten by the next step
