@@ -1196,6 +1196,7 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         if n > nd and not fp8:
             cu_pre = plan.cu_seqlens[nd:] - nd  # decode entries hold one token each
             max_chunk = max(c for _, _, c in plan.prefill)
+            max_ctx = max(st + c for _, st, c in plan.prefill)
         for layer in layer_order:
             if layer % 4 != 3:  # a GDN layer: the scheduled requests' state slots
                 g = gdn_ordinal(layer)
@@ -1232,7 +1233,8 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                 sp = stamps.span(stream) if rec is not None else None
                 A.attn_prefill_paged(qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM), kp,
                                      vp, cu_pre, plan.seq_lens[nd:], plan.block_tables[nd:],
-                                     max_chunk, out=outp[:tp * Q_HEADS * HEAD_DIM].view(
+                                     max_chunk, max_seqlen_k=max_ctx,
+                                     out=outp[:tp * Q_HEADS * HEAD_DIM].view(
                                          tp, Q_HEADS, HEAD_DIM))
                 if rec is not None:
                     rec.append(("prefill_attn", sp.end(stream)))
@@ -1356,8 +1358,15 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     }
     if not fp8 and pre_pairs:
         n_pre = LAYERS * sum(1 for x in info if x[6])
+        pre_tf = pre_flops / n_pre / (pre_ms / 1e3) / 1e12
         res["prefill_attn_us_per_layer"] = round(pre_ms * 1e3, 2)
-        res["prefill_attn_TFLOPs"] = round(pre_flops / n_pre / (pre_ms / 1e3) / 1e12, 2)
+        res["prefill_attn_TFLOPs"] = round(pre_tf, 2)
+        res["roofline_prefill_attention"] = {
+            "bound": "mfma", "kernel": "prefill_attn_kernel + prefill_merge_kernel "
+            "(mkv_prefill_attention_bf16, paged, key ranges split)",
+            "achieved": round(pre_tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(pre_tf / MFMA_BF16_PEAK_TFLOPS, 4), "mean_launch_us": round(pre_ms * 1e3, 2),
+            "flop_per_launch": round(pre_flops / n_pre)}
     if hybrid:
         gdn_ms = _timed(recs, "gdn")
         res["gdn_us_per_layer"] = round(gdn_ms * 1e3, 2)

@@ -532,8 +532,19 @@ int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v, int6
                                int32_t table_width, const int32_t* cu_seqlens_q,
                                const int32_t* cu_seqlens_k, const int32_t* seq_lens_k,
                                int32_t batch, int64_t num_q_tokens, int32_t max_seqlen_q,
-                               float softmax_scale, int32_t causal, void* out, int32_t* err,
-                               void* stream);
+                               float softmax_scale, int32_t causal, int32_t splits,
+                               int32_t split_len, void* out, void* workspace,
+                               int64_t workspace_bytes, int32_t* err, void* stream);
+
+/*
+ * Workspace of mkv_prefill_attention_bf16 with `splits` key ranges (0 for
+ * one): with splits > 1 every (query tile, KV head) is cut into ranges of
+ * split_len keys (a multiple of 32) that separate workgroups attend to, and a
+ * second kernel merges their (max, sum, output) per query row and head. That
+ * fills the GPU when a step has few, short chunks. No reference counterpart.
+ */
+int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_q_heads,
+                                              int32_t splits);
 
 /*
  * On-device check of what the fp8 kernels rely on. Adds into counts[7]

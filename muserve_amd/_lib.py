@@ -65,7 +65,9 @@ SIGNATURES: dict[str, list] = {
     "mkv_zero_blocks": [_P, _I64, _I32, _I64, _I64, _P, _I32, _P, _P],
     "mkv_block_hash_sha256": [_P, _P, _P, _I32, _I32, _P, _P, _P],
     "mkv_prefill_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _P,
-                                   _P, _I32, _I64, _I32, _F32, _I32, _P, _P, _P],
+                                   _P, _I32, _I64, _I32, _F32, _I32, _I32, _I32, _P, _P, _I64,
+                                   _P, _P],
+    "mkv_prefill_attention_workspace_bytes": [_I64, _I32, _I32],
     "mkv_check_conversions": [_P, _P],
     "mkv_bm_state_bytes": [_I32],
     "mkv_bm_layout": [_I32, _P],
@@ -79,7 +81,8 @@ SIGNATURES: dict[str, list] = {
     "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
                                  _I32, _I32, _F32, _P, _P, _I64, _P, _P],
 }
-_INT64_RESULT = {"mkv_bm_state_bytes", "mkv_decode_attention_workspace_bytes"}
+_INT64_RESULT = {"mkv_bm_state_bytes", "mkv_decode_attention_workspace_bytes",
+                 "mkv_prefill_attention_workspace_bytes"}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

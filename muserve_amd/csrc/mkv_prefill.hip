@@ -75,6 +75,10 @@ struct PrefillArgs {
   uint8_t* out;          // [Tq, Hq, 256] bf16
   int32_t hkv;
   int32_t causal;
+  int32_t splits;        // key ranges per (query tile, KV head); 1: output directly
+  int32_t split_len;     // keys per range (a multiple of the KV tile)
+  float* part;           // splits > 1: [Tq, Hq, splits, 256] unnormalised outputs
+  float* ml;             // splits > 1: [Tq, Hq, splits, 2] (max, sum), log2 units
   float scale_log2;
   int32_t* err;
 };
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int64_t b = blockIdx.y, hk = blockIdx.z;
+  const int64_t b = blockIdx.y, hk = blockIdx.z / a.splits, split = blockIdx.z % a.splits;
   const int32_t qs = a.cu_q[b];
   const int32_t nq_raw = a.cu_q[b + 1] - qs;
   // query offsets outside the buffer, or more queries than the launch covers:
@@ -151,6 +155,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const int32_t last_q = (qt + kQTok < nq ? qt + kQTok : nq) - 1;  // the workgroup's last
   int64_t kv_end = a.causal ? shift + last_q + 1 : nk;
   if (kv_end > nk) kv_end = nk;
+  // this workgroup's key range (the whole range with one split)
+  const int64_t kv_begin = split * (int64_t)a.split_len;
+  if (a.splits > 1 && kv_begin + a.split_len < kv_end) kv_end = kv_begin + a.split_len;
 
   // Q as the A operand: row n = query token q0 + n, dims 32 s + 8 g .. +7
   bf16x8 qa[8];
@@ -205,8 +212,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       }
     }
   };
-  if (kv_end > 0) fetch(0);
-  for (int64_t kv0 = 0; kv0 < kv_end; kv0 += kKvTile) {
+  if (kv_end > kv_begin) fetch(kv_begin);
+  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += kKvTile) {
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
       const int c = tid + kPThreads * u;
@@ -272,22 +279,60 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     __syncthreads();  // the tiles are rewritten by the next step
   }
 
-  // out[token q0 + 4 g + i][h][16 j + n] = O / l (zeros for a row that saw nothing)
+  // one range: out[token q0 + 4 g + i][h][16 j + n] = O / l (zeros for a row
+  // that saw nothing); several: this range's (max, sum, O) for the merge
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int32_t t = q0 + 4 * g + i;
     if (t >= nq) continue;
-    uint16_t* orow = reinterpret_cast<uint16_t*>(a.out + (((int64_t)qs + t) * hq + h) * kPRow);
-    const float L = l_run[i];
+    const int64_t row = ((int64_t)qs + t) * hq + h;
+    if (a.splits == 1) {
+      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out + row * kPRow);
+      const float L = l_run[i];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) orow[16 * j + n] = bf16_bits(L > 0.f ? o[j][i] / L : 0.f);
+      for (int j = 0; j < 16; ++j) orow[16 * j + n] = bf16_bits(L > 0.f ? o[j][i] / L : 0.f);
+    } else {
+      const int64_t at = row * a.splits + split;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a.part[at * kPD + 16 * j + n] = o[j][i];
+      if (n == 0) {
+        a.ml[at * 2] = m_run[i];
+        a.ml[at * 2 + 1] = l_run[i];
+      }
+    }
   }
+}
+
+// Combines the key ranges of one (query row, head): one workgroup of 256
+// threads (a dim each) per row and head; the rows past a sequence's queries
+// were never written and are skipped by the caller's bounds (rows < Tq).
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  const int64_t row = blockIdx.x;  // (token, query head)
+  const int d = threadIdx.x;
+  const int64_t at0 = row * a.splits;
+  float M = -INFINITY;
+  for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, a.ml[(at0 + sp) * 2]);
+  float O = 0.f, L = 0.f;
+  for (int sp = 0; sp < a.splits; ++sp) {
+    const float m = a.ml[(at0 + sp) * 2];
+    const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    O += f * a.part[(at0 + sp) * kPD + d];
+    L += f * a.ml[(at0 + sp) * 2 + 1];
+  }
+  reinterpret_cast<uint16_t*>(a.out + row * kPRow)[d] = bf16_bits(L > 0.f ? O / L : 0.f);
 }
 
 }  // namespace
 }  // namespace mkv
 
 using namespace mkv;
+
+extern "C" int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_q_heads,
+                                                         int32_t splits) {
+  if (num_q_tokens < 0 || num_q_heads <= 0 || splits <= 0) return -1;
+  if (splits == 1) return 0;
+  return num_q_tokens * num_q_heads * splits * (kPD + 2) * 4;
+}
 
 extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v,
                                           int64_t kv_units, int32_t num_kv_heads,
@@ -296,8 +341,9 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
                                           int32_t table_width, const int32_t* cu_seqlens_q,
                                           const int32_t* cu_seqlens_k, const int32_t* seq_lens_k,
                                           int32_t batch, int64_t num_q_tokens, int32_t max_seqlen_q,
-                                          float softmax_scale, int32_t causal, void* out,
-                                          int32_t* err, void* stream) {
+                                          float softmax_scale, int32_t causal, int32_t splits,
+                                          int32_t split_len, void* out, void* workspace,
+                                          int64_t workspace_bytes, int32_t* err, void* stream) {
   clear_error();
   MKV_REQUIRE(batch >= 0 && kv_units >= 0 && num_kv_heads > 0 && num_q_heads > 0 &&
                   max_seqlen_q >= 0 && num_q_tokens >= 0 && table_width >= 0 &&
@@ -310,7 +356,15 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
               num_q_heads / num_kv_heads);
   MKV_REQUIRE(num_kv_heads <= 65535 && batch <= 65535, MKV_E_UNSUPPORTED,
               "mkv_prefill_attention_bf16: batch or KV heads above 65535");
+  MKV_REQUIRE(splits >= 1 && (splits == 1 || (split_len > 0 && split_len % kKvTile == 0)) &&
+                  (int64_t)num_kv_heads * splits <= 65535,
+              MKV_E_INVALID, "mkv_prefill_attention_bf16: bad key split (%d x %d)", splits,
+              split_len);
   if (batch == 0 || max_seqlen_q == 0) return MKV_OK;
+  const int64_t need = mkv_prefill_attention_workspace_bytes(num_q_tokens, num_q_heads, splits);
+  MKV_REQUIRE(splits == 1 || (workspace && workspace_bytes >= need && aligned16(workspace)),
+              MKV_E_INVALID, "mkv_prefill_attention_bf16: workspace of %lld bytes required",
+              (long long)need);
   MKV_REQUIRE(q && k && v && cu_seqlens_q && out && err &&
                   (page_table ? seq_lens_k != nullptr : cu_seqlens_k != nullptr),
               MKV_E_INVALID, "mkv_prefill_attention_bf16: null pointer");
@@ -332,10 +386,17 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
   a.out = static_cast<uint8_t*>(out);
   a.hkv = num_kv_heads;
   a.causal = causal ? 1 : 0;
+  a.splits = splits;
+  a.split_len = splits > 1 ? split_len : 0;
+  a.part = static_cast<float*>(workspace);
+  a.ml = splits > 1 ? a.part + num_q_tokens * num_q_heads * splits * kPD : nullptr;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.err = err;
   const dim3 grid((unsigned)((max_seqlen_q + kQTok - 1) / kQTok), (unsigned)batch,
-                  (unsigned)num_kv_heads);
+                  (unsigned)(num_kv_heads * splits));
   hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPThreads), 0, as_stream(stream), a);
+  if (splits > 1 && num_q_tokens > 0)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(num_q_tokens * num_q_heads)),
+                       dim3(256), 0, as_stream(stream), a);
   return check_launch("mkv_prefill_attention_bf16");
 }

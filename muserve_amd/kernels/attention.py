@@ -68,7 +68,7 @@ def attn_prefill(
     head, head_dim 256; fp32 softmax and accumulation, probabilities rounded
     to bf16 for the P V product, one bf16 rounding of the output."""
     return _prefill(q, k, v, None, cu_seqlens_q, cu_seqlens_k, None, max_seqlen_q, softmax_scale,
-                    causal, out)
+                    causal, out, max_seqlen_k)
 
 
 def attn_prefill_paged(
@@ -82,6 +82,7 @@ def attn_prefill_paged(
     softmax_scale: float | None = None,
     causal: bool = True,
     *,
+    max_seqlen_k: int | None = None,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """attn_prefill over the paged pool, for chunked prefill: a chunk's
@@ -89,14 +90,22 @@ def attn_prefill_paged(
     cached prefix and to themselves, read through the block table — the
     prefill counterpart of attn_decode. With a scheduler plan, the prefill
     entries are plan.cu_seqlens / plan.seq_lens / plan.block_tables past the
-    decode entries."""
+    decode entries. ``max_seqlen_k`` (default: what the table holds) bounds
+    cache_seqlens; a tight bound lets short steps split the keys better."""
     if page_table is None:
         raise ValueError("attn_prefill_paged reads the paged pool: page_table is required")
     return _prefill(q, k_cache, v_cache, page_table, cu_seqlens_q, None, cache_seqlens,
-                    max_seqlen_q, softmax_scale, causal, out)
+                    max_seqlen_q, softmax_scale, causal, out, max_seqlen_k)
 
 
-def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scale, causal, out):
+PREFILL_Q_TILE = 32            # query tokens per workgroup of the prefill kernel
+PREFILL_MIN_WORKGROUPS = 512   # below this many query tiles, key ranges are split
+PREFILL_SPLIT_MIN = 256        # keys per range at least
+_prefill_ws: dict[torch.device, torch.Tensor] = {}
+
+
+def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scale, causal, out,
+             max_seqlen_k=None):
     dev = _lib.require_gpu(q, k, v, page_table, cu_q, cu_k, lens_k)
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise TypeError("attn_prefill takes bf16 q, k and v")
@@ -129,11 +138,30 @@ def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scal
         raise ValueError("out must be a contiguous tensor shaped like q")
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     units = k.shape[0]
+    # key-range splits when the query tiles alone would leave most CUs idle
+    max_k = int(max_seqlen_k) if max_seqlen_k is not None else page_table.shape[1] * 16
+    tiles = -(-int(max_seqlen_q) // PREFILL_Q_TILE) * batch * Hkv
+    splits = 1
+    if tiles < PREFILL_MIN_WORKGROUPS and max_k > PREFILL_SPLIT_MIN:
+        splits = min(-(-PREFILL_MIN_WORKGROUPS // max(tiles, 1)), -(-max_k // PREFILL_SPLIT_MIN))
+    split_len = -(-max_k // splits // 32) * 32 if splits > 1 else 0
+    if splits > 1:
+        splits = -(-max_k // split_len)
+    ws, ws_bytes = None, 0
+    if splits > 1:
+        ws_bytes = _lib.load().mkv_prefill_attention_workspace_bytes(Tq, Hq, splits)
+        ws = _prefill_ws.get(dev)
+        if ws is None or ws.numel() < ws_bytes:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            _prefill_ws[dev] = ws
+    # the workspace is reused by later calls on the stream: calls on one
+    # device must be issued on one stream (or be ordered by the caller)
     _lib.call("mkv_prefill_attention_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), units, Hkv,
               Hq, D, _lib.ptr(page_table), page_table.stride(0) if page_table is not None else 0,
               page_table.shape[1] if page_table is not None else 0, cu_q.data_ptr(),
               _lib.ptr(cu_k), _lib.ptr(lens_k), batch, Tq, int(max_seqlen_q), scale,
-              1 if causal else 0, out.data_ptr(), _errword(dev).ptr(), _lib.stream_of(dev))
+              1 if causal else 0, splits, split_len, out.data_ptr(), _lib.ptr(ws), ws_bytes,
+              _errword(dev).ptr(), _lib.stream_of(dev))
     return out
 
 

@@ -55,6 +55,27 @@ def test_contiguous_varlen_matches_oracle(causal):
     within(out, want)
 
 
+def test_many_sequences_without_key_splits():
+    """64 sequences of 256 queries fill 512 workgroups: one key range each,
+    the output written by the attention kernel itself."""
+    case("attn_prefill 64 x 256 tokens (no key splits)")
+    lens = [256] * 64
+    g, cu = seqs(lens, 33)
+    T = int(cu[-1])
+    q = torch.randn(T, 4, 256, generator=g).bfloat16()
+    k = torch.randn(T, 1, 256, generator=g).bfloat16()
+    v = torch.randn(T, 1, 256, generator=g).bfloat16()
+    out = A.attn_prefill(q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV), cu.to(DEV), 256, 256)
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    sample = 4  # the oracle on the first sequences (each is independent)
+    n = 256 * sample
+    want = att.prefill_attention(q[:n].float().numpy(), k[:n].float().numpy(),
+                                 v[:n].float().numpy(), cu[:sample + 1].numpy(), 256 ** -0.5, True,
+                                 cu_k=cu[:sample + 1].numpy(), stats=True)
+    within(out[:n], want)
+
+
 def test_contiguous_with_prefix_two_kv_heads_and_scale():
     """nk > nq (a prefix before the queries), 2 KV heads (8 query heads), a
     softmax scale of 0.1, and a sequence with more queries than keys."""
