@@ -53,7 +53,8 @@ constexpr int kPThreads = 512;     // 8 waves
 constexpr int kPWaves = kPThreads / 64;
 constexpr int kPG = 4;             // query heads per KV head
 constexpr int kQTok = 32;          // query tokens per workgroup (16 per wave)
-constexpr int kKvTile = 32;        // KV tokens per step
+constexpr int kKvTile = 64;        // KV tokens per step
+constexpr int kNQ = kKvTile / 16;  // 16-token quarters of a KV tile
 constexpr int kKStride = kPD + 8;   // bf16 per staged K row (padded against bank conflicts)
 constexpr int kVStride = kPD + 16;  // bf16 per staged V row
 constexpr int kPStride = kKvTile + 8;   // bf16 per P row
@@ -223,34 +224,43 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     __syncthreads();
     if (kv0 + kKvTile < kv_end) fetch(kv0 + kKvTile);  // in flight while this tile computes
 
-    // S = Q K^T for the two 16-token halves: lane holds rows 4 g + i, token n
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    // S = Q K^T for the tile's 16-token quarters: lane holds rows 4 g + i,
+    // token 16 q + n
+    f32x4 sq[kNQ];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(&k_lds[n][32 * s + 8 * g]);
-      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(&k_lds[16 + n][32 * s + 8 * g]);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], k0, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], k1, s1, 0, 0, 0);
-    }
-    const int64_t t0 = kv0 + n, t1 = kv0 + 16 + n;
+    for (int q = 0; q < kNQ; ++q) sq[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int q = 0; q < kNQ; ++q) {
+        const bf16x8 kk = *reinterpret_cast<const bf16x8*>(&k_lds[16 * q + n][32 * s + 8 * g]);
+        sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], kk, sq[q], 0, 0, 0);
+      }
     float alpha[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool ok0 = t0 < nk && (!a.causal || t0 <= qpos[i]);
-      const bool ok1 = t1 < nk && (!a.causal || t1 <= qpos[i]);
-      const float v0 = ok0 ? s0[i] * a.scale_log2 : -INFINITY;
-      const float v1 = ok1 ? s1[i] * a.scale_log2 : -INFINITY;
-      const float mx = row_max16(fmaxf(v0, v1));
+      float v[kNQ], mx = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < kNQ; ++q) {
+        const int64_t tq = kv0 + 16 * q + n;
+        const bool ok = tq < nk && (!a.causal || tq <= qpos[i]);
+        v[q] = ok ? sq[q][i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, v[q]);
+      }
+      mx = row_max16(mx);
       const float m_new = fmaxf(m_run[i], mx);
       const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // a row with nothing seen yet
       alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - m_ref);
-      const float p0 = __builtin_amdgcn_exp2f(v0 - m_ref);
-      const float p1 = __builtin_amdgcn_exp2f(v1 - m_ref);
-      const float ps = row_sum16(p0 + p1);
+      float ps = 0.f;
+#pragma unroll
+      for (int q = 0; q < kNQ; ++q) {
+        const float pq = __builtin_amdgcn_exp2f(v[q] - m_ref);
+        ps += pq;
+        p_lds[wave][4 * g + i][16 * q + n] = bf16_bits(pq);
+      }
+      ps = row_sum16(ps);
       l_run[i] = l_run[i] * alpha[i] + ps;
       m_run[i] = m_new;
-      p_lds[wave][4 * g + i][n] = bf16_bits(p0);
-      p_lds[wave][4 * g + i][16 + n] = bf16_bits(p1);
     }
     // rescale only when some row's maximum moved (uniform branch)
     const bool moved = alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f;
@@ -263,18 +273,21 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // O += P V: A = P (row n, tokens 8 g .. +7), B = V (tokens 8 g .. +7,
-    // dim 16 j + n) by two transposing loads of 4 tokens each
-    const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&p_lds[wave][n][8 * g]);
-    const uint16_t* vbase = &v_lds[8 * g + (n >> 2)][4 * (n & 3)];
+    // O += P V in 32-token steps: A = P (row n, tokens 32 t + 8 g .. +7),
+    // B = V (those tokens, dim 16 j + n) by two transposing loads of 4 tokens
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const s16x4 lo = lds_read_tr16(vbase + 16 * j);
-      const s16x4 hi = lds_read_tr16(vbase + 4 * kVStride + 16 * j);
-      const bf16x8 vb = __builtin_bit_cast(
-          bf16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y,
-                                                                 hi.z, hi.w});
-      o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[j], 0, 0, 0);
+    for (int t = 0; t < kKvTile / 32; ++t) {
+      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&p_lds[wave][n][32 * t + 8 * g]);
+      const uint16_t* vbase = &v_lds[32 * t + 8 * g + (n >> 2)][4 * (n & 3)];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const s16x4 lo = lds_read_tr16(vbase + 16 * j);
+        const s16x4 hi = lds_read_tr16(vbase + 4 * kVStride + 16 * j);
+        const bf16x8 vb = __builtin_bit_cast(
+            bf16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x,
+                                                                   hi.y, hi.z, hi.w});
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[j], 0, 0, 0);
+      }
     }
     __syncthreads();  // the tiles are rewritten by the next step
   }

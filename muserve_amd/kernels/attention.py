@@ -99,6 +99,7 @@ def attn_prefill_paged(
 
 
 PREFILL_Q_TILE = 32            # query tokens per workgroup of the prefill kernel
+PREFILL_KV_TILE = 64           # keys per step of the prefill kernel (key ranges are multiples)
 PREFILL_MIN_WORKGROUPS = 512   # below this many query tiles, key ranges are split
 PREFILL_SPLIT_MIN = 256        # keys per range at least
 _prefill_ws: dict[torch.device, torch.Tensor] = {}
@@ -144,7 +145,7 @@ def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scal
     splits = 1
     if tiles < PREFILL_MIN_WORKGROUPS and max_k > PREFILL_SPLIT_MIN:
         splits = min(-(-PREFILL_MIN_WORKGROUPS // max(tiles, 1)), -(-max_k // PREFILL_SPLIT_MIN))
-    split_len = -(-max_k // splits // 32) * 32 if splits > 1 else 0
+    split_len = -(-max_k // splits // PREFILL_KV_TILE) * PREFILL_KV_TILE if splits > 1 else 0
     if splits > 1:
         splits = -(-max_k // split_len)
     ws, ws_bytes = None, 0
