@@ -12,19 +12,21 @@
 // wave w holds query head 4*hk + w % 4 for tokens 16 (w / 4) .. +15, so the 8
 // waves share every K/V tile through LDS. The next tile's global loads are
 // issued before the current tile is computed (held in registers, stored to LDS
-// after it). Per 32-token KV tile:
+// after it). Per 64-token KV tile:
 //   * the tile is staged in LDS, K and V both as token rows (16-byte
 //     stores); the S product reads K operands as 16-byte LDS loads, the P V
 //     product reads V operands with gfx950's transposing LDS load
 //     (ds_read_b64_tr_b16), so V is never transposed by hand;
 //   * S = Q K^T on MFMA (v_mfma_f32_16x16x32_bf16): A = 16 query rows x 32
 //     dims held in registers for the whole loop, B = 16 K rows; 8 steps over
-//     head_dim 256 for each 16-token half;
-//   * online softmax in fp32 on the 4 rows x 2 tokens a lane holds (exp2,
+//     head_dim 256 for each 16-token quarter;
+//   * online softmax in fp32 on the 4 rows x 4 tokens a lane holds (exp2,
 //     log2(e) folded into the scale), reductions over the 16 lanes of a row
 //     by DPP moves;
-//   * P goes through a per-wave LDS tile to become the A operand (16 rows x
-//     32 tokens, bf16); O += P V on MFMA, 16 blocks of 16 dims.
+//   * P goes through a per-wave LDS tile to become the A operand: a lane
+//     rounds its 4 rows of one token to bf16 by packed conversions and stores
+//     them as one 8-byte piece of the token-major tile, read back by the same
+//     transposing load as V; O += P V on MFMA, 16 blocks of 16 dims.
 // The output is O / l, rounded to bf16 once.
 #include <math.h>
 
@@ -57,7 +59,6 @@ constexpr int kKvTile = 64;        // KV tokens per step
 constexpr int kNQ = kKvTile / 16;  // 16-token quarters of a KV tile
 constexpr int kKStride = kPD + 8;   // bf16 per staged K row (padded against bank conflicts)
 constexpr int kVStride = kPD + 16;  // bf16 per staged V row
-constexpr int kPStride = kKvTile + 8;   // bf16 per P row
 constexpr int kStage = kKvTile * kPRow / 16 / kPThreads;  // 16-byte K (and V) chunks per thread
 
 struct PrefillArgs {
@@ -86,6 +87,14 @@ struct PrefillArgs {
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) { return f32_to_bf16_rne(x); }
 
+// two floats to bf16 (round to nearest even) by one v_cvt_pk_bf16_f32; the
+// probabilities it rounds are finite and non-negative
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
 // All-reduce over the 16 lanes of a row with DPP moves (VALU, no LDS round
 // trip): swap neighbours, swap pairs, mirror within 8, mirror within 16.
 template <int CTRL>
@@ -113,7 +122,8 @@ __device__ __forceinline__ float row_sum16(float x) {
 __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKvTile][kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[kKvTile][kVStride];
-  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPWaves][16][kPStride];
+  // P of each wave, token-major: [token][row]
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPWaves][kKvTile][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -171,13 +181,16 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
                                             : u32x4{0u, 0u, 0u, 0u});
   }
   // this lane's C rows 4 g + i: query positions, running max and sum
+  // and the last key each row sees (keys and positions fit int32: the
+  // lengths and offsets are int32)
   float m_run[4], l_run[4];
-  int64_t qpos[4];
+  int32_t lastk[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m_run[i] = -INFINITY;
     l_run[i] = 0.f;
-    qpos[i] = shift + q0 + 4 * g + i;
+    const int64_t qpos = shift + q0 + 4 * g + i;
+    lastk[i] = (int32_t)(a.causal && qpos < nk - 1 ? qpos : nk - 1);
   }
   f32x4 o[16];
 #pragma unroll
@@ -236,16 +249,18 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
         const bf16x8 kk = *reinterpret_cast<const bf16x8*>(&k_lds[16 * q + n][32 * s + 8 * g]);
         sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], kk, sq[q], 0, 0, 0);
       }
+    // scores to probabilities in place: token 16 q + n is seen by row 4 g + i
+    // when 16 q <= lastk[i] - kv0 - n
+    const int32_t kv0i = (int32_t)kv0;
     float alpha[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v[kNQ], mx = -INFINITY;
+      const int32_t rel = lastk[i] - kv0i - n;
+      float mx = -INFINITY;
 #pragma unroll
       for (int q = 0; q < kNQ; ++q) {
-        const int64_t tq = kv0 + 16 * q + n;
-        const bool ok = tq < nk && (!a.causal || tq <= qpos[i]);
-        v[q] = ok ? sq[q][i] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, v[q]);
+        sq[q][i] = 16 * q <= rel ? sq[q][i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sq[q][i]);
       }
       mx = row_max16(mx);
       const float m_new = fmaxf(m_run[i], mx);
@@ -254,14 +269,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       float ps = 0.f;
 #pragma unroll
       for (int q = 0; q < kNQ; ++q) {
-        const float pq = __builtin_amdgcn_exp2f(v[q] - m_ref);
-        ps += pq;
-        p_lds[wave][4 * g + i][16 * q + n] = bf16_bits(pq);
+        sq[q][i] = __builtin_amdgcn_exp2f(sq[q][i] - m_ref);
+        ps += sq[q][i];
       }
       ps = row_sum16(ps);
       l_run[i] = l_run[i] * alpha[i] + ps;
       m_run[i] = m_new;
     }
+#pragma unroll
+    for (int q = 0; q < kNQ; ++q)
+      *reinterpret_cast<uint2*>(&p_lds[wave][16 * q + n][4 * g]) =
+          uint2{bf16_pack(sq[q][0], sq[q][1]), bf16_pack(sq[q][2], sq[q][3])};
     // rescale only when some row's maximum moved (uniform branch)
     const bool moved = alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f;
     if (__builtin_amdgcn_ballot_w64(moved)) {
@@ -273,11 +291,16 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // O += P V in 32-token steps: A = P (row n, tokens 32 t + 8 g .. +7),
-    // B = V (those tokens, dim 16 j + n) by two transposing loads of 4 tokens
+    // O += P V in 32-token steps: A = P (row n, tokens 32 t + 8 g .. +7) and
+    // B = V (those tokens, dim 16 j + n), each by two transposing loads of 4
+    // tokens
 #pragma unroll
     for (int t = 0; t < kKvTile / 32; ++t) {
-      const bf16x8 pa = *reinterpret_cast<const bf16x8*>(&p_lds[wave][n][32 * t + 8 * g]);
+      const uint16_t* pbase = &p_lds[wave][32 * t + 8 * g + (n >> 2)][4 * (n & 3)];
+      const s16x4 plo = lds_read_tr16(pbase), phi = lds_read_tr16(pbase + 4 * 16);
+      const bf16x8 pa = __builtin_bit_cast(
+          bf16x8, (short __attribute__((ext_vector_type(8)))){plo.x, plo.y, plo.z, plo.w, phi.x,
+                                                              phi.y, phi.z, phi.w});
       const uint16_t* vbase = &v_lds[32 * t + 8 * g + (n >> 2)][4 * (n & 3)];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
