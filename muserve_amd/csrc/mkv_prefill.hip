@@ -291,21 +291,24 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // O += P V in 32-token steps: A = P (row n, tokens 32 t + 8 g .. +7) and
-    // B = V (those tokens, dim 16 j + n), each by two transposing loads of 4
-    // tokens
+    // O += P V in 32-token steps: A = P (row n) and B = V (dim 16 j + n) over
+    // the same 8 tokens, each by two transposing loads of 4 tokens. The sum
+    // runs over the tokens in any order: lane group g takes tokens
+    // 32 t + 4 g .. +3 (elements 0-3) and 32 t + 16 + 4 g .. +3 (elements 4-7),
+    // so the 32 lanes of one LDS cycle read 8 consecutive rows, whose 32-byte
+    // pieces (V rows 544 bytes apart, P rows 32) fall on distinct banks
 #pragma unroll
     for (int t = 0; t < kKvTile / 32; ++t) {
-      const uint16_t* pbase = &p_lds[wave][32 * t + 8 * g + (n >> 2)][4 * (n & 3)];
-      const s16x4 plo = lds_read_tr16(pbase), phi = lds_read_tr16(pbase + 4 * 16);
+      const uint16_t* pbase = &p_lds[wave][32 * t + 4 * g + (n >> 2)][4 * (n & 3)];
+      const s16x4 plo = lds_read_tr16(pbase), phi = lds_read_tr16(pbase + 16 * 16);
       const bf16x8 pa = __builtin_bit_cast(
           bf16x8, (short __attribute__((ext_vector_type(8)))){plo.x, plo.y, plo.z, plo.w, phi.x,
                                                               phi.y, phi.z, phi.w});
-      const uint16_t* vbase = &v_lds[32 * t + 8 * g + (n >> 2)][4 * (n & 3)];
+      const uint16_t* vbase = &v_lds[32 * t + 4 * g + (n >> 2)][4 * (n & 3)];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const s16x4 lo = lds_read_tr16(vbase + 16 * j);
-        const s16x4 hi = lds_read_tr16(vbase + 4 * kVStride + 16 * j);
+        const s16x4 hi = lds_read_tr16(vbase + 16 * kVStride + 16 * j);
         const bf16x8 vb = __builtin_bit_cast(
             bf16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x,
                                                                    hi.y, hi.z, hi.w});
