@@ -10,9 +10,10 @@
 //
 // A workgroup (8 waves) takes 32 query tokens of one sequence and KV head;
 // wave w holds query head 4*hk + w % 4 for tokens 16 (w / 4) .. +15, so the 8
-// waves share every K/V tile through LDS. The next tile's global loads are
-// issued before the current tile is computed (held in registers, stored to LDS
-// after it). Per 64-token KV tile:
+// waves share every K/V tile through LDS. K/V tiles are double-buffered in
+// LDS with one barrier per tile: while tile i is computed, tile i + 1 goes
+// from registers into the other buffer and tile i + 2's global loads are
+// issued. Per 64-token KV tile:
 //   * the tile is staged in LDS, K and V both as token rows (16-byte
 //     stores); the S product reads K operands as 16-byte LDS loads, the P V
 //     product reads V operands with gfx950's transposing LDS load
@@ -120,8 +121,9 @@ __device__ __forceinline__ float row_sum16(float x) {
 }
 
 __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKvTile][kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kKvTile][kVStride];
+  // two K/V tile buffers: tile i + 1 is stored while tile i is computed
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKvTile][kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kKvTile][kVStride];
   // P of each wave, token-major: [token][row]
   __shared__ __attribute__((aligned(16))) uint16_t p_lds[kPWaves][kKvTile][16];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   for (int j = 0; j < 16; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int32_t* trow = a.table ? a.table + b * a.tstride : nullptr;
 
-  // K and V of tokens kv0 .. kv0+31 into registers: this thread's 16-byte
+  // K and V of tokens kv0 .. kv0+63 into registers: this thread's 16-byte
   // chunks c = tid + kPThreads u (token c / 32, dims 8 (c % 32) ..); a token
   // past the keys, or on a page outside the pool, is zeros
   u32x4 kreg[kStage], vreg[kStage];
@@ -226,16 +228,24 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       }
     }
   };
-  if (kv_end > kv_begin) fetch(kv_begin);
-  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += kKvTile) {
+  auto stage = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < kStage; ++u) {
       const int c = tid + kPThreads * u;
-      *reinterpret_cast<u32x4*>(&k_lds[c >> 5][(c & 31) * 8]) = kreg[u];
-      *reinterpret_cast<u32x4*>(&v_lds[c >> 5][(c & 31) * 8]) = vreg[u];
+      *reinterpret_cast<u32x4*>(&k_lds[buf][c >> 5][(c & 31) * 8]) = kreg[u];
+      *reinterpret_cast<u32x4*>(&v_lds[buf][c >> 5][(c & 31) * 8]) = vreg[u];
     }
-    __syncthreads();
-    if (kv0 + kKvTile < kv_end) fetch(kv0 + kKvTile);  // in flight while this tile computes
+  };
+  // one barrier per tile: tile i + 1 goes into the buffer that tile i - 1
+  // used, which every wave left before the barrier that ended tile i - 1
+  if (kv_end > kv_begin) {
+    fetch(kv_begin);
+    stage(0);
+    if (kv_begin + kKvTile < kv_end) fetch(kv_begin + kKvTile);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += kKvTile, buf ^= 1) {
 
     // S = Q K^T for the tile's 16-token quarters: lane holds rows 4 g + i,
     // token 16 q + n
@@ -246,7 +256,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     for (int s = 0; s < 8; ++s)
 #pragma unroll
       for (int q = 0; q < kNQ; ++q) {
-        const bf16x8 kk = *reinterpret_cast<const bf16x8*>(&k_lds[16 * q + n][32 * s + 8 * g]);
+        const bf16x8 kk =
+            *reinterpret_cast<const bf16x8*>(&k_lds[buf][16 * q + n][32 * s + 8 * g]);
         sq[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], kk, sq[q], 0, 0, 0);
       }
     // scores to probabilities in place: token 16 q + n is seen by row 4 g + i
@@ -280,6 +291,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     for (int q = 0; q < kNQ; ++q)
       *reinterpret_cast<uint2*>(&p_lds[wave][16 * q + n][4 * g]) =
           uint2{bf16_pack(sq[q][0], sq[q][1]), bf16_pack(sq[q][2], sq[q][3])};
+    if (kv0 + kKvTile < kv_end) {  // the next tile into the other buffer; the one after in flight
+      stage(buf ^ 1);
+      if (kv0 + 2 * kKvTile < kv_end) fetch(kv0 + 2 * kKvTile);
+    }
     // rescale only when some row's maximum moved (uniform branch)
     const bool moved = alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f;
     if (__builtin_amdgcn_ballot_w64(moved)) {
@@ -304,7 +319,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       const bf16x8 pa = __builtin_bit_cast(
           bf16x8, (short __attribute__((ext_vector_type(8)))){plo.x, plo.y, plo.z, plo.w, phi.x,
                                                               phi.y, phi.z, phi.w});
-      const uint16_t* vbase = &v_lds[32 * t + 4 * g + (n >> 2)][4 * (n & 3)];
+      const uint16_t* vbase = &v_lds[buf][32 * t + 4 * g + (n >> 2)][4 * (n & 3)];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const s16x4 lo = lds_read_tr16(vbase + 16 * j);
@@ -315,7 +330,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, o[j], 0, 0, 0);
       }
     }
-    __syncthreads();  // the tiles are rewritten by the next step
+    __syncthreads();  // tile i + 1 stored; tile i's buffer free for tile i + 2
   }
 
   // one range: out[token q0 + 4 g + i][h][16 j + n] = O / l (zeros for a row
