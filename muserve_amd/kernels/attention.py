@@ -100,7 +100,7 @@ def attn_prefill_paged(
 
 PREFILL_Q_TILE = 32            # query tokens per workgroup of the prefill kernel
 PREFILL_KV_TILE = 64           # keys per step of the prefill kernel (key ranges are multiples)
-PREFILL_MIN_WORKGROUPS = 512   # below this many query tiles, key ranges are split
+PREFILL_MIN_WORKGROUPS = 768   # below this many query tiles, key ranges are split
 PREFILL_SPLIT_MIN = 256        # keys per range at least
 _prefill_ws: dict[torch.device, torch.Tensor] = {}
 
