@@ -193,3 +193,34 @@ def test_bad_page_and_bad_offsets_are_flagged():
     A.attn_prefill(q, k, k.clone(), cu, cu_k, 20, 25)
     with pytest.raises(_lib.MkvDeviceError, match="table"):
         A.check_errors(DEV)
+
+
+@pytest.mark.parametrize("split_len", [64, 128, 192])
+def test_forced_key_splits_through_the_c_abi(split_len):
+    """Key ranges of one, two and three 64-key tiles (the double-buffered
+    loop's prologue-only, one-store and store-plus-prefetch cases), ranges
+    that end inside a sequence or past its causal limit, and the merge, with
+    the split chosen by the caller of the C ABI."""
+    lens = [1, 63, 64, 65, 128, 129, 200, 383]
+    case(f"mkv_prefill_attention_bf16 forced split_len {split_len}, lens {lens}")
+    g, cu = seqs(lens, 38 + split_len)
+    T, max_k = int(cu[-1]), max(lens)
+    q = torch.randn(T, 4, 256, generator=g).bfloat16().to(DEV)
+    k = torch.randn(T, 1, 256, generator=g).bfloat16().to(DEV)
+    v = torch.randn(T, 1, 256, generator=g).bfloat16().to(DEV)
+    splits = -(-max_k // split_len)
+    lib = _lib.load()
+    ws_bytes = lib.mkv_prefill_attention_workspace_bytes(T, 4, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    cu_d = cu.to(DEV)
+    _lib.call("mkv_prefill_attention_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), T, 1, 4, 256,
+              None, 0, 0, cu_d.data_ptr(), cu_d.data_ptr(), None, len(lens), T, max_k,
+              256 ** -0.5, 1, splits, split_len, out.data_ptr(), ws.data_ptr(), ws_bytes,
+              A._errword(DEV).ptr(), _lib.stream_of(DEV))
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.prefill_attention(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                 v.float().cpu().numpy(), cu.numpy(), 256 ** -0.5, True,
+                                 cu_k=cu.numpy(), stats=True)
+    within(out, want)
