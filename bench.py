@@ -303,6 +303,7 @@ class Stamps:
         hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
                                             ctypes.c_void_p]
         hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        hip.hipStreamWaitEvent.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint]
         self._hip = hip
         self._events: list[ctypes.c_void_p] = []
 
@@ -314,6 +315,11 @@ class Stamps:
             raise RuntimeError("hipEventRecord failed")
         self._events.append(ev)
         return ev
+
+    def wait(self, stream, ev: ctypes.c_void_p) -> None:
+        """Work queued on ``stream`` after this waits for ``ev``."""
+        if self._hip.hipStreamWaitEvent(ctypes.c_void_p(stream.cuda_stream), ev, 0) != 0:
+            raise RuntimeError("hipStreamWaitEvent failed")
 
     def ms(self, a: ctypes.c_void_p, b: ctypes.c_void_p) -> float:
         out = ctypes.c_float()
@@ -1102,7 +1108,7 @@ def sched_requests(n: int, seed: int = SCHED_SEED) -> tuple[np.ndarray, np.ndarr
 
 
 def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
-              hybrid: bool = False) -> dict:
+              hybrid: bool = False, serial_prefill: bool = False) -> dict:
     """Continuous-batching serving steps on one TP rank, driven by the
     scheduler's step plan: a backlog of requests, at most 256 running, a
     4096-token chunked-prefill budget per step (muserve/config.py:33,40).
@@ -1169,6 +1175,11 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         cbuf = torch.empty((SCHED_BATCH, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
         cout = torch.empty(SCHED_BATCH, C, dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
+    # the prefill chunks' attention (MFMA-bound) runs on a second stream of
+    # default priority, beside the decode attention (HBM-bound): both read
+    # the layer's pool after its append and write separate outputs; the
+    # streams join at the end of the step, before the plan buffers are reused
+    side = None if (serial_prefill or fp8) else torch.cuda.Stream(dev)
     stamps = Stamps()
     log(f"pool: {pages} pages x {LAYERS} layers ({kv_dtype}); {n_req} queued requests "
         f"(prompt median {int(np.median(prompts))}, max {int(prompts.max())})"
@@ -1216,6 +1227,8 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                          vin[l, :T * HEAD_DIM].view(T, 1, HEAD_DIM), layer=l)
             if rec is not None:
                 rec.append(("append", sp.end(stream)))
+            if side is not None and n > nd:
+                appended = stamps.record(stream)
             if nd:
                 kp, vp = cache.get_kv_by_layer(l)
                 sp = stamps.span(stream) if rec is not None else None
@@ -1230,14 +1243,21 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             if n > nd and not fp8:  # the prefill chunks attend to their prefix and themselves
                 kp, vp = cache.get_kv_by_layer(l)
                 tp = T - nd
-                sp = stamps.span(stream) if rec is not None else None
-                A.attn_prefill_paged(qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM), kp,
-                                     vp, cu_pre, plan.seq_lens[nd:], plan.block_tables[nd:],
-                                     max_chunk, max_seqlen_k=max_ctx,
-                                     out=outp[:tp * Q_HEADS * HEAD_DIM].view(
-                                         tp, Q_HEADS, HEAD_DIM))
+                ps = stream
+                if side is not None:
+                    stamps.wait(side, appended)
+                    ps = side
+                sp = stamps.span(ps) if rec is not None else None
+                with torch.cuda.stream(ps):
+                    A.attn_prefill_paged(qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM),
+                                         kp, vp, cu_pre, plan.seq_lens[nd:],
+                                         plan.block_tables[nd:], max_chunk, max_seqlen_k=max_ctx,
+                                         out=outp[:tp * Q_HEADS * HEAD_DIM].view(
+                                             tp, Q_HEADS, HEAD_DIM))
                 if rec is not None:
-                    rec.append(("prefill_attn", sp.end(stream)))
+                    rec.append(("prefill_attn", sp.end(ps)))
+        if side is not None and n > nd:
+            stamps.wait(stream, stamps.record(side))
         if info is not None:
             info.append((T, nd, len(plan.prefill), lens, plan.block_tables.shape[1], n,
                          [(st, c) for _, st, c in plan.prefill]))
@@ -1366,7 +1386,10 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             "(mkv_prefill_attention_bf16, paged, key ranges split)",
             "achieved": round(pre_tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(pre_tf / MFMA_BF16_PEAK_TFLOPS, 4), "mean_launch_us": round(pre_ms * 1e3, 2),
-            "flop_per_launch": round(pre_flops / n_pre)}
+            "flop_per_launch": round(pre_flops / n_pre),
+            "stream": "main, after the decode attention" if side is None else
+                      "second stream, concurrent with the decode attention (launch time "
+                      "measured while sharing the GPU)"}
     if hybrid:
         gdn_ms = _timed(recs, "gdn")
         res["gdn_us_per_layer"] = round(gdn_ms * 1e3, 2)
@@ -1688,6 +1711,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--serial-prefill", action="store_true",
+                    help="sched workloads: prefill attention on the main stream, after the "
+                         "decode attention (default: beside it on a second stream)")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
@@ -1711,9 +1737,10 @@ def main() -> int:
               "decode_attn_fp8": lambda *a: run_decode_attn(*a, fp8=True),
               "offload": run_offload,
               "gdn_decode": lambda *a: run_gdn_state(*a, fused_conv=True),
-              "sched": run_sched,
+              "sched": lambda *a: run_sched(*a, serial_prefill=args.serial_prefill),
               "sched_fp8": lambda *a: run_sched(*a, fp8=True),
-              "sched_hybrid": lambda *a: run_sched(*a, hybrid=True),
+              "sched_hybrid": lambda *a: run_sched(*a, hybrid=True,
+                                                   serial_prefill=args.serial_prefill),
               "prefill_attn": run_prefill_attn}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
