@@ -1179,7 +1179,11 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     # default priority, beside the decode attention (HBM-bound): both read
     # the layer's pool after its append and write separate outputs; the
     # streams join at the end of the step, before the plan buffers are reused
-    side = None if (serial_prefill or fp8) else torch.cuda.Stream(dev)
+    side = None if serial_prefill else torch.cuda.Stream(dev)
+    # fp8 pools: the prefill entries' context windows are dequantised to bf16
+    # by the packed block-table gather, then attended by attn_prefill over
+    # contiguous K/V (the reference's fp8 chunked-prefill flow)
+    deq = {"rows": 0, "k": None, "v": None}
     stamps = Stamps()
     log(f"pool: {pages} pages x {LAYERS} layers ({kv_dtype}); {n_req} queued requests "
         f"(prompt median {int(np.median(prompts))}, max {int(prompts.max())})"
@@ -1204,10 +1208,20 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         # what the kernel writes), for the byte count
         ent = plan.upload[:8 * nd].reshape(nd, 8)
         lens = ent[:, 1] + ent[:, 2]
-        if n > nd and not fp8:
+        if n > nd:
             cu_pre = plan.cu_seqlens[nd:] - nd  # decode entries hold one token each
             max_chunk = max(c for _, _, c in plan.prefill)
             max_ctx = max(st + c for _, st, c in plan.prefill)
+            if fp8:  # packed bf16 windows: sequence b's context at cu_ctx[b]
+                ctx_rows = sum(st + c for _, st, c in plan.prefill)
+                cu_ctx = torch.zeros(n - nd + 1, dtype=torch.int32, device=dev)
+                cu_ctx[1:] = torch.cumsum(plan.seq_lens[nd:], 0)
+                if deq["rows"] < ctx_rows:  # grown, never freed (the side stream reads it)
+                    rows = max(ctx_rows, 2 * deq["rows"])
+                    deq["k"] = torch.empty(rows, 1, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+                    deq["v"] = torch.empty_like(deq["k"])
+                    deq.setdefault("kept", []).append((deq["k"], deq["v"]))
+                    deq["rows"] = rows
         for layer in layer_order:
             if layer % 4 != 3:  # a GDN layer: the scheduled requests' state slots
                 g = gdn_ordinal(layer)
@@ -1240,20 +1254,30 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                                   out=out[l, :nd])
                 if rec is not None:
                     rec.append(("attn", sp.end(stream)))
-            if n > nd and not fp8:  # the prefill chunks attend to their prefix and themselves
+            if n > nd:  # the prefill chunks attend to their prefix and themselves
                 kp, vp = cache.get_kv_by_layer(l)
                 tp = T - nd
+                qv = qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM)
+                ov = outp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM)
                 ps = stream
                 if side is not None:
                     stamps.wait(side, appended)
                     ps = side
-                sp = stamps.span(ps) if rec is not None else None
                 with torch.cuda.stream(ps):
-                    A.attn_prefill_paged(qp[:tp * Q_HEADS * HEAD_DIM].view(tp, Q_HEADS, HEAD_DIM),
-                                         kp, vp, cu_pre, plan.seq_lens[nd:],
-                                         plan.block_tables[nd:], max_chunk, max_seqlen_k=max_ctx,
-                                         out=outp[:tp * Q_HEADS * HEAD_DIM].view(
-                                             tp, Q_HEADS, HEAD_DIM))
+                    if fp8:
+                        sp = stamps.span(ps) if rec is not None else None
+                        kd, vd = deq["k"][:ctx_rows], deq["v"][:ctx_rows]
+                        cache.gather(l, plan.block_tables[nd:], plan.seq_lens[nd:],
+                                     out_len=max_ctx, cu_out=cu_ctx, out=(kd, vd))
+                        if rec is not None:
+                            rec.append(("prefill_dequant", sp.end(ps)))
+                    sp = stamps.span(ps) if rec is not None else None
+                    if fp8:
+                        A.attn_prefill(qv, kd, vd, cu_pre, cu_ctx, max_chunk, max_ctx, out=ov)
+                    else:
+                        A.attn_prefill_paged(qv, kp, vp, cu_pre, plan.seq_lens[nd:],
+                                             plan.block_tables[nd:], max_chunk,
+                                             max_seqlen_k=max_ctx, out=ov)
                 if rec is not None:
                     rec.append(("prefill_attn", sp.end(ps)))
         if side is not None and n > nd:
@@ -1376,14 +1400,17 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             "algorithmic_bytes_per_launch": round(attn_b / attn_launches),
         },
     }
-    if not fp8 and pre_pairs:
+    if pre_pairs:
         n_pre = LAYERS * sum(1 for x in info if x[6])
         pre_tf = pre_flops / n_pre / (pre_ms / 1e3) / 1e12
         res["prefill_attn_us_per_layer"] = round(pre_ms * 1e3, 2)
         res["prefill_attn_TFLOPs"] = round(pre_tf, 2)
+        if fp8:
+            res["prefill_dequant_us_per_layer"] = round(_timed(recs, "prefill_dequant") * 1e3, 2)
         res["roofline_prefill_attention"] = {
             "bound": "mfma", "kernel": "prefill_attn_kernel + prefill_merge_kernel "
-            "(mkv_prefill_attention_bf16, paged, key ranges split)",
+            + ("(mkv_prefill_attention_bf16 over the dequantised contiguous windows, key ranges "
+               "split)" if fp8 else "(mkv_prefill_attention_bf16, paged, key ranges split)"),
             "achieved": round(pre_tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(pre_tf / MFMA_BF16_PEAK_TFLOPS, 4), "mean_launch_us": round(pre_ms * 1e3, 2),
             "flop_per_launch": round(pre_flops / n_pre),
