@@ -49,6 +49,7 @@ extern "C" {
 #define MKV_DEVERR_STATE_SLOT 8  /* state-pool slot outside [0, pool_slots)    */
 #define MKV_DEVERR_NEW_PAGE 16   /* decode step needed a page but none was given */
 #define MKV_DEVERR_BM 32         /* block manager: malformed request or op order */
+#define MKV_DEVERR_DUP 64        /* mkv_check_unique: an index appears twice   */
 
 /* ---- meta ------------------------------------------------------------- */
 
@@ -92,6 +93,12 @@ int mkv_append_bf16(void* k_pool, void* v_pool, int64_t pool_layer_stride,
  * [B,S,H,D] layout muserve/model/qwen35_model.py:223-249 hands to decode), or
  * out_offsets[b] + i in packed mode (varlen [total, row] output).
  * Output planes of consecutive layers are out_layer_stride bytes apart.
+ * Packed mode: out_offsets holds batch + 1 entries, and out_layer_stride is
+ * also the capacity of one layer's output (out_layer_stride / row_bytes rows;
+ * pass the buffer's size even for one layer). Sequence b's rows are written
+ * only inside [out_offsets[b], out_offsets[b+1]) and inside that capacity: a
+ * sequence that does not fit (or a negative offset) is cut to the room there
+ * is and sets MKV_DEVERR_TABLE.
  *
  * Replaces SequenceKVState.to_page_table_tensor + the contiguous K/V that
  * decode attention reads (muserve/kv_cache.py:149-158,
@@ -175,6 +182,23 @@ int mkv_step_plan(int32_t* block_tables, int64_t table_stride, int32_t table_wid
                   int32_t* step_lens, int32_t* rows_out, int64_t* cu_seqlens,
                   int32_t* err, void* stream);
 
+/*
+ * Opt-in duplicate check for the index lists the kernels above and below
+ * require to be unique (append slot mappings, state-pool scatter / conv /
+ * zero slots): every index in [0, limit) of ids[0..n) (int64 when id_bytes
+ * is 8, int32 when 4) that appears more than once sets MKV_DEVERR_DUP;
+ * indices outside [0, limit), such as the append's -1, are ignored (the
+ * consuming kernel flags range faults itself). bitmap is caller-owned device
+ * memory of at least ceil(limit / 32) words, zero before the first call; each
+ * call leaves it zero again. Calls sharing a bitmap must be ordered (one
+ * stream). Issue it before the kernel it guards, on the same stream.
+ * No reference counterpart: the reference only requires unique indices
+ * (muserve/kv_cache.py:111-112, torch index_put_, whose winner among
+ * repeated indices is undefined).
+ */
+int mkv_check_unique(const void* ids, int32_t id_bytes, int64_t n, int64_t limit,
+                     uint32_t* bitmap, int64_t bitmap_words, int32_t* err, void* stream);
+
 /* ---- fp8 e4m3fn quantize-on-append / dequant-gather --------------------- */
 
 /*
@@ -198,7 +222,8 @@ int mkv_append_fp8(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
                    int32_t* err, void* stream);
 
 /*
- * Dequant-gather: like mkv_gather_bf16 (same position/padding rules), with
+ * Dequant-gather: like mkv_gather_bf16 (same position, padding and packed
+ * bounds rules, with bf16 output rows of heads * head_dim * 2 bytes), with
  * each output element bf16_rne(float(q) * scale) for its (token, head) scale.
  * No reference counterpart (the reference keeps no fp8 KV); the formula is
  * the inverse of _fast_fp8_quantize's scaling.
@@ -485,6 +510,22 @@ int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_
                               void* stream);
 
 /*
+ * The same over an fp16 pool: q, k_cache, v_cache and out are fp16 (scores on
+ * the fp16 MFMA, fp32 softmax and accumulation, out rounded to fp16 RNE).
+ * fp16 is the reference's default pool dtype (muserve/config.py:37
+ * KV_DTYPE = "float16"), and its attn_decode takes q and caches of one dtype
+ * (muserve/kernels/attention.py:29-42). Same limits, workspace and error bits
+ * as mkv_decode_attention_bf16.
+ */
+int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_cache,
+                             int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
+                             int32_t head_dim, const int32_t* page_table, int64_t table_stride,
+                             int32_t table_width, const int32_t* seq_lens, int32_t batch,
+                             int32_t max_seq_len, float softmax_scale, void* out,
+                             void* workspace, int64_t workspace_bytes, int32_t* err,
+                             void* stream);
+
+/*
  * The same over an fp8 pool, with the dequantisation fused: k_codes / v_codes
  * are [num_pages, 16, num_kv_heads, 256] e4m3fn codes (16-byte aligned) and
  * k_scales / v_scales the [num_pages, 16, num_kv_heads] fp32 scales that
@@ -539,9 +580,11 @@ int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v, int6
 /*
  * Workspace of mkv_prefill_attention_bf16 with `splits` key ranges (0 for
  * one): with splits > 1 every (query tile, KV head) is cut into ranges of
- * split_len keys (a multiple of 32) that separate workgroups attend to, and a
- * second kernel merges their (max, sum, output) per query row and head. That
- * fills the GPU when a step has few, short chunks. No reference counterpart.
+ * split_len keys (a multiple of 64; the last range runs to the sequence's
+ * last key) that separate workgroups attend to, and a second kernel merges
+ * their (max, sum, output) per query row and head, writing only the rows of
+ * the sequences' queries. That fills the GPU when a step has few, short
+ * chunks. No reference counterpart.
  */
 int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_q_heads,
                                               int32_t splits);

@@ -11,6 +11,7 @@ device word (``DeviceErrors``) that callers check at their sync points.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -26,6 +27,7 @@ DEVERR_TABLE = 4
 DEVERR_STATE_SLOT = 8
 DEVERR_NEW_PAGE = 16
 DEVERR_BM = 32
+DEVERR_DUP = 64
 _DEVERR_TEXT = {
     DEVERR_SLOT: "slot_mapping entry out of range",
     DEVERR_PAGE: "page id out of range",
@@ -33,7 +35,13 @@ _DEVERR_TEXT = {
     DEVERR_STATE_SLOT: "state-pool slot out of range",
     DEVERR_NEW_PAGE: "decode step needed a new page but none was supplied",
     DEVERR_BM: "block manager: malformed request or release of a request not admitted",
+    DEVERR_DUP: "an index that must be unique appears more than once",
 }
+
+# Default of the opt-in duplicate-index check (PagedKVCache.check_unique,
+# StatePool.check_unique): on when MUSERVE_KV_CHECK_UNIQUE is set to anything
+# but "" or "0". Off by default: it costs two small launches per guarded call.
+CHECK_UNIQUE_DEFAULT = os.environ.get("MUSERVE_KV_CHECK_UNIQUE", "") not in ("", "0")
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -48,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "mkv_gather_bf16": [_P, _P, _I64, _I64, _P, _I64, _I32, _P, _P, _I32, _I64, _P, _P, _P,
                         _I64, _I32, _I32, _P, _P],
     "mkv_decode_slots": [_P, _P, _I64, _I32, _P, _I32, _I64, _P, _P, _P],
+    "mkv_check_unique": [_P, _I32, _I64, _I64, _P, _I64, _P, _P],
     "mkv_step_plan": [_P, _I64, _I32, _I32, _P, _I32, _P, _I32, _I64, _P, _P, _I64, _P, _I64, _I32,
                       _P, _P, _P, _P, _P],
     "mkv_append_fp8": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I32,
@@ -78,6 +87,8 @@ SIGNATURES: dict[str, list] = {
     "mkv_decode_attention_workspace_bytes": [_I32, _I32, _I32, _I32],
     "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
                                   _I32, _F32, _P, _P, _I64, _P, _P],
+    "mkv_decode_attention_f16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
+                                 _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
                                  _I32, _I32, _F32, _P, _P, _I64, _P, _P],
 }
@@ -177,6 +188,25 @@ def check_conversions(device: torch.device | str = "cuda") -> dict[str, int]:
     counts = torch.zeros(len(CONVERSION_COUNTERS), dtype=torch.int64, device=dev)
     call("mkv_check_conversions", counts.data_ptr(), stream_of(dev))
     return dict(zip(CONVERSION_COUNTERS, counts.cpu().tolist()))
+
+
+class UniqueCheck:
+    """Bitmap over the indices [0, limit) for mkv_check_unique; zero between
+    calls (each call clears the words it set). Use it on one stream."""
+
+    def __init__(self, device: torch.device, limit: int):
+        self.limit = int(limit)
+        self.bits = torch.zeros(max(1, (self.limit + 31) // 32), dtype=torch.int32, device=device)
+
+    def run(self, ids: torch.Tensor, err: "DeviceErrors") -> None:
+        """Flags (DEVERR_DUP in ``err``) any index of ``ids`` in [0, limit)
+        that appears twice; asynchronous on the current stream."""
+        if ids.dtype not in (torch.int32, torch.int64) or not ids.is_contiguous():
+            raise TypeError("ids must be a contiguous int32 or int64 tensor")
+        if ids.numel() == 0:
+            return
+        call("mkv_check_unique", ids.data_ptr(), ids.element_size(), ids.numel(), self.limit,
+             self.bits.data_ptr(), self.bits.numel(), err.ptr(), stream_of(ids.device))
 
 
 class DeviceErrors:

@@ -40,6 +40,7 @@ namespace mkv {
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -78,6 +79,35 @@ struct AttnArgs {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return bits_f32(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return bits_f32(w & 0xffff0000u); }
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// One 16 x 16 x 32 MFMA step of the scores over 16-bit rows: fp16 pools use
+// the fp16 instruction, bf16 pools (and fp8 codes converted to bf16) the
+// bf16 one. Operands travel as raw 16-byte registers.
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// An output element in the pool's 16-bit type: round to nearest even (fp16
+// overflows to infinity, as torch's float -> half conversion does).
+template <bool F16>
+__device__ __forceinline__ uint16_t out_bits(float x) {
+  if constexpr (F16)
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  else
+    return f32_to_bf16_rne(x);
+}
 
 // Orders this wave's LDS writes before its later LDS reads (other lanes').
 __device__ __forceinline__ void wave_sync() {
@@ -115,8 +145,8 @@ __device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
 // e4m3fn codes with an fp32 scale per (token, KV head); a token's score is
 // scale_k * (q . codes) and its V weight p * scale_v, so the codes convert
 // exactly to bf16 MFMA operands and no product is rounded before the fp32
-// accumulation.
-template <int G, bool FP8>
+// accumulation. F16: q, caches and out are fp16 instead of bf16.
+template <int G, bool FP8, bool F16>
 __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t hk, int64_t c,
                                            int64_t len, int64_t nch,
                                            float (&p_lds)[kAttnWaves][kIterTokens][16],
@@ -140,13 +170,13 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   // 64 contiguous bytes of each of the 16 rows): bf16, step s = r covers dims
   // 8*(4s+g) .. +7; fp8, a chunk holds 16 codes, step s = 2r+h covers dims
   // 16*(4r+g) + 8h .. +7, the q chunk 8r + 2g + h.
-  bf16x8 qb[8];
+  u32x4 qb[8];
   const uint8_t* qrow = a.q + ((b * a.hkv + hk) * G + (n < G ? n : 0)) * kRowBytes;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
     const u32x4 w = n < G ? ld16(qrow + chunk * 16) : u32x4{0u, 0u, 0u, 0u};
-    qb[s] = __builtin_bit_cast(bf16x8, w);
+    qb[s] = w;
   }
   float m_run = -INFINITY, l_run = 0.f;  // head n
   float o[G][4];
@@ -180,7 +210,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   // V rows one by one as P V consumes this one's, into the same registers.
   // Past the wave's last page the loads repeat that page (cache hits) and the
   // tokens are masked.
-  typedef typename std::conditional<FP8, u32x4, bf16x8>::type KReg;
+  typedef u32x4 KReg;
   typedef typename std::conditional<FP8, uint32_t, u32x2>::type VReg;
   constexpr int kKRegs = FP8 ? 4 : 8;
   KReg ka[PPI][kKRegs];
@@ -199,7 +229,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) ka[u][s] = __builtin_bit_cast(bf16x8, ld16(kp + (4 * s + g) * 16));
+      for (int s = 0; s < 8; ++s) ka[u][s] = ld16(kp + (4 * s + g) * 16);
     }
   };
   auto load_v = [&](int u, int64_t row, int t) {
@@ -230,9 +260,11 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].x, ka[u][r].y),
-                                                          qb[2 * r], sc[u], 0, 0, 0);
+                                                          __builtin_bit_cast(bf16x8, qb[2 * r]),
+                                                          sc[u], 0, 0, 0);
           sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].z, ka[u][r].w),
-                                                          qb[2 * r + 1], sc[u], 0, 0, 0);
+                                                          __builtin_bit_cast(bf16x8, qb[2 * r + 1]),
+                                                          sc[u], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -242,7 +274,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
       } else {
 #pragma unroll
         for (int s = 0; s < 8; ++s)
-          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[u][s], qb[s], sc[u], 0, 0, 0);
+          sc[u] = mfma16<F16>(ka[u][s], qb[s], sc[u]);
       }
       load_k(u, nrow[u]);
     }
@@ -300,6 +332,11 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
           v1 = lo.y;
           v2 = hi.x;
           v3 = hi.y;
+        } else if constexpr (F16) {
+          v0 = f16_lo(vr[u][t].x);
+          v1 = f16_hi(vr[u][t].x);
+          v2 = f16_lo(vr[u][t].y);
+          v3 = f16_hi(vr[u][t].y);
         } else {
           v0 = bf16_lo(vr[u][t].x);
           v1 = bf16_hi(vr[u][t].x);
@@ -342,7 +379,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
       L += f * l_w[w][h];
     }
     if (nch == 1) {
-      reinterpret_cast<uint16_t*>(out + h * kRowBytes)[d] = f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
+      reinterpret_cast<uint16_t*>(out + h * kRowBytes)[d] = out_bits<F16>(L > 0.f ? O / L : 0.f);
     } else {
       const int64_t at = ((b * a.hkv + hk) * a.chunks + c) * G + h;
       a.part[at * kHeadDim + d] = O;
@@ -354,7 +391,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   }
 }
 
-template <int G, bool FP8>
+template <int G, bool FP8, bool F16>
 // two workgroups per CU: without the bound the G = 8 kernels take 256 VGPRs
 // plus accumulation registers, one wave per SIMD
 __global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a) {
@@ -488,7 +525,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a)
     const int64_t b = pair / a.hkv, hk = pair % a.hkv;
     const int64_t len = attn_len(a, b, false);
     if (c < 0) c = (int32_t)(len / kChunk);
-    attn_chunk<G, FP8>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w, l_w,
+    attn_chunk<G, FP8, F16>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w, l_w,
                        o_w);
   }
 }
@@ -496,7 +533,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a)
 // Merges the chunk states of one (sequence, KV head, query head) of a
 // sequence longer than one chunk: the chunks' maximum by a block reduction,
 // then a thread per dim sums the rescaled partial rows (loads 8 chunks deep).
-template <int G>
+template <int G, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
   __shared__ float red[kAttnWaves];
   // the chunk kernel has finished (stream order): its counter starts from
@@ -528,7 +565,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
     L += f * ld_const(a.ml + at * 2 + 1);
   }
   uint8_t* out = a.out + (pr * G + h) * kRowBytes;
-  reinterpret_cast<uint16_t*>(out)[tid] = f32_to_bf16_rne(L > 0.f ? O / L : 0.f);
+  reinterpret_cast<uint16_t*>(out)[tid] = out_bits<F16>(L > 0.f ? O / L : 0.f);
 }
 
 inline int64_t attn_chunks(int32_t max_seq_len) {
@@ -550,13 +587,13 @@ int attn_grid() {
   return cus[dev] * 4;
 }
 
-template <int G, bool FP8>
+template <int G, bool FP8, bool F16>
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8>), dim3((unsigned)attn_grid()), dim3(kAttnThreads), 0,
-                     st, a);
+  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16>), dim3((unsigned)attn_grid()),
+                     dim3(kAttnThreads), 0, st, a);
   // the merge kernel also resets the work counter: one workgroup when no
   // sequence spans two chunks
-  hipLaunchKernelGGL(attn_merge_kernel<G>, dim3(a.chunks > 1 ? (unsigned)(a.pairs * G) : 1u),
+  hipLaunchKernelGGL((attn_merge_kernel<G, F16>), dim3(a.chunks > 1 ? (unsigned)(a.pairs * G) : 1u),
                      dim3(kAttnThreads), 0, st, a);
 }
 
@@ -576,9 +613,22 @@ extern "C" int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t n
 
 namespace {
 
-// Shared by both entry points: `fn` names the caller in error messages; the
-// scale planes are null for bf16 caches.
-int decode_attention(const char* fn, bool fp8, const void* q, const void* k_cache,
+// Element kinds of the pool the entry points read.
+enum AttnKind { kAttnBf16, kAttnFp8, kAttnF16 };
+
+template <int G>
+void launch_kind(AttnKind kind, const AttnArgs& a, hipStream_t st) {
+  if (kind == kAttnFp8)
+    launch_attn<G, true, false>(a, st);
+  else if (kind == kAttnF16)
+    launch_attn<G, false, true>(a, st);
+  else
+    launch_attn<G, false, false>(a, st);
+}
+
+// Shared by the entry points: `fn` names the caller in error messages; the
+// scale planes are null for 16-bit caches.
+int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k_cache,
                      const void* v_cache, const float* k_scales, const float* v_scales,
                      int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
                      int32_t head_dim, const int32_t* page_table, int64_t table_stride,
@@ -597,11 +647,11 @@ int decode_attention(const char* fn, bool fp8, const void* q, const void* k_cach
               num_q_heads / num_kv_heads);
   if (batch == 0) return MKV_OK;
   MKV_REQUIRE(q && k_cache && v_cache && page_table && seq_lens && out && err &&
-                  (!fp8 || (k_scales && v_scales)),
+                  (kind != kAttnFp8 || (k_scales && v_scales)),
               MKV_E_INVALID, "%s: null pointer", fn);
   MKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
               MKV_E_ALIGN, "%s: q, caches and out must be 16-byte aligned", fn);
-  MKV_REQUIRE(!fp8 || (aligned4(k_scales) && aligned4(v_scales)), MKV_E_ALIGN,
+  MKV_REQUIRE(kind != kAttnFp8 || (aligned4(k_scales) && aligned4(v_scales)), MKV_E_ALIGN,
               "%s: scale planes must be 4-byte aligned", fn);
   MKV_REQUIRE((int64_t)batch * num_kv_heads <= kMaxPairs, MKV_E_UNSUPPORTED,
               "%s: batch x KV heads above %d", fn, kMaxPairs);
@@ -634,20 +684,11 @@ int decode_attention(const char* fn, bool fp8, const void* q, const void* k_cach
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.err = err;
   const hipStream_t st = as_stream(stream);
-  if (fp8) {
-    switch (G) {
-      case 1: launch_attn<1, true>(a, st); break;
-      case 2: launch_attn<2, true>(a, st); break;
-      case 4: launch_attn<4, true>(a, st); break;
-      default: launch_attn<8, true>(a, st); break;
-    }
-  } else {
-    switch (G) {
-      case 1: launch_attn<1, false>(a, st); break;
-      case 2: launch_attn<2, false>(a, st); break;
-      case 4: launch_attn<4, false>(a, st); break;
-      default: launch_attn<8, false>(a, st); break;
-    }
+  switch (G) {
+    case 1: launch_kind<1>(kind, a, st); break;
+    case 2: launch_kind<2>(kind, a, st); break;
+    case 4: launch_kind<4>(kind, a, st); break;
+    default: launch_kind<8>(kind, a, st); break;
   }
   return check_launch(fn);
 }
@@ -662,7 +703,7 @@ extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, con
                                          int32_t batch, int32_t max_seq_len, float softmax_scale,
                                          void* out, void* workspace, int64_t workspace_bytes,
                                          int32_t* err, void* stream) {
-  return decode_attention("mkv_decode_attention_bf16", false, q, k_cache, v_cache, nullptr,
+  return decode_attention("mkv_decode_attention_bf16", kAttnBf16, q, k_cache, v_cache, nullptr,
                           nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
                           table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
                           out, workspace, workspace_bytes, err, stream);
@@ -677,8 +718,22 @@ extern "C" int mkv_decode_attention_fp8(const void* q, const void* k_codes, cons
                                         int32_t batch, int32_t max_seq_len, float softmax_scale,
                                         void* out, void* workspace, int64_t workspace_bytes,
                                         int32_t* err, void* stream) {
-  return decode_attention("mkv_decode_attention_fp8", true, q, k_codes, v_codes, k_scales,
+  return decode_attention("mkv_decode_attention_fp8", kAttnFp8, q, k_codes, v_codes, k_scales,
                           v_scales, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
+                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
+                          out, workspace, workspace_bytes, err, stream);
+}
+
+extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_cache,
+                                        int64_t num_pages, int32_t num_kv_heads,
+                                        int32_t num_q_heads, int32_t head_dim,
+                                        const int32_t* page_table, int64_t table_stride,
+                                        int32_t table_width, const int32_t* seq_lens,
+                                        int32_t batch, int32_t max_seq_len, float softmax_scale,
+                                        void* out, void* workspace, int64_t workspace_bytes,
+                                        int32_t* err, void* stream) {
+  return decode_attention("mkv_decode_attention_f16", kAttnF16, q, k_cache, v_cache, nullptr,
+                          nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
                           table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
                           out, workspace, workspace_bytes, err, stream);
 }

@@ -63,7 +63,8 @@ struct GatherArgs {
   const int32_t* starts;
   uint32_t batch;
   int64_t out_len;
-  const int64_t* out_offsets;
+  const int64_t* out_offsets;  // packed mode: batch + 1 row offsets
+  int64_t out_rows;            // packed mode: rows one layer's output holds
   uint8_t* k_out;
   uint8_t* v_out;
   int64_t out_layer_stride;
@@ -108,6 +109,20 @@ struct GatherTile {
     if (start < 0) {  // malformed window: padding only, never a negative page
       nvalid = 0;
       start = 0;
+    }
+    if (a.out_offsets) {
+      // packed rows of sequence b stay inside [out_offsets[b], out_offsets[b+1])
+      // and inside the output; offsets that leave less room are flagged and
+      // the sequence is cut to the room there is (none for a negative start)
+      const int64_t o0 = ld_const(a.out_offsets + b);
+      int64_t o1 = ld_const(a.out_offsets + b + 1);
+      o1 = o1 < a.out_rows ? o1 : a.out_rows;
+      const int64_t room = o0 < 0 ? 0 : (o1 > o0 ? o1 - o0 : 0);
+      if (room < nvalid || o0 < 0) {
+        if (blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x == 0)
+          raise_err(a.err, MKV_DEVERR_TABLE);
+        nvalid = room < nvalid ? room : nvalid;
+      }
     }
     const int64_t up = (nvalid + ROWS - 1) / ROWS * ROWS;
     data_end = up < a.out_len ? up : a.out_len;
@@ -206,18 +221,22 @@ inline dim3 gather_grid(const GatherArgs& a, int rows, int32_t num_layers) {
 }
 
 // Fills the argument block common to mkv_gather_bf16 and mkv_gather_dequant_fp8.
+// out_row_bytes is the size of one output row: in packed mode
+// out_layer_stride / out_row_bytes is the capacity of one layer's output.
 inline int fill_gather_args(GatherArgs& a, const char* fn, const void* k_pool, const void* v_pool,
                             int64_t pool_layer_stride, int64_t num_pages,
                             const int32_t* block_tables, int64_t table_stride, int32_t table_width,
                             const int32_t* seq_lens, const int32_t* starts, int32_t batch,
                             int64_t out_len, const int64_t* out_offsets, void* k_out, void* v_out,
-                            int64_t out_layer_stride, int32_t* err) {
+                            int64_t out_layer_stride, int32_t out_row_bytes, int32_t* err) {
   if (!(k_pool && v_pool && block_tables && seq_lens && k_out && v_out && err))
     return set_error(MKV_E_INVALID, "%s: null pointer", fn);
   if (!(aligned16(k_pool) && aligned16(v_pool) && aligned16(k_out) && aligned16(v_out) &&
         pool_layer_stride % 16 == 0 && out_layer_stride % 16 == 0))
     return set_error(MKV_E_ALIGN, "%s: pointers and strides must be 16-byte aligned", fn);
   if (out_len >= (1ll << 31)) return set_error(MKV_E_UNSUPPORTED, "%s: out_len too large", fn);
+  if (out_offsets && out_layer_stride < 0)
+    return set_error(MKV_E_INVALID, "%s: negative output capacity", fn);
   if (batch > 65535) return set_error(MKV_E_UNSUPPORTED, "%s: batch %d > 65535", fn, batch);
   a = GatherArgs{};
   a.k_pool = (const uint8_t*)k_pool;
@@ -232,6 +251,7 @@ inline int fill_gather_args(GatherArgs& a, const char* fn, const void* k_pool, c
   a.batch = (uint32_t)batch;
   a.out_len = out_len;
   a.out_offsets = out_offsets;
+  a.out_rows = out_offsets ? out_layer_stride / out_row_bytes : 0;
   a.k_out = (uint8_t*)k_out;
   a.v_out = (uint8_t*)v_out;
   a.out_layer_stride = out_layer_stride;

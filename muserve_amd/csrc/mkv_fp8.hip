@@ -287,7 +287,7 @@ extern "C" int mkv_gather_dequant_fp8(const void* k_pool, const void* v_pool, co
   const int rc = fill_gather_args(a, "mkv_gather_dequant_fp8", k_pool, v_pool, pool_layer_stride,
                                   num_pages, block_tables, table_stride, table_width, seq_lens,
                                   starts, batch, out_len, out_offsets, k_out, v_out,
-                                  out_layer_stride, err);
+                                  out_layer_stride, num_heads * kHeadDim * 2, err);
   if (rc != MKV_OK) return rc;
   a.k_scale = k_scale;
   a.v_scale = v_scale;

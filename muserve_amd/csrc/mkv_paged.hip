@@ -356,7 +356,7 @@ extern "C" int mkv_gather_bf16(const void* k_pool, const void* v_pool, int64_t p
   const int rc = fill_gather_args(a, "mkv_gather_bf16", k_pool, v_pool, pool_layer_stride,
                                   num_pages, block_tables, table_stride, table_width, seq_lens,
                                   starts, batch, out_len, out_offsets, k_out, v_out,
-                                  out_layer_stride, err);
+                                  out_layer_stride, row_bytes > 0 ? row_bytes : 1, err);
   if (rc != MKV_OK) return rc;
   hipStream_t s = as_stream(stream);
   switch (row_bytes) {

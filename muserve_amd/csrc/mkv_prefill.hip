@@ -168,9 +168,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const int32_t last_q = (qt + kQTok < nq ? qt + kQTok : nq) - 1;  // the workgroup's last
   int64_t kv_end = a.causal ? shift + last_q + 1 : nk;
   if (kv_end > nk) kv_end = nk;
-  // this workgroup's key range (the whole range with one split)
+  // this workgroup's key range (the whole range with one split); the last
+  // range runs to the sequence's end, so a split_len * splits below the real
+  // key count never drops keys
   const int64_t kv_begin = split * (int64_t)a.split_len;
-  if (a.splits > 1 && kv_begin + a.split_len < kv_end) kv_end = kv_begin + a.split_len;
+  if (split + 1 < a.splits && kv_begin + a.split_len < kv_end) kv_end = kv_begin + a.split_len;
 
   // Q as the A operand: row n = query token q0 + n, dims 32 s + 8 g .. +7
   bf16x8 qa[8];
@@ -357,11 +359,20 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   }
 }
 
-// Combines the key ranges of one (query row, head): one workgroup of 256
-// threads (a dim each) per row and head; the rows past a sequence's queries
-// were never written and are skipped by the caller's bounds (rows < Tq).
+// Combines the key ranges of one (query token, query head): one workgroup of
+// 256 threads (a dim each) per query t < max_seqlen_q of sequence b (grid.y)
+// and head (grid.z). It writes exactly the rows the attention kernel wrote
+// ranges for: the same query offsets and bounds decide, so rows of `out`
+// outside every sequence's queries are left alone, as with one range.
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-  const int64_t row = blockIdx.x;  // (token, query head)
+  const int32_t b = blockIdx.y;
+  const int32_t qs = a.cu_q[b];
+  const int32_t nq_raw = a.cu_q[b + 1] - qs;
+  const bool q_ok = qs >= 0 && nq_raw >= 0 && (int64_t)qs + nq_raw <= a.num_q;
+  const int32_t nq = q_ok ? (nq_raw < a.max_q ? nq_raw : a.max_q) : 0;
+  const int32_t t = blockIdx.x;
+  if (t >= nq) return;
+  const int64_t row = ((int64_t)qs + t) * ((int64_t)a.hkv * kPG) + blockIdx.z;
   const int d = threadIdx.x;
   const int64_t at0 = row * a.splits;
   float M = -INFINITY;
@@ -408,8 +419,8 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
   MKV_REQUIRE(num_q_heads == kPG * num_kv_heads, MKV_E_UNSUPPORTED,
               "mkv_prefill_attention_bf16: %d query heads per KV head unsupported (4)",
               num_q_heads / num_kv_heads);
-  MKV_REQUIRE(num_kv_heads <= 65535 && batch <= 65535, MKV_E_UNSUPPORTED,
-              "mkv_prefill_attention_bf16: batch or KV heads above 65535");
+  MKV_REQUIRE(num_q_heads <= 65535 && batch <= 65535, MKV_E_UNSUPPORTED,
+              "mkv_prefill_attention_bf16: batch or query heads above 65535");
   MKV_REQUIRE(splits >= 1 && (splits == 1 || (split_len > 0 && split_len % kKvTile == 0)) &&
                   (int64_t)num_kv_heads * splits <= 65535,
               MKV_E_INVALID, "mkv_prefill_attention_bf16: bad key split (%d x %d)", splits,
@@ -450,7 +461,8 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
                   (unsigned)(num_kv_heads * splits));
   hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPThreads), 0, as_stream(stream), a);
   if (splits > 1 && num_q_tokens > 0)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(num_q_tokens * num_q_heads)),
+    hipLaunchKernelGGL(prefill_merge_kernel,
+                       dim3((unsigned)max_seqlen_q, (unsigned)batch, (unsigned)num_q_heads),
                        dim3(256), 0, as_stream(stream), a);
   return check_launch("mkv_prefill_attention_bf16");
 }

@@ -167,22 +167,27 @@ def _prefill(q, k, v, page_table, cu_q, cu_k, lens_k, max_seqlen_q, softmax_scal
 
 
 def attn_decode(
-    q: torch.Tensor,                    # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16
-    k_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] bf16
-    v_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] bf16
+    q: torch.Tensor,                    # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16 / fp16
+    k_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] same
+    v_cache: torch.Tensor,              # [num_pages, PAGE_SIZE, NUM_KV_HEADS, HEAD_DIM] same
     cache_seqlens: torch.Tensor,        # [B] int32 — current kv length per seq
     page_table: torch.Tensor | None,    # [B, max_pages] int32 — paged kv index
     softmax_scale: float | None = None,
     *,
     max_seqlen: int | None = None,
     out: torch.Tensor | None = None,
-) -> torch.Tensor:                      # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16
-    """``max_seqlen`` bounds ``cache_seqlens`` (default: what the page table
+) -> torch.Tensor:                      # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16 / fp16
+    """bf16 or fp16 caches (fp16 is the reference's default pool dtype,
+    muserve/config.py:37), with q and the output in the caches' dtype.
+    ``max_seqlen`` bounds ``cache_seqlens`` (default: what the page table
     holds) and sizes the launch; a tighter bound launches fewer empty
     workgroups. ``out`` may be given to write in place."""
-    if k_cache.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16:
-        raise TypeError("attn_decode takes bf16 caches (attn_decode_fp8 reads fp8 ones)")
-    return _decode("mkv_decode_attention_bf16", q, k_cache, v_cache, None, None, cache_seqlens,
+    fns = {torch.bfloat16: "mkv_decode_attention_bf16", torch.float16: "mkv_decode_attention_f16"}
+    if k_cache.dtype not in fns or v_cache.dtype != k_cache.dtype:
+        raise TypeError("attn_decode takes bf16 or fp16 caches (attn_decode_fp8 reads fp8 ones)")
+    if q.dtype != k_cache.dtype:
+        raise TypeError(f"q is {q.dtype}, the caches {k_cache.dtype}: they must match")
+    return _decode(fns[k_cache.dtype], q, k_cache, v_cache, None, None, cache_seqlens,
                    page_table, softmax_scale, max_seqlen, out)
 
 
@@ -221,8 +226,9 @@ def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_tab
     P, page, Hkv, Dk = k_cache.shape
     if one != 1 or page != 16 or D != HEAD_DIM or Dk != D or v_cache.shape != k_cache.shape:
         raise ValueError(f"unsupported shapes q {tuple(q.shape)}, cache {tuple(k_cache.shape)}")
-    if q.dtype != torch.bfloat16:
-        raise TypeError("attn_decode takes a bf16 query")
+    if q.dtype != (torch.float16 if k_cache.dtype == torch.float16 else torch.bfloat16):
+        raise TypeError(f"attn_decode takes a {'fp16' if k_cache.dtype == torch.float16 else 'bf16'}"
+                        " query")
     if cache_seqlens.dtype != torch.int32 or page_table.dtype != torch.int32:
         raise TypeError("cache_seqlens and page_table must be int32")
     if not (q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()

@@ -91,6 +91,9 @@ class PagedKVCache:
         self._free_pages = list(range(num_gpu_pages))
         self._num_free = num_gpu_pages
         self._errors = _lib.DeviceErrors(device) if device.type == "cuda" else None
+        # opt-in: report a slot that appears twice in one append (MkvDeviceError)
+        self.check_unique = _lib.CHECK_UNIQUE_DEFAULT
+        self._unique: _lib.UniqueCheck | None = None
 
         if rank == 0 and verbose:
             nbytes = self.cache.numel() * self.cache.element_size()
@@ -196,7 +199,9 @@ class PagedKVCache:
         """Slot-mapped append. ``slot_mapping`` [T] int64 (slot = page*16 +
         offset; -1 skips a token); k/v [T, H, D] for ``layer``, or
         [L, T, H, D] for layers 0..L-1 when ``layer`` is None. Slots must be
-        unique. For an fp8 pool k/v are bf16 and are quantised on the way in."""
+        unique (with ``check_unique`` set, a repeat is reported as
+        MkvDeviceError at the next ``check_errors``). For an fp8 pool k/v are
+        bf16 and are quantised on the way in."""
         dev = self._gpu()
         if slot_mapping.dtype != torch.int64 or slot_mapping.device != dev:
             slot_mapping = slot_mapping.to(device=dev, dtype=torch.int64)
@@ -222,6 +227,10 @@ class PagedKVCache:
         _lib.require_gpu(k, v, slot_mapping, self.cache)
         if T == 0:
             return
+        if self.check_unique:
+            if self._unique is None:
+                self._unique = _lib.UniqueCheck(dev, self.num_slots)
+            self._unique.run(slot_mapping, self._errors)
         esz = self.cache.element_size()
         kp = self.cache[first, 0]
         vp = self.cache[first, 1]
@@ -256,7 +265,10 @@ class PagedKVCache:
         returns (k, v) of shape [B, out_len, H, D] with rows past a sequence's
         end zero — the [B,S,H,D] decode layout of
         muserve/model/qwen35_model.py:223-249. Packed mode writes sequence b's
-        rows at ``cu_out[b]`` of [total, H, D] buffers. With ``layer`` None the
+        rows at ``cu_out[b]`` of [total, H, D] buffers (``cu_out`` holds B+1
+        offsets; a sequence whose window does not fit between ``cu_out[b]`` and
+        ``cu_out[b+1]``, or past the buffer's end, is cut there and flagged
+        as MkvDeviceError at the next ``check_errors``). With ``layer`` None the
         first ``num_layers`` layers are gathered into [L, ...] outputs in one
         launch. fp8 pools are dequantised to bf16. ``out`` reuses buffers.
         """
@@ -276,14 +288,13 @@ class PagedKVCache:
             raise ValueError("block_tables rows must be contiguous")
         out_dtype = torch.bfloat16 if self.dtype == _FP8 else self.dtype
         rows = (B * out_len) if cu_out is None else None
+        if cu_out is not None and cu_out.numel() != B + 1:
+            raise ValueError("cu_out must hold B+1 offsets")
         if out is None:
             if cu_out is None:
                 shape = (B, out_len, self.kv_heads, self.head_dim)
             else:
-                total = int(cu_out[-1].item()) if cu_out.numel() > B else None
-                if total is None:
-                    raise ValueError("cu_out must hold B+1 offsets")
-                shape = (total, self.kv_heads, self.head_dim)
+                shape = (max(0, int(cu_out[-1].item())), self.kv_heads, self.head_dim)
             if layer is None:
                 shape = (L, *shape)
             k_out = torch.empty(shape, dtype=out_dtype, device=dev)
@@ -297,6 +308,9 @@ class PagedKVCache:
             if rows is not None and (k_out.numel() != L * rows * self.row_elems
                                      or v_out.numel() != k_out.numel()):
                 raise ValueError(f"out buffers must hold exactly {L}x{rows} rows")
+            if rows is None and (k_out.numel() % (L * self.row_elems) != 0
+                                 or v_out.numel() != k_out.numel()):
+                raise ValueError(f"packed out buffers must hold whole rows for {L} layers")
         _lib.require_gpu(block_tables, seq_lens, k_out, v_out, self.cache)
         if starts is not None:
             starts = starts.to(device=dev, dtype=torch.int32).contiguous()

@@ -12,7 +12,9 @@ this module keeps them resident in two pools indexed by a request slot:
 
 ``gather(layer, slots)`` copies a batch's entries into contiguous buffers and
 ``scatter`` writes updated entries back, both layer's pools in one launch.
-Slot ids within a ``scatter`` must be unique.
+Slot ids within a ``scatter`` (and ``reset``, ``conv_decode``,
+``decode_gather``) must be unique; with ``check_unique`` set a repeat is
+reported as MkvDeviceError at the next ``check_errors``.
 """
 from __future__ import annotations
 
@@ -48,6 +50,10 @@ class StatePool:
                                  device=self.device) if conv_shape is not None else None)
         self._free = list(range(num_slots))
         self._errors = _lib.DeviceErrors(self.device) if self.device.type == "cuda" else None
+        # opt-in: report a slot that appears twice where slots must be unique
+        # (scatter, reset, the in-place conv) as MkvDeviceError
+        self.check_unique = _lib.CHECK_UNIQUE_DEFAULT
+        self._unique: _lib.UniqueCheck | None = None
 
     # slot bookkeeping: a LIFO stack, like the KV page free list
     def alloc_slot(self) -> int:
@@ -65,12 +71,17 @@ class StatePool:
     def _entry_bytes(self, t: torch.Tensor) -> int:
         return t[0, 0].numel() * t.element_size()
 
-    def _check(self, slots: torch.Tensor) -> torch.Tensor:
+    def _check(self, slots: torch.Tensor, unique: bool = False) -> torch.Tensor:
         if self.device.type != "cuda":
             raise RuntimeError(f"StatePool on {self.device}: the slot kernels need a ROCm GPU")
         if slots.dtype != torch.int32 or slots.device != self.device:
             slots = slots.to(device=self.device, dtype=torch.int32)
-        return slots.contiguous()
+        slots = slots.contiguous()
+        if unique and self.check_unique:
+            if self._unique is None:
+                self._unique = _lib.UniqueCheck(self.device, self.num_slots)
+            self._unique.run(slots, self._errors)
+        return slots
 
     def reset(self, slots) -> None:
         """Zeroes the recurrent and conv states of ``slots`` in every layer, the
@@ -79,7 +90,7 @@ class StatePool:
         reused across requests. Slots must be unique; one launch per pool."""
         if not isinstance(slots, torch.Tensor):
             slots = torch.as_tensor(list(slots), dtype=torch.int32)
-        slots = self._check(slots)
+        slots = self._check(slots, unique=True)
         n = slots.numel()
         if n == 0:
             return
@@ -107,7 +118,7 @@ class StatePool:
     def scatter(self, layer: int, slots: torch.Tensor, state: torch.Tensor,
                 conv: torch.Tensor | None = None) -> None:
         """state[layer, slots] = state; conv[layer, slots] = conv (unique slots)."""
-        slots = self._check(slots)
+        slots = self._check(slots, unique=True)
         self._move("mkv_state_scatter", layer, slots, state, conv)
 
     def _move(self, fn: str, layer: int, slots: torch.Tensor, st: torch.Tensor,
@@ -158,7 +169,7 @@ class StatePool:
     def _conv_args(self, layer, slots, x, weight, out):
         if self.conv is None:
             raise RuntimeError("this pool keeps no conv states")
-        slots = self._check(slots)
+        slots = self._check(slots, unique=True)
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"GDN layer {layer} out of range (pool has {self.num_layers})")
         C, W = self.conv.shape[2], self.conv.shape[3]

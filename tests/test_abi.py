@@ -75,3 +75,11 @@ def test_empty_calls_are_no_ops():
 def test_call_raises_with_message():
     with pytest.raises(_lib.MkvError, match="token_bytes 3"):
         _lib.call("mkv_block_hash_sha256", FAKE, FAKE, FAKE, 1, 3, FAKE, FAKE, None)
+
+
+def test_check_unique_arguments():
+    rc, msg = _rc("mkv_check_unique", FAKE, 2, 4, 16, FAKE, 1, FAKE, None)
+    assert rc == -1 and "id_bytes 2" in msg
+    rc, msg = _rc("mkv_check_unique", FAKE, 8, 4, 100, FAKE, 3, FAKE, None)
+    assert rc == -1 and "4 needed" in msg
+    assert _rc("mkv_check_unique", None, 8, 0, 100, None, 0, None, None)[0] == 0

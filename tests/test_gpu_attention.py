@@ -45,19 +45,21 @@ def build(seed, lens, Hq, Hkv, spare=5, width=None):
     return q, k, v, lens, table
 
 
-def within_one_ulp(got: torch.Tensor, want) -> None:
-    """want = (out, mass, smax) from att.decode_attention(..., stats=True)."""
+def within_one_ulp(got: torch.Tensor, want, mant: int = 7, min_exp: int = -126) -> None:
+    """want = (out, mass, smax) from att.decode_attention(..., stats=True).
+    mant / min_exp: mantissa bits and smallest normal exponent of the output
+    type (bf16: 7, -126; fp16: 10, -14, below which its ulp stays 2^-24)."""
     want, mass, smax = want
     got = got.float().cpu().numpy().astype(np.float64)
-    mag = np.maximum(np.abs(want), 2.0 ** -126)
-    tol = 2.0 ** (np.floor(np.log2(mag)) - 7) + 2.0 ** -16 * (1 + smax[..., None]) * mass
+    mag = np.maximum(np.abs(want), 2.0 ** min_exp)
+    tol = 2.0 ** (np.floor(np.log2(mag)) - mant) + 2.0 ** -16 * (1 + smax[..., None]) * mass
     err = np.abs(got - want)
     bad = err > tol
-    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements off by more than 1 bf16 ulp + "
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} elements off by more than 1 ulp + "
                            f"the fp32 term; worst {err[bad].max()} at {np.argwhere(bad)[0]}")
     # the fp32 term only matters where the output cancels: nearly every element
-    # is within one bf16 ulp of its own magnitude
-    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -13))) - 7)
+    # is within one ulp of its own magnitude
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** max(min_exp, -13)))) - mant)
     assert (err <= ulp).mean() > 0.999
 
 
@@ -115,6 +117,63 @@ def test_bad_page_and_long_sequence_are_flagged():
     with pytest.raises(_lib.MkvDeviceError) as e:
         A.check_errors(DEV)
     assert "page id out of range" in str(e.value) and "longer than its block table" in str(e.value)
+
+
+F16 = dict(mant=10, min_exp=-14)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 1), (1, 1), (8, 2)])
+def test_f16_matches_oracle(Hq, Hkv):
+    """fp16 pools (the reference's default KV dtype, muserve/config.py:37):
+    q, caches and output fp16; one fp16 ulp of float64 plus the fp32 term."""
+    lens = [1, 16, 17, 33, 511, 1024, 1025, 2049, 0, 3000]
+    case(f"decode attention fp16 Hq={Hq} Hkv={Hkv} lens {lens}")
+    q, k, v, lens, table = build(61 + Hq + 10 * Hkv, lens, Hq, Hkv)
+    q, k, v = q.half(), k.half(), v.half()
+    got, want = run(q, k, v, lens, table)
+    assert got.dtype == torch.float16
+    within_one_ulp(got, want, **F16)
+
+
+def test_f16_reads_the_default_pool():
+    """PagedKVCache() with the reference's default dtype (fp16): append, then
+    attn_decode over the pool's layer views against the oracle."""
+    rng = np.random.default_rng(62)
+    lens = rng.integers(1, 1500, 12)
+    case(f"default fp16 pool append then decode attention, lens {lens.tolist()}")
+    cache = PagedKVCache(int(sum(-(-int(n) // 16) for n in lens)) + 4, num_layers=2, device=DEV,
+                         verbose=False)
+    assert cache.dtype == torch.float16
+    from muserve_amd.kv_cache import SequenceKVState, prefill_slot_mapping
+    seqs = [SequenceKVState() for _ in lens]
+    slots = prefill_slot_mapping(cache, seqs, [int(n) for n in lens])
+    g = torch.Generator().manual_seed(62)
+    T = int(lens.sum())
+    kv = torch.randn(T, 1, 256, generator=g).half()
+    cache.append(slots, kv.to(DEV), (-kv).to(DEV), layer=1)
+    table = np.zeros((len(lens), max(len(s.page_table) for s in seqs)), dtype=np.int32)
+    for b, s in enumerate(seqs):
+        table[b, :len(s.page_table)] = s.page_table
+    q = torch.randn(len(lens), 1, 4, 256, generator=g).half()
+    out = A.attn_decode(q.to(DEV), *cache.get_kv_by_layer(1),
+                        torch.from_numpy(lens.astype(np.int32)).to(DEV),
+                        torch.from_numpy(table).to(DEV))
+    torch.cuda.synchronize()
+    cache.check_errors()
+    A.check_errors(DEV)
+    kc, vc = cache.get_kv_by_layer(1)
+    want = att.decode_attention(q[:, 0].float().numpy(), kc.float().cpu().numpy(),
+                                vc.float().cpu().numpy(), lens, table, 256 ** -0.5, stats=True)
+    within_one_ulp(out[:, 0], want, **F16)
+
+
+def test_dtype_mismatch_is_rejected():
+    case("attn_decode with a bf16 query over fp16 caches (rejected on the host)")
+    q = torch.zeros(1, 1, 4, 256, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(2, 16, 1, 256, dtype=torch.float16, device=DEV)
+    with pytest.raises(TypeError, match="must match"):
+        A.attn_decode(q, kc, kc, torch.ones(1, dtype=torch.int32, device=DEV),
+                      torch.zeros(1, 1, dtype=torch.int32, device=DEV))
 
 
 def test_decode_config_shape_against_oracle():

@@ -142,3 +142,81 @@ def test_prefix_config_full_trace_against_model():
     status, model = run_block_manager(P=65536, n=4096, batch=256, seed=104, n_templates=64,
                                       template_len=4096, suffix=(64, 1024), width=320)
     assert len(model.evicted) > 50000
+
+
+@pytest.mark.timeout(600)
+def test_gdn_config_interleaved_with_decode_appends_against_oracle():
+    """The hybrid decode step at full size, 60 layers in model order for 3
+    steps: every attention layer (l % 4 == 3, muserve/memory/kv_cache.py:20)
+    appends the step's decode token of 256 sequences (slots from the device
+    decode step, lognormal contexts, seed 102), every GDN layer gathers the
+    256 requests' recurrent + conv states from the 1024-slot pools, updates
+    them (x * 0.5 + layer, conv + step) and scatters them back. The CPU oracle
+    does the same on copies of both state pools and of the KV pool; at the end
+    all three pools are compared byte for byte."""
+    from muserve_amd.kv_cache import BlockTables
+    from muserve_amd.state_pool import gdn_ordinal
+    from oracle import paged as pref
+    from oracle import state as sref
+
+    S, G, B, L, STEPS = 1024, 45, 256, 15, 3
+    case(f"full size: 60 layers in model order x {STEPS} steps, GDN pools 45 x 1024 slots, "
+         f"decode appends on 15 layers, batch {B}")
+    pool = StatePool(num_layers=G, num_slots=S, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(105)
+    pool.state.normal_(generator=gen)
+    pool.conv.normal_(generator=gen)
+    cpu_state = torch.empty(pool.state.shape, dtype=pool.state.dtype)
+    cpu_conv = pool.conv.cpu()
+    for g in range(G):
+        cpu_state[g].copy_(pool.state[g])
+    slots = torch.randperm(S, generator=torch.Generator().manual_seed(105))[:B].to(torch.int32)
+    slots_d = slots.to(DEV)
+
+    ctx = bench.context_lengths()
+    pages = int(np.sum(-(-(ctx + STEPS) // 16))) + 64
+    cache = PagedKVCache(pages, num_layers=L, dtype=torch.bfloat16, device=DEV, verbose=False)
+    cache.shuffle_free_list(torch.Generator().manual_seed(102))
+    pmodel = pref.PoolModel(pages, list(cache._free_pages))
+    seqs = [SequenceKVState() for _ in range(B)]
+    oseqs = [pref.SeqModel() for _ in range(B)]
+    for s_, o_, n in zip(seqs, oseqs, ctx):
+        reserve_tokens(cache, s_, int(n))
+        o_.add_tokens(pmodel, int(n))
+    bt = BlockTables(cache, seqs, max_pages=int(-(-(int(ctx.max()) + STEPS) // 16)))
+    cpu_kv = torch.zeros(cache.cache.shape, dtype=torch.bfloat16)
+    kg = torch.Generator().manual_seed(5)
+
+    for step in range(STEPS):
+        kv_slots = bt.decode_step()
+        want_slots = pref.decode_step(pmodel, oseqs)
+        assert kv_slots.cpu().tolist() == want_slots, f"step {step}"
+        want_slots = torch.tensor(want_slots)
+        for layer in range(60):
+            if layer % 4 == 3:
+                a = layer // 4
+                k = torch.randn(B, 1, 256, generator=kg).bfloat16()
+                v = torch.randn(B, 1, 256, generator=kg).bfloat16()
+                cache.append(kv_slots, k.to(DEV), v.to(DEV), layer=a)
+                pref.append(cpu_kv, want_slots, k, v, layer=a)
+                continue
+            g = gdn_ordinal(layer)
+            st, cv = pool.gather(g, slots_d)
+            st.mul_(0.5).add_(float(g + 1))
+            cv.add_(float(step + 1))
+            pool.scatter(g, slots_d, st, cv)
+            ost = sref.gather(cpu_state, g, slots)
+            ocv = sref.gather(cpu_conv, g, slots)
+            ost.mul_(0.5).add_(float(g + 1))
+            ocv.add_(float(step + 1))
+            sref.scatter(cpu_state, g, slots, ost)
+            sref.scatter(cpu_conv, g, slots, ocv)
+    torch.cuda.synchronize()
+    pool.check_errors()
+    cache.check_errors()
+    for g in range(G):
+        assert torch.equal(pool.state[g].cpu().view(torch.int32), cpu_state[g].view(torch.int32)), g
+    assert torch.equal(pool.conv.cpu().view(torch.int16), cpu_conv.view(torch.int16))
+    for a in range(L):
+        assert torch.equal(cache.cache[a].cpu().view(torch.int16), cpu_kv[a].view(torch.int16)), a
+    assert [s.page_table for s in seqs] == [s.page_table for s in oseqs]

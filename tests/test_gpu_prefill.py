@@ -224,3 +224,91 @@ def test_forced_key_splits_through_the_c_abi(split_len):
                                  v.float().cpu().numpy(), cu.numpy(), 256 ** -0.5, True,
                                  cu_k=cu.numpy(), stats=True)
     within(out, want)
+
+
+def _one_hot_keys(n_rows, heads=1):
+    """V row j = e_(j mod 256) (bf16 ones): with a zero query every visible
+    key has weight 1 / n, so output dim d is (visible keys j = d mod 256) / n
+    and one key more or less changes a dim by about 1 / n, far above the
+    rounding (the worst-case tolerance above cannot see a single key once a
+    row attends to a few hundred)."""
+    v = torch.zeros(n_rows, heads, 256)
+    idx = torch.arange(n_rows)
+    v[idx, :, idx % 256] = 1.0
+    return v.bfloat16()
+
+
+def _one_hot_want(nq, nk, causal):
+    """Closed form for a zero query over one-hot keys: [nq, 256] float64."""
+    out = np.zeros((nq, 256))
+    d = np.arange(256)
+    for t in range(nq):
+        last = nk - nq + t if causal else nk - 1  # bottom-right causal alignment
+        if last < 0:
+            continue
+        n = last + 1
+        cnt = np.where(d <= last, (last - d) // 256 + 1, 0)
+        out[t] = cnt / n
+    return out
+
+
+def _bf16_close(got, want):
+    got = got.float().cpu().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    err = np.abs(got - want)
+    assert (err <= ulp).all(), f"worst {err.max()} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_understated_max_seqlen_k_keeps_every_key(causal):
+    """A max_seqlen_k below the real key count (600 for 2000 keys): the split
+    ranges cover 3 x 256 keys, and the last range must run to the end."""
+    nq = nk = 2000
+    case(f"attn_prefill one-hot keys, {nk} keys, max_seqlen_k 600, causal={causal}")
+    q = torch.zeros(nq, 4, 256).bfloat16().to(DEV)
+    k = torch.randn(nk, 1, 256, generator=torch.Generator().manual_seed(41)).bfloat16().to(DEV)
+    v = _one_hot_keys(nk).to(DEV)
+    cu = torch.tensor([0, nq], dtype=torch.int32, device=DEV)
+    out = A.attn_prefill(q, k, v, cu, cu, nq, 600, causal=causal)
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = _one_hot_want(nq, nk, causal)
+    for h in range(4):
+        _bf16_close(out[:, h], want)
+
+
+def test_one_hot_keys_pin_every_tile_and_split_boundary():
+    """Sequences with a prefix (nk > nq) and lengths around the 64-key tiles
+    and the split boundaries, with forced key splits through the C ABI: each
+    output dim counts its visible keys exactly, so a key dropped or added at
+    any tile or range boundary shows."""
+    nqs = [1, 63, 64, 65, 129, 300]
+    nks = [1, 64, 127, 65, 300, 777]
+    case(f"mkv_prefill_attention_bf16 one-hot keys, forced splits of 128, nq {nqs} nk {nks}")
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(nqs)]), dtype=torch.int32)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(nks)]), dtype=torch.int32)
+    Tq, Tk = int(cu_q[-1]), int(cu_k[-1])
+    q = torch.zeros(Tq + 7, 4, 256).bfloat16().to(DEV)  # 7 rows past every sequence
+    k = torch.randn(Tk, 1, 256, generator=torch.Generator().manual_seed(42)).bfloat16().to(DEV)
+    v = torch.cat([_one_hot_keys(n) for n in nks]).to(DEV)
+    split_len, max_k = 128, max(nks)
+    splits = -(-max_k // split_len)
+    lib = _lib.load()
+    ws_bytes = lib.mkv_prefill_attention_workspace_bytes(Tq + 7, 4, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    canary = torch.full((Tq + 7, 4, 256), 0x1234, dtype=torch.int16, device=DEV)
+    out = canary.clone().view(torch.bfloat16)
+    cu_qd, cu_kd = cu_q.to(DEV), cu_k.to(DEV)
+    _lib.call("mkv_prefill_attention_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), Tk, 1, 4,
+              256, None, 0, 0, cu_qd.data_ptr(), cu_kd.data_ptr(), None, len(nqs), Tq + 7,
+              max(nqs), 256 ** -0.5, 1, splits, split_len, out.data_ptr(), ws.data_ptr(),
+              ws_bytes, A._errword(DEV).ptr(), _lib.stream_of(DEV))
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    for b, (nq, nk) in enumerate(zip(nqs, nks)):
+        want = _one_hot_want(nq, nk, True)
+        rows = out[int(cu_q[b]):int(cu_q[b + 1])]
+        for h in range(4):
+            _bf16_close(rows[:, h], want)
+    # rows outside every sequence's queries are left alone by the merge
+    assert torch.equal(out[Tq:].view(torch.int16), canary[Tq:])

@@ -146,3 +146,25 @@ def test_get_kv_by_layer_views_alias_the_pool():
     k, v = c.get_kv_by_layer(0)
     assert k.shape == (4, 16, 1, 256) and k.data_ptr() == c.cache[0, 0].data_ptr()
     assert v.data_ptr() == c.cache[0, 1].data_ptr()
+
+
+@pytest.mark.parametrize("free_bytes,dtype,want", [
+    # the reference's own case (muserve/kv_cache.py:60-73): 60 layers, 1 KV
+    # head of 256, 2-byte elements -> 983,040 bytes a page; 288e9 free bytes
+    # leave 259.2e9 after the 10 % reserve -> 263,671.875 pages
+    (288_000_000_000, torch.float16, 263_671),
+    (288_000_000_000, torch.bfloat16, 263_671),
+    # fp8: 256 code bytes + a 4-byte scale per (token, head) -> 499,200 bytes
+    # a page; 259.2e9 / 499,200 = 519,230.77
+    (288_000_000_000, torch.float8_e4m3fn, 519_230),
+    # the reserve is int(free * 0.10), taken before the division:
+    # 1,000,000,007 - 100,000,000 = 900,000,007 -> 915.52 -> the 1024 floor
+    (1_000_000_007, torch.float16, 1024),
+    # just above the floor: 1,200,000,000 - 120,000,000 = 1.08e9 -> 1098.63
+    (1_200_000_000, torch.bfloat16, 1098),
+])
+def test_estimate_pages_closed_form(monkeypatch, free_bytes, dtype, want):
+    """_estimate_pages against the reference's arithmetic worked out by hand
+    (elements sized by the dtype; fp8 counts its per-token scale)."""
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (free_bytes, 2 * free_bytes))
+    assert PagedKVCache._estimate_pages("cuda:0", 1, dtype) == want
