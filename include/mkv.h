@@ -510,6 +510,31 @@ int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_
                               void* stream);
 
 /*
+ * mkv_decode_attention_bf16 without a workspace argument and without any
+ * allocation: the work counters and chunk partials live in a file-scope
+ * device array of the library (48 MiB, one copy per GPU, held until the
+ * process ends), whose address the first call on each device looks up with
+ * that device current. No counterpart in the reference: it is for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation). The caller still passes the
+ * inputs, out and err. Limit: batch x num_q_heads x ceil(max_seq_len / 1024)
+ * chunk states must fit the array (at most 48,770 of them when max_seq_len >
+ * 1024, e.g. batch 256 x 4 query heads up to 47 x 1024 tokens); a larger call
+ * returns MKV_E_UNSUPPORTED and launches nothing. Calls on one GPU share the
+ * array: calls that overlap on one GPU (different streams, or threads without
+ * ordering) race and must not be issued; calls ordered on one stream are
+ * safe. Results are bit-for-bit those of mkv_decode_attention_bf16 (the same
+ * kernels). Same arguments, limits and error bits otherwise.
+ */
+int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                      int64_t num_pages, int32_t num_kv_heads,
+                                      int32_t num_q_heads, int32_t head_dim,
+                                      const int32_t* page_table, int64_t table_stride,
+                                      int32_t table_width, const int32_t* seq_lens,
+                                      int32_t batch, int32_t max_seq_len, float softmax_scale,
+                                      void* out, int32_t* err, void* stream);
+
+/*
  * The same over an fp16 pool: q, k_cache, v_cache and out are fp16 (scores on
  * the fp16 MFMA, fp32 softmax and accumulation, out rounded to fp16 RNE).
  * fp16 is the reference's default pool dtype (muserve/config.py:37

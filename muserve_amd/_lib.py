@@ -87,6 +87,8 @@ SIGNATURES: dict[str, list] = {
     "mkv_decode_attention_workspace_bytes": [_I32, _I32, _I32, _I32],
     "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
                                   _I32, _F32, _P, _P, _I64, _P, _P],
+    "mkv_decode_attention_bf16_noalloc": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
+                                          _I32, _I32, _F32, _P, _P, _P],
     "mkv_decode_attention_f16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
                                  _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,

@@ -32,6 +32,7 @@
 // lengths. The merge kernel, which runs next, resets the counter.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "mkv_device.h"
@@ -736,4 +737,87 @@ extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, cons
                           nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
                           table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
                           out, workspace, workspace_bytes, err, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The same bf16 decode attention for callers that cannot allocate (code under
+// HIP graph capture, tight serving loops): the workspace is a file-scope
+// device array, one copy per GPU, held until the process ends.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Room for the work counters and the chunk partials of batch x query heads x
+// chunks <= 48,770 (e.g. batch 256, 4 query heads, max_seq_len up to 47 x
+// 1024 tokens).
+constexpr int64_t kNoAllocScratchBytes = 48ll << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+__global__ void zero_queue_kernel(int32_t* queue) {
+  if (threadIdx.x < kQueueBytes / 4) queue[threadIdx.x] = 0;
+}
+
+// The current device's copy of `scratch`. In host code the array's name is
+// only a stand-in for the symbol: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only
+// that address is ever handed to a kernel. The first call on a device also
+// zeroes the work counters on the caller's stream (a fill kernel, not a
+// memset node); every call leaves them zero again (the merge kernel resets
+// them), as it does for a caller's workspace.
+int scratch_of_current_device(const char* fn, hipStream_t st, void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(MKV_E_LAUNCH, "%s: no usable current device (%s)", fn,
+                     ge != hipSuccess ? hipGetErrorString(ge) : "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(MKV_E_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", fn,
+                       hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_queue_kernel, dim3(1), dim3(64), 0, st, static_cast<int32_t*>(p));
+    const int rc = check_launch(fn);
+    if (rc != MKV_OK) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MKV_OK;
+}
+
+}  // namespace
+
+extern "C" int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_cache,
+                                                 const void* v_cache, int64_t num_pages,
+                                                 int32_t num_kv_heads, int32_t num_q_heads,
+                                                 int32_t head_dim, const int32_t* page_table,
+                                                 int64_t table_stride, int32_t table_width,
+                                                 const int32_t* seq_lens, int32_t batch,
+                                                 int32_t max_seq_len, float softmax_scale,
+                                                 void* out, int32_t* err, void* stream) {
+  static const char* fn = "mkv_decode_attention_bf16_noalloc";
+  clear_error();
+  const int64_t need =
+      mkv_decode_attention_workspace_bytes(batch, num_kv_heads, num_q_heads, max_seq_len);
+  MKV_REQUIRE(need <= kNoAllocScratchBytes, MKV_E_UNSUPPORTED,
+              "%s: batch %d x %d query heads x %lld chunks of 1024 tokens need %lld bytes of "
+              "scratch, the static scratch holds %lld",
+              fn, batch, num_q_heads, (long long)attn_chunks(max_seq_len), (long long)need,
+              (long long)kNoAllocScratchBytes);
+  if (batch == 0) return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr,
+                                          num_pages, num_kv_heads, num_q_heads, head_dim,
+                                          page_table, table_stride, table_width, seq_lens, batch,
+                                          max_seq_len, softmax_scale, out, nullptr, 0, err,
+                                          stream);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(fn, as_stream(stream), &ws);
+  if (rc != MKV_OK) return rc;
+  return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr, num_pages,
+                          num_kv_heads, num_q_heads, head_dim, page_table, table_stride,
+                          table_width, seq_lens, batch, max_seq_len, softmax_scale, out, ws,
+                          kNoAllocScratchBytes, err, stream);
 }
