@@ -12,7 +12,13 @@ block table into padded contiguous [256, Lpad, 1, 256] K and V (zero padding).
 Prints one JSON line. ``value`` is algorithmic HBM bytes per step / step
 time (GB/s); ``roofline`` is the gather kernel's algorithmic bytes per launch
 / its mean launch time from HIP events on its stream, against 8 TB/s;
-``cpu_baseline`` times the CPU oracle's gather on one layer of one step.
+``cpu_baseline`` times the CPU oracle (torch-CPU restatement of the reference)
+on 3 whole decode steps (15 layers of append + padded gather) on the host's
+cores, after which the GPU runs the same 3 steps and the pools are compared.
+After the headline's timed region, the default run also measures the other
+configurations (``secondary``): fp8 chunked prefill (append and dequant-gather
+separately), the GDN state slots in model order and MALL-cold, and the
+prefix cache (us per request, hashing and block manager apart).
 """
 from __future__ import annotations
 
@@ -81,35 +87,81 @@ def step_bytes(lens: np.ndarray) -> tuple[float, float, float]:
     return float(LAYERS * (gather + append)), float(gather), float(LAYERS * useful)
 
 
-def cpu_baseline(cache, bt, lens_now: np.ndarray, gpu_out) -> dict:
-    """The oracle's gather (torch-CPU index_select per sequence) on the last
-    layer of the current step, timed on the host; also checks the GPU result
-    of that layer (the last one the timed loop gathered) against it."""
+CPU_STEPS = 3  # whole decode steps the CPU baseline times
+
+
+def cpu_threads() -> dict:
+    """Sets torch's CPU threads to every core this process may run on (its
+    affinity set, capped by OMP_NUM_THREADS where the host sets it: a GPU box
+    gives one GPU's job a share of the host's cores) and describes them."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
+    torch.set_num_threads(threads)
+    return {"cores": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": affinity, "omp_num_threads": omp or None, "cpu_model": _cpu_model()}
+
+
+def cpu_baseline_steps(cache, seqs, kin, vin, first: int, n_steps: int, gpu_step) -> dict:
+    """The oracle's decode step on the host's cores, for n_steps whole steps
+    (the slot assignment of oracle.paged.decode_step, then per layer the
+    slot-mapped append and the padded gather of K and V: torch-CPU
+    index_put_ / index_select, restating muserve/kv_cache.py:102-158 and the
+    [B,S,H,D] layout of muserve/model/qwen35_model.py:223-249), on a copy of
+    the GPU pool taken after the timed loop, with the inputs of steps
+    first .. first+n_steps-1. The GPU then runs the same steps (gpu_step) and
+    its pool and last gather are compared with the CPU's byte for byte."""
     from oracle import paged as ref
 
-    threads = torch.get_num_threads()
-    lpad = int(gpu_out[0].shape[1])
-    kplane = cache.cache[LAYERS - 1, 0].cpu()
-    vplane = cache.cache[LAYERS - 1, 1].cpu()
-    bt_cpu = bt.tables.cpu()
-    sl = torch.from_numpy(lens_now.astype(np.int32))
+    info = cpu_threads()
+    cpu_cache = cache.cache.cpu()
+    pool = ref.PoolModel(cache.num_pages, list(cache._free_pages))
+    oseqs = []
+    for s in seqs:
+        o = ref.SeqModel()
+        o.page_table, o.seq_len = list(s.page_table), s.seq_len
+        oseqs.append(o)
+    k_cpu = kin[first:first + n_steps].cpu()
+    v_cpu = vin[first:first + n_steps].cpu()
+    nbytes = 0.0
     t0 = time.perf_counter()
-    k_ref = ref.gather_padded(kplane, bt_cpu, sl, lpad)
-    v_ref = ref.gather_padded(vplane, bt_cpu, sl, lpad)
+    for j in range(n_steps):
+        slots = torch.tensor(ref.decode_step(pool, oseqs), dtype=torch.int64)
+        lens = np.array([o.seq_len for o in oseqs], dtype=np.int64)
+        width = max(len(o.page_table) for o in oseqs)
+        table = np.zeros((len(oseqs), width), dtype=np.int32)
+        for b, o in enumerate(oseqs):
+            table[b, :len(o.page_table)] = o.page_table
+        bt = torch.from_numpy(table)
+        sl = torch.from_numpy(lens.astype(np.int32))
+        lpad = int(-(-int(lens.max()) // 16) * 16)
+        for l in range(LAYERS):
+            ref.append(cpu_cache, slots, k_cpu[j, l], v_cpu[j, l], layer=l)
+            k_ref = ref.gather_padded(cpu_cache[l, 0], bt, sl, lpad)
+            v_ref = ref.gather_padded(cpu_cache[l, 1], bt, sl, lpad)
+        nbytes += step_bytes(lens)[0]
     dt = time.perf_counter() - t0
-    _, gbytes, _ = step_bytes(lens_now)
-    same = bool(torch.equal(gpu_out[0].cpu().view(torch.int16), k_ref.view(torch.int16)) and
-                torch.equal(gpu_out[1].cpu().view(torch.int16), v_ref.view(torch.int16)))
+    for j in range(n_steps):
+        kout, vout = gpu_step(first + j)
+    torch.cuda.synchronize()
+    cache.check_errors()
+    same_gather = bool(torch.equal(kout.cpu().view(torch.int16), k_ref.view(torch.int16)) and
+                       torch.equal(vout.cpu().view(torch.int16), v_ref.view(torch.int16)))
+    same_pool = all(torch.equal(cache.cache[l].cpu().view(torch.int16),
+                                cpu_cache[l].view(torch.int16)) for l in range(LAYERS))
     return {
-        "value": round(gbytes / dt / 1e9, 3),
+        "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
-        "cores": threads,
+        **info,
         "kind": "port",
-        "sample": (f"oracle gather (torch-CPU index_select, {threads} threads) of one layer's K, V "
-                   f"of one decode step at batch {B}, Lpad {lpad}: {dt:.2f} s"),
+        "sample": (f"{n_steps} whole decode steps of the oracle (slot assignment, then per layer "
+                   f"the append and the padded K/V gather, torch-CPU, {info['cores']} threads) at "
+                   f"batch {B}, {LAYERS} layers, Lpad {lpad}: {dt:.2f} s, "
+                   f"{1e3 * dt / n_steps:.0f} ms per step"),
         "seconds": round(dt, 3),
-        "cpu_model": _cpu_model(),
-        "gpu_matches_cpu_on_sampled_layer": same,
+        "ms_per_step": round(1e3 * dt / n_steps, 1),
+        "gpu_pool_matches_cpu_after_the_steps": same_pool,
+        "gpu_last_gather_matches_cpu": same_gather,
     }
 
 
@@ -162,7 +214,8 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     ctx = context_lengths()
-    total_steps = warmup + steps
+    # the CPU baseline's steps run on the GPU too, after the timed loop
+    total_steps = warmup + steps + (CPU_STEPS if with_cpu else 0)
     pages = int(np.sum(-(-(ctx + total_steps) // 16))) + 64
     log(f"pool: {pages} pages x {LAYERS} layers (ctx sum {int(ctx.sum())}, max {int(ctx.max())})")
     cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
@@ -222,13 +275,12 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for j in range(steps):
-        out = one_step(warmup + j, recs[j], step_spans)
+        one_step(warmup + j, recs[j], step_spans)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     cache.check_errors()
     mean_gather_s = _timed(recs, "gather") / 1e3
     mean_gather_bytes = gather_bytes / steps
-    lens_now = bt._lens.copy()
 
     traffic, ratio = counter_traffic()
     step_s = elapsed / steps
@@ -279,8 +331,9 @@ def run_decode(steps: int, warmup: int, with_cpu: bool) -> dict:
         },
     }
     if with_cpu:
-        log("cpu baseline (one layer of one step)")
-        res["cpu_baseline"] = cpu_baseline(cache, bt, lens_now, out)
+        log(f"cpu baseline ({CPU_STEPS} whole steps of the oracle)")
+        res["cpu_baseline"] = cpu_baseline_steps(cache, seqs, kin, vin, warmup + steps, CPU_STEPS,
+                                                 one_step)
     return res
 
 
@@ -606,6 +659,30 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool, fused_conv: bool = Fa
     elapsed = time.perf_counter() - t0
     pool.check_errors()
     cache.check_errors()
+    cold = None
+    if not fused_conv:
+        # MALL-cold: the 45 layers' gathers back to back into 45 separate
+        # buffers (a 5.8 GiB working set, 23x the 256 MB MALL), then their
+        # scatters: every byte of both moves comes from or goes to HBM
+        sbufs = [torch.empty((B, *pool.state.shape[2:]), dtype=pool.state.dtype, device=dev)
+                 for _ in range(G)]
+        cbufs = [torch.empty((B, *pool.conv.shape[2:]), dtype=pool.conv.dtype, device=dev)
+                 for _ in range(G)]
+        cold = []
+        for _ in range(3):
+            rec = []
+            for g in range(G):
+                sp = stamps.span(stream)
+                pool.gather(g, slots, out=(sbufs[g], cbufs[g]))
+                rec.append(("gather", sp.end(stream)))
+            for g in range(G):
+                sp = stamps.span(stream)
+                pool.scatter(g, slots, sbufs[g], cbufs[g])
+                rec.append(("scatter", sp.end(stream)))
+            cold.append(rec)
+        torch.cuda.synchronize()
+        pool.check_errors()
+        del sbufs, cbufs
     rec_bytes = 8 * 128 * 128 * 4
     entry = rec_bytes + (0 if fused_conv else 2048 * 4 * 2)
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
@@ -647,6 +724,19 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool, fused_conv: bool = Fa
     }
     if fused_conv:
         res["conv_bytes_per_layer"] = conv_bytes
+    if cold is not None:
+        cg, cs = _timed(cold[1:], "gather"), _timed(cold[1:], "scatter")
+        res["mall_cold"] = {
+            "what": ("the 45 gathers back to back into separate buffers (5.8 GiB working set), "
+                     "then the 45 scatters, so no byte is served by the 256 MB MALL; mean of "
+                     "the last 2 of 3 rounds"),
+            "pct_of_hbm_peak": round(100 * 2 * move_bytes / ((cg + cs) / 1e3) / 1e9 / HBM_PEAK_GBS,
+                                     2),
+            "kernels": [
+                _kernel_roofline("state_move_kernel<true> (mkv_state_gather)", move_bytes, cg,
+                                 ratios.get("state_move_kernel<true>")),
+                _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, cs,
+                                 ratios.get("state_move_kernel<false>"))]}
     if with_cpu:
         from oracle import state as ref
         n = 32
@@ -1398,8 +1488,17 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                                if ratio else None),
             "mean_launch_us": round(attn_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": round(attn_b / attn_launches),
+            # with the prefill attention on a second stream the two kernels
+            # share the GPU, and the event span above times the decode
+            # attention while it does: not a per-kernel figure (run with
+            # --serial-prefill for that)
+            "concurrent": side is not None,
         },
     }
+    if side is not None:
+        res["roofline"]["note"] = ("measured while the prefill attention ran beside it on a "
+                                   "second stream; the per-kernel fraction comes from "
+                                   "--serial-prefill, the step-level figure is `value`")
     if pre_pairs:
         n_pre = LAYERS * sum(1 for x in info if x[6])
         pre_tf = pre_flops / n_pre / (pre_ms / 1e3) / 1e12
@@ -1413,7 +1512,7 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                "split)" if fp8 else "(mkv_prefill_attention_bf16, paged, key ranges split)"),
             "achieved": round(pre_tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(pre_tf / MFMA_BF16_PEAK_TFLOPS, 4), "mean_launch_us": round(pre_ms * 1e3, 2),
-            "flop_per_launch": round(pre_flops / n_pre),
+            "flop_per_launch": round(pre_flops / n_pre), "concurrent": side is not None,
             "stream": "main, after the decode attention" if side is None else
                       "second stream, concurrent with the decode attention (launch time "
                       "measured while sharing the GPU)"}
@@ -1730,6 +1829,44 @@ def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
             "bytes_written": nbytes, "launches": reps}
 
 
+def _summary(r: dict, keep: tuple[str, ...]) -> dict:
+    """A secondary configuration's result, compacted for the headline line:
+    its metric and value, the named extra keys, and per kernel the
+    algorithmic bytes per launch, the event-timed mean launch and the
+    fraction of the HBM roofline."""
+    def kern(k: dict) -> dict:
+        return {key: k[key] for key in ("kernel", "bound", "algorithmic_bytes_per_launch",
+                                         "mean_launch_us", "achieved", "frac",
+                                         "traffic_to_algorithmic", "us_per_request", "launch_ms",
+                                         "GB_hashed_per_s") if key in k}
+    out = {"workload": r["config"]["workload"], "metric": r["metric"], "value": r["value"],
+           "unit": r["unit"], "ms_per_step": r["ms_per_step"]}
+    out.update({k: r[k] for k in keep if k in r})
+    out["kernels"] = [kern(k) for k in r["roofline"]["kernels"]]
+    if "mall_cold" in r:
+        out["mall_cold"] = {"pct_of_hbm_peak": r["mall_cold"]["pct_of_hbm_peak"],
+                            "kernels": [kern(k) for k in r["mall_cold"]["kernels"]]}
+    return out
+
+
+def run_secondary() -> dict:
+    """The other configurations, after the headline (each on a fresh pool,
+    with its default sizes): fp8 chunked prefill, GDN state slots in model
+    order (and MALL-cold), the prefix cache."""
+    out = {}
+    for name, fn, steps, warmup, keep in (
+            ("fp8_prefill", run_fp8_prefill, 12, 3, ("pct_of_hbm_peak", "appended_tokens_per_s")),
+            ("gdn_state", run_gdn_state, 50, 5, ("pct_of_hbm_peak", "state_move_ms_per_step")),
+            ("prefix", run_prefix, 5, 1, ("requests_per_s", "phase_ms", "evictions",
+                                          "page_hit_rate", "cow_copies"))):
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        log(f"secondary: {name}")
+        out[name] = _summary(fn(steps, warmup, False), keep)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--calibrate", action="store_true",
@@ -1738,6 +1875,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="default workload: skip the other configurations after the headline")
     ap.add_argument("--serial-prefill", action="store_true",
                     help="sched workloads: prefill attention on the main stream, after the "
                          "decode attention (default: beside it on a second stream)")
@@ -1788,6 +1927,8 @@ def main() -> int:
     gc.freeze()
     gc.disable()
     res = runner(steps, warmup, not args.no_cpu_baseline)
+    if args.workload == "decode" and not args.no_secondary:
+        res["secondary"] = run_secondary()
     print(json.dumps(res), flush=True)
     return 0
 
