@@ -103,7 +103,11 @@ __device__ __forceinline__ u32x4 quantise_row(const u32x4 r0, const u32x4 r1, fl
 // One 16-lane group per (token, head) row of one (layer, K|V): grid.x covers
 // the rows, grid.y is layer * 2 + K|V. The slot and both source loads are
 // issued together; a group whose row is past the end exits as a whole, so the
-// shuffles only ever read lanes of the same live row.
+// shuffles only ever read lanes of the same live row. Source rows are read
+// once and pool rows are not read back this step: non-temporal loads and
+// stores (6 % faster than ordinary ones on the chunked-prefill shape; more
+// rows per group, K and V in one workgroup, 128- or 512-thread workgroups
+// and a persistent grid measured no faster).
 __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   const uint32_t lane = threadIdx.x & (kLanesPerRow - 1);
   const uint32_t row = blockIdx.x * kRowsPerWg + threadIdx.x / kLanesPerRow;
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   const int64_t slot = a.slots[t];
   const uint8_t* src = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride +
                        (int64_t)t * a.src_token_stride + (int64_t)h * (kHeadDim * 2) + lane * 32;
-  const u32x4 r0 = ld16(src), r1 = ld16(src + 16);
+  const u32x4 r0 = ld_nt(src), r1 = ld_nt(src + 16);
   if (slot < 0 || slot >= a.num_slots) {  // -1 skips the token; anything else is an error
     if (slot != -1 && lane == 0 && h == 0 && !is_v) raise_err(a.err, MKV_DEVERR_SLOT);
     return;
@@ -123,11 +127,11 @@ __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   float scale;
   const u32x4 codes = quantise_row(r0, r1, scale);
   uint8_t* pool = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
-  st16(pool + slot * ((int64_t)a.num_heads * kHeadDim) + (int64_t)h * kHeadDim + lane * 16, codes);
+  st_nt(pool + slot * ((int64_t)a.num_heads * kHeadDim) + (int64_t)h * kHeadDim + lane * 16, codes);
   if (lane == 0) {
     float* sp = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(is_v ? a.v_scale : a.k_scale) +
                                          (int64_t)l * a.scale_layer_stride);
-    sp[slot * a.num_heads + h] = scale;
+    __builtin_nontemporal_store(scale, sp + slot * a.num_heads + h);
   }
 }
 
