@@ -140,6 +140,18 @@ class PagedKVCache:
     def num_free_tokens(self) -> int:
         return self._num_free * self.page_size
 
+    def reserve_range(self, lo: int, hi: int) -> None:
+        """Takes pages [lo, hi) out of the free list for good (the others keep
+        their order): a block manager that owns those pages hands them out
+        itself. All of them must be free."""
+        if not 0 <= lo <= hi <= self.num_pages:
+            raise ValueError(f"page range [{lo}, {hi}) outside the pool of {self.num_pages}")
+        keep = [p for p in self._free_pages if not lo <= p < hi]
+        if len(self._free_pages) - len(keep) != hi - lo:
+            raise RuntimeError(f"pages [{lo}, {hi}) are not all free")
+        self._free_pages = keep
+        self._num_free = len(keep)
+
     def shuffle_free_list(self, generator: torch.Generator) -> None:
         """Replaces the free list by a seeded permutation of the free pages."""
         perm = torch.randperm(len(self._free_pages), generator=generator).tolist()

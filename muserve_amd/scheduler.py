@@ -31,6 +31,25 @@ Attached to a ``PagedKVCache`` it also plans whole steps for the pool:
   ``max_seq_len`` (``finish_request``). Its pages and row are freed at the
   next ``plan_step``.
 
+With a ``BlockManager`` attached (``block_manager=``), admissions reuse
+cached prompt pages. The block manager owns pool pages [0, its num_pages)
+(taken out of the cache's free list); the cache's free list keeps the rest
+for each request's private pages. A request's shareable pages are the full
+pages before its last prompt token, fb = (n - 1) // 16. Its admission hashes
+them on the GPU (``mkv_block_hash_sha256``) and admits them through
+``mkv_bm_step`` (leading cached pages shared and pinned, the others taken from
+the block manager's free stack or by evicting its least recently released
+cached page, their hashes registered); the chunked prefill then starts at its
+first uncached page, and its tail page (the page of its last prompt token,
+where decoding continues) and decode pages come from the private list. A
+finished request's release returns its cached pages to the block manager's
+LRU instead of a free list. Admission candidates are the queue's head while
+the budget, counted as if nothing were cached, is not spent, a row and a
+private page are free; the block manager's work for a step (releases, then
+the candidates' admits) runs on a side stream, and the host waits for its
+results (hits and page ids) before it plans the chunks. ``oracle/sched.py``
+(``PrefixSchedulerModel``) states the policy.
+
 Entries are ordered decode tokens first (running order), then prefill chunks,
 so ``plan.block_tables[:plan.num_decode]`` and ``plan.seq_lens[:plan.num_decode]``
 are what ``attn_decode`` reads for the decode half. A plan's device tensors
@@ -84,6 +103,13 @@ class InferenceRequest:
     seq: Optional[SequenceKVState] = None
     row: int = -1
     num_prefilled: int = 0
+    # prefix reuse: shareable pages (held by the block manager), how many of
+    # them were cache hits, and how many of the row's pages the device table
+    # holds
+    fb: int = 0
+    hits: int = 0
+    dev_held: int = 0
+    bm_id: int = -1  # its request id in the block manager
 
     @property
     def total_len(self) -> int:
@@ -108,7 +134,10 @@ class StepPlan:
     block_tables: torch.Tensor          # [num_entries, width] int32
     seq_lens: torch.Tensor              # [num_entries] int32, after the step
     rows: torch.Tensor                  # [num_entries] int32 batch rows / GDN state slots
-    admitted: list[InferenceRequest] = field(default_factory=list)  # the last prefill entries
+    admitted: list[InferenceRequest] = field(default_factory=list)  # admitted this step
+    fresh: list[int] = field(default_factory=list)  # entries whose request starts here
+    skipped_tokens: int = 0             # prompt tokens found in the prefix cache this step
+    bm_ops: list[int] = field(default_factory=list)  # block-manager ops of this step
 
     @property
     def num_decode(self) -> int:
@@ -132,7 +161,7 @@ class ContinuousBatchScheduler:
     def __init__(self, max_batch_size: int = 8, max_seq_len: int = 32768,
                  device: torch.device = None, *, kv_cache: PagedKVCache | None = None,
                  chunked_prefill_size: int = CHUNKED_PREFILL_SIZE,
-                 eos_token_id: int | None = None, state_pool=None):
+                 eos_token_id: int | None = None, state_pool=None, block_manager=None):
         self.max_batch_size = max_batch_size
         self.max_seq_len = max_seq_len
         self.device = device
@@ -155,6 +184,25 @@ class ContinuousBatchScheduler:
             raise ValueError(f"state pool has {state_pool.num_slots} slots for "
                              f"{max_batch_size} batch rows")
         self.state_pool = state_pool
+        self.block_manager = block_manager
+        self.bm_held = 0          # sum of fb over requests admitted to the block manager
+        self.prefix_skipped = 0   # prompt tokens served from cached pages so far
+        if block_manager is not None:
+            if kv_cache is None:
+                raise ValueError("prefix reuse needs the paged pool (kv_cache=...)")
+            bm = block_manager
+            if bm.device != kv_cache.device or bm.num_pages > kv_cache.num_pages:
+                raise ValueError("the block manager must own a page range of the cache's pool")
+            if bm.tables.shape[0] != 2 * max_batch_size or bm.tables.shape[1] < self.width:
+                raise ValueError(f"the block manager needs {2 * max_batch_size} requests (twice "
+                                 f"the batch) and >= {self.width} pages per request")
+            kv_cache.reserve_range(0, bm.num_pages)
+            # block-manager request ids: a FIFO of twice the batch, so an id
+            # released in a step is not admitted again in that step (an admit
+            # takes the front, a release appends); each id's length stays
+            # until its release, which reads it
+            self._bm_ids = deque(range(2 * max_batch_size))
+            self._bm_ntok = np.zeros(2 * max_batch_size, dtype=np.int64)
         if kv_cache is not None:
             if chunked_prefill_size <= 0:
                 raise ValueError("chunked_prefill_size must be positive")
@@ -241,12 +289,40 @@ class ContinuousBatchScheduler:
                         for _ in range(self._RING)]
         self._events = [None] * self._RING
         self._ring = 0
+        if self.block_manager is not None:
+            # one block-manager round per step: candidates' prompt tokens (their
+            # sum stays below budget + one prompt), per-row hash offsets and
+            # lengths, the ops; read back: status, hits and page rows
+            max_tok = self.chunked_prefill_size + self.max_seq_len
+            W = self.width
+            self._bm = dict(
+                side=torch.cuda.Stream(dev),  # default priority, like every stream here
+                tok_h=torch.empty(max_tok, dtype=torch.int64, pin_memory=True),
+                tok_d=torch.empty(max_tok, **i64),
+                meta_h=torch.empty(8 * (B + 1), dtype=torch.int64, pin_memory=True),
+                meta_d=torch.empty(8 * (B + 1), **i64),
+                hashes=torch.empty(max_tok // KV_PAGE_SIZE + 1, **i64),
+                back_h=torch.empty(B * (2 + W), dtype=torch.int32, pin_memory=True),
+                errors=_lib.DeviceErrors(dev),
+                last=None,  # the previous round's end (its copies read the staging buffers)
+            )
 
-    def _retire(self, lst: list[InferenceRequest]) -> list[InferenceRequest]:
+    def _retire(self, lst: list[InferenceRequest],
+                ops: list[int] | None = None) -> list[InferenceRequest]:
         keep = []
         for r in lst:
             if r.is_done:
-                if r.seq is not None:
+                if r.seq is not None and ops is not None:
+                    # prefix reuse: the shareable pages go back through the
+                    # block manager (to its LRU when cached), the rest to the
+                    # private list
+                    if r.fb > 0:
+                        ops.append(-(r.bm_id + 1))
+                        self._bm_ids.append(r.bm_id)
+                        self.bm_held -= r.fb
+                    self.kv_cache.free_pages(r.seq.page_table[r.fb:])
+                    r.seq.page_table = []
+                elif r.seq is not None:
                     self.kv_cache.free_pages(r.seq.page_table)
                     r.seq.page_table = []
                 if r.row >= 0:
@@ -264,6 +340,8 @@ class ContinuousBatchScheduler:
             raise RuntimeError("plan_step needs a PagedKVCache (kv_cache=...)")
         if self._last is not None:
             raise RuntimeError("complete_step the previous plan before planning another")
+        if self.block_manager is not None:
+            return self._plan_host_prefix()
         cache = self.kv_cache
         P = KV_PAGE_SIZE
         with self.lock:
@@ -338,11 +416,185 @@ class ContinuousBatchScheduler:
                 r.num_prefilled += count
             up = np.array(flat + pages, dtype=np.int32)
             decode = [e[0] for e in rec[:len(self.running_batch)]]
+            for r, *_ in rec:
+                r.dev_held = len(r.seq.page_table)
             plan = StepPlan(decode=decode, prefill=prefill, num_tokens=tok_off, upload=up,
                             slot_mapping=None, positions=None, cu_seqlens=None,
-                            block_tables=None, seq_lens=None, rows=None, admitted=admitted)
+                            block_tables=None, seq_lens=None, rows=None, admitted=admitted,
+                            fresh=list(range(n - len(admitted), n)))
             self._last = plan
             return plan
+
+    def _plan_host_prefix(self) -> StepPlan | None:
+        """plan_host with prefix reuse (the module docstring; the policy of
+        oracle.sched.PrefixSchedulerModel)."""
+        cache = self.kv_cache
+        P = KV_PAGE_SIZE
+        with self.lock:
+            ops: list[int] = []
+            self.running_batch = self._retire(self.running_batch, ops)
+            self.prefilling = self._retire(self.prefilling, ops)
+            entries = []  # (request, start, count)
+            for r in self.running_batch:
+                seq = r.seq
+                if seq.seq_len >= len(seq.page_table) * P:
+                    seq.page_table += cache.alloc_pages(1)  # the reference's OOM error if none
+                entries.append((r, seq.seq_len, 1))
+                seq.seq_len += 1
+            budget = self.chunked_prefill_size
+            prefill: list[tuple[InferenceRequest, int, int]] = []
+
+            def chunk(r: InferenceRequest) -> None:
+                nonlocal budget
+                n = min(len(r.input_ids) - r.num_prefilled, budget)
+                if n <= 0:
+                    return
+                start = r.seq.seq_len
+                entries.append((r, start, n))
+                prefill.append((r, start, n))
+                r.seq.seq_len += n
+                r.num_prefilled += n
+                budget -= n
+
+            for r in self.prefilling:
+                chunk(r)
+            cands: list[InferenceRequest] = []
+            wc = budget
+            while (wc > 0 and self.waiting_queue and cache.num_free_pages > len(cands)
+                   and len(self.running_batch) + len(self.prefilling) + len(cands)
+                   < self.max_batch_size):
+                r = self.waiting_queue.popleft()
+                r.fb = (len(r.input_ids) - 1) // P
+                last = self.bm_held + r.fb > self.block_manager.num_pages
+                r.row = heapq.heappop(self._free_rows)
+                cands.append(r)
+                self.bm_held += r.fb
+                wc -= len(r.input_ids)
+                if last:
+                    break
+            result = self._bm_round(ops, cands)
+            admitted, skipped = [], 0
+            for r in cands:
+                table, r.hits = [], 0
+                if r.fb > 0:
+                    status, r.hits, table = result[r.bm_id]
+                    if status != 0:  # OOM: only the last candidate can get it
+                        self._bm_ids.appendleft(r.bm_id)
+                        r.bm_id = -1
+                        self.bm_held -= r.fb
+                        heapq.heappush(self._free_rows, r.row)
+                        r.row = -1
+                        r.fb = 0
+                        self.waiting_queue.appendleft(r)
+                        continue
+                r.seq = SequenceKVState(max_pages=self.width)
+                r.seq.page_table = list(table) + cache.alloc_pages(1)
+                r.seq.seq_len = r.num_prefilled = r.hits * P
+                r.dev_held = 0
+                skipped += r.hits * P
+                r.state = RequestState.PREFILLING
+                self.prefilling.append(r)
+                admitted.append(r)
+                chunk(r)
+            self.prefix_skipped += skipped
+            ops += [r.bm_id for r in cands if r.fb > 0]
+            if not entries:  # (the round above issued the releases)
+                return None
+            flat, pages, fresh = [], [], []
+            tok_off = 0
+            for i, (r, start, count) in enumerate(entries):
+                new = r.seq.page_table[r.dev_held:]
+                if r.dev_held == 0:
+                    fresh.append(i)
+                flat += (r.row, start, count, r.dev_held, len(new), len(pages), tok_off, 0)
+                pages += new
+                r.dev_held = len(r.seq.page_table)
+                tok_off += count
+            up = np.array(flat + pages, dtype=np.int32)
+            decode = [e[0] for e in entries[:len(self.running_batch)]]
+            plan = StepPlan(decode=decode, prefill=prefill, num_tokens=tok_off, upload=up,
+                            slot_mapping=None, positions=None, cu_seqlens=None,
+                            block_tables=None, seq_lens=None, rows=None, admitted=admitted,
+                            fresh=fresh, skipped_tokens=skipped, bm_ops=ops)
+            self._last = plan
+            return plan
+
+    def _bm_round(self, ops: list[int], cands: list[InferenceRequest]) -> dict:
+        """The step's block-manager work on the side stream: page hashes of
+        the candidates' shareable pages, then one mkv_bm_step with the
+        releases and the admits (block-manager ids taken here). Waits for it
+        only when there are admits, and returns {id: (status, hits, pages)}."""
+        admits = [r for r in cands if r.fb > 0]
+        for r in admits:
+            r.bm_id = self._bm_ids.popleft()
+            self._bm_ntok[r.bm_id] = r.fb * KV_PAGE_SIZE
+        ops = list(ops) + [r.bm_id for r in admits]
+        if not ops:
+            return {}
+        if self._dev is None:
+            raise RuntimeError("prefix reuse runs the block manager on a ROCm GPU")
+        b = self._bm
+        bm = self.block_manager
+        B = 2 * self.max_batch_size  # block-manager ids
+        P = KV_PAGE_SIZE
+        dev = self.kv_cache.device
+        # host staging: tokens of the shareable pages in id order (so the
+        # per-id hash offsets are a prefix sum), then the meta block: hash
+        # tok/page offsets (n+1 each), per-id hash offsets (B+1), per-id token
+        # counts (B), ops (candidate order)
+        if b["last"] is not None:
+            b["last"].synchronize()  # the staging buffers are free again
+            b["last"] = None
+        n = len(admits)
+        admits = sorted(admits, key=lambda r: r.bm_id)
+        lens = np.array([r.fb * P for r in admits], dtype=np.int64)
+        cu_t = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        tok = b["tok_h"].numpy()
+        for i, r in enumerate(admits):
+            tok[cu_t[i]:cu_t[i + 1]] = r.input_ids[:r.fb * P]
+        per_row = np.zeros(B, dtype=np.int64)
+        for r in admits:
+            per_row[r.bm_id] = r.fb
+        ntok = self._bm_ntok
+        meta = b["meta_h"].numpy()
+        m = 0
+        for arr in (cu_t, cu_t // P, np.concatenate([[0], np.cumsum(per_row)]), ntok,
+                    np.array(ops, dtype=np.int64)):
+            meta[m:m + len(arr)] = arr
+            m += len(arr)
+        side = b["side"]
+        with torch.cuda.stream(side):
+            if n:
+                b["tok_d"][:int(cu_t[-1])].copy_(b["tok_h"][:int(cu_t[-1])], non_blocking=True)
+            b["meta_d"][:m].copy_(b["meta_h"][:m], non_blocking=True)
+            md = b["meta_d"]
+            o_cut, o_cup, o_hash = 0, n + 1, 2 * (n + 1)
+            o_ntok, o_ops = o_hash + B + 1, o_hash + 2 * B + 1
+            if n:
+                _lib.call("mkv_block_hash_sha256", b["tok_d"].data_ptr(), md[o_cut:].data_ptr(),
+                          md[o_cup:].data_ptr(), n, 8, b["hashes"].data_ptr(),
+                          b["errors"].ptr(), side.cuda_stream)
+            bm.step(md[o_ops:o_ops + len(ops)].to(torch.int32), b["hashes"],
+                    md[o_hash:o_hash + B + 1], md[o_ntok:o_ntok + B].to(torch.int32))
+            if not n:
+                b["last"] = torch.cuda.Event()
+                b["last"].record(side)
+                return {}
+            rows = torch.tensor([r.bm_id for r in admits], dtype=torch.int64).to(dev,
+                                                                                   non_blocking=True)
+            W = max(r.fb for r in admits)
+            back = torch.cat([bm.status.index_select(0, rows), bm.hits.index_select(0, rows),
+                              bm.tables.index_select(0, rows)[:, :W].reshape(-1)])
+            out = b["back_h"][:back.numel()]
+            out.copy_(back, non_blocking=True)
+            done = torch.cuda.Event()
+            done.record(side)
+        done.synchronize()
+        v = out.numpy()
+        status, hits = v[:n], v[n:2 * n]
+        tables = v[2 * n:].reshape(n, W)
+        return {r.bm_id: (int(status[i]), int(hits[i]), tables[i, :r.fb].tolist())
+                for i, r in enumerate(admits)}
 
     def plan_step(self) -> StepPlan | None:
         """Schedules one step and writes its device tensors (one upload, one
@@ -395,9 +647,13 @@ class ContinuousBatchScheduler:
         plan.block_tables = d["step_tables"][:n, :width]
         plan.seq_lens = d["step_lens"][:n]
         plan.rows = d["rows"][:n]
-        if self.state_pool is not None and plan.admitted:
-            # the admitted requests are the last prefill entries
-            self.state_pool.reset(plan.rows[n - len(plan.admitted):])
+        if self.state_pool is not None and plan.fresh:
+            # requests whose first entry this is start from zero GDN states
+            idx = plan.fresh
+            if idx == list(range(idx[0], idx[0] + len(idx))):
+                self.state_pool.reset(plan.rows[idx[0]:idx[0] + len(idx)])
+            else:
+                self.state_pool.reset(plan.rows[torch.tensor(idx, device=plan.rows.device)])
         return plan
 
     def complete_step(self, plan: StepPlan, next_tokens=None) -> list[InferenceRequest]:
@@ -433,6 +689,11 @@ class ContinuousBatchScheduler:
         return done
 
     def check_errors(self) -> None:
-        """Synchronises and raises MkvDeviceError if a step plan was malformed."""
+        """Synchronises and raises MkvDeviceError if a step plan was malformed
+        (or, with prefix reuse, a block-manager round flagged a fault)."""
         if self._dev is not None:
             self._dev["errors"].check("ContinuousBatchScheduler")
+        if self.block_manager is not None and self._dev is not None:
+            self._bm["side"].synchronize()
+            self._bm["errors"].check("ContinuousBatchScheduler page hashes")
+            self.block_manager.check_errors()

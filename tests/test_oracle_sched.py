@@ -134,3 +134,123 @@ def test_oracle_invariants(seed):
             break
     assert all(r.state == S.FINISHED for r in reqs)
     assert sorted(pool.free) == list(range(40))
+
+
+# ---- prefix reuse through the block manager (PrefixSchedulerModel) ----
+
+from oracle.blocks import BlockManagerModel  # noqa: E402
+
+
+def _prefix_model(chunk=40, B=4, bm_pages=8, private=(8, 16), max_seq_len=128):
+    pool = pg.PoolModel(private[1], list(range(*private)))
+    return S.PrefixSchedulerModel(B, chunk, BlockManagerModel(bm_pages), pool, max_seq_len)
+
+
+def test_prefix_model_known_trace():
+    """Worked out by hand: A = T + 5 tokens and B = T + 3 tokens share a
+    48-token template T (3 shareable pages each), C has 10 tokens of its own.
+    Budget 40 per step, block-manager pages 0..7 (popped 7, 6, 5, ...),
+    private pages 8..15 (popped 15, 14, ...)."""
+    T = list(range(1000, 1048))
+    A = S.PReq("A", T + [1, 2, 3, 4, 5], max_new_tokens=2)
+    Bq = S.PReq("B", T + [6, 7, 8], max_new_tokens=2)
+    C = S.PReq("C", list(range(2000, 2010)), max_new_tokens=2)
+    m = _prefix_model()
+    for r in (A, Bq, C):
+        m.add(r)
+    # step 1: A is the only candidate (40 - 53 < 0 ends the candidates); its
+    # three template pages are fresh (7, 6, 5), its tail page 15; 40 tokens
+    s1 = m.step()
+    assert s1["ops"] == [0] and s1["admitted"] == [("A", 0, 0)] and s1["skipped"] == 0
+    assert s1["counts"] == [40] and s1["starts"] == [0]
+    assert s1["slots"] == list(range(112, 128)) + list(range(96, 112)) + list(range(80, 88))
+    m.complete()
+    # step 2: A's last 13 tokens (page 5's second half, tail page 15), then B
+    # hits all three template pages: 48 tokens skipped, its 3 tokens go to its
+    # tail page 14
+    s2 = m.step()
+    assert s2["ops"] == [1] and s2["admitted"] == [("B", 1, 3)] and s2["skipped"] == 48
+    assert s2["rids"] == ["A", "B"] and s2["starts"] == [40, 48] and s2["counts"] == [13, 3]
+    assert s2["slots"] == list(range(88, 96)) + list(range(240, 245)) + [224, 225, 226]
+    assert s2["tables"][1][:4] == [7, 6, 5, 14]
+    assert m.complete() == []
+    # step 3: A and B decode in their tail pages; C (no shareable page, no
+    # block-manager op) prefills into page 13
+    s3 = m.step()
+    assert s3["ops"] == [] and s3["kinds"] == ["decode", "decode", "prefill"]
+    assert s3["slots"] == [245, 227] + list(range(208, 218))
+    assert {r.rid for r in m.complete()} == {"A", "B"}
+    # step 4: A and B release their pages in retire order; the template pages
+    # reach refcount 0 with B's release, tail first: LRU 5, 6, 7
+    s4 = m.step()
+    assert s4["ops"] == [-1, -2] and s4["slots"] == [218]
+    assert m.bm.lru_order() == [5, 6, 7]
+    assert m.pool.free == [8, 9, 10, 11, 12, 15, 14]
+    assert m.skipped == 48
+    m.bm.check_invariants()
+
+
+def _random_prompts(rng, n, lo, hi, vocab=151936):
+    return [rng.integers(0, vocab, int(rng.integers(lo, hi))).tolist() for _ in range(n)]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_prefix_model_reduces_to_chunked_without_sharing(seed):
+    """With no prompt prefix in common and pools that never run out, prefix
+    reuse changes nothing in the schedule: the same entries (request, kind,
+    start, count, row) step for step as ChunkedSchedulerModel."""
+    rng = np.random.default_rng(seed)
+    prompts = _random_prompts(rng, 60, 1, 300)
+    outs = rng.integers(1, 40, 60)
+    pm = S.PrefixSchedulerModel(8, 128, BlockManagerModel(100000),
+                                pg.PoolModel(200000, list(range(100000, 200000))), 4096)
+    cm = S.ChunkedSchedulerModel(8, 128, pg.PoolModel(100000), 4096)
+    for i, (p, o) in enumerate(zip(prompts, outs)):
+        pm.add(S.PReq(i, p, int(o)))
+        cm.add(S.Req(i, len(p), int(o)))
+    for _ in range(2000):
+        a, b = pm.step(), cm.step()
+        key = ("rids", "kinds", "starts", "counts", "rows", "lens")
+        assert {k: a[k] for k in key} == {k: b[k] for k in key}
+        assert a["skipped"] == 0
+        pm.complete()
+        cm.complete()
+        if not (pm.waiting or pm.running or pm.prefilling):
+            break
+    assert not (cm.waiting or cm.running or cm.prefilling)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_prefix_model_invariants_on_shared_prompts(seed):
+    """Zipf-shared templates with small pools (evictions, a block manager that
+    turns candidates away, private pages running short): block-manager
+    invariants after every step, every slot of a step distinct and inside its
+    request's pages, the private pages partitioned between the list and the
+    live requests, and no hit page read before it is written (the model
+    asserts it)."""
+    rng = np.random.default_rng(seed)
+    templates = [rng.integers(0, 151936, 96).tolist() for _ in range(4)]
+    zipf = 1.0 / np.arange(1, 5) ** 1.1
+    prompts = []
+    for _ in range(80):
+        t = templates[rng.choice(4, p=zipf / zipf.sum())]
+        prompts.append(t[:int(rng.integers(20, 97))] + rng.integers(0, 151936,
+                                                                    int(rng.integers(0, 40))).tolist())
+    m = S.PrefixSchedulerModel(6, 64, BlockManagerModel(40),
+                               pg.PoolModel(80, list(range(40, 80))), 512)
+    reqs = [S.PReq(i, p, int(rng.integers(1, 30))) for i, p in enumerate(prompts)]
+    for r in reqs:
+        m.add(r)
+    for _ in range(5000):
+        s = m.step()
+        m.bm.check_invariants()
+        assert len(set(s["slots"])) == len(s["slots"])
+        live = m.running + m.prefilling
+        private_held = [p for r in live for p in r.seq.page_table[r.fb:]]
+        assert sorted(private_held + m.pool.free) == list(range(40, 80))
+        assert all(p < 40 for r in live for p in r.seq.page_table[:r.fb])
+        m.complete()
+        if not (m.waiting or m.running or m.prefilling):
+            break
+    assert all(r.state == S.FINISHED for r in reqs)
+    assert m.skipped > 0 and m.bm.evicted
