@@ -1198,7 +1198,7 @@ def sched_requests(n: int, seed: int = SCHED_SEED) -> tuple[np.ndarray, np.ndarr
 
 
 def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
-              hybrid: bool = False, serial_prefill: bool = False) -> dict:
+              hybrid: bool = False, serial_prefill: bool = False, prefix: bool = False) -> dict:
     """Continuous-batching serving steps on one TP rank, driven by the
     scheduler's step plan: a backlog of requests, at most 256 running, a
     4096-token chunked-prefill budget per step (muserve/config.py:33,40).
@@ -1214,7 +1214,11 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     zeroed at admission): decode entries through the fused recurrent gather +
     in-place decode conv, prefill entries through a gather of both states,
     then a scatter of the recurrent states back (the GDN recurrence itself is
-    model math and is not run)."""
+    model math and is not run).
+    prefix: the prefix-cache configuration's prompts (Zipf(1.1) over 64
+    templates of 4096 ids + a 64..1024-token suffix) served with prefix reuse:
+    a block manager owns most of the pool, admissions hash their prompts on
+    the GPU and skip the cached pages' tokens."""
     from muserve_amd.kernels import attention as A
     from muserve_amd.kv_cache import PagedKVCache
     from muserve_amd.scheduler import ContinuousBatchScheduler, InferenceRequest
@@ -1227,10 +1231,23 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     pages = SCHED_BATCH * width + 64  # every running request can reach max_seq: no OOM
     n_req = 4096
     prompts, outs = sched_requests(n_req)
+    bm = None
+    if prefix:
+        from muserve_amd.block_manager import BlockManager
+        token_ids = prefix_requests(n_req, seed=104)
+        prompts = np.array([len(x) for x in token_ids], dtype=np.int64)
+        # block manager: every running request's shareable pages plus the
+        # 64 templates' pages (16,384) cached; private: a tail page and the
+        # decode pages of every running request
+        bm_pages = SCHED_BATCH * int(-(-prompts.max() // 16)) + 64 * 4096 // 16
+        pages = bm_pages + SCHED_BATCH * (SCHED_MAX_NEW // 16 + 2) + 64
     kv_dtype = torch.float8_e4m3fn if fp8 else torch.bfloat16
     cache = PagedKVCache(pages, num_layers=LAYERS, kv_heads=1, head_dim=HEAD_DIM,
                          dtype=kv_dtype, device=dev, verbose=False)
     cache.shuffle_free_list(torch.Generator().manual_seed(SCHED_SEED))
+    if prefix:
+        bm = BlockManager(bm_pages, 2 * SCHED_BATCH, width, dev,
+                          free_order=np.random.default_rng(SCHED_SEED).permutation(bm_pages))
     free0 = list(cache._free_pages)
     chunk = 4096
     gen = torch.Generator(device=dev).manual_seed(SCHED_SEED)
@@ -1240,9 +1257,10 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         pool.state.normal_(generator=gen)
         pool.conv.normal_(generator=gen)
     s = ContinuousBatchScheduler(max_batch_size=SCHED_BATCH, max_seq_len=max_seq, kv_cache=cache,
-                                 chunked_prefill_size=chunk, state_pool=pool)
+                                 chunked_prefill_size=chunk, state_pool=pool, block_manager=bm)
     for i in range(n_req):
-        s.add_request(InferenceRequest(request_id=str(i), input_ids=[0] * int(prompts[i]),
+        ids = token_ids[i].tolist() if prefix else [0] * int(prompts[i])
+        s.add_request(InferenceRequest(request_id=str(i), input_ids=ids,
                                        max_new_tokens=int(outs[i])))
     max_t = SCHED_BATCH + chunk
     kin = torch.empty(LAYERS, max_t * HEAD_DIM, dtype=torch.bfloat16, device=dev)
@@ -1391,6 +1409,7 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     info: list = []
     log(f"timing {steps} steps ({s.num_running} running, {s.num_prefilling} prefilling, "
         f"{s.num_waiting} waiting)")
+    skipped0 = s.prefix_skipped
     step_spans: list = []
     t0 = time.perf_counter()
     for j in range(steps):
@@ -1452,8 +1471,11 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                  "output lengths; a sampled token is a placeholder)"),
         "config": {
             "workload": ("continuous-batching serving on one TP rank: 4096 queued requests, "
-                         "prompts lognormal(median 1024, sigma 1, clip 16..8192), outputs "
-                         "uniform 32..512 tokens, at most 256 running, 4096-token chunked "
+                         + ("prompts Zipf(1.1) over 64 templates of 4096 random ids + a "
+                            "64..1024-token suffix (seed 104) with prefix reuse through the "
+                            "block manager" if prefix else
+                            "prompts lognormal(median 1024, sigma 1, clip 16..8192)")
+                         + ", outputs uniform 32..512 tokens, at most 256 running, 4096-token chunked "
                          "prefill budget per step; 15 attention layers, 1 KV head x 256, "
                          + ("fp8 e4m3fn" if fp8 else "bf16") + " pool of 16-token pages, "
                          "4 query heads"
@@ -1520,7 +1542,22 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         gdn_ms = _timed(recs, "gdn")
         res["gdn_us_per_layer"] = round(gdn_ms * 1e3, 2)
         res["gdn_GBps"] = round(gdn_b / steps / 45 / (gdn_ms / 1e3) / 1e9, 2)
-    if with_cpu:
+    if prefix:
+        skipped = s.prefix_skipped - skipped0
+        prompt_tok = tokens - decode_tokens + skipped  # prefill tokens computed + served
+        res["prefix"] = {
+            "block_manager_pages": bm.num_pages, "private_pages": pages - bm.num_pages,
+            "prompt_tokens_skipped": int(skipped),
+            "prompt_tokens_computed": int(tokens - decode_tokens),
+            "skipped_fraction": round(skipped / max(1, prompt_tok), 4),
+            "prompt_tokens_per_s_incl_skipped": round(prompt_tok / elapsed, 1),
+            "evictions": int(bm.counters()[6]),
+            "note": ("the timed steps' prompt tokens found in cached pages (never computed or "
+                     "appended); plan_host_us includes the block-manager round (mkv_bm_step on "
+                     "a side stream: the step's releases and admits) and the wait for its "
+                     "results; prompts are hashed on the side stream when they are queued"),
+        }
+    if with_cpu and not prefix:
         log("cpu baseline (scheduler oracle: per-token page bookkeeping of the same trace)")
         res["cpu_baseline"] = sched_cpu_baseline(prompts, outs, pages, free0, chunk, max_seq,
                                                  first_slots, warmup, steps)
@@ -1883,7 +1920,8 @@ def main() -> int:
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
-                             "sched", "sched_fp8", "sched_hybrid", "prefill_attn"],
+                             "sched", "sched_fp8", "sched_hybrid", "sched_prefix",
+                             "prefill_attn"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -1906,6 +1944,8 @@ def main() -> int:
               "sched": lambda *a: run_sched(*a, serial_prefill=args.serial_prefill),
               "sched_fp8": lambda *a: run_sched(*a, fp8=True),
               "sched_hybrid": lambda *a: run_sched(*a, hybrid=True,
+                                                   serial_prefill=args.serial_prefill),
+              "sched_prefix": lambda *a: run_sched(*a, prefix=True,
                                                    serial_prefill=args.serial_prefill),
               "prefill_attn": run_prefill_attn}[args.workload]
     steps, warmup = args.steps, args.warmup

@@ -110,6 +110,7 @@ class InferenceRequest:
     hits: int = 0
     dev_held: int = 0
     bm_id: int = -1  # its request id in the block manager
+    page_hashes: Optional[torch.Tensor] = field(default=None, repr=False)  # until admitted
 
     @property
     def total_len(self) -> int:
@@ -202,6 +203,7 @@ class ContinuousBatchScheduler:
             # takes the front, a release appends); each id's length stays
             # until its release, which reads it
             self._bm_ids = deque(range(2 * max_batch_size))
+            self._unhashed: list[InferenceRequest] = []  # queued, page hashes not yet launched
             self._bm_ntok = np.zeros(2 * max_batch_size, dtype=np.int64)
         if kv_cache is not None:
             if chunked_prefill_size <= 0:
@@ -221,6 +223,8 @@ class ContinuousBatchScheduler:
                                  f"max_seq_len {self.max_seq_len}")
         with self.lock:
             self.waiting_queue.append(request)
+            if self.block_manager is not None:
+                self._unhashed.append(request)
 
     def schedule_step(self) -> tuple[list[InferenceRequest], list[InferenceRequest]]:
         """(prefill_requests, decode_requests): drop finished requests, decode
@@ -290,18 +294,13 @@ class ContinuousBatchScheduler:
         self._events = [None] * self._RING
         self._ring = 0
         if self.block_manager is not None:
-            # one block-manager round per step: candidates' prompt tokens (their
-            # sum stays below budget + one prompt), per-row hash offsets and
+            # one block-manager round per step: per-id hash offsets and
             # lengths, the ops; read back: status, hits and page rows
-            max_tok = self.chunked_prefill_size + self.max_seq_len
             W = self.width
             self._bm = dict(
                 side=torch.cuda.Stream(dev),  # default priority, like every stream here
-                tok_h=torch.empty(max_tok, dtype=torch.int64, pin_memory=True),
-                tok_d=torch.empty(max_tok, **i64),
                 meta_h=torch.empty(8 * (B + 1), dtype=torch.int64, pin_memory=True),
                 meta_d=torch.empty(8 * (B + 1), **i64),
-                hashes=torch.empty(max_tok // KV_PAGE_SIZE + 1, **i64),
                 back_h=torch.empty(B * (2 + W), dtype=torch.int32, pin_memory=True),
                 errors=_lib.DeviceErrors(dev),
                 last=None,  # the previous round's end (its copies read the staging buffers)
@@ -431,6 +430,7 @@ class ContinuousBatchScheduler:
         cache = self.kv_cache
         P = KV_PAGE_SIZE
         with self.lock:
+            self._hash_queued()
             ops: list[int] = []
             self.running_batch = self._retire(self.running_batch, ops)
             self.prefilling = self._retire(self.prefilling, ops)
@@ -487,6 +487,7 @@ class ContinuousBatchScheduler:
                         r.fb = 0
                         self.waiting_queue.appendleft(r)
                         continue
+                r.page_hashes = None  # admitted: the block manager holds what it needs
                 r.seq = SequenceKVState(max_pages=self.width)
                 r.seq.page_table = list(table) + cache.alloc_pages(1)
                 r.seq.seq_len = r.num_prefilled = r.hits * P
@@ -519,11 +520,41 @@ class ContinuousBatchScheduler:
             self._last = plan
             return plan
 
+    def _hash_queued(self) -> None:
+        """Page hashes of the shareable pages of every request queued since
+        the last step, in one launch on the side stream. A request waits in
+        the queue for at least this step, so its chain of SHA-256 pages (one
+        lane walks it) is not on the admission's path; the hashes stay on the
+        device with the request until its admission."""
+        todo, self._unhashed = self._unhashed, []
+        todo = [r for r in todo if (len(r.input_ids) - 1) // KV_PAGE_SIZE > 0]
+        if not todo:
+            return
+        P = KV_PAGE_SIZE
+        fbs = np.array([(len(r.input_ids) - 1) // P for r in todo], dtype=np.int64)
+        cu_t = np.concatenate([[0], np.cumsum(fbs * P)]).astype(np.int64)
+        tok = np.empty(int(cu_t[-1]), dtype=np.int64)
+        for i, r in enumerate(todo):
+            tok[cu_t[i]:cu_t[i + 1]] = r.input_ids[:int(fbs[i]) * P]
+        offs = np.concatenate([cu_t, cu_t // P])
+        dev = self.kv_cache.device
+        side = self._bm["side"]
+        with torch.cuda.stream(side):
+            tok_d = torch.from_numpy(tok).to(dev)
+            offs_d = torch.from_numpy(offs).to(dev)
+            out = torch.empty(int(cu_t[-1]) // P, dtype=torch.int64, device=dev)
+            _lib.call("mkv_block_hash_sha256", tok_d.data_ptr(), offs_d.data_ptr(),
+                      offs_d[len(todo) + 1:].data_ptr(), len(todo), 8, out.data_ptr(),
+                      self._bm["errors"].ptr(), side.cuda_stream)
+        for i, r in enumerate(todo):
+            r.page_hashes = out[int(cu_t[i]) // P:int(cu_t[i + 1]) // P]
+
     def _bm_round(self, ops: list[int], cands: list[InferenceRequest]) -> dict:
-        """The step's block-manager work on the side stream: page hashes of
-        the candidates' shareable pages, then one mkv_bm_step with the
-        releases and the admits (block-manager ids taken here). Waits for it
-        only when there are admits, and returns {id: (status, hits, pages)}."""
+        """The step's block-manager work on the side stream: one mkv_bm_step
+        with the releases and the candidates' admits (block-manager ids taken
+        here; the candidates' page hashes were computed when they were
+        queued). Waits for it only when there are admits, and returns
+        {id: (status, hits, pages)}."""
         admits = [r for r in cands if r.fb > 0]
         for r in admits:
             r.bm_id = self._bm_ids.popleft()
@@ -536,46 +567,33 @@ class ContinuousBatchScheduler:
         b = self._bm
         bm = self.block_manager
         B = 2 * self.max_batch_size  # block-manager ids
-        P = KV_PAGE_SIZE
         dev = self.kv_cache.device
-        # host staging: tokens of the shareable pages in id order (so the
-        # per-id hash offsets are a prefix sum), then the meta block: hash
-        # tok/page offsets (n+1 each), per-id hash offsets (B+1), per-id token
-        # counts (B), ops (candidate order)
+        # the meta block: per-id hash offsets (B+1; the admits' hashes are
+        # concatenated in id order, so the offsets are a prefix sum), per-id
+        # token counts (B), ops (candidate order)
         if b["last"] is not None:
-            b["last"].synchronize()  # the staging buffers are free again
+            b["last"].synchronize()  # the staging buffer is free again
             b["last"] = None
         n = len(admits)
         admits = sorted(admits, key=lambda r: r.bm_id)
-        lens = np.array([r.fb * P for r in admits], dtype=np.int64)
-        cu_t = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-        tok = b["tok_h"].numpy()
-        for i, r in enumerate(admits):
-            tok[cu_t[i]:cu_t[i + 1]] = r.input_ids[:r.fb * P]
-        per_row = np.zeros(B, dtype=np.int64)
+        per_id = np.zeros(B, dtype=np.int64)
         for r in admits:
-            per_row[r.bm_id] = r.fb
-        ntok = self._bm_ntok
+            per_id[r.bm_id] = r.fb
         meta = b["meta_h"].numpy()
         m = 0
-        for arr in (cu_t, cu_t // P, np.concatenate([[0], np.cumsum(per_row)]), ntok,
+        for arr in (np.concatenate([[0], np.cumsum(per_id)]), self._bm_ntok,
                     np.array(ops, dtype=np.int64)):
             meta[m:m + len(arr)] = arr
             m += len(arr)
         side = b["side"]
         with torch.cuda.stream(side):
-            if n:
-                b["tok_d"][:int(cu_t[-1])].copy_(b["tok_h"][:int(cu_t[-1])], non_blocking=True)
             b["meta_d"][:m].copy_(b["meta_h"][:m], non_blocking=True)
             md = b["meta_d"]
-            o_cut, o_cup, o_hash = 0, n + 1, 2 * (n + 1)
-            o_ntok, o_ops = o_hash + B + 1, o_hash + 2 * B + 1
-            if n:
-                _lib.call("mkv_block_hash_sha256", b["tok_d"].data_ptr(), md[o_cut:].data_ptr(),
-                          md[o_cup:].data_ptr(), n, 8, b["hashes"].data_ptr(),
-                          b["errors"].ptr(), side.cuda_stream)
-            bm.step(md[o_ops:o_ops + len(ops)].to(torch.int32), b["hashes"],
-                    md[o_hash:o_hash + B + 1], md[o_ntok:o_ntok + B].to(torch.int32))
+            o_ntok, o_ops = B + 1, 2 * B + 1
+            hashes = (torch.cat([r.page_hashes for r in admits]) if n
+                      else b["meta_d"][:1])  # (no admit reads a hash)
+            bm.step(md[o_ops:o_ops + len(ops)].to(torch.int32), hashes, md[:B + 1],
+                    md[o_ntok:o_ntok + B].to(torch.int32))
             if not n:
                 b["last"] = torch.cuda.Event()
                 b["last"].record(side)
