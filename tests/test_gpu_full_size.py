@@ -54,7 +54,7 @@ def test_decode_config_append_gather_round_trip():
     cache.check_errors()
 
 
-def test_fp8_config_append_and_window_sampled_against_oracle():
+def test_fp8_config_append_and_window_against_oracle():
     case("full size: fp8 pool of 262160 pages x 15 layers, 32 x 2048-token chunks into 128k contexts")
     R, CHUNK, CTX, WIN, L = 32, 2048, 131072, 8192, 15
     cache = PagedKVCache(R * CTX // 16 + 16, num_layers=L, dtype=torch.float8_e4m3fn, device=DEV,
@@ -62,7 +62,6 @@ def test_fp8_config_append_and_window_sampled_against_oracle():
     cache.shuffle_free_list(torch.Generator().manual_seed(103))
     seqs = [SequenceKVState() for _ in range(R)]
     prior = CTX - CHUNK
-    g = torch.Generator().manual_seed(103)
     gen = torch.Generator(device=DEV).manual_seed(103)
 
     def kv(t):
@@ -78,38 +77,122 @@ def test_fp8_config_append_and_window_sampled_against_oracle():
     sl = torch.from_numpy(np.concatenate(
         [slot_mapping_for(s, reserve_tokens(cache, s, fill), fill) for s in seqs])).to(DEV)
     cache.append(sl, kv(len(sl)), kv(len(sl)))
-    chunk_slots = np.concatenate([slot_mapping_for(s, reserve_tokens(cache, s, CHUNK), CHUNK)
-                                  for s in seqs])
+    chunk_slots = torch.from_numpy(np.concatenate(
+        [slot_mapping_for(s, reserve_tokens(cache, s, CHUNK), CHUNK) for s in seqs])).to(DEV)
     k, v = kv(R * CHUNK), kv(R * CHUNK)
-    cache.append(torch.from_numpy(chunk_slots).to(DEV), k, v)
+    cache.append(chunk_slots, k, v)
     cache.check_errors()
-    # sampled appended rows vs the oracle's quantiser (codes and scales, bit for bit)
-    pick = torch.randperm(R * CHUNK, generator=g)[:4096]
-    for layer in (0, L - 1):
+    # every appended row of every layer vs the oracle's quantiser (codes and
+    # scales, bit for bit)
+    for layer in range(L):
         for kvi, x in ((0, k), (1, v)):
-            q, sc = ref.quantize_rows(x[layer, pick].cpu())
-            slot = torch.from_numpy(chunk_slots)[pick]
-            got_q = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[slot.to(DEV)].cpu()
-            got_s = cache.scales[layer, kvi].reshape(-1, 1)[slot.to(DEV)].cpu()
-            assert torch.equal(got_q, q) and torch.equal(got_s.view(torch.int32), sc.view(torch.int32))
-    # dequant-gather of every request's last 8192 tokens, sampled against the oracle
+            q, sc = ref.quantize_rows(x[layer].cpu())
+            got_q = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[chunk_slots].cpu()
+            got_s = cache.scales[layer, kvi].reshape(-1, 1)[chunk_slots].cpu()
+            assert torch.equal(got_q, q), (layer, kvi)
+            assert torch.equal(got_s.view(torch.int32), sc.view(torch.int32)), (layer, kvi)
+    # dequant-gather of every request's last 8192 tokens in every layer vs the
+    # oracle's dequantisation of the pool rows the tables name
     bt = _tables(seqs, CTX // 16)
     lens = torch.full((R,), CTX, dtype=torch.int32, device=DEV)
     starts = lens - WIN
     cu = torch.arange(R + 1, dtype=torch.int64, device=DEV) * WIN
-    out_rows = torch.randperm(R * WIN, generator=g)[:4096]
-    b_idx, i_idx = out_rows // WIN, out_rows % WIN
-    pos = CTX - WIN + i_idx
-    tables = bt.cpu().to(torch.int64)
-    slot = tables[b_idx, pos // 16] * 16 + pos % 16
-    for layer in (0, 7, L - 1):
+    pos = torch.arange(CTX - WIN, CTX, device=DEV)
+    slot = (bt.to(torch.int64)[:, pos // 16] * 16 + pos % 16).reshape(-1)  # [R * WIN]
+    for layer in range(L):
         kd, vd = cache.gather(layer, bt, lens, out_len=WIN, starts=starts, cu_out=cu)
         for kvi, got in ((0, kd), (1, vd)):
-            codes = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[slot.to(DEV)].cpu()
-            scales = cache.scales[layer, kvi].reshape(-1, 1)[slot.to(DEV)].cpu()
+            codes = cache.cache[layer, kvi].view(torch.uint8).reshape(-1, 1, 256)[slot].cpu()
+            scales = cache.scales[layer, kvi].reshape(-1, 1)[slot].cpu()
             want = ref.dequant_rows(codes, scales)
-            assert torch.equal(got[out_rows.to(DEV)].cpu().view(torch.int16), want.view(torch.int16))
+            assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16)), (layer, kvi)
     cache.check_errors()
+
+
+@pytest.mark.timeout(600)
+def test_decode_config_steps_against_oracle():
+    """The decode configuration's step sequence at full size: 256 sequences
+    (lognormal lengths, seed 102), 15 layers, 3 steps of device slot
+    assignment (pages taken at page boundaries from a shuffled free list),
+    all-layer appends and padded gathers of the grown tables. Per step: the
+    slots equal the oracle's decode_step, the device tables and lengths equal
+    the oracle's; the appended rows sit at the oracle's slots; every layer's
+    padded gather equals torch's index_select of the same rows on the device,
+    and its first and last sequences equal the CPU oracle's gather; at the end
+    an int64 checksum of each layer's pool equals the one before the steps
+    with the overwritten rows swapped for the appended ones (nothing else
+    was written)."""
+    from muserve_amd.kv_cache import BlockTables
+    from oracle import paged as pref
+
+    B, L, STEPS = 256, 15, 3
+    ctx = bench.context_lengths()
+    case(f"full size: {STEPS} decode steps, batch {B}, {L} layers, ctx sum {int(ctx.sum())}")
+    pages = int(np.sum(-(-(ctx + STEPS) // 16))) + 64
+    cache = PagedKVCache(pages, num_layers=L, dtype=torch.bfloat16, device=DEV, verbose=False)
+    gen = torch.Generator(device=DEV).manual_seed(102)
+    for l in range(L):
+        cache.cache[l].normal_(generator=gen)
+    cache.shuffle_free_list(torch.Generator().manual_seed(102))
+    pm = pref.PoolModel(pages, list(cache._free_pages))
+    seqs = [SequenceKVState() for _ in range(B)]
+    oseqs = [pref.SeqModel() for _ in range(B)]
+    for s_, o_, n in zip(seqs, oseqs, ctx):
+        reserve_tokens(cache, s_, int(n))
+        o_.add_tokens(pm, int(n))
+    width = int(-(-(int(ctx.max()) + STEPS) // 16))
+    bt = BlockTables(cache, seqs, max_pages=width)
+
+    def checksum(l):
+        return int(cache.cache[l].view(torch.int16).sum(dtype=torch.int64))
+
+    before = [checksum(l) for l in range(L)]
+    delta = [0] * L
+    for step in range(STEPS):
+        slots = bt.decode_step()
+        want = pref.decode_step(pm, oseqs)
+        assert slots.cpu().tolist() == want, f"step {step}: slots"
+        otab = torch.zeros(B, width, dtype=torch.int32)
+        for b, o in enumerate(oseqs):
+            otab[b, :len(o.page_table)] = torch.tensor(o.page_table, dtype=torch.int32)
+        olens = torch.tensor([o.seq_len for o in oseqs], dtype=torch.int32)
+        assert torch.equal(bt.tables.cpu(), otab) and torch.equal(bt.seq_lens.cpu(), olens)
+        kn = torch.randn(L, B, 1, 256, generator=gen, device=DEV).bfloat16()
+        vn = torch.randn(L, B, 1, 256, generator=gen, device=DEV).bfloat16()
+        idx = torch.tensor(want, dtype=torch.int64, device=DEV)
+        for l in range(L):
+            old = cache.cache[l].reshape(2, -1, 256)[:, idx]
+            delta[l] -= int(old.view(torch.int16).sum(dtype=torch.int64))
+        cache.append(slots, kn, vn)
+        for l in range(L):
+            new = cache.cache[l].reshape(2, -1, 256)[:, idx]
+            assert torch.equal(new[0].view(torch.int16), kn[l, :, 0].view(torch.int16)), (step, l)
+            assert torch.equal(new[1].view(torch.int16), vn[l, :, 0].view(torch.int16)), (step, l)
+            delta[l] += int(new.view(torch.int16).sum(dtype=torch.int64))
+        W = bt.padded_len()
+        pos = torch.arange(W, device=DEV)
+        valid = pos[None, :] < bt.seq_lens.to(torch.int64)[:, None]  # [B, W]
+        rows = (bt.tables.to(torch.int64)[:, (pos // 16).clamp(max=width - 1)] * 16 + pos % 16)
+        rows = torch.where(valid, rows, torch.zeros_like(rows))
+        for l in range(L):
+            kd, vd = cache.gather(l, bt.tables, bt.seq_lens, out_len=W)
+            for kvi, got in ((0, kd), (1, vd)):
+                plane = cache.cache[l, kvi].reshape(-1, 256)
+                ref_out = plane.index_select(0, rows.reshape(-1)).reshape(B, W, 256)
+                ref_out = torch.where(valid[..., None], ref_out, torch.zeros_like(ref_out))
+                assert torch.equal(got[:, :, 0].view(torch.int16), ref_out.view(torch.int16)), \
+                    (step, l, kvi)
+                if l in (0, L - 1):  # the CPU oracle on the first and the last sequence
+                    for b in (0, B - 1):
+                        cpu_plane = cache.cache[l, kvi][otab[b, :len(oseqs[b].page_table)]
+                                                        .to(DEV).to(torch.int64)].cpu()
+                        t = torch.arange(len(oseqs[b].page_table), dtype=torch.int32)[None]
+                        w = pref.gather_padded(cpu_plane, t, olens[b:b + 1], W)
+                        assert torch.equal(got[b].cpu().view(torch.int16),
+                                           w[0].view(torch.int16)), (step, l, kvi, b)
+            del kd, vd
+    cache.check_errors()
+    assert [checksum(l) for l in range(L)] == [b + d for b, d in zip(before, delta)]
 
 
 def test_gdn_config_gather_scatter_identities():
