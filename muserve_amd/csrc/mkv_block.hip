@@ -57,6 +57,7 @@ constexpr int kOpChunk = 1024;  // ops whose request metadata is staged in LDS a
 // tid + j*kBmThreads for j < kHeld. Longer requests re-read the rest.
 constexpr int kHeld = 1;
 constexpr int kSetSize = 2048;  // LDS set of the table slots an admit claims
+static_assert(kSetSize == 1 << 11, "set_add's default size");
 
 enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen, kNumCtr = 16 };
 enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
@@ -71,6 +72,7 @@ constexpr int kRunMaxOps = 1024;               // releases retired in bulk per s
 constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
 constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
 enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kRunSpan,
+              kRunNext,  // the first op left to the step kernel (after the run and the groups)
               kRunNumCtr = 16 };
 
 struct BmLayout {
@@ -268,12 +270,13 @@ __device__ __forceinline__ int64_t uni64(int64_t v) {
   return (int64_t)((uint64_t)hi << 32 | lo);
 }
 
-// Adds x >= 0 to an LDS set of kSetSize slots; false if it was already there
-// (or the set is full: callers add at most half of kSetSize values).
+// Adds x >= 0 to an LDS set of 2^kBits slots; false if it was already there
+// (or the set is full: callers add at most half as many values as slots).
+template <int kBits = 11>
 __device__ __forceinline__ bool set_add(int32_t* set, int32_t x) {
-  uint32_t i = ((uint32_t)x * 2654435761u) >> 21;
-  static_assert(kSetSize == 1 << 11, "the hash takes 11 bits");
-  for (int n = 0; n < kSetSize; ++n, i = (i + 1) & (kSetSize - 1)) {
+  constexpr int kSize = 1 << kBits;
+  uint32_t i = ((uint32_t)x * 2654435761u) >> (32 - kBits);
+  for (int n = 0; n < kSize; ++n, i = (i + 1) & (kSize - 1)) {
     const int32_t prev = atomicCAS(&set[i], -1, x);
     if (prev == -1) return true;
     if (prev == x) return false;
@@ -335,13 +338,21 @@ struct Found {
   bool tomb;  // a miss's insertion slot is a tombstone
 };
 
-// Looks up key h. Never runs concurrently with a writer of the table.
-__device__ Found tab_find(const BmState& s, uint64_t h) {
+__device__ __forceinline__ int64_t tab_home(const BmState& s, uint64_t h) {
+  return slot_of(h) & (s.C - 1);
+}
+__device__ __forceinline__ u32x4 tab_entry(const BmState& s, int64_t i) {
+  return *reinterpret_cast<const u32x4*>(s.ent + i * kEntBytes);
+}
+
+// Looks up key h given the entry e at its home slot i (loaded by the caller, so
+// that several lookups can have their first loads in flight together). Never
+// runs concurrently with a writer of the table.
+__device__ Found tab_find_at(const BmState& s, uint64_t h, int64_t i, u32x4 e) {
   const int64_t mask = s.C - 1;
-  int64_t i = slot_of(h) & mask;
   int64_t first_free = -1;
   for (int64_t n = 0; n < s.C; ++n) {
-    const u32x4 e = *reinterpret_cast<const u32x4*>(s.ent + i * kEntBytes);
+    if (n > 0) e = tab_entry(s, i);
     const int32_t v = (int32_t)e.z;
     if (v == kEmpty)
       return Found{-1, 0, (int32_t)(first_free >= 0 ? first_free : i), first_free >= 0};
@@ -350,6 +361,11 @@ __device__ Found tab_find(const BmState& s, uint64_t h) {
     i = (i + 1) & mask;
   }
   return Found{-1, 0, (int32_t)first_free, first_free >= 0};
+}
+
+__device__ __forceinline__ Found tab_find(const BmState& s, uint64_t h) {
+  const int64_t i = tab_home(s, h);
+  return tab_find_at(s, h, i, tab_entry(s, i));
 }
 
 // Claims slot i for (h, page, refcount ref) if it still holds `expect` (empty
@@ -658,8 +674,7 @@ __device__ void admit(const BmArgs& a, int32_t r, int32_t n, int32_t nhash, int6
     later[j] = false;
     reg_pg[j] = 0;
     if (!reg[j]) continue;
-    const int64_t i = tid + (int64_t)j * kBmThreads;
-    const int32_t p = i < kHeld * kBmThreads ? al.new_pg[i] : row[i];
+    const int32_t p = al.new_pg[tid + j * kBmThreads];  // j < kHeld: always in LDS
     reg_pg[j] = p;
     *rec_hash(s, p) = hk[j];
     *rec_flag(s, p) = 1;
@@ -783,6 +798,428 @@ __device__ __forceinline__ void fetch_hashes(const BmArgs& a, const OpMeta& om, 
     const int64_t i = threadIdx.x + (int64_t)j * kBmThreads;
     h[j] = adm && i < nh ? a.hashes[h0 + i] : 0;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Group admits: up to kGroup consecutive admits resolved from one round of
+// loads.
+//
+// A single admit waits for several dependent memory round trips (its probe,
+// the LRU window's ring entries and then their records, the liveness of the
+// keys it registers), separated by barriers. A group issues those loads once
+// for all its members, against the state S0 at the group's start, resolves
+// the members in op order from registers and LDS, and writes the state once
+// at the end. While a group resolves, global memory holds S0, except for
+// evictions found past the preloaded LRU window, which are written at once:
+// an evicted page has no other live ring entry, so no later read of the ring
+// sees a difference.
+//
+// Thread i owns table position i of every member (members have at most
+// kBmThreads pages). A page key hashes a request's whole prefix up to the end
+// of that page, so a key occurs at one position only: which members share a
+// key at position i (a class), and which of them hit it from the probe or
+// registered it, is in thread i's own registers as 8-bit masks. What other
+// threads need is in LDS: bitmaps over the pages evicted and pinned
+// (refcount 0 in S0, then hit) in the group, the preloaded LRU window and
+// free-stack top, the evicted pages handed to the positions that take them,
+// and per member and position the probe result and the page it gets.
+//
+// Member u at position i, from S0's probe result p0 (page or -1):
+//   present  = p0 >= 0 and not evicted in the group, or an earlier member of
+//              its class registered the key (then that member's page);
+//   k        = the first position not present;
+//   pinned   = hits (< k) from the probe with refcount 0 in S0 that no earlier
+//              member of the class hit (those are held already);
+//   OOM      = take > free + evictable - pinned (then nothing changes);
+//   takes    = the free stack's top, then the LRU window's oldest entries that
+//              are live in S0 and not pinned in the group;
+//   register = positions k..m-1 whose key is not present after the takes.
+// Refcounts written at the end: a page hit from the probe gets its S0 count +
+// 2 per member hitting it (written by the last of them); a taken page 2 (1
+// for a partial last page, which the child copies) + 2 per later member
+// hitting its registration; a copy-on-write page 1.
+//
+// The member loop is rolled (its code once, for the instruction cache) and
+// reaches per-member data only through LDS and mask shifts; the set-up and
+// write-back loops over members are unrolled and keep the keys, probe pages,
+// slots and refcounts in registers.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 8;
+constexpr int32_t kGroupMaxPages = 1 << 17;  // two page bitmaps in LDS, 16 KiB each
+constexpr int kWin = 2 * kBmThreads;         // preloaded LRU window entries
+constexpr int kFreePre = 2 * kBmThreads;     // preloaded free-stack entries
+constexpr int kClaimBits = 12;               // LDS set of claimed table slots
+constexpr int kGroupRegCap = (1 << kClaimBits) / 2;  // registrations per group, at most
+constexpr int32_t kPinBit = 1 << 30;  // probe result: refcount 0 in S0 (pages < 2^28)
+static_assert(kGroup <= 8, "a class mask is one byte per member");
+
+struct GroupLds {
+  uint32_t ev[kGroupMaxPages / 32];   // pages evicted in the group
+  uint32_t pn[kGroupMaxPages / 32];   // pages pinned in the group
+  int32_t probe[kGroup][kBmThreads];  // S0 probe: page | kPinBit, or -1
+  int32_t page[kGroup][kBmThreads];   // the page a member's position gets
+  int32_t win_pg[kWin];               // LRU window: the page if live in S0, else -1
+  int32_t win_slot[kWin];             // the table slot of its key
+  uint32_t win_ev[kWin / 32];         // window positions evicted
+  int32_t fpre[kFreePre];             // free-stack entries from the top
+  int32_t take_pg[kBmThreads + 2];    // one member's evicted pages, in take order
+  int32_t claims[1 << kClaimBits];    // table slots claimed by registrations
+  uint64_t pinmask[kGroup][kBmWaves];  // per member and wave: pinning hits
+  int32_t wave_miss[kGroup][kBmWaves]; // per member and wave: the first miss
+  int32_t hits[kGroup];  // per member: its hits, or -1 if it got OOM
+  int32_t copy_pg[kGroup];
+  int32_t reused;  // registrations that reused a tombstone
+};
+
+__device__ __forceinline__ bool bit_get(const uint32_t* b, int32_t p) {
+  return (b[p >> 5] >> (p & 31)) & 1u;
+}
+__device__ __forceinline__ void bit_set(uint32_t* b, int32_t p) {
+  atomicOr(&b[p >> 5], 1u << (p & 31));
+}
+// The members sharing member u's key at this position (its class, u excluded).
+__device__ __forceinline__ uint32_t class_of(uint64_t cls, int u) {
+  return (uint32_t)(cls >> (8 * u)) & 0xffu;
+}
+
+// The next kGroup ops' request metadata, staged in LDS by the group kernel;
+// a member is a valid admit of at most kBmThreads pages that fits its table.
+struct GroupMeta {
+  int32_t op[kGroup], ntok[kGroup], nhash[kGroup], ok[kGroup];
+  int64_t h0[kGroup];
+};
+
+// Admits the g staged members (all eligible). Returns how many it processed: fewer when the registrations would outgrow the claim
+// set, and the rest start the next group.
+__device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c, Shared& sh,
+                           GroupLds& gl, int& buf) {
+  static_assert(kWin == 2 * kBmThreads && kFreePre == 2 * kBmThreads, "two entries per thread");
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
+  if (c.tombs > s.C / 4) tab_rebuild(a, c);
+  const int64_t head0 = c.head, free0 = c.free_top, log0 = c.log_len, qm = s.Q - 1;
+  const int64_t span = c.tail - head0;
+  const int64_t wlen = span < kWin ? span : kWin;
+
+  // 1. loads against S0: the members' page hashes, then their home entries;
+  //    the LRU window's ring entries, then their records; the free stack's top
+  int32_t mm[kGroup];
+  uint64_t key[kGroup];
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {
+    mm[u] = u < g ? uni(om.nhash[u]) : 0;
+    key[u] = i < mm[u] ? a.hashes[om.h0[u] + i] : 0;
+  }
+  uint64_t went[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t w = tid + j * kBmThreads;
+    went[j] = w < wlen ? s.ring[(head0 + w) & qm] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t t = tid + j * kBmThreads;
+    if (t < free0) gl.fpre[t] = s.free_list[free0 - 1 - t];
+  }
+  u32x4 e0[kGroup];
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u)
+    e0[u] = i < mm[u] ? tab_entry(s, tab_home(s, key[u])) : u32x4{0u, 0u, 0u, 0u};
+  RecHead wh[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t w = tid + j * kBmThreads;
+    wh[j] = w < wlen ? rec_head(s, (int32_t)(uint32_t)went[j]) : RecHead{0, 0, 0u, 0};
+  }
+  const int32_t nw = (s.P + 31) >> 5;
+  for (int32_t w = tid; w < nw; w += kBmThreads) {
+    gl.ev[w] = 0;
+    gl.pn[w] = 0;
+  }
+  for (int w = tid; w < (1 << kClaimBits); w += kBmThreads) gl.claims[w] = -1;
+  if (tid < kWin / 32) gl.win_ev[tid] = 0;
+  if (tid == 0) gl.reused = 0;
+  int32_t p0[kGroup], slot0[kGroup], ref0[kGroup];
+  uint32_t mtomb = 0;  // bit u: the insertion slot of member u's key is a tombstone
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {
+    p0[u] = -1;
+    ref0[u] = 0;
+    slot0[u] = -1;
+    if (i < mm[u]) {
+      const Found f = tab_find_at(s, key[u], tab_home(s, key[u]), e0[u]);
+      p0[u] = f.page;
+      ref0[u] = f.ref;
+      slot0[u] = f.slot;
+      mtomb |= f.tomb ? 1u << u : 0u;
+    }
+    if (u < g) gl.probe[u][i] = p0[u] < 0 ? -1 : (p0[u] | (ref0[u] == 0 ? kPinBit : 0));
+  }
+  uint64_t cls = 0;  // byte u: the members with member u's key here
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u)
+#pragma unroll
+    for (int v = u + 1; v < kGroup; ++v)
+      if (i < mm[u] && i < mm[v] && key[u] == key[v])
+        cls |= 1ull << (8 * u + v) | 1ull << (8 * v + u);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t w = tid + j * kBmThreads;
+    if (w < wlen) {
+      const int32_t p = (int32_t)(uint32_t)went[j];
+      gl.win_pg[w] = live(wh[j], (uint32_t)(went[j] >> 32)) ? p : -1;
+      gl.win_slot[w] = wh[j].slot;
+    }
+  }
+  __syncthreads();
+
+  // 2. the members in op order
+  // idx-th entry from the S0 top. The global read is volatile so that it stays
+  // a load of its own: merged with the LDS read into one flat load, it would
+  // wait for every outstanding memory operation.
+  auto free_at = [&](int64_t idx) -> int32_t {
+    if (idx < kFreePre) return gl.fpre[idx];
+    return *static_cast<const volatile int32_t*>(s.free_list + (free0 - 1 - idx));
+  };
+  // bit u at this position: member u hit from the probe / hit a registration
+  // of its class / registers its key
+  uint32_t mprobe = 0, mgroup = 0, mreg = 0;
+  int done = 0;
+  int64_t regs = 0;  // registrations so far, bounded from above
+#pragma unroll 1
+  for (int u = 0; u < g; ++u) {
+    const int32_t m = uni(om.nhash[u]), n = uni(om.ntok[u]), r = uni(om.op[u]);
+    if (u > 0 && regs + m > kGroupRegCap) break;
+    const int32_t np = (n + 15) / 16;
+    const bool cow = (n & 15) != 0;
+    done = u + 1;
+    const uint32_t bit = 1u << u, below = bit - 1u;
+    const uint32_t ecls = class_of(cls, u);
+    // hits
+    int32_t pw = -1, cur = -1;
+    bool from_probe = false;
+    if (i < m) {
+      pw = gl.probe[u][i];
+      const uint32_t regd = ecls & mreg & below;
+      if (pw >= 0 && !bit_get(gl.ev, pw & ~kPinBit)) {
+        cur = pw & ~kPinBit;
+        from_probe = true;
+      } else if (regd) {
+        cur = gl.page[__builtin_ctz(regd)][i];
+      }
+    }
+    const bool pinnable = from_probe && (pw & kPinBit) && !(ecls & mprobe & below);
+    // per wave: the first miss and the pinnable hits, from ballots
+    const uint64_t mb = __ballot(i < m && cur < 0);
+    const uint64_t pmask = __ballot(pinnable);
+    if (lane == 0) {
+      gl.pinmask[u][wave] = pmask;
+      gl.wave_miss[u][wave] = mb ? wave * 64 + (int32_t)__builtin_ctzll(mb) : INT_MAX;
+    }
+    __syncthreads();
+    int32_t k = m;
+#pragma unroll
+    for (int w = kBmWaves - 1; w >= 0; --w) {
+      const int32_t x = gl.wave_miss[u][w];
+      k = x < k ? x : k;
+    }
+    k = uni(k);
+    int32_t pinned = 0;
+#pragma unroll
+    for (int w = 0; w < kBmWaves; ++w) {
+      const uint64_t em = gl.pinmask[u][w];
+      const int32_t lim = k - w * 64;
+      pinned += lim <= 0 ? 0 : __popcll(lim >= 64 ? em : em & ((1ull << lim) - 1ull));
+    }
+    pinned = uni(pinned);
+    const int64_t take = np - k + (cow ? 1 : 0);
+    if (take > c.free_top + c.evictable - pinned) {  // OOM: nothing changes
+      if (tid == 0) {
+        gl.hits[u] = -1;
+        a.status[r] = kStOom;
+        a.hits[r] = 0;
+        a.child_last[r] = a.cow_src[r] = a.cow_dst[r] = -1;
+      }
+      continue;
+    }
+    if (tid == 0) gl.hits[u] = k;
+    regs += m - k;
+    if (i < k) {
+      if (from_probe)
+        mprobe |= bit;
+      else
+        mgroup |= bit;
+      if (pinnable) bit_set(gl.pn, cur);
+    }
+    c.evictable -= pinned;
+    // takes: the free stack's top first (positions read their own page)
+    const int64_t from_free = take < c.free_top ? take : c.free_top;
+    const int64_t fbase = free0 - c.free_top;
+    int32_t pgu = i < k ? cur : -1;
+    if (i >= k && i < np && i - k < from_free) pgu = free_at(fbase + i - k);
+    if (tid == 0) gl.copy_pg[u] = cow && take - 1 < from_free ? free_at(fbase + take - 1) : -1;
+    c.free_top -= from_free;
+    //        then LRU victims in order, handed to their positions through LDS
+    const int64_t want_all = take - from_free;
+    if (want_all > 0) {
+      if (pinned > 0) __syncthreads();  // the pins are visible to the scan
+      int64_t got_all = 0, pos = c.head - head0;
+      while (got_all < want_all) {
+        if (pos >= span) {  // fewer live entries than counted: state is corrupt
+          if (tid == 0) raise_err(a.err, MKV_DEVERR_BM);
+          break;
+        }
+        const int64_t want = want_all - got_all;
+        const int64_t w = pos + tid;
+        bool ok = false;
+        int32_t vp = 0, vslot = 0;
+        if (w < wlen) {
+          vp = gl.win_pg[w];
+          vslot = gl.win_slot[w];
+          ok = vp >= 0 && !bit_get(gl.pn, vp);
+        } else if (w < span) {  // past the preloaded window: from memory (still S0)
+          const uint64_t e = s.ring[(head0 + w) & qm];
+          vp = (int32_t)(uint32_t)e;
+          const RecHead h = rec_head(s, vp);
+          vslot = h.slot;
+          ok = live(h, (uint32_t)(e >> 32)) && !bit_get(gl.pn, vp);
+        }
+        int32_t rank, unused_r, total, unused_t;
+        block_rank2(ok, false, rank, unused_r, total, unused_t, sh, buf);
+        if (ok && rank < want) {
+          bit_set(gl.ev, vp);
+          gl.take_pg[got_all + rank] = vp;
+          if (w < wlen) {
+            bit_set(gl.win_ev, (int32_t)w);
+          } else {
+            *ent_page(s, vslot) = kTomb;
+            *rec_flag(s, vp) = 0;
+            const int64_t li = c.log_len + got_all + rank;
+            if (li < a.evict_cap) a.evict_log[li] = vp;
+          }
+          if (rank == want - 1) sh.new_head = w + 1;
+        }
+        __syncthreads();
+        const int64_t got = total < want ? total : want;
+        pos = total >= want ? uni64(sh.new_head) : (pos + kBmThreads < span ? pos + kBmThreads : span);
+        got_all += got;
+      }
+      c.head = head0 + pos;
+      c.evictable -= got_all;
+      c.tombs += got_all;
+      c.log_len += got_all;
+      const int64_t ti = i - k - from_free;
+      if (i >= k && i < np && ti >= 0) pgu = ti < got_all ? gl.take_pg[ti] : -1;
+      if (tid == 0 && cow && take - 1 >= from_free)
+        gl.copy_pg[u] = take - 1 - from_free < got_all ? gl.take_pg[take - 1 - from_free] : -1;
+    }
+    // registrations: positions k..m-1 whose key is absent after the takes
+    // (this member's eviction bits are visible: its scan ended with a barrier)
+    if (i >= k && i < m && pgu >= 0) {
+      const bool present = (pw >= 0 && !bit_get(gl.ev, pw & ~kPinBit)) || (ecls & mreg & below);
+      if (!present) mreg |= bit;
+    }
+    if (i < np) gl.page[u][i] = pgu;
+  }
+  __syncthreads();  // the members' pages and results are visible
+
+  // 3. write the state: tables, refcounts, results
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {
+    if (u >= done) break;
+    const int32_t k = uni(gl.hits[u]);
+    if (k < 0) continue;
+    const int32_t r = uni(om.op[u]), n = uni(om.ntok[u]);
+    const int32_t np = (n + 15) / 16;
+    const bool cow = (n & 15) != 0;
+    const uint32_t bit = 1u << u, below = bit - 1u, above = ~(bit | below);
+    const uint32_t ecls = class_of(cls, u);
+    if (i < np) {
+      const int32_t pgu = gl.page[u][i];
+      a.tables[(int64_t)r * a.tstride + i] = pgu;
+      if (mprobe & bit) {  // the last member of the class holding it writes the count
+        if (!(ecls & mprobe & above)) {
+          const int32_t ref = ref0[u] + 2 * (1 + __popc(ecls & mprobe & below));
+          *rec_ref(s, p0[u]) = ref;
+          *ent_ref(s, slot0[u]) = ref;
+        }
+      } else if (i >= k && pgu >= 0) {
+        int32_t ref = (cow && i == np - 1) ? 1 : 2;
+        if (mreg & bit) ref += 2 * __popc(ecls & mgroup & above);
+        *rec_ref(s, pgu) = ref;
+      }
+      if (i == np - 1) {
+        if (cow)
+          a.cow_src[r] = pgu;
+        else
+          a.child_last[r] = pgu;
+      }
+    }
+    if (tid == 0) {
+      a.hits[r] = k;
+      a.status[r] = kStOk;
+      if (cow) {
+        const int32_t cp = gl.copy_pg[u];
+        a.cow_dst[r] = a.child_last[r] = cp;
+        if (cp >= 0) *rec_ref(s, cp) = 1;
+      } else {
+        a.cow_src[r] = a.cow_dst[r] = -1;
+        if (np == 0) a.child_last[r] = -1;
+      }
+    }
+  }
+  //    evictions from the preloaded window: the key leaves the table; the log
+  //    follows window order (every eviction past the window came later)
+  {
+    const bool ea = tid < wlen && bit_get(gl.win_ev, tid);
+    const bool eb = tid + kBmThreads < wlen && bit_get(gl.win_ev, tid + kBmThreads);
+    int32_t ra, rb, ta, tb;
+    block_rank2(ea, eb, ra, rb, ta, tb, sh, buf);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!(j == 0 ? ea : eb)) continue;
+      const int w = tid + j * kBmThreads;
+      const int32_t p = gl.win_pg[w];
+      *ent_page(s, gl.win_slot[w]) = kTomb;
+      *rec_flag(s, p) = 0;
+      const int64_t li = log0 + (j == 0 ? ra : ta + rb);
+      if (li < a.evict_cap) a.evict_log[li] = p;
+    }
+  }
+  __syncthreads();  // tombstones and cleared flags land before registrations
+  //    registrations: the probe's slot for the key (its insertion slot, or
+  //    the slot of its evicted entry), claimed in LDS; the rest by CAS
+  int32_t reused = 0;
+  uint32_t later = 0;
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {
+    const uint32_t bit = 1u << u;
+    if (!(mreg & bit)) continue;
+    const int32_t p = gl.page[u][i];
+    const int32_t ref = 2 + 2 * __popc(class_of(cls, u) & mgroup & ~((bit << 1) - 1u));
+    *rec_hash(s, p) = key[u];
+    *rec_flag(s, p) = 1;
+    if (slot0[u] >= 0 && set_add<kClaimBits>(gl.claims, slot0[u])) {
+      *reinterpret_cast<u32x4*>(s.ent + (int64_t)slot0[u] * kEntBytes) =
+          u32x4{(uint32_t)key[u], (uint32_t)(key[u] >> 32), (uint32_t)p, (uint32_t)ref};
+      *rec_slot(s, p) = slot0[u];
+      reused += (p0[u] >= 0 || (mtomb & bit)) ? 1 : 0;
+    } else {
+      later |= bit;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kGroup; ++u) {  // the keys that lost their slot
+    const uint32_t bit = 1u << u;
+    if (!(later & bit)) continue;
+    const int32_t ref = 2 + 2 * __popc(class_of(cls, u) & mgroup & ~((bit << 1) - 1u));
+    reused += tab_insert(s, key[u], gl.page[u][i], ref) == 1;
+  }
+  if (reused) atomicAdd(&gl.reused, reused);
+  __syncthreads();
+  c.tombs -= uni(gl.reused);
+  return done;
 }
 
 // ---------------------------------------------------------------------------
@@ -1217,6 +1654,67 @@ __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
   }
 }
 
+// The admits after the leading run of releases, in groups, while they are
+// valid and at most kBmThreads pages long; the step kernel takes the ops from
+// the first one that is not (kRunNext). A kernel of its own, so that the
+// single-request path's registers do not crowd the group's.
+__global__ __launch_bounds__(kBmThreads) void bm_group_kernel(BmArgs a) {
+  __shared__ Shared sh;
+  __shared__ GroupLds gl;
+  __shared__ GroupMeta gm;
+  const BmState& s = a.s;
+  int32_t t = (int32_t)s.run_ctr[kRunOps];
+  if (s.P > kGroupMaxPages) {  // the page bitmaps do not fit in LDS
+    if (threadIdx.x == 0) s.run_ctr[kRunNext] = t;
+    return;
+  }
+  int buf = 0;
+  Ctrs c;
+  c.free_top = s.ctr[kFreeTop];
+  c.head = s.ctr[kHead];
+  c.tail = s.ctr[kTail];
+  c.next_stamp = s.ctr[kNextStamp];
+  c.evictable = s.ctr[kEvictable];
+  c.tombs = s.ctr[kTombs];
+  c.log_len = s.ctr[kLogLen];
+  while (t < a.num_ops) {
+    if (threadIdx.x < kGroup) {
+      const int u = threadIdx.x, j = t + u;
+      int32_t op = -1, n = 0, nh = -1, ok = 0;
+      int64_t h0 = 0;
+      if (j < a.num_ops) {
+        op = a.ops[j];
+        if (op >= 0 && op < a.num_requests) {
+          n = a.ntok[op];
+          h0 = a.hash_off[op];
+          const int64_t m = a.hash_off[op + 1] - h0, np = ((int64_t)n + 15) / 16;
+          nh = (n >= 0 && m == n / 16) ? (int32_t)m : -1;
+          ok = nh >= 0 && np <= a.twidth && np <= kBmThreads;
+        }
+      }
+      gm.op[u] = op;
+      gm.ntok[u] = n;
+      gm.nhash[u] = nh;
+      gm.h0[u] = h0;
+      gm.ok[u] = ok;
+    }
+    __syncthreads();
+    int g = 0;
+    while (g < kGroup && gm.ok[g]) ++g;
+    g = uni(g);
+    if (g == 0) break;
+    t += group_admit(a, gm, g, c, sh, gl, buf);  // ends with a barrier
+  }
+  if (threadIdx.x == 0) {
+    s.run_ctr[kRunNext] = t;
+    s.ctr[kFreeTop] = c.free_top;
+    s.ctr[kHead] = c.head;
+    s.ctr[kEvictable] = c.evictable;
+    s.ctr[kTombs] = c.tombs;
+    s.ctr[kLogLen] = c.log_len;
+  }
+}
+
 __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   __shared__ Shared sh;
   __shared__ OpMeta om;
@@ -1236,9 +1734,10 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
     sh.tomb_reused[threadIdx.x] = 0;
   }
   for (int i = threadIdx.x; i < kSetSize; i += kBmThreads) al.claims[i] = -1;
-  uint64_t cur[kHeld], nxt[kHeld] = {};
-  // the leading run of releases (if any) was retired by the run kernels
-  const int32_t start = (int32_t)a.s.run_ctr[kRunOps];
+  uint64_t cur[kHeld] = {}, nxt[kHeld] = {};
+  // the leading run of releases (if any) was retired by the run kernels, and
+  // the admits after it by the group kernel
+  const int32_t start = (int32_t)a.s.run_ctr[kRunNext];
   for (int32_t base = start; base < a.num_ops; base += kOpChunk) {
     const int cnt = a.num_ops - base < kOpChunk ? a.num_ops - base : kOpChunk;
     for (int t = threadIdx.x; t < cnt; t += kBmThreads) {
@@ -1420,6 +1919,7 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
   hipLaunchKernelGGL(run_scan_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(run_push_kernel, dim3(kRunGrid * kRunUnroll), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   return check_launch("mkv_bm_step");
 }
