@@ -897,9 +897,13 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   const BmState& s = a.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
   if (c.tombs > s.C / 4) tab_rebuild(a, c);
-  const int64_t head0 = c.head, free0 = c.free_top, log0 = c.log_len, qm = s.Q - 1;
-  const int64_t span = c.tail - head0;
-  const int64_t wlen = span < kWin ? span : kWin;
+  // ring positions relative to head0 (a span is below Q < 2^31), free-stack
+  // counts (below P) and registration counts fit 32 bits
+  const int64_t head0 = c.head, log0 = c.log_len, qm = s.Q - 1;
+  const int32_t span = (int32_t)(c.tail - head0), free0 = (int32_t)c.free_top;
+  const int32_t wlen = span < kWin ? span : kWin;
+  int32_t free_top = free0, evictable = (int32_t)c.evictable, pos = 0;
+  int64_t log_len = log0, tombs = c.tombs;
 
   // 1. loads against S0: the members' page hashes, then their home entries;
   //    the LRU window's ring entries, then their records; the free stack's top
@@ -913,12 +917,12 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   uint64_t went[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t w = tid + j * kBmThreads;
+    const int32_t w = tid + j * kBmThreads;
     went[j] = w < wlen ? s.ring[(head0 + w) & qm] : 0;
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t t = tid + j * kBmThreads;
+    const int32_t t = tid + j * kBmThreads;
     if (t < free0) gl.fpre[t] = s.free_list[free0 - 1 - t];
   }
   u32x4 e0[kGroup];
@@ -928,7 +932,7 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   RecHead wh[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t w = tid + j * kBmThreads;
+    const int32_t w = tid + j * kBmThreads;
     wh[j] = w < wlen ? rec_head(s, (int32_t)(uint32_t)went[j]) : RecHead{0, 0, 0u, 0};
   }
   const int32_t nw = (s.P + 31) >> 5;
@@ -964,7 +968,7 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
         cls |= 1ull << (8 * u + v) | 1ull << (8 * v + u);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int64_t w = tid + j * kBmThreads;
+    const int32_t w = tid + j * kBmThreads;
     if (w < wlen) {
       const int32_t p = (int32_t)(uint32_t)went[j];
       gl.win_pg[w] = live(wh[j], (uint32_t)(went[j] >> 32)) ? p : -1;
@@ -977,7 +981,7 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   // idx-th entry from the S0 top. The global read is volatile so that it stays
   // a load of its own: merged with the LDS read into one flat load, it would
   // wait for every outstanding memory operation.
-  auto free_at = [&](int64_t idx) -> int32_t {
+  auto free_at = [&](int32_t idx) -> int32_t {
     if (idx < kFreePre) return gl.fpre[idx];
     return *static_cast<const volatile int32_t*>(s.free_list + (free0 - 1 - idx));
   };
@@ -985,7 +989,7 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   // of its class / registers its key
   uint32_t mprobe = 0, mgroup = 0, mreg = 0;
   int done = 0;
-  int64_t regs = 0;  // registrations so far, bounded from above
+  int32_t regs = 0;  // registrations so far, bounded from above
 #pragma unroll 1
   for (int u = 0; u < g; ++u) {
     const int32_t m = uni(om.nhash[u]), n = uni(om.ntok[u]), r = uni(om.op[u]);
@@ -1032,8 +1036,8 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
       pinned += lim <= 0 ? 0 : __popcll(lim >= 64 ? em : em & ((1ull << lim) - 1ull));
     }
     pinned = uni(pinned);
-    const int64_t take = np - k + (cow ? 1 : 0);
-    if (take > c.free_top + c.evictable - pinned) {  // OOM: nothing changes
+    const int32_t take = np - k + (cow ? 1 : 0);
+    if (take > free_top + evictable - pinned) {  // OOM: nothing changes
       if (tid == 0) {
         gl.hits[u] = -1;
         a.status[r] = kStOom;
@@ -1051,26 +1055,26 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
         mgroup |= bit;
       if (pinnable) bit_set(gl.pn, cur);
     }
-    c.evictable -= pinned;
+    evictable -= pinned;
     // takes: the free stack's top first (positions read their own page)
-    const int64_t from_free = take < c.free_top ? take : c.free_top;
-    const int64_t fbase = free0 - c.free_top;
+    const int32_t from_free = take < free_top ? take : free_top;
+    const int32_t fbase = free0 - free_top;
     int32_t pgu = i < k ? cur : -1;
     if (i >= k && i < np && i - k < from_free) pgu = free_at(fbase + i - k);
     if (tid == 0) gl.copy_pg[u] = cow && take - 1 < from_free ? free_at(fbase + take - 1) : -1;
-    c.free_top -= from_free;
+    free_top -= from_free;
     //        then LRU victims in order, handed to their positions through LDS
-    const int64_t want_all = take - from_free;
+    const int32_t want_all = take - from_free;
     if (want_all > 0) {
       if (pinned > 0) __syncthreads();  // the pins are visible to the scan
-      int64_t got_all = 0, pos = c.head - head0;
+      int32_t got_all = 0;
       while (got_all < want_all) {
         if (pos >= span) {  // fewer live entries than counted: state is corrupt
           if (tid == 0) raise_err(a.err, MKV_DEVERR_BM);
           break;
         }
-        const int64_t want = want_all - got_all;
-        const int64_t w = pos + tid;
+        const int32_t want = want_all - got_all;
+        const int32_t w = pos + tid;
         bool ok = false;
         int32_t vp = 0, vslot = 0;
         if (w < wlen) {
@@ -1094,21 +1098,20 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
           } else {
             *ent_page(s, vslot) = kTomb;
             *rec_flag(s, vp) = 0;
-            const int64_t li = c.log_len + got_all + rank;
+            const int64_t li = log_len + got_all + rank;
             if (li < a.evict_cap) a.evict_log[li] = vp;
           }
           if (rank == want - 1) sh.new_head = w + 1;
         }
         __syncthreads();
-        const int64_t got = total < want ? total : want;
-        pos = total >= want ? uni64(sh.new_head) : (pos + kBmThreads < span ? pos + kBmThreads : span);
+        const int32_t got = total < want ? total : want;
+        pos = total >= want ? uni((int32_t)sh.new_head) : (pos + kBmThreads < span ? pos + kBmThreads : span);
         got_all += got;
       }
-      c.head = head0 + pos;
-      c.evictable -= got_all;
-      c.tombs += got_all;
-      c.log_len += got_all;
-      const int64_t ti = i - k - from_free;
+      evictable -= got_all;
+      tombs += got_all;
+      log_len += got_all;
+      const int32_t ti = i - k - from_free;
       if (i >= k && i < np && ti >= 0) pgu = ti < got_all ? gl.take_pg[ti] : -1;
       if (tid == 0 && cow && take - 1 >= from_free)
         gl.copy_pg[u] = take - 1 - from_free < got_all ? gl.take_pg[take - 1 - from_free] : -1;
@@ -1218,7 +1221,11 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
   }
   if (reused) atomicAdd(&gl.reused, reused);
   __syncthreads();
-  c.tombs -= uni(gl.reused);
+  c.free_top = free_top;
+  c.head = head0 + pos;
+  c.evictable = evictable;
+  c.log_len = log_len;
+  c.tombs = tombs - uni(gl.reused);
   return done;
 }
 
