@@ -416,7 +416,8 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
  * (a leading run of up to 1024 releases is retired by many-workgroup passes,
- * the rest on one workgroup): op r >= 0
+ * the admits after it by one workgroup in groups of eight, the rest on one
+ * workgroup one op at a time): op r >= 0
  * admits request r, op -(r+1) releases it (r < num_requests, the length of
  * the per-request arrays; hash_offsets has num_requests+1 entries, tables
  * num_requests rows). Request r has num_tokens[r]

@@ -8,9 +8,10 @@ on the device: a request's full 16-token pages are keyed by the SHA-256 prefix
 hash of ``PrefixCache._hash_tokens`` (``prefix_hash.page_hashes``), the
 longest run of leading cached pages is shared (refcounted), the rest come from
 the free stack or by evicting the least recently released cached page, and a
-forked request's partial last page is copied on write. Requests are processed
-in op order by one workgroup, so eviction order is deterministic and equal to
-the sequential OrderedDict model.
+forked request's partial last page is copied on write. Requests are resolved
+in op order by one workgroup (admits eight at a time, against loads shared by
+the eight), so eviction order is deterministic and equal to the sequential
+OrderedDict model.
 
 Typical step for a batch of requests (all on the stream, no host sync)::
 

@@ -3,10 +3,13 @@
 //
 // Semantics (one request at a time, in op order): see mkv_bm_step in mkv.h.
 // Eviction order must equal a sequential OrderedDict model, so requests are
-// processed in order by a single 512-thread workgroup and the parallelism is
-// inside a request: every page hash of a request is probed at once, pins and
+// resolved in order by one 512-thread workgroup, and the parallelism is inside
+// a request: every page hash of a request is probed at once, pins and
 // refcount updates are one lane per page, and allocation / release positions
-// come from wavefront ballots + popcount prefix ranks.
+// come from wavefront ballots + popcount prefix ranks. A leading run of
+// releases is retired on many CUs; the admits after it go eight at a time
+// through the group kernel (one round of loads for the eight, then a
+// sequential resolution in LDS); the step kernel runs whatever is left.
 //
 // A request costs a few dependent memory round trips, so the layout keeps
 // that chain short:
