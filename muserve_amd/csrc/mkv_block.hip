@@ -75,8 +75,27 @@ constexpr int kRunMaxOps = 1024;               // releases retired in bulk per s
 constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
 constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
 enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kRunSpan,
-              kRunNext,  // the first op left to the step kernel (after the run and the groups)
+              kRunNext,  // the first op left to the next stage (speculation, groups, step)
               kRunNumCtr = 16 };
+
+// The speculative resolution of a step's admits (many CUs; see the
+// speculation kernels): up to kSpecOps admits of up to kSpecPos pages each,
+// a first-occurrence table of absent keys, and an LRU window of kSpecWin
+// entries.
+constexpr int kSpecOps = 1024;
+constexpr int kSpecPos = 512;
+constexpr int kFoBits = 19;
+constexpr int64_t kFoCap = 1ll << kFoBits;
+constexpr int kFoMaxProbe = 512;  // a longer probe counts as a violation
+constexpr int kSpecWin = 1 << 17;
+enum SpecCtr { kSpN,        // admits speculated
+               kSpBad,      // first admit the speculation may get wrong (<= kSpN)
+               kSpF,        // free-stack entries at the step's start
+               kSpLive,     // evictable pages at the step's start
+               kSpHead,     // LRU head at the step's start
+               kSpWin,      // window entries read
+               kSpReused,   // registrations that reused a tombstone
+               kSpNumCtr = 16 };
 
 struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
@@ -85,6 +104,9 @@ struct BmLayout {
   int64_t run_ctr, run_off, run_child, run_page, run_bits, run_wpre;
   // ring compaction scratch: a copy of the ring span, live bits, their prefix counts
   int64_t cmp_ring, cmp_bits, cmp_pre;
+  // speculation scratch
+  int64_t sp_ctr, sp_req, sp_ntok, sp_m, sp_h0, sp_k, sp_take, sp_pinned, sp_T, sp_p0, sp_fo,
+      sp_first, sp_evt, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -123,6 +145,24 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.cmp_ring = take(l.Q * 8);
   l.cmp_bits = take(l.Q / 32 * 4);
   l.cmp_pre = take(l.Q / 32 * 4);
+  l.sp_ctr = take(kSpNumCtr * 8);
+  l.sp_req = take(kSpecOps * 4);
+  l.sp_ntok = take(kSpecOps * 4);
+  l.sp_m = take(kSpecOps * 4);
+  l.sp_h0 = take(kSpecOps * 8);
+  l.sp_k = take(kSpecOps * 4);
+  l.sp_take = take(kSpecOps * 4);
+  l.sp_pinned = take(kSpecOps * 4);
+  l.sp_T = take((kSpecOps + 1) * 8);
+  l.sp_p0 = take((int64_t)kSpecOps * kSpecPos * 8);
+  l.sp_fo = take(kFoCap * 16);
+  l.sp_first = take((int64_t)P * 4);
+  l.sp_evt = take((int64_t)P * 4);
+  l.sp_wpg = take(kSpecWin * 4);
+  l.sp_wslot = take(kSpecWin * 4);
+  l.sp_wflag = take(kSpecWin);
+  l.sp_victim = take(kSpecWin * 4);
+  l.sp_vpos = take(kSpecWin * 4);
   l.bytes = o;
   return l;
 }
@@ -143,6 +183,27 @@ struct BmState {
   uint64_t* cmp_ring;  // compaction: the ring span [head, tail) copied out
   uint32_t* cmp_bits;  // compaction: live bit per copied entry
   uint32_t* cmp_pre;   // compaction: live entries before each bit word
+  // speculation (per admit j < kSpecOps, position i < kSpecPos)
+  int64_t* sp_ctr;     // SpecCtr values
+  int32_t* sp_req;     // request id
+  int32_t* sp_ntok;    // tokens
+  int32_t* sp_m;       // page hashes
+  int64_t* sp_h0;      // first page hash
+  int32_t* sp_k;       // hits
+  int32_t* sp_take;    // pages taken
+  int32_t* sp_pinned;  // pages it pins (refcount 0 before, first admit to hit them)
+  int64_t* sp_T;       // takes before it (exclusive prefix sum)
+  int2* sp_p0;         // [j][i] {page | kPinBit at the step's start, or -1, or -(c+2) for
+                       //  a key first held at occurrence c = admit * kSpecPos + position
+                       //  of an earlier admit; table slot | kTombBit}
+  uint8_t* sp_fo;      // first-occurrence table: {u64 key, i32 first occurrence, i32 -}
+  int32_t* sp_first;   // [P] first admit pinning the page (INT_MAX none)
+  int32_t* sp_evt;     // [P] admit evicting the page (INT_MAX none)
+  int32_t* sp_wpg;     // [w] LRU window: page
+  int32_t* sp_wslot;   //     its key's table slot
+  uint8_t* sp_wflag;   //     0 dead, 1 a victim candidate, 2 live but pinned in the step
+  int32_t* sp_victim;  // [v] the v-th eviction's page
+  int32_t* sp_vpos;    //     its window position
   int64_t C, Q;
   int32_t P;
 };
@@ -166,6 +227,24 @@ inline BmState bm_state(void* base, int32_t P) {
   s.cmp_ring = reinterpret_cast<uint64_t*>(b + l.cmp_ring);
   s.cmp_bits = reinterpret_cast<uint32_t*>(b + l.cmp_bits);
   s.cmp_pre = reinterpret_cast<uint32_t*>(b + l.cmp_pre);
+  s.sp_ctr = reinterpret_cast<int64_t*>(b + l.sp_ctr);
+  s.sp_req = reinterpret_cast<int32_t*>(b + l.sp_req);
+  s.sp_ntok = reinterpret_cast<int32_t*>(b + l.sp_ntok);
+  s.sp_m = reinterpret_cast<int32_t*>(b + l.sp_m);
+  s.sp_h0 = reinterpret_cast<int64_t*>(b + l.sp_h0);
+  s.sp_k = reinterpret_cast<int32_t*>(b + l.sp_k);
+  s.sp_take = reinterpret_cast<int32_t*>(b + l.sp_take);
+  s.sp_pinned = reinterpret_cast<int32_t*>(b + l.sp_pinned);
+  s.sp_T = reinterpret_cast<int64_t*>(b + l.sp_T);
+  s.sp_p0 = reinterpret_cast<int2*>(b + l.sp_p0);
+  s.sp_fo = b + l.sp_fo;
+  s.sp_first = reinterpret_cast<int32_t*>(b + l.sp_first);
+  s.sp_evt = reinterpret_cast<int32_t*>(b + l.sp_evt);
+  s.sp_wpg = reinterpret_cast<int32_t*>(b + l.sp_wpg);
+  s.sp_wslot = reinterpret_cast<int32_t*>(b + l.sp_wslot);
+  s.sp_wflag = b + l.sp_wflag;
+  s.sp_victim = reinterpret_cast<int32_t*>(b + l.sp_victim);
+  s.sp_vpos = reinterpret_cast<int32_t*>(b + l.sp_vpos);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -854,6 +933,7 @@ constexpr int kFreePre = 2 * kBmThreads;     // preloaded free-stack entries
 constexpr int kClaimBits = 12;               // LDS set of claimed table slots
 constexpr int kGroupRegCap = (1 << kClaimBits) / 2;  // registrations per group, at most
 constexpr int32_t kPinBit = 1 << 30;  // probe result: refcount 0 in S0 (pages < 2^28)
+constexpr int32_t kTombBit = 1 << 30;  // a miss's insertion slot is a tombstone (slots < 2^30)
 static_assert(kGroup <= 8, "a class mask is one byte per member");
 
 struct GroupLds {
@@ -1664,6 +1744,570 @@ __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Speculative resolution of a step's admits, on many CUs.
+//
+// The admits after the release run (up to kSpecOps valid admits of at most
+// kSpecPos pages, distinct requests) are resolved together against the state
+// S at the step's start, modelling exactly what earlier admits of the step do
+// to later ones in the common case:
+//   - a key absent at S is a hit for every admit after the first one holding
+//     it (that one registers it: its first occurrence);
+//   - a page hit at refcount 0 is pinned by the first admit hitting it;
+//   - takes come in op order: the free stack's top, then the LRU's oldest
+//     entries that are live at S and pinned by no admit of the step.
+// Each admit is then checked for what this does not model:
+//   - an OOM (against running free / evictable counts);
+//   - a hit on, or a key it would register again after, a page that an
+//     earlier admit (or, past its hits, itself) evicts;
+//   - an LRU entry pinned in the step that an earlier admit's takes reach
+//     (sequentially it would be that admit's victim);
+//   - a window or first-occurrence table too small.
+// The admits before the first violation are exactly what the sequential order
+// gives, and are committed on many CUs; the group kernel takes the rest.
+//
+// Refcounts: a hit adds 2 (parent and child), a taken page its base (2, 1
+// for a partial last page the child copies, 1 for a copy-on-write page), by
+// atomic adds: every page it takes is at refcount 0 at S. A last pass copies
+// the cached pages' counts into their table entries.
+// ---------------------------------------------------------------------------
+constexpr int kSpecThreads = 512;
+constexpr int kSpecGrid = 1024;
+static_assert(kSpecPos == kSpecThreads, "a position per thread");
+
+__device__ __forceinline__ uint64_t* fo_key(const BmState& s, int64_t i) {
+  return reinterpret_cast<uint64_t*>(s.sp_fo + i * 16);
+}
+__device__ __forceinline__ int32_t* fo_first(const BmState& s, int64_t i) {
+  return reinterpret_cast<int32_t*>(s.sp_fo + i * 16 + 8);
+}
+__device__ __forceinline__ int32_t* spec_bad(const BmState& s) {
+  return reinterpret_cast<int32_t*>(s.sp_ctr + kSpBad);  // the value fits 32 bits
+}
+
+// Records key h (absent at S) as held at occurrence code = admit * kSpecPos +
+// position; the table keeps the smallest code. False if h is 0 (the empty key)
+// or its probe runs past kFoMaxProbe slots.
+__device__ bool fo_insert(const BmState& s, uint64_t h, int32_t code) {
+  if (h == 0) return false;
+  int64_t i = slot_of(h) & (kFoCap - 1);
+  for (int n = 0; n < kFoMaxProbe; ++n, i = (i + 1) & (kFoCap - 1)) {
+    const unsigned long long prev = atomicCAS(reinterpret_cast<unsigned long long*>(fo_key(s, i)),
+                                              0ull, (unsigned long long)h);
+    if (prev == 0ull || prev == h) {
+      atomicMin(fo_first(s, i), code);
+      return true;
+    }
+  }
+  return false;
+}
+
+// The first occurrence code of key h (INT_MAX if none), after every insert.
+__device__ int32_t fo_find(const BmState& s, uint64_t h) {
+  int64_t i = slot_of(h) & (kFoCap - 1);
+  for (int n = 0; n < kFoMaxProbe; ++n, i = (i + 1) & (kFoCap - 1)) {
+    const uint64_t k = *fo_key(s, i);
+    if (k == h) return *fo_first(s, i);
+    if (k == 0) return INT_MAX;
+  }
+  return INT_MAX;
+}
+
+// The t-th page the step's admits take, in op order (victims past the window
+// cannot belong to a committed admit: the scan marks the first admit lacking
+// one as a violation; the bound only keeps a broken state in range).
+__device__ __forceinline__ int32_t spec_take_at(const BmState& s, int64_t t, int64_t F) {
+  const int64_t v = t - F;
+  return t < F ? s.free_list[F - 1 - t] : s.sp_victim[v < kSpecWin ? v : kSpecWin - 1];
+}
+
+// tab_insert for inserts from many workgroups at once (one kernel): slot
+// states are read and written at device scope, so a slot another workgroup
+// claims is seen as taken.
+__device__ int32_t tab_insert_dev(const BmState& s, uint64_t h, int32_t page, int32_t ref,
+                                  int64_t hint) {
+  const int64_t mask = s.C - 1;
+  auto claim = [&](int64_t i, int32_t expect) -> bool {
+    if (atomicCAS(ent_page(s, i), expect, kBusy) != expect) return false;
+    *ent_key(s, i) = h;
+    *ent_ref(s, i) = ref;
+    *rec_slot(s, page) = (int32_t)i;
+    __threadfence();
+    __hip_atomic_store(ent_page(s, i), page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  };
+  if (hint >= 0) {
+    if (claim(hint, kEmpty)) return 0;
+    if (claim(hint, kTomb)) return 1;
+  }
+  int64_t i = slot_of(h) & mask;
+  for (int64_t n = 0; n < 2 * s.C; ++n) {
+    const int32_t v =
+        __hip_atomic_load(ent_page(s, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v == kEmpty || v == kTomb) {
+      if (claim(i, v)) return v == kTomb ? 1 : 0;
+      continue;  // claimed by another workgroup meanwhile: read the slot again
+    }
+    i = (i + 1) & mask;
+  }
+  return -1;
+}
+
+// 1. Clears the first-occurrence table and the per-page first pins and
+//    eviction times.
+__global__ __launch_bounds__(256) void spec_clear_kernel(BmState s) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t i = g; i < kFoCap; i += stride)
+    *reinterpret_cast<u32x4*>(s.sp_fo + i * 16) = u32x4{0u, 0u, (uint32_t)INT_MAX, 0u};
+  for (int64_t p = g; p < s.P; p += stride) {
+    s.sp_first[p] = INT_MAX;
+    s.sp_evt[p] = INT_MAX;
+  }
+}
+
+// 2. The admits to speculate: the leading valid admits after the release run
+//    (at most kSpecOps, of at most kSpecPos pages), cut before a request that
+//    repeats; their metadata and the step's starting counters.
+__global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
+  constexpr int kOpt = kSpecOps / kSpecThreads;
+  static_assert(kOpt * kSpecThreads == kSpecOps, "ops split evenly over the threads");
+  __shared__ int32_t cut;
+  __shared__ uint32_t key[2 * kSpecOps], firsti[2 * kSpecOps];
+  const BmState& s = a.s;
+  const int tid = threadIdx.x;
+  const int32_t start = (int32_t)s.run_ctr[kRunOps];
+  const int32_t left = a.num_ops - start;
+  const int limit = left < kSpecOps ? left : kSpecOps;
+  if (tid == 0) cut = limit;
+  for (int i = tid; i < 2 * kSpecOps; i += kSpecThreads) {
+    key[i] = 0xffffffffu;
+    firsti[i] = 0xffffffffu;
+  }
+  __syncthreads();
+  int32_t r[kOpt], n[kOpt], m[kOpt];
+  int64_t h0[kOpt];
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    r[u] = -1;
+    n[u] = m[u] = 0;
+    h0[u] = 0;
+    if (j >= limit) continue;
+    const int32_t op = a.ops[start + j];
+    bool ok = op >= 0 && op < a.num_requests;
+    if (ok) {
+      r[u] = op;
+      n[u] = a.ntok[op];
+      h0[u] = a.hash_off[op];
+      const int64_t mm = a.hash_off[op + 1] - h0[u], np = ((int64_t)n[u] + 15) / 16;
+      ok = n[u] >= 0 && mm == n[u] / 16 && np <= a.twidth && np <= kSpecPos;
+      m[u] = (int32_t)mm;
+    }
+    if (!ok) atomicMin(&cut, j);
+  }
+  __syncthreads();
+  const int lim2 = cut;
+  // a request admitted twice: the speculation stops before the second
+  uint32_t slot[kOpt];
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    slot[u] = 0;
+    if (j >= lim2) continue;
+    uint32_t q = ((uint32_t)r[u] * 2654435761u) & (2 * kSpecOps - 1);
+    for (;;) {  // at most kSpecOps of 2 kSpecOps slots are taken
+      const uint32_t prev = atomicCAS(&key[q], 0xffffffffu, (uint32_t)r[u]);
+      if (prev == 0xffffffffu || prev == (uint32_t)r[u]) break;
+      q = (q + 1) & (2 * kSpecOps - 1);
+    }
+    atomicMin(&firsti[q], (uint32_t)j);
+    slot[u] = q;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    if (j < lim2 && firsti[slot[u]] != (uint32_t)j) atomicMin(&cut, j);
+  }
+  __syncthreads();
+  const int nspec = cut;
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    if (j >= nspec) continue;
+    s.sp_req[j] = r[u];
+    s.sp_ntok[j] = n[u];
+    s.sp_m[j] = m[u];
+    s.sp_h0[j] = h0[u];
+  }
+  if (tid == 0) {
+    s.sp_ctr[kSpN] = nspec;
+    s.sp_ctr[kSpBad] = nspec;
+    s.sp_ctr[kSpF] = s.ctr[kFreeTop];
+    s.sp_ctr[kSpLive] = s.ctr[kEvictable];
+    s.sp_ctr[kSpHead] = s.ctr[kHead];
+    s.sp_ctr[kSpWin] = 0;
+    s.sp_ctr[kSpReused] = 0;
+    s.run_ctr[kRunNext] = start;
+  }
+}
+
+// 3. Every speculated admit's page hashes looked up at S (a workgroup per
+//    admit); keys absent at S enter the first-occurrence table.
+__global__ __launch_bounds__(256) void spec_probe_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const int32_t m = s.sp_m[j];
+    const int64_t h0 = s.sp_h0[j];
+    int2* out = s.sp_p0 + (int64_t)j * kSpecPos;
+    for (int32_t i = threadIdx.x; i < m; i += blockDim.x) {
+      const uint64_t h = a.hashes[h0 + i];
+      const Found f = tab_find(s, h);
+      if (f.page >= 0) {
+        out[i] = int2{f.page | (f.ref == 0 ? kPinBit : 0), f.slot};
+      } else {
+        out[i] = int2{-1, f.slot | (f.tomb ? kTombBit : 0)};
+        if (!fo_insert(s, h, j * kSpecPos + i)) atomicMin(spec_bad(s), j);
+      }
+    }
+  }
+}
+
+// 4. Per admit: its hits (a key absent at S is present if an earlier admit
+//    holds it: the position records that occurrence), its takes, and the
+//    first admit pinning each page it hits at refcount 0. An admit holding a
+//    key absent at S twice is left to the sequential path.
+__global__ __launch_bounds__(kSpecThreads) void spec_hits_kernel(BmArgs a) {
+  __shared__ int32_t wave_miss[kBmWaves];
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const int32_t m = s.sp_m[j], nt = s.sp_ntok[j];
+    int2 v = int2{-1, -1};
+    bool present = false;
+    if (i < m) {
+      v = s.sp_p0[(int64_t)j * kSpecPos + i];
+      if (v.x >= 0) {
+        present = true;
+      } else {
+        const int32_t f = fo_find(s, a.hashes[s.sp_h0[j] + i]);
+        if (f / kSpecPos < j) {
+          present = true;
+          v.x = -(f + 2);
+          s.sp_p0[(int64_t)j * kSpecPos + i].x = v.x;
+        } else if (f != j * kSpecPos + i) {
+          atomicMin(spec_bad(s), j);
+        }
+      }
+    }
+    const uint64_t mb = __ballot(i < m && !present);
+    if (lane == 0) wave_miss[wave] = mb ? wave * 64 + (int32_t)__builtin_ctzll(mb) : INT_MAX;
+    __syncthreads();
+    int32_t k = m;
+#pragma unroll
+    for (int w = 0; w < kBmWaves; ++w) k = wave_miss[w] < k ? wave_miss[w] : k;
+    if (tid == 0) {
+      s.sp_k[j] = k;
+      s.sp_take[j] = (nt + 15) / 16 - k + ((nt & 15) ? 1 : 0);
+    }
+    if (i < k && v.x >= 0 && (v.x & kPinBit)) atomicMin(&s.sp_first[v.x & ~kPinBit], j);
+    __syncthreads();  // wave_miss is rewritten for the next admit
+  }
+}
+
+// 5. Per admit: the pages it pins (it is their first pinner).
+__global__ __launch_bounds__(kSpecThreads) void spec_pins_kernel(BmArgs a) {
+  __shared__ int32_t wave_cnt[kBmWaves];
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
+    const int32_t k = s.sp_k[j];
+    bool pins = false;
+    if (i < k) {
+      const int32_t x = s.sp_p0[(int64_t)j * kSpecPos + i].x;
+      pins = x >= 0 && (x & kPinBit) && s.sp_first[x & ~kPinBit] == j;
+    }
+    const int32_t c = __popcll(__ballot(pins));
+    if (lane == 0) wave_cnt[wave] = c;
+    __syncthreads();
+    if (tid == 0) {
+      int32_t t = 0;
+#pragma unroll
+      for (int w = 0; w < kBmWaves; ++w) t += wave_cnt[w];
+      s.sp_pinned[j] = t;
+    }
+    __syncthreads();
+  }
+}
+
+// 6. The LRU window the takes may reach: each entry's page, its key's slot,
+//    and whether it is a victim candidate (live at S, pinned by no admit of
+//    the step), live but pinned, or dead.
+__global__ __launch_bounds__(256) void spec_window_kernel(BmArgs a) {
+  __shared__ int64_t part[4];
+  const BmState& s = a.s;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  // the evictions all admits would need, summed by every workgroup
+  int64_t mine = 0;
+  for (int32_t j = threadIdx.x; j < n; j += blockDim.x) mine += s.sp_take[j];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mine += __shfl_xor(mine, off);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mine;
+  __syncthreads();
+  const int64_t takes = part[0] + part[1] + part[2] + part[3];
+  const int64_t evict = takes - s.sp_ctr[kSpF];
+  const int64_t head = s.sp_ctr[kSpHead], span = s.ctr[kTail] - head;
+  int64_t W = evict <= 0 ? 0 : evict + evict / 2 + 4096;
+  W = W < span ? W : span;
+  W = W < kSpecWin ? W : kSpecWin;
+  if (blockIdx.x == 0 && threadIdx.x == 0) s.sp_ctr[kSpWin] = W;
+  const int64_t qm = s.Q - 1;
+  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < W;
+       w += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t e = s.ring[(head + w) & qm];
+    const int32_t p = (int32_t)(uint32_t)e;
+    const RecHead h = rec_head(s, p);
+    const bool lv = live(h, (uint32_t)(e >> 32));
+    s.sp_wpg[w] = p;
+    s.sp_wslot[w] = h.slot;
+    s.sp_wflag[w] = !lv ? 0 : (s.sp_first[p] != INT_MAX ? 2 : 1);
+  }
+}
+
+// 7. One workgroup: the takes' prefix sums, the OOM checks, and the victims.
+//    Victim v (the (v+1)-th candidate in window order) is take F + v, which
+//    belongs to the admit whose prefix range holds it; a pinned live entry is
+//    reached by the admit owning the take index it is passed at.
+__global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
+  constexpr int kOpt = kSpecOps / kSpecThreads;
+  __shared__ int64_t T[kSpecOps + 1];
+  __shared__ int64_t wave_tot[2][kBmWaves];
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  if (n == 0) return;
+  const int64_t F = s.sp_ctr[kSpF], live0 = s.sp_ctr[kSpLive];
+  // exclusive prefix sums of takes and pins, kOpt consecutive admits per thread
+  int64_t tk[kOpt], pn[kOpt], st = 0, sp = 0;
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    tk[u] = j < n ? s.sp_take[j] : 0;
+    pn[u] = j < n ? s.sp_pinned[j] : 0;
+    st += tk[u];
+    sp += pn[u];
+  }
+  int64_t it = st, ip = sp;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t a1 = __shfl_up(it, d), a2 = __shfl_up(ip, d);
+    if (lane >= d) {
+      it += a1;
+      ip += a2;
+    }
+  }
+  if (lane == 63) {
+    wave_tot[0][wave] = it;
+    wave_tot[1][wave] = ip;
+  }
+  __syncthreads();
+  int64_t bt = it - st, bp = ip - sp;
+#pragma unroll
+  for (int w = 0; w < kBmWaves; ++w) {
+    bt += w < wave ? wave_tot[0][w] : 0;
+    bp += w < wave ? wave_tot[1][w] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < kOpt; ++u) {
+    const int j = tid * kOpt + u;
+    if (j < n) {
+      T[j] = bt;
+      s.sp_T[j] = bt;
+      // OOM: the takes exceed the free stack left plus the evictable pages
+      // left, minus the ones this admit pins
+      const int64_t free_j = F - bt > 0 ? F - bt : 0;
+      const int64_t ev_j = live0 - bp - (bt - F > 0 ? bt - F : 0);
+      if (tk[u] > free_j + ev_j - pn[u]) atomicMin(spec_bad(s), j);
+    }
+    bt += tk[u];
+    bp += pn[u];
+  }
+  if (tid == kSpecThreads - 1) {
+    T[n] = bt;  // the last thread's running sum covers every admit
+    s.sp_T[n] = bt;
+  }
+  __syncthreads();
+  const int64_t total = T[n];
+  const int64_t E = total - F > 0 ? total - F : 0;  // evictions wanted
+  const int64_t W = s.sp_ctr[kSpWin];
+  // the admit owning take index t (t < total)
+  auto owner = [&](int64_t t) -> int32_t {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (T[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
+  // candidates before each window entry: per thread a contiguous slice
+  const int64_t per = (W + kSpecThreads - 1) / kSpecThreads;
+  const int64_t w0 = tid * per, w1 = w0 + per < W ? w0 + per : W;
+  int64_t cnt = 0;
+  for (int64_t w = w0; w < w1; ++w) cnt += s.sp_wflag[w] == 1;
+  int64_t inc = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t o = __shfl_up(inc, d);
+    if (lane >= d) inc += o;
+  }
+  __syncthreads();  // wave_tot is reused
+  if (lane == 63) wave_tot[0][wave] = inc;
+  __syncthreads();
+  int64_t before = inc - cnt, ncand = 0;
+#pragma unroll
+  for (int w = 0; w < kBmWaves; ++w) {
+    before += w < wave ? wave_tot[0][w] : 0;
+    ncand += wave_tot[0][w];
+  }
+  for (int64_t w = w0; w < w1; ++w) {
+    const uint8_t f = s.sp_wflag[w];
+    if (f == 1) {
+      if (before < E) {
+        const int32_t p = s.sp_wpg[w];
+        s.sp_victim[before] = p;
+        s.sp_vpos[before] = (int32_t)w;
+        s.sp_evt[p] = owner(F + before);
+      }
+      ++before;
+    } else if (f == 2 && before < E) {  // passed while take F + before is wanted
+      const int32_t u = owner(F + before);
+      if (u < s.sp_first[s.sp_wpg[w]]) atomicMin(spec_bad(s), u);
+    }
+  }
+  if (tid == 0 && ncand < E) atomicMin(spec_bad(s), owner(F + ncand));  // window too short
+}
+
+// 8. Per admit before the first violation so far: a page it finds at S that
+//    an earlier admit evicts, or that it evicts itself past its hits, makes it
+//    (and everything after) sequential.
+__global__ __launch_bounds__(kSpecThreads) void spec_verify_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int32_t bad0 = *spec_bad(s);
+  for (int32_t j = blockIdx.x; j < bad0; j += gridDim.x) {
+    const int32_t i = threadIdx.x;
+    if (i >= s.sp_m[j]) continue;
+    const int32_t x = s.sp_p0[(int64_t)j * kSpecPos + i].x;
+    if (x < 0) continue;
+    const int32_t et = s.sp_evt[x & ~kPinBit];
+    if (et < j || (et == j && i >= s.sp_k[j])) atomicMin(spec_bad(s), j);
+  }
+}
+
+// 9. The admits before the first violation, a workgroup per admit: tables,
+//    refcounts, cached flags and hashes, registrations (insertion by
+//    compare-and-swap at the slot found at S), results.
+__global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int32_t bad = *spec_bad(s);
+  const int64_t F = s.sp_ctr[kSpF];
+  int32_t reused = 0;
+  for (int32_t j = blockIdx.x; j < bad; j += gridDim.x) {
+    const int32_t r = s.sp_req[j], nt = s.sp_ntok[j], m = s.sp_m[j], k = s.sp_k[j];
+    const int32_t np = (nt + 15) / 16;
+    const bool cow = (nt & 15) != 0;
+    const int64_t T = s.sp_T[j];
+    const int32_t i = threadIdx.x;
+    if (i < np) {
+      const int2 v = i < m ? s.sp_p0[(int64_t)j * kSpecPos + i] : int2{-1, -1};
+      int32_t page;
+      if (i < k) {
+        if (v.x >= 0) {
+          page = v.x & ~kPinBit;
+        } else {  // the key an earlier admit w registers at its position iw
+          const int32_t code = -(v.x + 2), w = code / kSpecPos, iw = code % kSpecPos;
+          page = spec_take_at(s, s.sp_T[w] + iw - s.sp_k[w], F);
+        }
+        atomicAdd(rec_ref(s, page), 2);
+      } else {
+        page = spec_take_at(s, T + i - k, F);
+        atomicAdd(rec_ref(s, page), (cow && i == np - 1) ? 1 : 2);
+        const bool reg = i < m && v.x == -1;  // absent at S, and this is its first holder
+        *rec_flag(s, page) = reg ? 1 : 0;
+        if (reg) {
+          const uint64_t h = a.hashes[s.sp_h0[j] + i];
+          *rec_hash(s, page) = h;
+          reused += tab_insert_dev(s, h, page, 2, v.y & ~kTombBit) == 1;
+        }
+      }
+      a.tables[(int64_t)r * a.tstride + i] = page;
+      if (i == np - 1) {
+        if (cow)
+          a.cow_src[r] = page;
+        else
+          a.child_last[r] = page;
+      }
+    }
+    if (i == 0) {
+      a.hits[r] = k;
+      a.status[r] = kStOk;
+      if (cow) {
+        const int32_t cp = spec_take_at(s, T + np - k, F);
+        atomicAdd(rec_ref(s, cp), 1);
+        *rec_flag(s, cp) = 0;
+        a.cow_dst[r] = a.child_last[r] = cp;
+      } else {
+        a.cow_src[r] = a.cow_dst[r] = -1;
+        if (np == 0) a.child_last[r] = -1;
+      }
+    }
+  }
+  if (reused) atomicAdd(reinterpret_cast<unsigned long long*>(s.sp_ctr + kSpReused),
+                        (unsigned long long)reused);
+}
+
+// 10. The evictions' tombstones and log, the cached pages' refcounts copied
+//     into their table entries, and the counters.
+__global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
+  const BmState& s = a.s;
+  const int32_t bad = *spec_bad(s);
+  const int64_t F = s.sp_ctr[kSpF];
+  const int64_t taken = bad > 0 ? s.sp_T[bad] : 0;  // takes of the committed admits
+  int64_t evicted = taken - F > 0 ? taken - F : 0;
+  evicted = evicted < kSpecWin ? evicted : kSpecWin;  // (always: see spec_take_at)
+  const int64_t log0 = s.ctr[kLogLen];
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < evicted;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    *ent_page(s, s.sp_wslot[s.sp_vpos[v]]) = kTomb;
+    if (log0 + v < a.evict_cap) a.evict_log[log0 + v] = s.sp_victim[v];
+  }
+  for (int32_t j = blockIdx.x; j < bad; j += gridDim.x) {
+    const int32_t i = threadIdx.x;
+    if (i >= (s.sp_ntok[j] + 15) / 16) continue;
+    const int32_t p = a.tables[(int64_t)s.sp_req[j] * a.tstride + i];
+    const RecHead h = rec_head(s, p);
+    if (h.flag & 1) *ent_ref(s, h.slot) = h.ref;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < 64) {  // one wave: the pins of the committed admits
+    int64_t pins = 0;
+    for (int32_t j = threadIdx.x; j < bad; j += 64) pins += s.sp_pinned[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) pins += __shfl_xor(pins, off);
+    if (threadIdx.x == 0) {
+      const int32_t start = (int32_t)s.run_ctr[kRunOps];
+      s.ctr[kFreeTop] = F - (taken < F ? taken : F);
+      if (evicted > 0) s.ctr[kHead] = s.sp_ctr[kSpHead] + s.sp_vpos[evicted - 1] + 1;
+      s.ctr[kEvictable] = s.sp_ctr[kSpLive] - pins - evicted;
+      s.ctr[kTombs] += evicted - s.sp_ctr[kSpReused];
+      s.ctr[kLogLen] = log0 + evicted;
+      s.run_ctr[kRunNext] = start + bad;
+    }
+  }
+}
+
 // The admits after the leading run of releases, in groups, while they are
 // valid and at most kBmThreads pages long; the step kernel takes the ops from
 // the first one that is not (kRunNext). A kernel of its own, so that the
@@ -1673,7 +2317,7 @@ __global__ __launch_bounds__(kBmThreads) void bm_group_kernel(BmArgs a) {
   __shared__ GroupLds gl;
   __shared__ GroupMeta gm;
   const BmState& s = a.s;
-  int32_t t = (int32_t)s.run_ctr[kRunOps];
+  int32_t t = (int32_t)s.run_ctr[kRunNext];  // after the run and the speculated admits
   if (s.P > kGroupMaxPages) {  // the page bitmaps do not fit in LDS
     if (threadIdx.x == 0) s.run_ctr[kRunNext] = t;
     return;
@@ -1929,6 +2573,16 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
   hipLaunchKernelGGL(run_scan_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(run_push_kernel, dim3(kRunGrid * kRunUnroll), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_clear_kernel, dim3(kSpecGrid), dim3(256), 0, st, a.s);
+  hipLaunchKernelGGL(spec_setup_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_probe_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(spec_hits_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_pins_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_window_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(spec_scan_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_verify_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_commit_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_finish_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   return check_launch("mkv_bm_step");
