@@ -412,18 +412,25 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * last-occurrence slots (P int32, -1 between steps), the scratch of the
  * many-workgroup passes (4.6 MiB for a release run of up to 2^20 page
  * references: counters, per-op offsets, page ids, bit arrays; plus 8.25 x Q
- * bytes for compacting the ring), and the total size.
+ * bytes for compacting the ring; plus 14.2 MiB + 8 x P bytes for resolving up
+ * to 1024 admits at once: per-admit metadata, per-position probe results, a
+ * first-occurrence table of absent hashes, per-page first pinner and
+ * eviction, the LRU window and its victims), and the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
- * (a leading run of up to 1024 releases is retired by many-workgroup passes,
- * the admits after it by one workgroup in groups of eight, the rest on one
- * workgroup one op at a time): op r >= 0
+ * (a leading run of up to 1024 releases is retired by many-workgroup passes;
+ * the admits after it, up to 1024 of at most 512 pages, are resolved
+ * together by many-workgroup passes against the state before them, every
+ * prediction checked, and the admits before the first one that may differ
+ * from the sequential result are committed; one workgroup takes the admits
+ * after that in groups of eight, and the rest one op at a time): op r >= 0
  * admits request r, op -(r+1) releases it (r < num_requests, the length of
  * the per-request arrays; hash_offsets has num_requests+1 entries, tables
  * num_requests rows). Request r has num_tokens[r]
  * tokens whose floor(n/16) page hashes are page_hashes[hash_offsets[r] ..
- * hash_offsets[r+1]); the hashes of one request must be distinct (prefix
- * hashes of different lengths are). Admit:
+ * hash_offsets[r+1]); a hash names one page position: equal hashes must sit
+ * at equal positions, in one request or in any two (prefix hashes of
+ * different lengths differ). Admit:
  *   k = number of leading page hashes found in the table;
  *   take = ceil(n/16) - k + (n % 16 != 0); if take > free + evictable - (hits
  *     now evictable): status OOM, nothing changes;

@@ -29,7 +29,7 @@ import torch
 from muserve_amd import _lib
 
 STATUS_ADMITTED, STATUS_OOM, STATUS_BAD, STATUS_RELEASED = 0, 1, 2, 3
-_FREE_TOP, _HEAD, _TAIL, _NEXT_STAMP, _EVICTABLE, _TOMBS, _LOG_LEN = range(7)
+_FREE_TOP, _HEAD, _TAIL, _NEXT_STAMP, _EVICTABLE, _TOMBS, _LOG_LEN, _SPEC_DONE, _SPEC_LEFT = range(9)
 
 
 def admit_op(r: int) -> int:
@@ -172,10 +172,14 @@ class BlockManager:
         table_ok = bool(np.all(ent[slot, 2] == cp) and np.all(ent[slot, 3] == ref[cp]) and
                         np.all(ent.view(np.uint64).reshape(-1, 2)[slot, 0] == phash[cp]) and
                         int(np.count_nonzero(ent[:, 2] >= 0)) == len(cp))
+        tombs_ok = int(np.count_nonzero(ent[:, 2] == -2)) == ctr[_TOMBS]
         # the release-run scratch's last-occurrence slots are -1 between steps
         last_ok = bool(np.all(self._arr("last", P, torch.int32).cpu().numpy() == -1))
         return {"free": free.tolist(), "lru": lru, "ref": ref.tolist(), "table_ok": table_ok,
-                "last_ok": last_ok,
+                "last_ok": last_ok, "tombs_ok": tombs_ok,
                 "cached": cached.tolist(),
                 "hash": [int(phash[p]) if cached[p] else None for p in range(P)],
-                "evictable": ctr[_EVICTABLE], "log_len": ctr[_LOG_LEN]}
+                "evictable": ctr[_EVICTABLE], "log_len": ctr[_LOG_LEN],
+                # admits resolved by the many-CU speculation / covered by it but
+                # left to the sequential kernels, since the manager was made
+                "spec_done": ctr[_SPEC_DONE], "spec_left": ctr[_SPEC_LEFT]}

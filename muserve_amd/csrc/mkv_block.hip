@@ -62,7 +62,10 @@ constexpr int kHeld = 1;
 constexpr int kSetSize = 2048;  // LDS set of the table slots an admit claims
 static_assert(kSetSize == 1 << 11, "set_add's default size");
 
-enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen, kNumCtr = 16 };
+enum Ctr { kFreeTop, kHead, kTail, kNextStamp, kEvictable, kTombs, kLogLen,
+           kSpecDone,  // admits resolved by the speculation, since init
+           kSpecLeft,  // admits it covered but left to the sequential path, since init
+           kNumCtr = 16 };
 enum Status { kStOk = 0, kStOom = 1, kStBad = 2, kStReleased = 3 };
 
 constexpr int32_t kEmpty = -1, kTomb = -2, kBusy = -3;
@@ -1854,10 +1857,15 @@ __device__ int32_t tab_insert_dev(const BmState& s, uint64_t h, int32_t page, in
 }
 
 // 1. Clears the first-occurrence table and the per-page first pins and
-//    eviction times.
+//    eviction times; when tombstones fill more than a quarter of the table,
+//    also every table entry (the setup kernel inserts the cached pages again).
+__device__ __forceinline__ bool spec_rebuilds(const BmState& s) { return s.ctr[kTombs] > s.C / 4; }
+
 __global__ __launch_bounds__(256) void spec_clear_kernel(BmState s) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (spec_rebuilds(s))
+    for (int64_t i = g; i < s.C; i += stride) *ent_page(s, i) = kEmpty;
   for (int64_t i = g; i < kFoCap; i += stride)
     *reinterpret_cast<u32x4*>(s.sp_fo + i * 16) = u32x4{0u, 0u, (uint32_t)INT_MAX, 0u};
   for (int64_t p = g; p < s.P; p += stride) {
@@ -1876,6 +1884,12 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
   __shared__ uint32_t key[2 * kSpecOps], firsti[2 * kSpecOps];
   const BmState& s = a.s;
   const int tid = threadIdx.x;
+  if (spec_rebuilds(s)) {  // the entries were cleared: insert the cached pages
+    for (int32_t p = tid; p < s.P; p += kSpecThreads)
+      if (*rec_flag(s, p) & 1) tab_insert(s, *rec_hash(s, p), p, *rec_ref(s, p));
+    __syncthreads();
+    if (tid == 0) s.ctr[kTombs] = 0;  // every workgroup read it in the clear kernel
+  }
   const int32_t start = (int32_t)s.run_ctr[kRunOps];
   const int32_t left = a.num_ops - start;
   const int limit = left < kSpecOps ? left : kSpecOps;
@@ -2303,6 +2317,8 @@ __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
       s.ctr[kEvictable] = s.sp_ctr[kSpLive] - pins - evicted;
       s.ctr[kTombs] += evicted - s.sp_ctr[kSpReused];
       s.ctr[kLogLen] = log0 + evicted;
+      s.ctr[kSpecDone] += bad;
+      s.ctr[kSpecLeft] += s.sp_ctr[kSpN] - bad;
       s.run_ctr[kRunNext] = start + bad;
     }
   }

@@ -58,17 +58,61 @@ def random_ops(seed):
     return ops_fn
 
 
+def synthetic_keys(n, seed, alphabet, max_pages, skew):
+    """Prefix keys over a small alphabet instead of SHA-256: key i mixes key
+    i-1 with symbol i (SplitMix64 finaliser), so equal keys mean equal
+    prefixes, as for page hashes. Symbols are drawn geometrically (parameter
+    `skew`), so requests of one step share prefixes of many lengths; the
+    rarest first symbol gives the key 0. Half the requests start with a prefix
+    of an earlier one."""
+    rng = np.random.default_rng(seed)
+    M = (1 << 64) - 1
+
+    def mix(prev, sym):
+        z = (prev * 0x9E3779B97F4A7C15 + sym + 1) & M
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+    lens, keys = [], []
+    for r in range(n):
+        nt = int(rng.integers(1, max_pages * 16 + 1))
+        m = nt // 16
+        sym = np.minimum(rng.geometric(skew, m) - 1, alphabet - 1)
+        if r and rng.random() < 0.5:
+            src = keys[int(rng.integers(0, r))]
+            c = int(rng.integers(0, min(len(src), m) + 1))
+        else:
+            src, c = [], 0
+        k = list(src[:c])
+        for i in range(c, m):
+            k.append(0 if i == 0 and sym[i] == alphabet - 1 else
+                     mix(k[-1] if i else 0x5EED, int(sym[i])))
+        lens.append(nt)
+        keys.append(k)
+    return lens, [np.array(k, dtype=np.uint64).view(np.int64) for k in keys]
+
+
 def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False,
-        ops_fn=bench.prefix_ops):
-    reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
-                                 template_len=template_len, suffix=suffix)
-    lens = [len(x) for x in reqs]
-    cu = np.concatenate([[0], np.cumsum(lens)])
-    flat = torch.from_numpy(np.concatenate(reqs)).to(DEV)
-    hashes, cu_pages = page_hashes(flat, cu)
-    hu = as_u64(hashes)
-    for r in (0, n // 2, n - 1):  # the GPU hashes are the prefix keys
-        assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r])
+        ops_fn=bench.prefix_ops, keys=None):
+    """Drives the manager through ops_fn's steps and checks it against the
+    model; returns the statuses, the model and the final snapshot. `keys` =
+    (token counts, per-request key lists) replaces the hashed prompts."""
+    if keys is None:
+        reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
+                                     template_len=template_len, suffix=suffix)
+        lens = [len(x) for x in reqs]
+        cu = np.concatenate([[0], np.cumsum(lens)])
+        flat = torch.from_numpy(np.concatenate(reqs)).to(DEV)
+        hashes, cu_pages = page_hashes(flat, cu)
+        hu = as_u64(hashes)
+        for r in (0, n // 2, n - 1):  # the GPU hashes are the prefix keys
+            assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r])
+    else:
+        lens, kl = keys
+        cu_pages = np.concatenate([[0], np.cumsum([len(k) for k in kl])]).astype(np.int64)
+        flat = np.concatenate([np.asarray(k, dtype=np.int64) for k in kl] + [np.zeros(0, np.int64)])
+        hashes = torch.from_numpy(flat).to(DEV)
+        hu = as_u64(hashes)
     free = np.random.default_rng(seed).permutation(P).tolist()
     bm = BlockManager(P, n, width, DEV, free_order=free, evict_log_capacity=1 << 20)
     model = BlockManagerModel(P, free)
@@ -97,6 +141,9 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
             for s, d in pairs:
                 cpu[:, :, d] = cpu[:, :, s]
     bm.check_errors()
+    ctr = bm.counters()
+    print(f"speculation: {ctr[7]} admits resolved, {ctr[8]} left to the sequential kernels",
+          flush=True)
     status = bm.status.cpu().tolist()
     hits, cl = bm.hits.cpu().tolist(), bm.child_last.cpu().tolist()
     cs, cd = bm.cow_src.cpu().tolist(), bm.cow_dst.cpu().tolist()
@@ -113,6 +160,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         assert (cl[r], cs[r], cd[r]) == (w["child_last"], w["cow_src"], w["cow_dst"]), r
     snap = bm.snapshot()
     assert snap["table_ok"]  # entries = cached pages, with their keys and refcounts
+    assert snap["tombs_ok"]  # the tombstone count matches the table
     assert snap["last_ok"] and snap["evictable"] == len(snap["lru"])
     assert snap["free"] == model.free
     assert snap["lru"] == model.lru_order()
@@ -134,19 +182,22 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         lead = next((i for i, p in enumerate(want_pages) if p < 0), len(h))
         assert hit[r] == lead, r
     assert bm.snapshot()["lru"] == snap["lru"]  # nothing moved
-    return status, model
+    return status, model, snap
 
 
 def test_small_pool_evictions_oom_and_cow():
     case("block manager: 72-page pool, 240 requests, batches of 6")
-    status, model = run(P=72, n=240, batch=6, seed=104, n_templates=6, template_len=128,
+    status, model, snap = run(P=72, n=240, batch=6, seed=104, n_templates=6, template_len=128,
                         suffix=(1, 120), width=32, with_data=True)
     assert OOM in status and len(model.evicted) > 100
+    # OOMs and same-step evictions of hit pages send admits to the sequential
+    # kernels; the rest are resolved by the many-CU speculation
+    assert snap["spec_done"] > 0 and snap["spec_left"] > 0
 
 
 def test_larger_trace_with_ring_compaction():
     case("block manager: 3000-page pool, 1200 requests, batches of 32")
-    status, model = run(P=3000, n=1200, batch=32, seed=7, n_templates=24, template_len=512,
+    status, model, snap = run(P=3000, n=1200, batch=32, seed=7, n_templates=24, template_len=512,
                         suffix=(16, 600), width=96)
     assert len(model.evicted) > 1000
 
@@ -155,7 +206,7 @@ def test_long_requests_past_the_register_held_pages():
     # up to 2600 pages per request: pages past the first 1024 of a request take
     # the kernel's memory-resident path (probe, pin, register)
     case("block manager: 5400-page pool, 14 requests of ~2300-2600 pages")
-    status, model = run(P=5400, n=14, batch=2, seed=11, n_templates=2, template_len=36000,
+    status, model, snap = run(P=5400, n=14, batch=2, seed=11, n_templates=2, template_len=36000,
                         suffix=(1, 5000), width=2600)
     assert len(model.evicted) > 500
 
@@ -164,7 +215,7 @@ def test_many_evictions_rebuild_the_table():
     # 72 pages and a 4096-slot table: ~10,800 evictions leave tombstones past
     # a quarter of the table many times over, so the table is rebuilt repeatedly
     case("block manager: 72-page pool, 1500 requests, batches of 6")
-    status, model = run(P=72, n=1500, batch=6, seed=21, n_templates=40, template_len=128,
+    status, model, snap = run(P=72, n=1500, batch=6, seed=21, n_templates=40, template_len=128,
                         suffix=(1, 120), width=32)
     assert len(model.evicted) > 2000
 
@@ -173,7 +224,7 @@ def test_long_release_runs():
     # batches of 100 requests of ~190-230 pages: runs of 100 releases dropping
     # ~21,000 page references, in a pool small enough to evict thousands
     case("block manager: 4000-page pool, 400 requests, batches of 100")
-    status, model = run(P=4000, n=400, batch=100, seed=9, n_templates=8, template_len=3000,
+    status, model, snap = run(P=4000, n=400, batch=100, seed=9, n_templates=8, template_len=3000,
                         suffix=(1, 600), width=240)
     assert len(model.evicted) > 4000
 
@@ -183,7 +234,7 @@ def test_release_run_past_the_reference_limit():
     # release run stops at the op boundary below 2^20 and the one-workgroup
     # step kernel releases the rest
     case("block manager: 5000-page pool, 2000 requests of ~1102 pages, batches of 1000")
-    status, model = run(P=5000, n=2000, batch=1000, seed=17, n_templates=1, template_len=17600,
+    status, model, snap = run(P=5000, n=2000, batch=1000, seed=17, n_templates=1, template_len=17600,
                         suffix=(1, 20), width=1102)
     assert OOM not in status
 
@@ -191,7 +242,7 @@ def test_release_run_past_the_reference_limit():
 @pytest.mark.parametrize("seed", [31, 32, 33])
 def test_random_release_runs_and_interleavings(seed):
     case(f"block manager: random op streams, 96-page pool, seed {seed}")
-    status, model = run(P=96, n=400, batch=8, seed=seed, n_templates=5, template_len=160,
+    status, model, snap = run(P=96, n=400, batch=8, seed=seed, n_templates=5, template_len=160,
                         suffix=(1, 100), width=32, with_data=seed == 31,
                         ops_fn=random_ops(seed))
     assert len(model.evicted) > 100
@@ -199,9 +250,29 @@ def test_random_release_runs_and_interleavings(seed):
 
 def test_single_releases_between_admits():
     case("block manager: 72-page pool, 240 requests, releases between admits")
-    status, model = run(P=72, n=240, batch=6, seed=105, n_templates=6, template_len=128,
+    status, model, snap = run(P=72, n=240, batch=6, seed=105, n_templates=6, template_len=128,
                         suffix=(1, 120), width=32, ops_fn=interleaved_ops)
     assert len(model.evicted) > 100
+
+
+@pytest.mark.parametrize("seed,P,batch,alphabet,skew,ops", [
+    (41, 96, 12, 16, 0.3, "random"),   # ~380 evictions, ~40 OOMs
+    (42, 300, 48, 16, 0.3, "batch"),   # ~1850 evictions
+    (43, 1000, 160, 32, 0.2, "batch"),  # ~6600 evictions
+])
+def test_prefix_keys_over_a_small_alphabet(seed, P, batch, alphabet, skew, ops):
+    # prefixes shared at every length inside one step (hits on pages that
+    # earlier admits of the step register), and the key 0: the many-CU
+    # resolution must resolve each admit exactly or hand it to the
+    # sequential kernels
+    case(f"block manager: recurring synthetic keys, {P}-page pool, batches of {batch}, "
+         f"alphabet {alphabet}, seed {seed}")
+    n = 12 * batch
+    status, model, snap = run(P=P, n=n, batch=batch, seed=seed, n_templates=0, template_len=0,
+                              suffix=None, width=12,
+                              keys=synthetic_keys(n, seed, alphabet, 12, skew),
+                              ops_fn=random_ops(seed) if ops == "random" else bench.prefix_ops)
+    assert len(model.evicted) > 200 and snap["spec_done"] > 0 and snap["spec_left"] > 0
 
 
 def test_duplicate_release_is_flagged_once():

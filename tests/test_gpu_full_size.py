@@ -222,9 +222,10 @@ def test_prefix_config_full_trace_against_model():
     # suffixes), batches of 256, 65536 pages: every admit, table, hit count,
     # copy-on-write pair, the 89k-entry eviction order and the final state
     case("full size: prefix cache, 4096 requests, 65536 pages, batches of 256")
-    status, model = run_block_manager(P=65536, n=4096, batch=256, seed=104, n_templates=64,
+    status, model, snap = run_block_manager(P=65536, n=4096, batch=256, seed=104, n_templates=64,
                                       template_len=4096, suffix=(64, 1024), width=320)
     assert len(model.evicted) > 50000
+    assert snap["spec_done"] + snap["spec_left"] == 4096  # every admit was speculated
 
 
 @pytest.mark.timeout(600)
