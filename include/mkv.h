@@ -428,9 +428,10 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * the per-request arrays; hash_offsets has num_requests+1 entries, tables
  * num_requests rows). Request r has num_tokens[r]
  * tokens whose floor(n/16) page hashes are page_hashes[hash_offsets[r] ..
- * hash_offsets[r+1]); a hash names one page position: equal hashes must sit
- * at equal positions, in one request or in any two (prefix hashes of
- * different lengths differ). Admit:
+ * hash_offsets[r+1]); they must be prefix keys: two requests' hashes at
+ * position i are equal only if their hashes at every position up to i are
+ * (a page hash keys the whole prefix up to its page, as the SHA-256 prefix
+ * hashes do; hashes of different lengths differ). Admit:
  *   k = number of leading page hashes found in the table;
  *   take = ceil(n/16) - k + (n % 16 != 0); if take > free + evictable - (hits
  *     now evictable): status OOM, nothing changes;
