@@ -931,13 +931,16 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
         "phase_ms": {"hash": round(hash_ms, 3), "block_manager": round(step_ms, 3),
                      "cow_copy": round(cow_ms, 3)},
         "hashing": "all prompts hashed in one launch on a second stream before the "
-                   "block-manager steps (one lane per request chain)",
+                   "block-manager steps (two lanes per request chain, message schedules "
+                   "by a second wave)",
         "roofline": {"kernels": [
             {"kernel": "block_hash_kernel (mkv_block_hash_sha256)", "bound": "integer ALU / latency",
-             "note": "one lane per request walks its SHA-256 chain; no HBM roofline claim",
+             "note": "the longest request's chain of SHA-256 rounds (two compressions per "
+                     "page, ~944 instructions each); no HBM roofline claim",
              "launch_ms": round(hash_ms, 3),
              "GB_hashed_per_s": round(8 * int(cu_t[-1]) / (hash_ms / 1e3) / 1e9, 3)},
-            {"kernel": "bm_step_kernel (mkv_bm_step)", "bound": "latency (one workgroup)",
+            {"kernel": "mkv_bm_step (release run, speculation, group and step kernels)",
+             "bound": "latency (a chain of small launches per batch)",
              "us_per_request": round(step_ms * 1e3 / n_req, 3)},
             _kernel_roofline("copy_pages_kernel (mkv_copy_blocks)", cow_bytes / len(ops_dev),
                              cow_ms / len(ops_dev))]},

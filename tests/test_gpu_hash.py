@@ -23,3 +23,18 @@ def test_page_hashes_match_hashlib(dtype):
     for r, x in enumerate(ids):
         want = ref.page_hashes(x)
         assert got[cu_p[r]:cu_p[r + 1]].tolist() == want, r
+
+
+def test_page_hashes_workgroup_without_pages():
+    # 32 requests of the first workgroup have no full page (it runs no step);
+    # the second mixes empty, partial and long requests
+    lens = [3] * 32 + [40, 0, 15, 600, 16, 2047]
+    case(f"page hashes {len(lens)} requests, a workgroup without pages")
+    rng = np.random.default_rng(5)
+    ids = [rng.integers(0, 151936, n).astype(np.int64) for n in lens]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    h, cu_p = page_hashes(torch.from_numpy(np.concatenate(ids)).to(DEV), cu)
+    got = as_u64(h)
+    assert cu_p[32] == 0
+    for r, x in enumerate(ids):
+        assert got[cu_p[r]:cu_p[r + 1]].tolist() == ref.page_hashes(x), r
