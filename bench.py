@@ -856,11 +856,13 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
     stamps = Stamps()
 
     def run_all(bm, rec=None):
-        # Page hashing depends only on the prompts, and one lane walks one
-        # request's chain, so all prompts are hashed in one launch (64 waves
-        # on 16 CUs take about as long as one batch's 4 waves) on a second
-        # stream; the block manager (one workgroup) then processes the batches
-        # in order, each step waiting for the hashes.
+        # Page hashing depends only on the prompts and is bound by the longest
+        # request's chain of compressions, so all prompts are hashed in one
+        # launch on a second stream; the block manager then processes the
+        # batches in order, each step waiting for the hashes, each followed by
+        # its batch's copy-on-write copies. (Copies on a third stream behind
+        # each step, overlapping the next step, made the trace slower: the
+        # copy kernel holds every CU while the step's small kernels wait.)
         with torch.cuda.stream(hash_stream):
             sp = stamps.span(hash_stream) if rec is not None else None
             page_hashes_range(tokens, tok_off, page_off, 0, n_req, hashes, herr)
