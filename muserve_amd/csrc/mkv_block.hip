@@ -91,6 +91,8 @@ constexpr int kFoBits = 19;
 constexpr int64_t kFoCap = 1ll << kFoBits;
 constexpr int kFoMaxProbe = 512;  // a longer probe counts as a violation
 constexpr int kSpecWin = 1 << 17;
+constexpr int kWinChunk = 256;                     // window entries per candidate count
+constexpr int kWinChunks = kSpecWin / kWinChunk;
 enum SpecCtr { kSpN,        // admits speculated
                kSpBad,      // first admit the speculation may get wrong (<= kSpN)
                kSpF,        // free-stack entries at the step's start
@@ -109,7 +111,7 @@ struct BmLayout {
   int64_t cmp_ring, cmp_bits, cmp_pre;
   // speculation scratch
   int64_t sp_ctr, sp_req, sp_ntok, sp_m, sp_h0, sp_k, sp_take, sp_pinned, sp_T, sp_p0, sp_fo,
-      sp_first, sp_evt, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos;
+      sp_first, sp_evt, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt, sp_wpre;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -166,6 +168,8 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.sp_wflag = take(kSpecWin);
   l.sp_victim = take(kSpecWin * 4);
   l.sp_vpos = take(kSpecWin * 4);
+  l.sp_wcnt = take(kWinChunks * 4);
+  l.sp_wpre = take(kWinChunks * 8);
   l.bytes = o;
   return l;
 }
@@ -207,6 +211,8 @@ struct BmState {
   uint8_t* sp_wflag;   //     0 dead, 1 a victim candidate, 2 live but pinned in the step
   int32_t* sp_victim;  // [v] the v-th eviction's page
   int32_t* sp_vpos;    //     its window position
+  int32_t* sp_wcnt;    // [c] victim candidates in window chunk c (kWinChunk entries)
+  int64_t* sp_wpre;    //     candidates before chunk c
   int64_t C, Q;
   int32_t P;
 };
@@ -248,6 +254,8 @@ inline BmState bm_state(void* base, int32_t P) {
   s.sp_wflag = b + l.sp_wflag;
   s.sp_victim = reinterpret_cast<int32_t*>(b + l.sp_victim);
   s.sp_vpos = reinterpret_cast<int32_t*>(b + l.sp_vpos);
+  s.sp_wcnt = reinterpret_cast<int32_t*>(b + l.sp_wcnt);
+  s.sp_wpre = reinterpret_cast<int64_t*>(b + l.sp_wpre);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -1824,19 +1832,19 @@ __device__ __forceinline__ int32_t spec_take_at(const BmState& s, int64_t t, int
   return t < F ? s.free_list[F - 1 - t] : s.sp_victim[v < kSpecWin ? v : kSpecWin - 1];
 }
 
-// tab_insert for inserts from many workgroups at once (one kernel): slot
-// states are read and written at device scope, so a slot another workgroup
-// claims is seen as taken.
+// tab_insert for inserts from many workgroups at once (one kernel that does
+// nothing else with the table): a slot is claimed by a device-scope
+// compare-and-swap of its page field straight to the page, and the key and
+// refcount follow with plain stores; nothing in the kernel reads a key, and
+// the next kernel sees them all.
 __device__ int32_t tab_insert_dev(const BmState& s, uint64_t h, int32_t page, int32_t ref,
                                   int64_t hint) {
   const int64_t mask = s.C - 1;
   auto claim = [&](int64_t i, int32_t expect) -> bool {
-    if (atomicCAS(ent_page(s, i), expect, kBusy) != expect) return false;
+    if (atomicCAS(ent_page(s, i), expect, page) != expect) return false;
     *ent_key(s, i) = h;
     *ent_ref(s, i) = ref;
     *rec_slot(s, page) = (int32_t)i;
-    __threadfence();
-    __hip_atomic_store(ent_page(s, i), page, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
   };
   if (hint >= 0) {
@@ -2032,70 +2040,94 @@ __global__ __launch_bounds__(kSpecThreads) void spec_hits_kernel(BmArgs a) {
   }
 }
 
-// 5. Per admit: the pages it pins (it is their first pinner).
-__global__ __launch_bounds__(kSpecThreads) void spec_pins_kernel(BmArgs a) {
-  __shared__ int32_t wave_cnt[kBmWaves];
+// 5. Per admit: the pages it pins (it is their first pinner). Then the LRU
+//    window the takes may reach: each entry's page, its key's slot, and
+//    whether it is a victim candidate (live at S, pinned by no admit of the
+//    step), live but pinned, or dead; and the candidates per chunk of
+//    kWinChunk entries.
+__global__ __launch_bounds__(kWinChunk) void spec_window_kernel(BmArgs a) {
+  constexpr int kWaves = kWinChunk / 64;
+  __shared__ int64_t part[kWaves];
+  __shared__ int32_t cnt[kWaves];
   const BmState& s = a.s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int32_t n = (int32_t)s.sp_ctr[kSpN];
   for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
     const int32_t k = s.sp_k[j];
-    bool pins = false;
-    if (i < k) {
+    int32_t c = 0;
+    for (int32_t i = tid; i < k; i += kWinChunk) {
       const int32_t x = s.sp_p0[(int64_t)j * kSpecPos + i].x;
-      pins = x >= 0 && (x & kPinBit) && s.sp_first[x & ~kPinBit] == j;
+      c += x >= 0 && (x & kPinBit) && s.sp_first[x & ~kPinBit] == j;
     }
-    const int32_t c = __popcll(__ballot(pins));
-    if (lane == 0) wave_cnt[wave] = c;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+    if (lane == 0) cnt[wave] = c;
     __syncthreads();
     if (tid == 0) {
       int32_t t = 0;
 #pragma unroll
-      for (int w = 0; w < kBmWaves; ++w) t += wave_cnt[w];
+      for (int w = 0; w < kWaves; ++w) t += cnt[w];
       s.sp_pinned[j] = t;
     }
-    __syncthreads();
+    __syncthreads();  // cnt is rewritten
   }
-}
-
-// 6. The LRU window the takes may reach: each entry's page, its key's slot,
-//    and whether it is a victim candidate (live at S, pinned by no admit of
-//    the step), live but pinned, or dead.
-__global__ __launch_bounds__(256) void spec_window_kernel(BmArgs a) {
-  __shared__ int64_t part[4];
-  const BmState& s = a.s;
-  const int32_t n = (int32_t)s.sp_ctr[kSpN];
   // the evictions all admits would need, summed by every workgroup
   int64_t mine = 0;
-  for (int32_t j = threadIdx.x; j < n; j += blockDim.x) mine += s.sp_take[j];
+  for (int32_t j = tid; j < n; j += kWinChunk) mine += s.sp_take[j];
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mine += __shfl_xor(mine, off);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mine;
+  if (lane == 0) part[wave] = mine;
   __syncthreads();
-  const int64_t takes = part[0] + part[1] + part[2] + part[3];
+  int64_t takes = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) takes += part[w];
   const int64_t evict = takes - s.sp_ctr[kSpF];
   const int64_t head = s.sp_ctr[kSpHead], span = s.ctr[kTail] - head;
   int64_t W = evict <= 0 ? 0 : evict + evict / 2 + 4096;
   W = W < span ? W : span;
   W = W < kSpecWin ? W : kSpecWin;
-  if (blockIdx.x == 0 && threadIdx.x == 0) s.sp_ctr[kSpWin] = W;
+  if (blockIdx.x == 0 && tid == 0) s.sp_ctr[kSpWin] = W;
   const int64_t qm = s.Q - 1;
-  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < W;
-       w += (int64_t)gridDim.x * blockDim.x) {
-    const uint64_t e = s.ring[(head + w) & qm];
-    const int32_t p = (int32_t)(uint32_t)e;
-    const RecHead h = rec_head(s, p);
-    const bool lv = live(h, (uint32_t)(e >> 32));
-    s.sp_wpg[w] = p;
-    s.sp_wslot[w] = h.slot;
-    s.sp_wflag[w] = !lv ? 0 : (s.sp_first[p] != INT_MAX ? 2 : 1);
+  for (int64_t c = blockIdx.x; c * kWinChunk < W; c += gridDim.x) {
+    const int64_t w = c * kWinChunk + tid;
+    uint8_t f = 0;
+    if (w < W) {
+      const uint64_t e = s.ring[(head + w) & qm];
+      const int32_t p = (int32_t)(uint32_t)e;
+      const RecHead h = rec_head(s, p);
+      const bool lv = live(h, (uint32_t)(e >> 32));
+      f = !lv ? 0 : (s.sp_first[p] != INT_MAX ? 2 : 1);
+      s.sp_wpg[w] = p;
+      s.sp_wslot[w] = h.slot;
+      s.sp_wflag[w] = f;
+    }
+    const int32_t cw = __popcll(__ballot(f == 1));
+    if (lane == 0) cnt[wave] = cw;
+    __syncthreads();
+    if (tid == 0) {
+      int32_t t = 0;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) t += cnt[v];
+      s.sp_wcnt[c] = t;
+    }
+    __syncthreads();  // cnt is rewritten
   }
 }
 
-// 7. One workgroup: the takes' prefix sums, the OOM checks, and the victims.
-//    Victim v (the (v+1)-th candidate in window order) is take F + v, which
-//    belongs to the admit whose prefix range holds it; a pinned live entry is
-//    reached by the admit owning the take index it is passed at.
+// The admit owning take index t (t < T[n]): the last j with T[j] <= t, T the
+// exclusive prefix sums of the admits' takes.
+__device__ __forceinline__ int32_t spec_owner(const int64_t* T, int32_t n, int64_t t) {
+  int32_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int32_t mid = (lo + hi + 1) >> 1;
+    if (T[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// 6. One workgroup: the takes' prefix sums, the OOM checks, and the
+//    candidates before each window chunk (the window too short for the
+//    evictions wanted makes the admit that lacks one a violation).
 __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   constexpr int kOpt = kSpecOps / kSpecThreads;
   __shared__ int64_t T[kSpecOps + 1];
@@ -2158,21 +2190,10 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   const int64_t total = T[n];
   const int64_t E = total - F > 0 ? total - F : 0;  // evictions wanted
   const int64_t W = s.sp_ctr[kSpWin];
-  // the admit owning take index t (t < total)
-  auto owner = [&](int64_t t) -> int32_t {
-    int lo = 0, hi = n - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (T[mid] <= t) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-  };
-  // candidates before each window entry: per thread a contiguous slice
-  const int64_t per = (W + kSpecThreads - 1) / kSpecThreads;
-  const int64_t w0 = tid * per, w1 = w0 + per < W ? w0 + per : W;
-  int64_t cnt = 0;
-  for (int64_t w = w0; w < w1; ++w) cnt += s.sp_wflag[w] == 1;
-  int64_t inc = cnt;
+  const int32_t nch = (int32_t)((W + kWinChunk - 1) / kWinChunk);  // <= kWinChunks
+  static_assert(kWinChunks <= kSpecThreads, "a chunk per thread");
+  const int64_t cc = tid < nch ? s.sp_wcnt[tid] : 0;
+  int64_t inc = cc;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int64_t o = __shfl_up(inc, d);
@@ -2181,28 +2202,54 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   __syncthreads();  // wave_tot is reused
   if (lane == 63) wave_tot[0][wave] = inc;
   __syncthreads();
-  int64_t before = inc - cnt, ncand = 0;
+  int64_t before = inc - cc, ncand = 0;
 #pragma unroll
   for (int w = 0; w < kBmWaves; ++w) {
     before += w < wave ? wave_tot[0][w] : 0;
     ncand += wave_tot[0][w];
   }
-  for (int64_t w = w0; w < w1; ++w) {
-    const uint8_t f = s.sp_wflag[w];
-    if (f == 1) {
-      if (before < E) {
-        const int32_t p = s.sp_wpg[w];
-        s.sp_victim[before] = p;
-        s.sp_vpos[before] = (int32_t)w;
-        s.sp_evt[p] = owner(F + before);
-      }
-      ++before;
-    } else if (f == 2 && before < E) {  // passed while take F + before is wanted
-      const int32_t u = owner(F + before);
+  if (tid < nch) s.sp_wpre[tid] = before;
+  if (tid == 0 && ncand < E) atomicMin(spec_bad(s), spec_owner(T, n, F + ncand));
+}
+
+// 7. Per window chunk (many CUs): victim v, the (v+1)-th candidate in window
+//    order, is take F + v, which belongs to the admit whose prefix range holds
+//    it; a live entry pinned in the step is passed by the admit owning the
+//    take index it is passed at, a violation if that admit comes before its
+//    first pinner (sequentially it would have evicted it).
+__global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
+  constexpr int kWaves = kWinChunk / 64;
+  __shared__ int64_t T[kSpecOps + 1];
+  __shared__ int32_t cnt[kWaves];
+  const BmState& s = a.s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t n = (int32_t)s.sp_ctr[kSpN];
+  const int64_t W = s.sp_ctr[kSpWin];
+  if (n == 0 || (int64_t)blockIdx.x * kWinChunk >= W) return;  // no chunk here
+  for (int32_t j = tid; j <= n; j += kWinChunk) T[j] = s.sp_T[j];
+  __syncthreads();
+  const int64_t F = s.sp_ctr[kSpF];
+  const int64_t E = T[n] - F > 0 ? T[n] - F : 0;
+  for (int64_t c = blockIdx.x; c * kWinChunk < W; c += gridDim.x) {
+    const int64_t w = c * kWinChunk + tid;
+    const uint8_t f = w < W ? s.sp_wflag[w] : 0;
+    const uint64_t bal = __ballot(f == 1);
+    if (lane == 0) cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int64_t before = s.sp_wpre[c] + __popcll(bal & ((1ull << lane) - 1ull));
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) before += v < wave ? cnt[v] : 0;
+    if (f == 1 && before < E) {
+      const int32_t p = s.sp_wpg[w];
+      s.sp_victim[before] = p;
+      s.sp_vpos[before] = (int32_t)w;
+      s.sp_evt[p] = spec_owner(T, n, F + before);
+    } else if (f == 2 && before < E) {
+      const int32_t u = spec_owner(T, n, F + before);
       if (u < s.sp_first[s.sp_wpg[w]]) atomicMin(spec_bad(s), u);
     }
+    __syncthreads();  // cnt is rewritten
   }
-  if (tid == 0 && ncand < E) atomicMin(spec_bad(s), owner(F + ncand));  // window too short
 }
 
 // 8. Per admit before the first violation so far: a page it finds at S that
@@ -2593,9 +2640,9 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   hipLaunchKernelGGL(spec_setup_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_probe_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
   hipLaunchKernelGGL(spec_hits_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
-  hipLaunchKernelGGL(spec_pins_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
-  hipLaunchKernelGGL(spec_window_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(spec_window_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
   hipLaunchKernelGGL(spec_scan_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
+  hipLaunchKernelGGL(spec_victims_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
   hipLaunchKernelGGL(spec_verify_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_commit_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_finish_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
