@@ -8,10 +8,13 @@ on the device: a request's full 16-token pages are keyed by the SHA-256 prefix
 hash of ``PrefixCache._hash_tokens`` (``prefix_hash.page_hashes``), the
 longest run of leading cached pages is shared (refcounted), the rest come from
 the free stack or by evicting the least recently released cached page, and a
-forked request's partial last page is copied on write. Requests are resolved
-in op order by one workgroup (admits eight at a time, against loads shared by
-the eight), so eviction order is deterministic and equal to the sequential
-OrderedDict model.
+forked request's partial last page is copied on write. A step's admits are
+resolved together on many CUs against the state at their start, every
+prediction checked; from the first admit that could differ from the
+sequential order, one workgroup resolves the rest in op order (admits eight
+at a time). Eviction order is deterministic and equal to the sequential
+OrderedDict model. Page hashes must be prefix keys (a hash at position i
+equal in two requests only if their hashes at every earlier position are).
 
 Typical step for a batch of requests (all on the stream, no host sync)::
 
