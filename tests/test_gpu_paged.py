@@ -199,6 +199,35 @@ def test_device_errors_are_reported_not_faulted():
         cache.check_errors()
 
 
+@pytest.mark.parametrize("layers,dtype,heads", [(3, torch.float8_e4m3fn, 1), (5, torch.float8_e4m3fn, 1),
+                                                (3, torch.bfloat16, 2), (7, torch.bfloat16, 1)])
+def test_copy_pages_page_sizes(layers, dtype, heads):
+    # 4 KiB (fp8), 8 KiB and 16 KiB pages over odd plane counts, skipped pairs,
+    # and the fp8 scale planes (64-byte pages)
+    case(f"copy_pages: {layers} layers, {dtype}, {heads} KV heads")
+    cache = PagedKVCache(40, num_layers=layers, kv_heads=heads, dtype=dtype, device=DEV,
+                         verbose=False)
+    g = torch.Generator().manual_seed(layers)
+    raw = torch.randint(0, 256, (cache.cache.numel() * cache.cache.element_size(),),
+                        generator=g, dtype=torch.uint8)
+    cache.cache.view(torch.uint8).view(-1).copy_(raw.to(DEV))
+    if cache.scales is not None:
+        cache.scales.copy_(torch.rand(cache.scales.shape, generator=g).to(DEV))
+    want = cache.cache.view(torch.uint8).cpu().clone()
+    want_s = cache.scales.cpu().clone() if cache.scales is not None else None
+    src, dst = [1, 5, 9, 30, -1, 12], [2, 6, 0, 31, 7, -1]
+    cache.copy_pages(src, dst)
+    for s_, d_ in zip(src, dst):
+        if s_ >= 0 and d_ >= 0:
+            want[:, :, d_] = want[:, :, s_]
+            if want_s is not None:
+                want_s[:, :, d_] = want_s[:, :, s_]
+    assert torch.equal(cache.cache.view(torch.uint8).cpu(), want)
+    if want_s is not None:
+        assert torch.equal(cache.scales.cpu(), want_s)
+    cache.check_errors()
+
+
 def test_copy_pages_and_kvcache():
     case("copy_pages (copy-on-write) and contiguous KVCache append/get")
     cache = PagedKVCache(16, num_layers=4, dtype=torch.bfloat16, device=DEV, verbose=False)
