@@ -275,6 +275,38 @@ def test_prefix_keys_over_a_small_alphabet(seed, P, batch, alphabet, skew, ops):
     assert len(model.evicted) > 200 and snap["spec_done"] > 0 and snap["spec_left"] > 0
 
 
+def test_eviction_wave_longer_than_the_lru_window():
+    # step 1 admits 512 requests of 512 fresh pages (262,144 pages cached once
+    # step 2 releases them); step 3 admits 400 more, whose 204,800 takes evict
+    # ~167k pages: more than the speculation's 131,072-entry LRU window, so
+    # the admit that runs past it and every later one go to the sequential
+    # kernels
+    case("block manager: 300,000-page pool, an eviction wave of ~167k pages in one step")
+    n, m = 912, 512
+    rng = np.random.default_rng(44)
+    keys = [rng.integers(1, 1 << 63, m, dtype=np.int64) for _ in range(n)]
+    lens = [16 * m] * n
+    steps = [list(range(512)), [-(r + 1) for r in range(512)], list(range(512, n))]
+    status, model, snap = run(P=300_000, n=n, batch=0, seed=44, n_templates=0, template_len=0,
+                              suffix=None, width=m, keys=(lens, keys),
+                              ops_fn=lambda n_, b_: steps)
+    assert len(model.evicted) > 131_072
+    assert snap["spec_done"] >= 512 and snap["spec_left"] > 0
+
+
+def test_request_admitted_twice_in_one_step():
+    # the speculation stops before a request's second admit in a step; the
+    # sequential kernels admit it again (the model overwrites its tables)
+    case("block manager: a request admitted twice in one step")
+    lens, keys = synthetic_keys(6, 45, 4, 6, 0.5)
+    steps = [[0, 1, 0, 2], [-1, -2, -3, 3, 4], [-4, -5, 5, 5]]
+    status, model, snap = run(P=64, n=6, batch=0, seed=45, n_templates=0, template_len=0,
+                              suffix=None, width=6, keys=(lens, keys),
+                              ops_fn=lambda n_, b_: steps)
+    admits = sum(op >= 0 for st in steps for op in st)
+    assert snap["spec_done"] < admits  # the repeats (and what follows) went sequential
+
+
 def test_duplicate_release_is_flagged_once():
     case("block manager: a request released twice in one step")
     reqs = bench.prefix_requests(3, seed=3, n_templates=1, template_len=64, suffix=(5, 20))
