@@ -111,7 +111,7 @@ struct BmLayout {
   int64_t cmp_ring, cmp_bits, cmp_pre;
   // speculation scratch
   int64_t sp_ctr, sp_req, sp_ntok, sp_m, sp_h0, sp_k, sp_take, sp_pinned, sp_T, sp_p0, sp_fo,
-      sp_first, sp_evt, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt, sp_wpre;
+      sp_first, sp_evt, sp_late, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt, sp_wpre;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -163,6 +163,7 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.sp_fo = take(kFoCap * 16);
   l.sp_first = take((int64_t)P * 4);
   l.sp_evt = take((int64_t)P * 4);
+  l.sp_late = take((int64_t)P * 4);
   l.sp_wpg = take(kSpecWin * 4);
   l.sp_wslot = take(kSpecWin * 4);
   l.sp_wflag = take(kSpecWin);
@@ -206,6 +207,7 @@ struct BmState {
   uint8_t* sp_fo;      // first-occurrence table: {u64 key, i32 first occurrence, i32 -}
   int32_t* sp_first;   // [P] first admit pinning the page (INT_MAX none)
   int32_t* sp_evt;     // [P] admit evicting the page (INT_MAX none)
+  int32_t* sp_late;    // [P] first admit holding the page (found at S) past its first miss
   int32_t* sp_wpg;     // [w] LRU window: page
   int32_t* sp_wslot;   //     its key's table slot
   uint8_t* sp_wflag;   //     0 dead, 1 a victim candidate, 2 live but pinned in the step
@@ -249,6 +251,7 @@ inline BmState bm_state(void* base, int32_t P) {
   s.sp_fo = b + l.sp_fo;
   s.sp_first = reinterpret_cast<int32_t*>(b + l.sp_first);
   s.sp_evt = reinterpret_cast<int32_t*>(b + l.sp_evt);
+  s.sp_late = reinterpret_cast<int32_t*>(b + l.sp_late);
   s.sp_wpg = reinterpret_cast<int32_t*>(b + l.sp_wpg);
   s.sp_wslot = reinterpret_cast<int32_t*>(b + l.sp_wslot);
   s.sp_wflag = b + l.sp_wflag;
@@ -1864,25 +1867,20 @@ __device__ int32_t tab_insert_dev(const BmState& s, uint64_t h, int32_t page, in
   return -1;
 }
 
-// 1. Clears the first-occurrence table and the per-page first pins and
-//    eviction times; when tombstones fill more than a quarter of the table,
-//    also every table entry (the setup kernel inserts the cached pages again).
-__device__ __forceinline__ bool spec_rebuilds(const BmState& s) { return s.ctr[kTombs] > s.C / 4; }
-
-__global__ __launch_bounds__(256) void spec_clear_kernel(BmState s) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (spec_rebuilds(s))
-    for (int64_t i = g; i < s.C; i += stride) *ent_page(s, i) = kEmpty;
+// The first-occurrence table and the per-page first pinner, evicting admit
+// and late holder are all-empty between steps: cleared once at init and by
+// the finish kernel of every step that used them, on many CUs.
+__device__ __forceinline__ void spec_clear_scratch(const BmState& s, int64_t g, int64_t stride) {
   for (int64_t i = g; i < kFoCap; i += stride)
     *reinterpret_cast<u32x4*>(s.sp_fo + i * 16) = u32x4{0u, 0u, (uint32_t)INT_MAX, 0u};
   for (int64_t p = g; p < s.P; p += stride) {
     s.sp_first[p] = INT_MAX;
     s.sp_evt[p] = INT_MAX;
+    s.sp_late[p] = INT_MAX;
   }
 }
 
-// 2. The admits to speculate: the leading valid admits after the release run
+// 1. The admits to speculate: the leading valid admits after the release run
 //    (at most kSpecOps, of at most kSpecPos pages), cut before a request that
 //    repeats; their metadata and the step's starting counters.
 __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
@@ -1892,11 +1890,10 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
   __shared__ uint32_t key[2 * kSpecOps], firsti[2 * kSpecOps];
   const BmState& s = a.s;
   const int tid = threadIdx.x;
-  if (spec_rebuilds(s)) {  // the entries were cleared: insert the cached pages
-    for (int32_t p = tid; p < s.P; p += kSpecThreads)
-      if (*rec_flag(s, p) & 1) tab_insert(s, *rec_hash(s, p), p, *rec_ref(s, p));
-    __syncthreads();
-    if (tid == 0) s.ctr[kTombs] = 0;  // every workgroup read it in the clear kernel
+  if (s.ctr[kTombs] > s.C / 4) {  // tombstones past a quarter of the table: rebuild it
+    Ctrs c;
+    tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
+    if (tid == 0) s.ctr[kTombs] = 0;
   }
   const int32_t start = (int32_t)s.run_ctr[kRunOps];
   const int32_t left = a.num_ops - start;
@@ -1975,7 +1972,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
   }
 }
 
-// 3. Every speculated admit's page hashes looked up at S (a workgroup per
+// 2. Every speculated admit's page hashes looked up at S (a workgroup per
 //    admit); keys absent at S enter the first-occurrence table.
 __global__ __launch_bounds__(256) void spec_probe_kernel(BmArgs a) {
   const BmState& s = a.s;
@@ -1997,7 +1994,7 @@ __global__ __launch_bounds__(256) void spec_probe_kernel(BmArgs a) {
   }
 }
 
-// 4. Per admit: its hits (a key absent at S is present if an earlier admit
+// 3. Per admit: its hits (a key absent at S is present if an earlier admit
 //    holds it: the position records that occurrence), its takes, and the
 //    first admit pinning each page it hits at refcount 0. An admit holding a
 //    key absent at S twice is left to the sequential path.
@@ -2036,11 +2033,15 @@ __global__ __launch_bounds__(kSpecThreads) void spec_hits_kernel(BmArgs a) {
       s.sp_take[j] = (nt + 15) / 16 - k + ((nt & 15) ? 1 : 0);
     }
     if (i < k && v.x >= 0 && (v.x & kPinBit)) atomicMin(&s.sp_first[v.x & ~kPinBit], j);
+    // a page found at S past the first miss: an eviction of it by this or an
+    // earlier admit would change what a later admit registers (with prefix
+    // keys there is none)
+    if (i >= k && i < m && v.x >= 0) atomicMin(&s.sp_late[v.x & ~kPinBit], j);
     __syncthreads();  // wave_miss is rewritten for the next admit
   }
 }
 
-// 5. Per admit: the pages it pins (it is their first pinner). Then the LRU
+// 4. Per admit: the pages it pins (it is their first pinner). Then the LRU
 //    window the takes may reach: each entry's page, its key's slot, and
 //    whether it is a victim candidate (live at S, pinned by no admit of the
 //    step), live but pinned, or dead; and the candidates per chunk of
@@ -2125,7 +2126,7 @@ __device__ __forceinline__ int32_t spec_owner(const int64_t* T, int32_t n, int64
   return lo;
 }
 
-// 6. One workgroup: the takes' prefix sums, the OOM checks, and the
+// 5. One workgroup: the takes' prefix sums, the OOM checks, and the
 //    candidates before each window chunk (the window too short for the
 //    evictions wanted makes the admit that lacks one a violation).
 __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
@@ -2212,11 +2213,13 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   if (tid == 0 && ncand < E) atomicMin(spec_bad(s), spec_owner(T, n, F + ncand));
 }
 
-// 7. Per window chunk (many CUs): victim v, the (v+1)-th candidate in window
+// 6. Per window chunk (many CUs): victim v, the (v+1)-th candidate in window
 //    order, is take F + v, which belongs to the admit whose prefix range holds
 //    it; a live entry pinned in the step is passed by the admit owning the
 //    take index it is passed at, a violation if that admit comes before its
-//    first pinner (sequentially it would have evicted it).
+//    first pinner (sequentially it would have evicted it). A hit is never a
+//    victim (pinned, or not in the LRU at all), so only pages held past a
+//    first miss can be read after their eviction.
 __global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
   constexpr int kWaves = kWinChunk / 64;
   __shared__ int64_t T[kSpecOps + 1];
@@ -2241,9 +2244,13 @@ __global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
     for (int v = 0; v < kWaves; ++v) before += v < wave ? cnt[v] : 0;
     if (f == 1 && before < E) {
       const int32_t p = s.sp_wpg[w];
+      const int32_t u = spec_owner(T, n, F + before);
       s.sp_victim[before] = p;
       s.sp_vpos[before] = (int32_t)w;
-      s.sp_evt[p] = spec_owner(T, n, F + before);
+      // a holder of p past its first miss at or after u finds it evicted;
+      // when the first holder comes before u, u itself is the (safe) cut
+      const int32_t lt = s.sp_late[p];
+      if (lt != INT_MAX) atomicMin(spec_bad(s), lt >= u ? lt : u);
     } else if (f == 2 && before < E) {
       const int32_t u = spec_owner(T, n, F + before);
       if (u < s.sp_first[s.sp_wpg[w]]) atomicMin(spec_bad(s), u);
@@ -2252,23 +2259,7 @@ __global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
   }
 }
 
-// 8. Per admit before the first violation so far: a page it finds at S that
-//    an earlier admit evicts, or that it evicts itself past its hits, makes it
-//    (and everything after) sequential.
-__global__ __launch_bounds__(kSpecThreads) void spec_verify_kernel(BmArgs a) {
-  const BmState& s = a.s;
-  const int32_t bad0 = *spec_bad(s);
-  for (int32_t j = blockIdx.x; j < bad0; j += gridDim.x) {
-    const int32_t i = threadIdx.x;
-    if (i >= s.sp_m[j]) continue;
-    const int32_t x = s.sp_p0[(int64_t)j * kSpecPos + i].x;
-    if (x < 0) continue;
-    const int32_t et = s.sp_evt[x & ~kPinBit];
-    if (et < j || (et == j && i >= s.sp_k[j])) atomicMin(spec_bad(s), j);
-  }
-}
-
-// 9. The admits before the first violation, a workgroup per admit: tables,
+// 7. The admits before the first violation, a workgroup per admit: tables,
 //    refcounts, cached flags and hashes, registrations (insertion by
 //    compare-and-swap at the slot found at S), results.
 __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
@@ -2330,8 +2321,8 @@ __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
                         (unsigned long long)reused);
 }
 
-// 10. The evictions' tombstones and log, the cached pages' refcounts copied
-//     into their table entries, and the counters.
+// 8. The evictions' tombstones and log, the cached pages' refcounts copied
+//    into their table entries, the counters, and the scratch cleared.
 __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int32_t bad = *spec_bad(s);
@@ -2352,6 +2343,9 @@ __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
     const RecHead h = rec_head(s, p);
     if (h.flag & 1) *ent_ref(s, h.slot) = h.ref;
   }
+  if (s.sp_ctr[kSpN] > 0)  // the next step finds its scratch empty
+    spec_clear_scratch(s, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                       (int64_t)gridDim.x * blockDim.x);
   if (blockIdx.x == 0 && threadIdx.x < 64) {  // one wave: the pins of the committed admits
     int64_t pins = 0;
     for (int32_t j = threadIdx.x; j < bad; j += 64) pins += s.sp_pinned[j];
@@ -2558,6 +2552,7 @@ __global__ __launch_bounds__(256) void bm_init_kernel(BmState s, const int32_t* 
   }
   for (int64_t q = g; q < s.Q; q += stride) s.ring[q] = 0;
   for (int64_t p = g; p < s.P; p += stride) s.last[p] = -1;
+  spec_clear_scratch(s, g, stride);
   if (g < kNumCtr) s.ctr[g] = g == kFreeTop ? s.P : (g == kNextStamp ? 1 : 0);
   if (g < kRunNumCtr) s.run_ctr[g] = 0;
 }
@@ -2636,14 +2631,12 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
   hipLaunchKernelGGL(run_scan_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(run_push_kernel, dim3(kRunGrid * kRunUnroll), dim3(kRunThreads), 0, st, a);
-  hipLaunchKernelGGL(spec_clear_kernel, dim3(kSpecGrid), dim3(256), 0, st, a.s);
   hipLaunchKernelGGL(spec_setup_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_probe_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
   hipLaunchKernelGGL(spec_hits_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_window_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
   hipLaunchKernelGGL(spec_scan_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_victims_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
-  hipLaunchKernelGGL(spec_verify_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_commit_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_finish_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
