@@ -412,14 +412,15 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * last-occurrence slots (P int32, -1 between steps), the scratch of the
  * many-workgroup passes (4.6 MiB for a release run of up to 2^20 page
  * references: counters, per-op offsets, page ids, bit arrays; plus 8.25 x Q
- * bytes for compacting the ring; plus 14.2 MiB + 12 x P bytes for resolving up
- * to 1024 admits at once: per-admit metadata, per-position probe results, a
- * first-occurrence table of absent hashes, per-page first pinner and
- * eviction, the LRU window and its victims), and the total size.
+ * bytes for compacting the ring; plus 26.2 MiB + 12 x P bytes for resolving up
+ * to 1024 admits of up to 2048 pages at once: per-admit metadata,
+ * per-position probe results, a first-occurrence table of absent hashes,
+ * per-page first pinner and eviction, the LRU window and its victims), and
+ * the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
  * (a leading run of up to 1024 releases is retired by many-workgroup passes;
- * the admits after it, up to 1024 of at most 512 pages, are resolved
+ * the admits after it, up to 1024 of at most 2048 pages, are resolved
  * together by many-workgroup passes against the state before them, every
  * prediction checked, and the admits before the first one that may differ
  * from the sequential result are committed; one workgroup takes the admits

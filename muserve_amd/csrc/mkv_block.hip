@@ -86,7 +86,7 @@ enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kR
 // a first-occurrence table of absent keys, and an LRU window of kSpecWin
 // entries.
 constexpr int kSpecOps = 1024;
-constexpr int kSpecPos = 512;
+constexpr int kSpecPos = 2048;
 constexpr int kFoBits = 19;
 constexpr int64_t kFoCap = 1ll << kFoBits;
 constexpr int kFoMaxProbe = 512;  // a longer probe counts as a violation
@@ -1787,7 +1787,8 @@ __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kSpecThreads = 512;
 constexpr int kSpecGrid = 1024;
-static_assert(kSpecPos == kSpecThreads, "a position per thread");
+constexpr int kPosPer = kSpecPos / kSpecThreads;  // positions per thread
+static_assert(kPosPer * kSpecThreads == kSpecPos, "positions split evenly over the threads");
 
 __device__ __forceinline__ uint64_t* fo_key(const BmState& s, int64_t i) {
   return reinterpret_cast<uint64_t*>(s.sp_fo + i * 16);
@@ -1999,44 +2000,62 @@ __global__ __launch_bounds__(256) void spec_probe_kernel(BmArgs a) {
 //    first admit pinning each page it hits at refcount 0. An admit holding a
 //    key absent at S twice is left to the sequential path.
 __global__ __launch_bounds__(kSpecThreads) void spec_hits_kernel(BmArgs a) {
-  __shared__ int32_t wave_miss[kBmWaves];
+  __shared__ int32_t wave_miss[kPosPer][kBmWaves];
   const BmState& s = a.s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i = tid;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int32_t n = (int32_t)s.sp_ctr[kSpN];
   for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
     const int32_t m = s.sp_m[j], nt = s.sp_ntok[j];
-    int2 v = int2{-1, -1};
-    bool present = false;
-    if (i < m) {
-      v = s.sp_p0[(int64_t)j * kSpecPos + i];
-      if (v.x >= 0) {
-        present = true;
-      } else {
-        const int32_t f = fo_find(s, a.hashes[s.sp_h0[j] + i]);
-        if (f / kSpecPos < j) {
+    const int nq = (m + kSpecThreads - 1) / kSpecThreads;  // position blocks in use (uniform)
+    // position i = q * kSpecThreads + tid
+    int2 v[kPosPer];
+#pragma unroll
+    for (int q = 0; q < kPosPer; ++q) {
+      const int32_t i = q * kSpecThreads + tid;
+      v[q] = int2{-1, -1};
+      if (q >= nq) continue;
+      bool present = false;
+      if (i < m) {
+        v[q] = s.sp_p0[(int64_t)j * kSpecPos + i];
+        if (v[q].x >= 0) {
           present = true;
-          v.x = -(f + 2);
-          s.sp_p0[(int64_t)j * kSpecPos + i].x = v.x;
-        } else if (f != j * kSpecPos + i) {
-          atomicMin(spec_bad(s), j);
+        } else {
+          const int32_t f = fo_find(s, a.hashes[s.sp_h0[j] + i]);
+          if (f / kSpecPos < j) {
+            present = true;
+            v[q].x = -(f + 2);
+            s.sp_p0[(int64_t)j * kSpecPos + i].x = v[q].x;
+          } else if (f != j * kSpecPos + i) {
+            atomicMin(spec_bad(s), j);
+          }
         }
       }
+      const uint64_t mb = __ballot(i < m && !present);
+      if (lane == 0)
+        wave_miss[q][wave] =
+            mb ? q * kSpecThreads + wave * 64 + (int32_t)__builtin_ctzll(mb) : INT_MAX;
     }
-    const uint64_t mb = __ballot(i < m && !present);
-    if (lane == 0) wave_miss[wave] = mb ? wave * 64 + (int32_t)__builtin_ctzll(mb) : INT_MAX;
     __syncthreads();
     int32_t k = m;
 #pragma unroll
-    for (int w = 0; w < kBmWaves; ++w) k = wave_miss[w] < k ? wave_miss[w] : k;
+    for (int q = 0; q < kPosPer; ++q)
+#pragma unroll
+      for (int w = 0; w < kBmWaves; ++w)
+        k = q < nq && wave_miss[q][w] < k ? wave_miss[q][w] : k;
     if (tid == 0) {
       s.sp_k[j] = k;
       s.sp_take[j] = (nt + 15) / 16 - k + ((nt & 15) ? 1 : 0);
     }
-    if (i < k && v.x >= 0 && (v.x & kPinBit)) atomicMin(&s.sp_first[v.x & ~kPinBit], j);
-    // a page found at S past the first miss: an eviction of it by this or an
-    // earlier admit would change what a later admit registers (with prefix
-    // keys there is none)
-    if (i >= k && i < m && v.x >= 0) atomicMin(&s.sp_late[v.x & ~kPinBit], j);
+#pragma unroll
+    for (int q = 0; q < kPosPer; ++q) {
+      const int32_t i = q * kSpecThreads + tid;
+      if (i < k && v[q].x >= 0 && (v[q].x & kPinBit))
+        atomicMin(&s.sp_first[v[q].x & ~kPinBit], j);
+      // a page found at S past the first miss: an eviction of it by this or
+      // an earlier admit would change what a later admit registers (with
+      // prefix keys there is none)
+      if (i >= k && i < m && v[q].x >= 0) atomicMin(&s.sp_late[v[q].x & ~kPinBit], j);
+    }
     __syncthreads();  // wave_miss is rewritten for the next admit
   }
 }
@@ -2272,8 +2291,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
     const int32_t np = (nt + 15) / 16;
     const bool cow = (nt & 15) != 0;
     const int64_t T = s.sp_T[j];
-    const int32_t i = threadIdx.x;
-    if (i < np) {
+    for (int32_t i = threadIdx.x; i < np; i += kSpecThreads) {
       const int2 v = i < m ? s.sp_p0[(int64_t)j * kSpecPos + i] : int2{-1, -1};
       int32_t page;
       if (i < k) {
@@ -2303,7 +2321,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
           a.child_last[r] = page;
       }
     }
-    if (i == 0) {
+    if (threadIdx.x == 0) {
       a.hits[r] = k;
       a.status[r] = kStOk;
       if (cow) {
@@ -2337,11 +2355,12 @@ __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
     if (log0 + v < a.evict_cap) a.evict_log[log0 + v] = s.sp_victim[v];
   }
   for (int32_t j = blockIdx.x; j < bad; j += gridDim.x) {
-    const int32_t i = threadIdx.x;
-    if (i >= (s.sp_ntok[j] + 15) / 16) continue;
-    const int32_t p = a.tables[(int64_t)s.sp_req[j] * a.tstride + i];
-    const RecHead h = rec_head(s, p);
-    if (h.flag & 1) *ent_ref(s, h.slot) = h.ref;
+    const int32_t np = (s.sp_ntok[j] + 15) / 16;
+    for (int32_t i = threadIdx.x; i < np; i += kSpecThreads) {
+      const int32_t p = a.tables[(int64_t)s.sp_req[j] * a.tstride + i];
+      const RecHead h = rec_head(s, p);
+      if (h.flag & 1) *ent_ref(s, h.slot) = h.ref;
+    }
   }
   if (s.sp_ctr[kSpN] > 0)  // the next step finds its scratch empty
     spec_clear_scratch(s, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,

@@ -275,6 +275,17 @@ def test_prefix_keys_over_a_small_alphabet(seed, P, batch, alphabet, skew, ops):
     assert len(model.evicted) > 200 and snap["spec_done"] > 0 and snap["spec_left"] > 0
 
 
+def test_requests_of_up_to_2048_pages_resolved_together():
+    # prompts of 16,000-token templates plus up to 16,000 more tokens (1,000 to
+    # ~1,970 pages): every admit fits the speculation's 2048 positions, and the
+    # pool is small enough for thousands of evictions
+    case("block manager: 24,000-page pool, 60 requests of 1000-1971 pages, batches of 12")
+    status, model, snap = run(P=24000, n=60, batch=12, seed=46, n_templates=3, template_len=16000,
+                              suffix=(1, 16000), width=1971)
+    assert len(model.evicted) > 5000
+    assert snap["spec_done"] > 30
+
+
 def test_eviction_wave_longer_than_the_lru_window():
     # step 1 admits 512 requests of 512 fresh pages (262,144 pages cached once
     # step 2 releases them); step 3 admits 400 more, whose 204,800 takes evict
