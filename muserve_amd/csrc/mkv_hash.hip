@@ -140,9 +140,11 @@ __global__ __launch_bounds__(kHashThreads) void block_hash_kernel(const uint8_t*
         if (finisher && k == 0 && i >= 1 && i <= pages)
           out[o0 + i - 1] = ((uint64_t)st.h[0] << 32) | st.h[1];
         if (k == bpp - 1) {  // end of page i: the odd lane takes the state
+          // adjacent lanes swap through DPP quad_perm [1,0,3,2] (lane ^ 1),
+          // a VALU operand modifier rather than an LDS permute round trip
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const uint32_t v = __shfl_xor(st.h[j], 1);
+            const uint32_t v = (uint32_t)__builtin_amdgcn_mov_dpp((int)st.h[j], 0xb1, 0xf, 0xf, false);
             if (finisher) st.h[j] = v;
           }
         }
