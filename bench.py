@@ -861,8 +861,10 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
         # launch on a second stream; the block manager then processes the
         # batches in order, each step waiting for the hashes, each followed by
         # its batch's copy-on-write copies. (Copies on a third stream behind
-        # each step, overlapping the next step, made the trace slower: the
-        # copy kernel holds every CU while the step's small kernels wait.)
+        # each step, overlapping the next step, did not pay: at full width
+        # the copy holds every CU while the step's small kernels wait, and on
+        # 128-256 workgroups it is hidden but slows the step's latency-bound
+        # kernels by about as much as it saves.)
         with torch.cuda.stream(hash_stream):
             sp = stamps.span(hash_stream) if rec is not None else None
             page_hashes_range(tokens, tok_off, page_off, 0, n_req, hashes, herr)
