@@ -275,6 +275,25 @@ def test_prefix_keys_over_a_small_alphabet(seed, P, batch, alphabet, skew, ops):
     assert len(model.evicted) > 200 and snap["spec_done"] > 0 and snap["spec_left"] > 0
 
 
+@pytest.mark.parametrize("seed,P,batch,alphabet,skew,ops,n", [
+    (48, 9000, 1500, 32, 0.2, "batch", 3000),        # 1500 admits a step: past the 1024 speculated
+    (49, 300, 40, 16, 0.3, "interleaved", 480),      # releases between the admits
+    (50, 4000, 600, 64, 0.1, "random", 1800),        # release runs, ~320 OOMs, ~2400 evictions
+    (51, 700, 200, 8, 0.4, "batch", 1200),           # ~400 OOMs in a tight pool
+])
+def test_speculation_edges_against_the_model(seed, P, batch, alphabet, skew, ops, n):
+    case(f"block manager: prefix keys, {P}-page pool, {n} requests, batches of {batch}, "
+         f"{ops} op order, seed {seed}")
+    fn = {"batch": bench.prefix_ops, "interleaved": interleaved_ops,
+          "random": random_ops(seed)}[ops]
+    status, model, snap = run(P=P, n=n, batch=batch, seed=seed, n_templates=0, template_len=0,
+                              suffix=None, width=12,
+                              keys=synthetic_keys(n, seed, alphabet, 12, skew), ops_fn=fn)
+    assert snap["spec_done"] > 0
+    if batch > 1024:  # the admits past the first 1024 of a step are the group kernel's
+        assert snap["spec_done"] + snap["spec_left"] < n
+
+
 def test_requests_of_up_to_2048_pages_resolved_together():
     # prompts of 16,000-token templates plus up to 16,000 more tokens (1,000 to
     # ~1,970 pages): every admit fits the speculation's 2048 positions, and the
