@@ -573,24 +573,33 @@ inline int64_t attn_chunks(int32_t max_seq_len) {
   return ((int64_t)max_seq_len + kChunk - 1) / kChunk;
 }
 
-// Workgroups of the chunk kernel: a few per CU drain the work list.
+// Workgroups of the chunk kernel: as many as are resident at once (CUs x the
+// kernel's occupancy, 2 per CU for four query heads), so that every
+// workgroup's static first item starts at once and the counter hands out the
+// rest in list order. A grid of 4 per CU left the second half's first items,
+// full chunks, to the end of the launch: 304.7 against 295.4 us per bf16
+// launch at batch 256, 102.4 against 100.4 us in the serving workload.
+template <int G, bool FP8, bool F16>
 int attn_grid() {
-  static int cus[64] = {};
+  static int grid[64] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
-  if (cus[dev] == 0) {
-    int n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (grid[dev] == 0) {
+    int n = 0, per = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cus[dev] = n;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_chunk_kernel<G, FP8, F16>,
+                                                     kAttnThreads, 0) != hipSuccess || per <= 0)
+      per = 2;
+    grid[dev] = n * per;
   }
-  return cus[dev] * 4;
+  return grid[dev];
 }
 
 template <int G, bool FP8, bool F16>
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16>), dim3((unsigned)attn_grid()),
+  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16>), dim3((unsigned)attn_grid<G, FP8, F16>()),
                      dim3(kAttnThreads), 0, st, a);
   // the merge kernel also resets the work counter: one workgroup when no
   // sequence spans two chunks
