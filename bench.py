@@ -17,8 +17,9 @@ on 3 whole decode steps (15 layers of append + padded gather) on the host's
 cores, after which the GPU runs the same 3 steps and the pools are compared.
 After the headline's timed region, the default run also measures the other
 configurations (``secondary``): fp8 chunked prefill (append and dequant-gather
-separately), the GDN state slots in model order and MALL-cold, and the
-prefix cache (us per request, hashing and block manager apart).
+separately), the GDN state slots in model order and MALL-cold, the prefix
+cache (us per request, hashing and block manager apart), and paged decode
+attention over bf16 and fp8 pools at the headline's shape (200 steps).
 """
 from __future__ import annotations
 
@@ -1886,7 +1887,8 @@ def _summary(r: dict, keep: tuple[str, ...]) -> dict:
     out = {"workload": r["config"]["workload"], "metric": r["metric"], "value": r["value"],
            "unit": r["unit"], "ms_per_step": r["ms_per_step"]}
     out.update({k: r[k] for k in keep if k in r})
-    out["kernels"] = [kern(k) for k in r["roofline"]["kernels"]]
+    roof = r["roofline"]
+    out["kernels"] = [kern(k) for k in (roof["kernels"] if "kernels" in roof else [roof])]
     if "mall_cold" in r:
         out["mall_cold"] = {"pct_of_hbm_peak": r["mall_cold"]["pct_of_hbm_peak"],
                             "kernels": [kern(k) for k in r["mall_cold"]["kernels"]]}
@@ -1896,13 +1898,17 @@ def _summary(r: dict, keep: tuple[str, ...]) -> dict:
 def run_secondary() -> dict:
     """The other configurations, after the headline (each on a fresh pool,
     with its default sizes): fp8 chunked prefill, GDN state slots in model
-    order (and MALL-cold), the prefix cache."""
+    order (and MALL-cold), the prefix cache, and paged decode attention over
+    bf16 and fp8 pools at the headline's shape."""
     out = {}
     for name, fn, steps, warmup, keep in (
             ("fp8_prefill", run_fp8_prefill, 12, 3, ("pct_of_hbm_peak", "appended_tokens_per_s")),
             ("gdn_state", run_gdn_state, 50, 5, ("pct_of_hbm_peak", "state_move_ms_per_step")),
             ("prefix", run_prefix, 5, 1, ("requests_per_s", "phase_ms", "evictions",
-                                          "page_hit_rate", "cow_copies"))):
+                                          "page_hit_rate", "cow_copies")),
+            ("decode_attn", run_decode_attn, 200, 10, ("pct_of_hbm_peak", "tokens_per_s")),
+            ("decode_attn_fp8", lambda st, wu, cpu: run_decode_attn(st, wu, cpu, fp8=True), 200,
+             10, ("pct_of_hbm_peak", "tokens_per_s"))):
         gc.collect()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
