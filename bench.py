@@ -1194,6 +1194,7 @@ SCHED_SEED = 106
 SCHED_BATCH = 256          # muserve/config.py:32-33 MAX_RUNNING_REQUESTS / MAX_DECODE_BATCH
 SCHED_MAX_PROMPT = 8192
 SCHED_MAX_NEW = 512
+SCHED_PHASE_EVERY = 4      # serving steps per step with per-phase event spans
 
 
 def sched_requests(n: int, seed: int = SCHED_SEED) -> tuple[np.ndarray, np.ndarray]:
@@ -1325,7 +1326,9 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         ent = plan.upload[:8 * nd].reshape(nd, 8)
         lens = ent[:, 1] + ent[:, 2]
         if n > nd:
-            cu_pre = plan.cu_seqlens[nd:] - nd  # decode entries hold one token each
+            # decode entries hold one token each; int32 once per step, as the
+            # attention kernels take it
+            cu_pre = (plan.cu_seqlens[nd:] - nd).to(torch.int32)
             max_chunk = max(c for _, _, c in plan.prefill)
             max_ctx = max(st + c for _, st, c in plan.prefill)
             if fp8:  # packed bf16 windows: sequence b's context at cu_ctx[b]
@@ -1422,7 +1425,9 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     t0 = time.perf_counter()
     for j in range(steps):
         step = stamps.span(stream)
-        one_step(recs[j], host, info)
+        # the per-phase spans on every SCHED_PHASE_EVERY-th step: each is two
+        # event records on the host, which a step of ~50 short launches feels
+        one_step(recs[j] if j % SCHED_PHASE_EVERY == 0 else None, host, info)
         step_spans.append(step.end(stream))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0

@@ -405,7 +405,9 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * free_order[0..P) (popped from the end; NULL = 0..P-1). mkv_bm_layout
  * writes 10 int64: table capacity C, ring capacity Q, then the byte offsets of
  * the counters (16 int64: free-stack top, ring head, ring tail, next stamp,
- * evictable pages, tombstones, eviction-log length), the table (C entries of
+ * evictable pages, tombstones, eviction-log length, then the running totals
+ * of admits the many-workgroup passes committed and of admits they covered
+ * but left to the one-workgroup kernels), the table (C entries of
  * {u64 key, i32 page, i32 copy of the page's refcount}), the page records (P x 32 bytes: i32 refcount, i32
  * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
  * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), the
@@ -419,7 +421,8 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order
- * (a leading run of up to 1024 releases is retired by many-workgroup passes;
+ * (a step of at most 8 ops runs on one workgroup, one op at a time;
+ * otherwise a leading run of 1 to 1024 releases is retired by many-workgroup passes;
  * the admits after it, up to 1024 of at most 2048 pages, are resolved
  * together by many-workgroup passes against the state before them, every
  * prediction checked, and the admits before the first one that may differ
@@ -463,6 +466,32 @@ int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_
                 int32_t* cow_src, int32_t* cow_dst, int32_t* status,
                 int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
                 void* stream);
+
+/*
+ * mkv_bm_step in two halves, for a caller that reads results back to the host
+ * (no counterpart in the reference). Called with the same arguments, in this
+ * order, on one stream, they are mkv_bm_step. _begin launches the release run
+ * and the many-workgroup resolution (nothing for a step of at most 8 ops);
+ * _end the one-workgroup kernels, which run every op left (none when the
+ * counter of committed admits grew by the number of admits in ops). Between the two, the committed admits' tables,
+ * hits, status and copy-on-write pairs are final, so a caller may copy them
+ * out before _end, whose workgroup needs 96 KiB of LDS and can wait for
+ * another kernel's workgroups to leave a CU.
+ */
+int mkv_bm_step_begin(void* state, int32_t num_pages, const int32_t* ops, int32_t num_ops,
+                      int32_t num_requests, const uint64_t* page_hashes,
+                      const int64_t* hash_offsets, const int32_t* num_tokens, int32_t* tables,
+                      int64_t table_stride, int32_t table_width, int32_t* hits,
+                      int32_t* child_last, int32_t* cow_src, int32_t* cow_dst, int32_t* status,
+                      int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
+                      void* stream);
+int mkv_bm_step_end(void* state, int32_t num_pages, const int32_t* ops, int32_t num_ops,
+                    int32_t num_requests, const uint64_t* page_hashes,
+                    const int64_t* hash_offsets, const int32_t* num_tokens, int32_t* tables,
+                    int64_t table_stride, int32_t table_width, int32_t* hits,
+                    int32_t* child_last, int32_t* cow_src, int32_t* cow_dst, int32_t* status,
+                    int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
+                    void* stream);
 
 /*
  * Read-only lookup in a block manager's table: for request r < num_requests

@@ -83,6 +83,10 @@ SIGNATURES: dict[str, list] = {
     "mkv_bm_init": [_P, _I32, _P, _P],
     "mkv_bm_step": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _P,
                     _I64, _P, _P],
+    "mkv_bm_step_begin": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P,
+                          _P, _I64, _P, _P],
+    "mkv_bm_step_end": [_P, _I32, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P,
+                        _P, _I64, _P, _P],
     "mkv_hash_probe": [_P, _I32, _P, _P, _I32, _P, _P, _P, _P],
     "mkv_decode_attention_workspace_bytes": [_I32, _I32, _I32, _I32],
     "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
@@ -176,7 +180,17 @@ def require_gpu(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+# torch's accessor of the current stream's raw handle (what its own kernel
+# launchers use): ~0.3 us against ~6 us for current_stream(device).cuda_stream,
+# which matters to steps made of many short launches
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """The hipStream_t (as an int) of torch's current stream on ``device``."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -12,9 +12,10 @@ forked request's partial last page is copied on write. A step's admits are
 resolved together on many CUs against the state at their start, every
 prediction checked; from the first admit that could differ from the
 sequential order, one workgroup resolves the rest in op order (admits eight
-at a time). Eviction order is deterministic and equal to the sequential
-OrderedDict model. Page hashes must be prefix keys (a hash at position i
-equal in two requests only if their hashes at every earlier position are).
+at a time). A step of at most 8 ops runs on one workgroup, one op at a time.
+Eviction order is deterministic and equal to the sequential OrderedDict
+model. Page hashes must be prefix keys (a hash at position i equal in two
+requests only if their hashes at every earlier position are).
 
 Typical step for a batch of requests (all on the stream, no host sync)::
 
@@ -75,14 +76,18 @@ class BlockManager:
         R, W = max_requests, max_pages_per_request
         i32 = dict(dtype=torch.int32, device=self.device)
         self.tables = torch.full((R, W), -1, **i32)
-        self.hits = torch.full((R,), -1, **i32)
+        # per request id: status and leading hits, the two rows of one tensor
+        # (a caller reads both back with one copy)
+        self.status_hits = torch.full((2, R), -1, **i32)
+        self.status, self.hits = self.status_hits[0], self.status_hits[1]
         self.child_last = torch.full((R,), -1, **i32)
         self.cow_src = torch.full((R,), -1, **i32)
         self.cow_dst = torch.full((R,), -1, **i32)
-        self.status = torch.full((R,), -1, **i32)
         self.evict_log = torch.full((max(evict_log_capacity, 1),), -1, **i32)
         self.evict_log_capacity = evict_log_capacity
         self.errors = _lib.DeviceErrors(self.device)
+        self._pending = None  # step_begin's arguments until step_end
+        self._keep = None
 
     def step(self, ops: torch.Tensor, page_hashes: torch.Tensor, hash_offsets: torch.Tensor,
              num_tokens: torch.Tensor) -> None:
@@ -90,6 +95,36 @@ class BlockManager:
         page_hashes: int64 device tensor of u64 page-hash bit patterns;
         hash_offsets: int64 [max_requests+1] offsets into it per request id;
         num_tokens: int32 [max_requests] prompt lengths."""
+        _lib.call("mkv_bm_step", *self._step_args(ops, page_hashes, hash_offsets, num_tokens))
+
+    def step_begin(self, ops: torch.Tensor, page_hashes: torch.Tensor, hash_offsets: torch.Tensor,
+                   num_tokens: torch.Tensor) -> None:
+        """The first half of ``step`` (same arguments): the release run and the
+        many-CU resolution of the admits after it. ``step_end`` must follow, on
+        the same stream, before anything else uses the manager. In between, the
+        admits the resolution committed (the growth of ``spec_done_word``) have
+        their final status, hits and table rows: when that growth equals the
+        number of admits in ops, ``step_end`` has nothing left to run."""
+        if self._pending is not None:
+            raise RuntimeError("step_begin twice without step_end")
+        args = self._step_args(ops, page_hashes, hash_offsets, num_tokens)
+        _lib.call("mkv_bm_step_begin", *args)
+        self._pending = args
+
+    def step_end(self) -> None:
+        """The second half of ``step``: the one-workgroup kernels over the ops
+        the resolution left."""
+        if self._pending is None:
+            raise RuntimeError("step_end without step_begin")
+        args, self._pending = self._pending, None
+        _lib.call("mkv_bm_step_end", *args)
+
+    def spec_done_word(self) -> torch.Tensor:
+        """Device view (int64, one element) of the running count of admits the
+        many-CU resolution committed, for an asynchronous copy."""
+        return self._arr("ctr", 16, torch.int64)[_SPEC_DONE:_SPEC_DONE + 1]
+
+    def _step_args(self, ops, page_hashes, hash_offsets, num_tokens) -> tuple:
         if not (isinstance(ops, torch.Tensor) and ops.device.type == "cuda"):
             host = np.asarray(ops.cpu() if isinstance(ops, torch.Tensor) else ops, dtype=np.int64)
             req = np.where(host >= 0, host, -(host + 1))
@@ -105,13 +140,15 @@ class BlockManager:
         if page_hashes.dtype != torch.int64:
             raise TypeError("page_hashes must hold u64 bit patterns in an int64 tensor")
         _lib.require_gpu(ops, hash_offsets, num_tokens, self.state)
-        _lib.call("mkv_bm_step", self.state.data_ptr(), self.num_pages, ops.data_ptr(),
-                  ops.numel(), self.tables.shape[0], page_hashes.data_ptr(), hash_offsets.data_ptr(),
-                  num_tokens.data_ptr(), self.tables.data_ptr(), self.tables.stride(0),
-                  self.tables.shape[1], self.hits.data_ptr(), self.child_last.data_ptr(),
-                  self.cow_src.data_ptr(), self.cow_dst.data_ptr(), self.status.data_ptr(),
-                  self.evict_log.data_ptr(), self.evict_log_capacity, self.errors.ptr(),
-                  _lib.stream_of(self.device))
+        # the tensors ride along (step_end's launch reads the same buffers)
+        self._keep = (ops, page_hashes, hash_offsets, num_tokens)
+        return (self.state.data_ptr(), self.num_pages, ops.data_ptr(),
+                ops.numel(), self.tables.shape[0], page_hashes.data_ptr(), hash_offsets.data_ptr(),
+                num_tokens.data_ptr(), self.tables.data_ptr(), self.tables.stride(0),
+                self.tables.shape[1], self.hits.data_ptr(), self.child_last.data_ptr(),
+                self.cow_src.data_ptr(), self.cow_dst.data_ptr(), self.status.data_ptr(),
+                self.evict_log.data_ptr(), self.evict_log_capacity, self.errors.ptr(),
+                _lib.stream_of(self.device))
 
     def probe(self, page_hashes: torch.Tensor, hash_offsets: torch.Tensor
               ) -> tuple[torch.Tensor, torch.Tensor]:

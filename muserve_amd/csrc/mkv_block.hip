@@ -76,6 +76,14 @@ constexpr int64_t kEntBytes = 16, kRecBytes = 32;
 // scratch lives in the state buffer.
 constexpr int kRunMaxOps = 1024;               // releases retired in bulk per step
 constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
+// The run takes a single leading release too: the speculation starts after
+// the run, so a release left to the step kernel would leave every admit
+// after it to the one-workgroup kernels.
+constexpr int kRunMinOps = 1;
+// A step of at most this many ops runs on the one-workgroup step kernel alone:
+// one launch, against fifteen dependent launches of a few microseconds each,
+// which a concurrent kernel that fills the GPU stretches to tens each.
+constexpr int kShortStepOps = 8;
 constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
 enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kRunSpan,
               kRunNext,  // the first op left to the next stage (speculation, groups, step)
@@ -324,6 +332,7 @@ struct BmArgs {
   int32_t* evict_log;
   int64_t evict_cap;
   int32_t* err;
+  int32_t from_start;  // the step kernel runs every op (a short step: no run, no speculation)
 };
 
 // Request metadata of a chunk of ops, staged in LDS.
@@ -1413,7 +1422,7 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   }
   __syncthreads();
   int n = first_non;
-  if (n < 2) {
+  if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
       decide_compaction(s, 0);
@@ -1489,7 +1498,7 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     }
     n = lo;  // ops after it are the step kernel's (it repeats any error bit)
   }
-  if (n < 2) {
+  if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
       decide_compaction(s, 0);
@@ -1552,7 +1561,7 @@ __global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
   const int64_t total = s.run_ctr[kRunTotal];
-  if (n < 2 || (int64_t)blockIdx.x * kRunChunk >= total) return;
+  if (n < kRunMinOps || (int64_t)blockIdx.x * kRunChunk >= total) return;
   run_stage(a, n, ro);
   for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
        c0 += (int64_t)gridDim.x * kRunChunk) {
@@ -1579,7 +1588,7 @@ __global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
 __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
-  const int64_t total = n < 2 ? 0 : s.run_ctr[kRunTotal];
+  const int64_t total = n < kRunMinOps ? 0 : s.run_ctr[kRunTotal];
   const int lane = threadIdx.x & 63;
   for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
        c0 += (int64_t)gridDim.x * kRunChunk) {
@@ -1625,7 +1634,7 @@ __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
       const uint64_t e = s.ring[(head + i) & qm];
       const int32_t pg = (int32_t)(uint32_t)e;
       s.cmp_ring[i] = e;
-      keep = live(rec_head(s, pg), (uint32_t)(e >> 32)) && (n < 2 || s.last[pg] < 0);
+      keep = live(rec_head(s, pg), (uint32_t)(e >> 32)) && (n < kRunMinOps || s.last[pg] < 0);
     }
     const uint64_t m = __ballot(keep);
     if (lane == 0 && i < span) {
@@ -1686,10 +1695,10 @@ __global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
   const bool cmp = s.run_ctr[kRunCompact] != 0;
-  if (n < 2 && !cmp) return;
+  if (n < kRunMinOps && !cmp) return;
   const int tid = threadIdx.x;
   int64_t n_lru = 0, n_free = 0, n_kept = 0;
-  if (n >= 2) {
+  if (n >= kRunMinOps) {
     const uint32_t* const bits[2] = {s.run_bits, s.run_bits + kRunMaxWords};
     uint32_t* const pre[2] = {s.run_wpre, s.run_wpre + kRunMaxWords};
     int64_t tot[2];
@@ -1698,7 +1707,7 @@ __global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
     n_free = tot[1];
   }
   if (cmp) {
-    if (n >= 2) __syncthreads();  // wave_tot is reused
+    if (n >= kRunMinOps) __syncthreads();  // wave_tot is reused
     const uint32_t* const bits[1] = {s.cmp_bits};
     uint32_t* const pre[1] = {s.cmp_pre};
     int64_t tot[1];
@@ -1717,14 +1726,14 @@ __global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
     s.ctr[kEvictable] += n_lru;
     s.ctr[kFreeTop] += n_free;
   }
-  for (int j = tid; j < (n >= 2 ? n : 0); j += kBmThreads)
+  for (int j = tid; j < (n >= kRunMinOps ? n : 0); j += kBmThreads)
     if (s.run_child[j] != -2) a.status[-(a.ops[j] + 1)] = kStReleased;
 }
 
 __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
-  const int64_t total = n < 2 ? 0 : s.run_ctr[kRunTotal];
+  const int64_t total = n < kRunMinOps ? 0 : s.run_ctr[kRunTotal];
   if (s.run_ctr[kRunCompact] != 0) {  // the kept entries, from the head in order
     const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
     for (int64_t i = (int64_t)blockIdx.x * kRunThreads + threadIdx.x; i < span;
@@ -2465,9 +2474,13 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   }
   for (int i = threadIdx.x; i < kSetSize; i += kBmThreads) al.claims[i] = -1;
   uint64_t cur[kHeld] = {}, nxt[kHeld] = {};
+  if (a.from_start && c.tombs > a.s.C / 4) {  // what the speculation's setup does otherwise
+    tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
+    if (threadIdx.x == 0) a.s.ctr[kTombs] = 0;
+  }
   // the leading run of releases (if any) was retired by the run kernels, and
-  // the admits after it by the group kernel
-  const int32_t start = (int32_t)a.s.run_ctr[kRunNext];
+  // the admits after it by the speculation and the group kernel
+  const int32_t start = a.from_start ? 0 : (int32_t)a.s.run_ctr[kRunNext];
   for (int32_t base = start; base < a.num_ops; base += kOpChunk) {
     const int cnt = a.num_ops - base < kOpChunk ? a.num_ops - base : kOpChunk;
     for (int t = threadIdx.x; t < cnt; t += kBmThreads) {
@@ -2609,23 +2622,25 @@ extern "C" int mkv_bm_init(void* state, int32_t num_pages, const int32_t* free_o
   return check_launch("mkv_bm_init");
 }
 
-extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_ops,
-                           int32_t num_requests, const uint64_t* page_hashes, const int64_t* hash_offsets,
-                           const int32_t* num_tokens, int32_t* tables, int64_t table_stride,
-                           int32_t table_width, int32_t* hits, int32_t* child_last,
-                           int32_t* cow_src, int32_t* cow_dst, int32_t* status,
-                           int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
-                           void* stream) {
-  clear_error();
+namespace {
+
+// The arguments of mkv_bm_step and its two halves, checked; MKV_OK with
+// a.num_ops == 0 means there is nothing to launch.
+int bm_step_args(BmArgs& a, const char* fn, void* state, int32_t num_pages, const int32_t* ops,
+                 int32_t num_ops, int32_t num_requests, const uint64_t* page_hashes,
+                 const int64_t* hash_offsets, const int32_t* num_tokens, int32_t* tables,
+                 int64_t table_stride, int32_t table_width, int32_t* hits, int32_t* child_last,
+                 int32_t* cow_src, int32_t* cow_dst, int32_t* status, int32_t* evict_log,
+                 int64_t evict_log_capacity, int32_t* err) {
+  a.num_ops = 0;
   MKV_REQUIRE(num_ops >= 0 && num_pages > 0 && table_width >= 0 && num_requests >= 0,
-              MKV_E_INVALID, "mkv_bm_step: bad sizes");
+              MKV_E_INVALID, "%s: bad sizes", fn);
   if (num_ops == 0) return MKV_OK;
   MKV_REQUIRE(state && ops && hash_offsets && num_tokens && tables && hits && child_last &&
                   cow_src && cow_dst && status && err,
-              MKV_E_INVALID, "mkv_bm_step: null pointer");
+              MKV_E_INVALID, "%s: null pointer", fn);
   MKV_REQUIRE(evict_log || evict_log_capacity == 0, MKV_E_INVALID,
-              "mkv_bm_step: eviction log capacity without a log");
-  BmArgs a;
+              "%s: eviction log capacity without a log", fn);
   a.s = bm_state(state, num_pages);
   a.ops = ops;
   a.num_ops = num_ops;
@@ -2644,7 +2659,14 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   a.evict_log = evict_log;
   a.evict_cap = evict_log_capacity;
   a.err = err;
-  const hipStream_t st = as_stream(stream);
+  a.from_start = num_ops <= kShortStepOps;
+  return MKV_OK;
+}
+
+// The leading run of releases, then the speculation over the admits after it;
+// nothing for a short step.
+void launch_bm_begin(const BmArgs& a, hipStream_t st) {
+  if (a.from_start) return;
   hipLaunchKernelGGL(run_setup_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(run_drop_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
   hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
@@ -2658,9 +2680,72 @@ extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, i
   hipLaunchKernelGGL(spec_victims_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
   hipLaunchKernelGGL(spec_commit_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_finish_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
-  hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+}
+
+// The ops the speculation left, in order: admits in groups, then one at a time
+// (a short step: every op, one at a time).
+void launch_bm_end(const BmArgs& a, hipStream_t st) {
+  if (!a.from_start) hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
   hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+}
+
+}  // namespace
+
+extern "C" int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_ops,
+                           int32_t num_requests, const uint64_t* page_hashes,
+                           const int64_t* hash_offsets, const int32_t* num_tokens,
+                           int32_t* tables, int64_t table_stride, int32_t table_width,
+                           int32_t* hits, int32_t* child_last, int32_t* cow_src,
+                           int32_t* cow_dst, int32_t* status, int32_t* evict_log,
+                           int64_t evict_log_capacity, int32_t* err, void* stream) {
+  clear_error();
+  BmArgs a;
+  const int rc = bm_step_args(a, "mkv_bm_step", state, num_pages, ops, num_ops, num_requests,
+                              page_hashes, hash_offsets, num_tokens, tables, table_stride,
+                              table_width, hits, child_last, cow_src, cow_dst, status, evict_log,
+                              evict_log_capacity, err);
+  if (rc != MKV_OK || a.num_ops == 0) return rc;
+  launch_bm_begin(a, as_stream(stream));
+  launch_bm_end(a, as_stream(stream));
   return check_launch("mkv_bm_step");
+}
+
+extern "C" int mkv_bm_step_begin(void* state, int32_t num_pages, const int32_t* ops,
+                                 int32_t num_ops, int32_t num_requests,
+                                 const uint64_t* page_hashes, const int64_t* hash_offsets,
+                                 const int32_t* num_tokens, int32_t* tables,
+                                 int64_t table_stride, int32_t table_width, int32_t* hits,
+                                 int32_t* child_last, int32_t* cow_src, int32_t* cow_dst,
+                                 int32_t* status, int32_t* evict_log,
+                                 int64_t evict_log_capacity, int32_t* err, void* stream) {
+  clear_error();
+  BmArgs a;
+  const int rc = bm_step_args(a, "mkv_bm_step_begin", state, num_pages, ops, num_ops,
+                              num_requests, page_hashes, hash_offsets, num_tokens, tables,
+                              table_stride, table_width, hits, child_last, cow_src, cow_dst,
+                              status, evict_log, evict_log_capacity, err);
+  if (rc != MKV_OK || a.num_ops == 0) return rc;
+  launch_bm_begin(a, as_stream(stream));
+  return check_launch("mkv_bm_step_begin");
+}
+
+extern "C" int mkv_bm_step_end(void* state, int32_t num_pages, const int32_t* ops,
+                               int32_t num_ops, int32_t num_requests,
+                               const uint64_t* page_hashes, const int64_t* hash_offsets,
+                               const int32_t* num_tokens, int32_t* tables, int64_t table_stride,
+                               int32_t table_width, int32_t* hits, int32_t* child_last,
+                               int32_t* cow_src, int32_t* cow_dst, int32_t* status,
+                               int32_t* evict_log, int64_t evict_log_capacity, int32_t* err,
+                               void* stream) {
+  clear_error();
+  BmArgs a;
+  const int rc = bm_step_args(a, "mkv_bm_step_end", state, num_pages, ops, num_ops,
+                              num_requests, page_hashes, hash_offsets, num_tokens, tables,
+                              table_stride, table_width, hits, child_last, cow_src, cow_dst,
+                              status, evict_log, evict_log_capacity, err);
+  if (rc != MKV_OK || a.num_ops == 0) return rc;
+  launch_bm_end(a, as_stream(stream));
+  return check_launch("mkv_bm_step_end");
 }
 
 extern "C" int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_hashes,

@@ -47,7 +47,9 @@ LRU instead of a free list. Admission candidates are the queue's head while
 the budget, counted as if nothing were cached, is not spent, a row and a
 private page are free; the block manager's work for a step (releases, then
 the candidates' admits) runs on a side stream, and the host waits for its
-results (hits and page ids) before it plans the chunks. ``oracle/sched.py``
+results (hits and page ids) before it plans the chunks: it reads them right
+after the many-CU passes when those committed every admit (the usual case),
+and otherwise after the one-workgroup kernels. ``oracle/sched.py``
 (``PrefixSchedulerModel``) states the policy.
 
 Entries are ordered decode tokens first (running order), then prefill chunks,
@@ -205,6 +207,9 @@ class ContinuousBatchScheduler:
             self._bm_ids = deque(range(2 * max_batch_size))
             self._unhashed: list[InferenceRequest] = []  # queued, page hashes not yet launched
             self._bm_ntok = np.zeros(2 * max_batch_size, dtype=np.int64)
+            # rounds whose results were read after the many-CU half / after
+            # the one-workgroup kernels
+            self.bm_early_rounds = self.bm_late_rounds = 0
         if kv_cache is not None:
             if chunked_prefill_size <= 0:
                 raise ValueError("chunked_prefill_size must be positive")
@@ -295,15 +300,20 @@ class ContinuousBatchScheduler:
         self._ring = 0
         if self.block_manager is not None:
             # one block-manager round per step: per-id hash offsets and
-            # lengths, the ops; read back: status, hits and page rows
-            W = self.width
+            # lengths, the ops; read back: status and hits of the 2B ids,
+            # the admits' (at most B) page rows
+            W = self.block_manager.tables.shape[1]
             self._bm = dict(
                 side=torch.cuda.Stream(dev),  # default priority, like every stream here
                 meta_h=torch.empty(8 * (B + 1), dtype=torch.int64, pin_memory=True),
                 meta_d=torch.empty(8 * (B + 1), **i64),
-                back_h=torch.empty(B * (2 + W), dtype=torch.int32, pin_memory=True),
+                # the results after each half of the round (a different buffer
+                # each, so a late copy never overwrites what the host reads)
+                back_a=torch.empty(B * (4 + W), dtype=torch.int32, pin_memory=True),
+                back_b=torch.empty(B * (4 + W), dtype=torch.int32, pin_memory=True),
+                count_h=torch.empty(2, dtype=torch.int64, pin_memory=True),
                 errors=_lib.DeviceErrors(dev),
-                last=None,  # the previous round's end (its copies read the staging buffers)
+                uploaded=None,  # the previous round's upload (it reads meta_h)
             )
 
     def _retire(self, lst: list[InferenceRequest],
@@ -567,52 +577,79 @@ class ContinuousBatchScheduler:
         b = self._bm
         bm = self.block_manager
         B = 2 * self.max_batch_size  # block-manager ids
-        dev = self.kv_cache.device
-        # the meta block: per-id hash offsets (B+1; the admits' hashes are
-        # concatenated in id order, so the offsets are a prefix sum), per-id
-        # token counts (B), ops (candidate order)
-        if b["last"] is not None:
-            b["last"].synchronize()  # the staging buffer is free again
-            b["last"] = None
+        if b["uploaded"] is not None:
+            b["uploaded"].synchronize()  # the previous round's upload read the staging buffer
+            b["uploaded"] = None
         n = len(admits)
         admits = sorted(admits, key=lambda r: r.bm_id)
         per_id = np.zeros(B, dtype=np.int64)
         for r in admits:
             per_id[r.bm_id] = r.fb
-        meta = b["meta_h"].numpy()
-        m = 0
-        for arr in (np.concatenate([[0], np.cumsum(per_id)]), self._bm_ntok,
-                    np.array(ops, dtype=np.int64)):
-            meta[m:m + len(arr)] = arr
-            m += len(arr)
+        # one upload: per-id hash offsets (B+1, int64; the admits' hashes are
+        # concatenated in id order, so the offsets are a prefix sum), then as
+        # int32: per-id token counts (B), the ops (candidate order), the
+        # admits' ids
+        b["meta_h"].numpy()[:B + 1] = np.concatenate([[0], np.cumsum(per_id)])
+        m32 = b["meta_h"].view(torch.int32).numpy()
+        o_ntok = 2 * (B + 1)
+        o_ops = o_ntok + B
+        o_rows = o_ops + len(ops)
+        m32[o_ntok:o_ops] = self._bm_ntok
+        m32[o_ops:o_rows] = ops
+        m32[o_rows:o_rows + n] = [r.bm_id for r in admits]
         side = b["side"]
         with torch.cuda.stream(side):
-            b["meta_d"][:m].copy_(b["meta_h"][:m], non_blocking=True)
-            md = b["meta_d"]
-            o_ntok, o_ops = B + 1, 2 * B + 1
+            md32 = b["meta_d"].view(torch.int32)
+            md32[:o_rows + n].copy_(b["meta_h"].view(torch.int32)[:o_rows + n], non_blocking=True)
+            b["uploaded"] = torch.cuda.Event()
+            b["uploaded"].record(side)
             hashes = (torch.cat([r.page_hashes for r in admits]) if n
                       else b["meta_d"][:1])  # (no admit reads a hash)
-            bm.step(md[o_ops:o_ops + len(ops)].to(torch.int32), hashes, md[:B + 1],
-                    md[o_ntok:o_ntok + B].to(torch.int32))
+            args = (md32[o_ops:o_rows], hashes, b["meta_d"][:B + 1], md32[o_ntok:o_ops])
             if not n:
-                b["last"] = torch.cuda.Event()
-                b["last"].record(side)
+                bm.step(*args)
                 return {}
-            rows = torch.tensor([r.bm_id for r in admits], dtype=torch.int64).to(dev,
-                                                                                   non_blocking=True)
-            W = max(r.fb for r in admits)
-            back = torch.cat([bm.status.index_select(0, rows), bm.hits.index_select(0, rows),
-                              bm.tables.index_select(0, rows)[:, :W].reshape(-1)])
-            out = b["back_h"][:back.numel()]
-            out.copy_(back, non_blocking=True)
-            done = torch.cuda.Event()
-            done.record(side)
-        done.synchronize()
-        v = out.numpy()
-        status, hits = v[:n], v[n:2 * n]
-        tables = v[2 * n:].reshape(n, W)
-        return {r.bm_id: (int(status[i]), int(hits[i]), tables[i, :r.fb].tolist())
+            # the committed-admit count around the many-CU half, and the
+            # results read back after it and again after the one-workgroup
+            # kernels (which wait for 96 KiB of LDS on a CU); the first copy
+            # is final when every admit was committed
+            ids = md32[o_rows:o_rows + n]
+            count = b["count_h"]
+            count[0:1].copy_(bm.spec_done_word(), non_blocking=True)
+            bm.step_begin(*args)
+            count[1:2].copy_(bm.spec_done_word(), non_blocking=True)
+            early = self._bm_read_back(b["back_a"], ids, B, side)
+            bm.step_end()
+            late = self._bm_read_back(b["back_b"], ids, B, side)
+        early[2].synchronize()
+        c = count.numpy()
+        if c[1] - c[0] == n:
+            self.bm_early_rounds += 1
+            sh, rows, _ = early
+        else:
+            self.bm_late_rounds += 1
+            sh, rows, ev = late
+            ev.synchronize()
+        st_hits = sh.numpy().reshape(2, B)
+        tables = rows.numpy().reshape(n, -1)
+        return {r.bm_id: (int(st_hits[0, r.bm_id]), int(st_hits[1, r.bm_id]),
+                          tables[i, :r.fb].tolist())
                 for i, r in enumerate(admits)}
+
+    def _bm_read_back(self, buf: torch.Tensor, ids: torch.Tensor, B: int,
+                      stream: torch.cuda.Stream) -> tuple:
+        """Copies (on ``stream``, the current one) the status and hits of every
+        block-manager id and the table rows of ``ids`` into the pinned ``buf``;
+        returns the two host views and an event after the copies."""
+        bm = self.block_manager
+        tab = bm.tables.index_select(0, ids)
+        sh = buf[:2 * B]
+        sh.copy_(bm.status_hits.view(-1), non_blocking=True)
+        rows = buf[2 * B:2 * B + tab.numel()]
+        rows.copy_(tab.view(-1), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        return sh, rows, ev
 
     def plan_step(self) -> StepPlan | None:
         """Schedules one step and writes its device tensors (one upload, one

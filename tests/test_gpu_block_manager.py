@@ -34,6 +34,27 @@ def interleaved_ops(n, batch):
     return out
 
 
+def serving_ops(seed, cap=16):
+    """The serving scheduler's pattern: per step the releases of a few finished
+    requests (often one; now and then half of them), then new admits while
+    fewer than cap are live."""
+    def ops_fn(n, batch):
+        rng = np.random.default_rng(seed)
+        live, out, nxt = [], [], 0
+        while nxt < n or live:
+            k = int(rng.integers(0, 4)) if rng.random() < 0.7 else len(live) // 2
+            k = min(len(live), k) if nxt < n else len(live)
+            idx = sorted(rng.choice(len(live), size=k, replace=False).tolist(), reverse=True)
+            rel = [live.pop(i) for i in idx]
+            room = max(0, cap - len(live))
+            new = list(range(nxt, min(n, nxt + min(room, int(rng.integers(0, batch + 1))))))
+            nxt += len(new)
+            live += new
+            out.append([-(r + 1) for r in rel] + new)
+        return out
+    return ops_fn
+
+
 def random_ops(seed):
     """Random op streams: per step a leading run of 0..all releases of live
     requests (random order), then new admits shuffled with more releases."""
@@ -93,10 +114,13 @@ def synthetic_keys(n, seed, alphabet, max_pages, skew):
 
 
 def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False,
-        ops_fn=bench.prefix_ops, keys=None):
+        ops_fn=bench.prefix_ops, keys=None, split=False):
     """Drives the manager through ops_fn's steps and checks it against the
     model; returns the statuses, the model and the final snapshot. `keys` =
-    (token counts, per-request key lists) replaces the hashed prompts."""
+    (token counts, per-request key lists) replaces the hashed prompts.
+    split: each step as step_begin + step_end; where the committed-admit
+    count grew by the step's admits, their results read between the halves
+    are checked too (snap["early_steps"] counts those steps)."""
     if keys is None:
         reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
                                      template_len=template_len, suffix=suffix)
@@ -124,8 +148,18 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     off = torch.from_numpy(cu_pages).to(DEV)
     ntok = torch.tensor(lens, dtype=torch.int32, device=DEV)
     want = {}
+    early_steps = 0
     for ops in ops_fn(n, batch):
-        bm.step(torch.tensor(ops, dtype=torch.int32), hashes, off, ntok)
+        admits = [o for o in ops if o >= 0]  # consecutive request ids
+        mid = None
+        if split:
+            before = int(bm.spec_done_word().item())
+            bm.step_begin(torch.tensor(ops, dtype=torch.int32), hashes, off, ntok)
+            if admits and int(bm.spec_done_word().item()) - before == len(admits):
+                mid = (bm.status.cpu().tolist(), bm.hits.cpu().tolist(), bm.tables.cpu())
+            bm.step_end()
+        else:
+            bm.step(torch.tensor(ops, dtype=torch.int32), hashes, off, ntok)
         pairs = []
         for op in ops:
             if op >= 0:
@@ -135,7 +169,13 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
                     pairs.append((want[op]["cow_src"], want[op]["cow_dst"]))
             elif -op - 1 in model.reqs:
                 model.release(-op - 1)
-        admits = [o for o in ops if o >= 0]  # consecutive request ids
+        if mid is not None:  # every admit's result was final after the first half
+            early_steps += 1
+            for op in admits:
+                assert mid[0][op] == want[op]["status"], op
+                if want[op]["status"] == OK:
+                    assert mid[1][op] == want[op]["hits"], op
+                    assert mid[2][op, :-(-lens[op] // 16)].tolist() == want[op]["table"], op
         if with_data and admits:
             bm.copy_on_write(cache, min(admits), min(admits) + len(admits))
             for s, d in pairs:
@@ -182,6 +222,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         lead = next((i for i, p in enumerate(want_pages) if p < 0), len(h))
         assert hit[r] == lead, r
     assert bm.snapshot()["lru"] == snap["lru"]  # nothing moved
+    snap["early_steps"] = early_steps
     return status, model, snap
 
 
@@ -246,6 +287,25 @@ def test_random_release_runs_and_interleavings(seed):
                         suffix=(1, 100), width=32, with_data=seed == 31,
                         ops_fn=random_ops(seed))
     assert len(model.evicted) > 100
+
+
+@pytest.mark.parametrize("seed,ops", [(61, "serving"), (62, "random")])
+def test_step_in_two_halves(seed, ops):
+    # step_begin + step_end is step. Steps of at most 8 ops run on the step
+    # kernel alone (in step_end); in longer ones a single leading release goes
+    # through the release run, so the admits after it are resolved on many CUs,
+    # and where every admit was committed by the first half its results are
+    # final there
+    case(f"block manager: step_begin + step_end, {ops} ops, seed {seed}")
+    fn = serving_ops(seed) if ops == "serving" else random_ops(seed)
+    steps = fn(240, 16)
+    assert sum(len(o) > 8 for o in steps) > 10
+    assert ops != "serving" or sum(len(o) <= 8 for o in steps) > 20
+    status, model, snap = run(P=192, n=240, batch=16, seed=seed, n_templates=6, template_len=128,
+                              suffix=(1, 120), width=32, ops_fn=fn, split=True)
+    if ops == "serving":  # (the CPU model admits every request of 21 long steps)
+        assert snap["early_steps"] > 10
+    assert len(model.evicted) > 50
 
 
 def test_single_releases_between_admits():

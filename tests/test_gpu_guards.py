@@ -134,3 +134,15 @@ def test_check_unique_entry_point_directly():
     with pytest.raises(_lib.MkvDeviceError):
         err.check()
     assert int(chk.bits.count_nonzero()) == 0
+
+
+def test_stream_of_is_torchs_current_stream():
+    # every entry point is launched on the stream stream_of returns: torch's
+    # current stream of the device, also inside a stream context
+    case("stream_of against torch.cuda.current_stream")
+    assert _lib.stream_of(DEV) == torch.cuda.current_stream(DEV).cuda_stream
+    side = torch.cuda.Stream(DEV)
+    with torch.cuda.stream(side):
+        assert _lib.stream_of(DEV) == side.cuda_stream
+        assert _lib.stream_of(torch.device("cuda")) == side.cuda_stream
+    assert _lib.stream_of(DEV) == torch.cuda.current_stream(DEV).cuda_stream

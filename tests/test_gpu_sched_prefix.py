@@ -83,6 +83,10 @@ def test_prefix_scheduler_matches_model(seed, bm_pages, private, chunk, batch, m
     s.check_errors()
     assert not pending and s.is_idle and steps > 20
     assert skipped == m.skipped > 0 and s.prefix_skipped == skipped
+    # rounds read after the many-CU half (every admit committed there) and
+    # after the one-workgroup kernels (short rounds, turn-aways)
+    print(f"block-manager rounds read early {s.bm_early_rounds}, late {s.bm_late_rounds}",
+          flush=True)
     # the block manager's state equals the model's: eviction order, free
     # stack, LRU order, refcounts (every request released)
     snap = bm.snapshot()
