@@ -1565,10 +1565,15 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
             "skipped_fraction": round(skipped / max(1, prompt_tok), 4),
             "prompt_tokens_per_s_incl_skipped": round(prompt_tok / elapsed, 1),
             "evictions": int(bm.counters()[6]),
+            # rounds with admits (warm-up included) whose results were read
+            # after the many-CU half / after the one-workgroup kernels (a
+            # round of at most 8 ops is the step kernel alone: late)
+            "block_manager_rounds_read": {"early": s.bm_early_rounds, "late": s.bm_late_rounds},
             "note": ("the timed steps' prompt tokens found in cached pages (never computed or "
-                     "appended); plan_host_us includes the block-manager round (mkv_bm_step on "
-                     "a side stream: the step's releases and admits) and the wait for its "
-                     "results; prompts are hashed on the side stream when they are queued"),
+                     "appended); plan_host_us includes the block-manager round "
+                     "(mkv_bm_step_begin/_end on a side stream: the step's releases and "
+                     "admits) and the wait for its results; prompts are hashed on the side "
+                     "stream when they are queued"),
         }
     if with_cpu and not prefix:
         log("cpu baseline (scheduler oracle: per-token page bookkeeping of the same trace)")
