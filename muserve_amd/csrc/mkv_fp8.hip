@@ -106,16 +106,21 @@ __device__ __forceinline__ u32x4 quantise_row(const u32x4 r0, const u32x4 r1, fl
 // shuffles only ever read lanes of the same live row. Source rows are read
 // once and pool rows are not read back this step: non-temporal loads and
 // stores (6 % faster than ordinary ones on the chunked-prefill shape; more
-// rows per group, K and V in one workgroup, 128- or 512-thread workgroups
-// and a persistent grid measured no faster).
+// rows per group, K and V in one workgroup, two rows per group, 128- or
+// 512-thread workgroups and a persistent grid measured no faster).
+// HEADS is the head count when it is 1 or 2 (0: any, read from the
+// arguments): a runtime 32-bit division ahead of the first load made the
+// one-head launch 10 % slower on the chunked-prefill shape.
+template <int HEADS>
 __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   const uint32_t lane = threadIdx.x & (kLanesPerRow - 1);
   const uint32_t row = blockIdx.x * kRowsPerWg + threadIdx.x / kLanesPerRow;
   if (row >= a.num_rows) return;
   const uint32_t l = blockIdx.y >> 1;
   const bool is_v = blockIdx.y & 1u;
-  const uint32_t t = row / a.num_heads;
-  const uint32_t h = row - t * a.num_heads;
+  const uint32_t nh = HEADS ? (uint32_t)HEADS : a.num_heads;
+  const uint32_t t = row / nh;
+  const uint32_t h = row - t * nh;
   const int64_t slot = a.slots[t];
   const uint8_t* src = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride +
                        (int64_t)t * a.src_token_stride + (int64_t)h * (kHeadDim * 2) + lane * 32;
@@ -127,11 +132,11 @@ __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   float scale;
   const u32x4 codes = quantise_row(r0, r1, scale);
   uint8_t* pool = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride;
-  st_nt(pool + slot * ((int64_t)a.num_heads * kHeadDim) + (int64_t)h * kHeadDim + lane * 16, codes);
+  st_nt(pool + slot * ((int64_t)nh * kHeadDim) + (int64_t)h * kHeadDim + lane * 16, codes);
   if (lane == 0) {
     float* sp = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(is_v ? a.v_scale : a.k_scale) +
                                          (int64_t)l * a.scale_layer_stride);
-    __builtin_nontemporal_store(scale, sp + slot * a.num_heads + h);
+    __builtin_nontemporal_store(scale, sp + slot * nh + h);
   }
 }
 
@@ -262,7 +267,12 @@ extern "C" int mkv_append_fp8(void* k_pool, void* v_pool, float* k_scale, float*
                   src_layer_stride, src_token_stride, slot_mapping, (uint32_t)rows,
                   (uint32_t)num_heads, err};
   dim3 grid((unsigned)((rows + kRowsPerWg - 1) / kRowsPerWg), (unsigned)(2 * num_layers));
-  hipLaunchKernelGGL(append_fp8_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+  if (num_heads == 1)
+    hipLaunchKernelGGL(append_fp8_kernel<1>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  else if (num_heads == 2)
+    hipLaunchKernelGGL(append_fp8_kernel<2>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(append_fp8_kernel<0>, grid, dim3(kThreads), 0, as_stream(stream), a);
   return check_launch("mkv_append_fp8");
 }
 

@@ -37,11 +37,15 @@ struct AppendArgs {
   int32_t* err;
 };
 
+// RC: 16-byte chunks per row when the row is one bf16 head of 256 (32),
+// 0 for any other row size, read from the arguments (a runtime division).
+template <int RC>
 __global__ __launch_bounds__(kThreads) void append_rows_kernel(AppendArgs a) {
   const uint32_t g = blockIdx.x * kThreads + threadIdx.x;
-  const uint32_t t = g / a.row_chunks;
+  const uint32_t rc = RC ? (uint32_t)RC : a.row_chunks;
+  const uint32_t t = g / rc;
   if (t >= a.num_tokens) return;
-  const uint32_t col = g - t * a.row_chunks;
+  const uint32_t col = g - t * rc;
   const uint32_t lkv = blockIdx.y;  // layer*2 + (0: K, 1: V)
   const uint32_t l = lkv >> 1;
   const bool is_v = lkv & 1u;
@@ -50,7 +54,7 @@ __global__ __launch_bounds__(kThreads) void append_rows_kernel(AppendArgs a) {
     if (slot != -1 && col == 0 && !is_v) raise_err(a.err, MKV_DEVERR_SLOT);
     return;
   }
-  const int64_t row_bytes = (int64_t)a.row_chunks * 16;
+  const int64_t row_bytes = (int64_t)rc * 16;
   const uint8_t* src = (is_v ? a.v_src : a.k_src) + (int64_t)l * a.src_layer_stride +
                        (int64_t)t * a.src_token_stride + (int64_t)col * 16;
   uint8_t* dst = (is_v ? a.v_pool : a.k_pool) + (int64_t)l * a.pool_layer_stride +
@@ -335,7 +339,10 @@ extern "C" int mkv_append_bf16(void* k_pool, void* v_pool, int64_t pool_layer_st
                (const uint8_t*)k_src, (const uint8_t*)v_src, src_layer_stride, src_token_stride,
                slot_mapping, (uint32_t)num_tokens, (uint32_t)(row_bytes / 16), err};
   dim3 grid((unsigned)((chunks + kThreads - 1) / kThreads), (unsigned)(2 * num_layers));
-  hipLaunchKernelGGL(append_rows_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+  if (row_bytes == 512)
+    hipLaunchKernelGGL(append_rows_kernel<32>, grid, dim3(kThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(append_rows_kernel<0>, grid, dim3(kThreads), 0, as_stream(stream), a);
   return check_launch("mkv_append_bf16");
 }
 

@@ -308,3 +308,19 @@ def test_fp8_decode_config_shape_against_oracle():
     q, k, v, lens, table = build(36, lens, 4, 1)
     got, want = run_fp8(q, *quantize(k, v), lens, table, max_seqlen=int(lens.max()))
     within_one_ulp(got, want)
+
+
+@pytest.mark.parametrize("batch,Hkv", [(4096, 1), (1500, 2), (300, 1)])
+def test_work_list_sizes(batch, Hkv):
+    # the chunk kernel's work list lives in LDS sized to batch x KV heads (in
+    # steps of 256 pairs, up to 4096): every size class, including the
+    # largest, where LDS caps the occupancy, over bf16 and fp8 pools
+    rng = np.random.default_rng(37 + batch)
+    lens = rng.integers(0, 1200, batch)
+    lens[::97] = 2048 + rng.integers(0, 2048, len(lens[::97]))  # some two- and three-chunk pairs
+    case(f"decode attention work list: batch {batch} x {Hkv} KV heads, {int(lens.sum())} tokens")
+    q, k, v, lens, table = build(38 + batch, lens, 4 * Hkv, Hkv)
+    got, want = run(q, k, v, lens, table)
+    within_one_ulp(got, want)
+    got, want = run_fp8(q, *quantize(k, v), lens, table)
+    within_one_ulp(got, want)
