@@ -38,7 +38,7 @@ def check_pool(cache, q_cpu, s_cpu):
     assert torch.equal(got_s.view(torch.int32), s_cpu.view(torch.int32))
 
 
-@pytest.mark.parametrize("H", [1, 2])
+@pytest.mark.parametrize("H", [1, 2, 3])  # 1 and 2: specialised kernels; 3: any head count
 def test_append_fp8_bit_exact(H):
     case(f"fp8 append H={H}")
     g = torch.Generator().manual_seed(103)
