@@ -14,7 +14,7 @@
 //     A = the K page, 16 contiguous bytes of a K row per lane loaded straight
 //     from the pool (row = lane % 16, 16-byte chunk 4*step + lane / 16);
 //     B = the G query heads (columns >= G zero) in the same dim order, held
-//     in LDS for the whole chunk; C = 4 scores per lane (tokens
+//     in registers for the whole chunk; C = 4 scores per lane (tokens
 //     4*(lane/16) + i, head lane % 16);
 //   * online softmax per head in fp32 (exp2, log2(e) folded into the scale);
 //     the page's probabilities go through a wave-private LDS tile;
@@ -54,7 +54,6 @@ constexpr int kPageTokens = 16;
 constexpr int kChunk = 1024;  // tokens per work item (512 measured 3 % slower, 2048 4 %)
 constexpr int kChunkPages = kChunk / kPageTokens;
 constexpr int kMaxPairs = 4096;  // batch x KV heads whose chunk prefix fits in LDS
-constexpr int kPairClass = 256;  // the work list's LDS is sized in steps of this many pairs
 constexpr int kPagesPerIter = 1;  // pages per wave iteration (2 measured 1.5 % slower on fp8)
 constexpr int kIterTokens = kPagesPerIter * kPageTokens;
 constexpr int kTailClasses = 32;  // length classes of the short chunks (32 tokens each)
@@ -147,24 +146,20 @@ __device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
 // e4m3fn codes with an fp32 scale per (token, KV head); a token's score is
 // scale_k * (q . codes) and its V weight p * scale_v, so the codes convert
 // exactly to bf16 MFMA operands and no product is rounded before the fp32
-// accumulation. F16: q, caches and out are fp16 instead of bf16. HKV: the
-// KV head count when it is 1 (a page's 16 scales are then contiguous, four
-// per lane group in one 16-byte load), 0 for any count read from `a`.
-template <int G, bool FP8, bool F16, int HKV>
+// accumulation. F16: q, caches and out are fp16 instead of bf16.
+template <int G, bool FP8, bool F16>
 __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t hk, int64_t c,
                                            int64_t len, int64_t nch,
                                            float (&p_lds)[kAttnWaves][kIterTokens][16],
                                            float (&al_lds)[kAttnWaves][16],
                                            float (&m_w)[kAttnWaves][G], float (&l_w)[kAttnWaves][G],
-                                           float (&o_w)[kAttnWaves][G][kHeadDim],
-                                           u32x4 (&q_lds)[8][64]) {
+                                           float (&o_w)[kAttnWaves][G][kHeadDim]) {
   constexpr int kCodeRow = FP8 ? kHeadDim : kRowBytes;  // bytes of one cached K or V row
   constexpr int PPI = kPagesPerIter;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar page ids
   const int n = lane & 15, g = lane >> 4;
-  const int64_t hkv = HKV ? (int64_t)HKV : (int64_t)a.hkv;
-  uint8_t* out = a.out + (b * hkv + hk) * G * kRowBytes;
+  uint8_t* out = a.out + (b * a.hkv + hk) * G * kRowBytes;
   if (len == 0) {  // nothing to attend to: zeros
     for (int i = threadIdx.x; i < G * kRowBytes / 16; i += kAttnThreads)
       st16(out + i * 16, u32x4{0u, 0u, 0u, 0u});
@@ -176,22 +171,14 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   // 64 contiguous bytes of each of the 16 rows): bf16, step s = r covers dims
   // 8*(4s+g) .. +7; fp8, a chunk holds 16 codes, step s = 2r+h covers dims
   // 16*(4r+g) + 8h .. +7, the q chunk 8r + 2g + h.
-  // The operand is the same for the four waves: it is kept in LDS (wave w
-  // writes steps 2w, 2w+1) and read back at each MFMA. Held in registers it
-  // took 32 VGPRs per lane and, with the rest, kept the kernel at two waves
-  // per SIMD; from LDS it runs at three. On the decode shape (batch 256,
-  // lognormal lengths) that measured +1.4 % for bf16 pools and within 1 % for
-  // fp8 against two waves with the operand in registers, and 4-5 % faster than
-  // three waves with it in registers (which spill): the kernel is not held
-  // back by the loads in flight.
-  const uint8_t* qrow = a.q + ((b * hkv + hk) * G + (n < G ? n : 0)) * kRowBytes;
+  u32x4 qb[8];
+  const uint8_t* qrow = a.q + ((b * a.hkv + hk) * G + (n < G ? n : 0)) * kRowBytes;
 #pragma unroll
-  for (int s = 2 * wave; s < 2 * wave + 2; ++s) {
+  for (int s = 0; s < 8; ++s) {
     const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
-    q_lds[s][lane] = n < G ? ld16(qrow + chunk * 16) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 w = n < G ? ld16(qrow + chunk * 16) : u32x4{0u, 0u, 0u, 0u};
+    qb[s] = w;
   }
-  __syncthreads();
-  auto qop = [&](int s) -> u32x4 { return q_lds[s][lane]; };
   float m_run = -INFINITY, l_run = 0.f;  // head n
   float o[G][4];
 #pragma unroll
@@ -199,7 +186,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[h][j] = 0.f;
 
-  const int64_t tok_stride = hkv * kCodeRow;
+  const int64_t tok_stride = (int64_t)a.hkv * kCodeRow;
   const int64_t pages = (len + kPageTokens - 1) / kPageTokens;
   const int64_t p_end = (c + 1) * (int64_t)kChunkPages < pages ? (c + 1) * (int64_t)kChunkPages : pages;
   const int32_t* trow = a.table + b * a.tstride;
@@ -216,7 +203,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   if (badmask && lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
   const int32_t pid_v = bad ? 0 : pid_raw;
   auto page_row = [&](int q) {  // page q's first (token, KV head) row; q >= np: page np-1
-    return (int64_t)__builtin_amdgcn_readlane(pid_v, q < np ? q : np - 1) * kPageTokens * hkv +
+    return (int64_t)__builtin_amdgcn_readlane(pid_v, q < np ? q : np - 1) * kPageTokens * a.hkv +
            hk;
   };
   // Software pipeline over iterations of PPI pages: the next iteration's K
@@ -236,20 +223,10 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
 #pragma unroll
       for (int r = 0; r < 4; ++r) ka[u][r] = ld16(kp + 16 * (4 * r + g));
       // (one load and shuffles instead: 1 % faster, 18 more VGPRs)
-      if constexpr (HKV == 1) {  // row is a page's first token: 64-byte aligned scales
-        const f32x4 k4 = *reinterpret_cast<const f32x4*>(a.ks + row + 4 * g);
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(a.vs + row + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sk[u][i] = k4[i];
-          svs[u][i] = v4[i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sk[u][i] = a.ks[row + (int64_t)(4 * g + i) * hkv];
-          svs[u][i] = a.vs[row + (int64_t)(4 * g + i) * hkv];
-        }
+      for (int i = 0; i < 4; ++i) {
+        sk[u][i] = a.ks[row + (int64_t)(4 * g + i) * a.hkv];
+        svs[u][i] = a.vs[row + (int64_t)(4 * g + i) * a.hkv];
       }
     } else {
 #pragma unroll
@@ -284,10 +261,10 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].x, ka[u][r].y),
-                                                          __builtin_bit_cast(bf16x8, qop(2 * r)),
+                                                          __builtin_bit_cast(bf16x8, qb[2 * r]),
                                                           sc[u], 0, 0, 0);
           sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].z, ka[u][r].w),
-                                                          __builtin_bit_cast(bf16x8, qop(2 * r + 1)),
+                                                          __builtin_bit_cast(bf16x8, qb[2 * r + 1]),
                                                           sc[u], 0, 0, 0);
         }
 #pragma unroll
@@ -298,7 +275,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
       } else {
 #pragma unroll
         for (int s = 0; s < 8; ++s)
-          sc[u] = mfma16<F16>(ka[u][s], qop(s), sc[u]);
+          sc[u] = mfma16<F16>(ka[u][s], qb[s], sc[u]);
       }
       load_k(u, nrow[u]);
     }
@@ -405,7 +382,7 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
     if (nch == 1) {
       reinterpret_cast<uint16_t*>(out + h * kRowBytes)[d] = out_bits<F16>(L > 0.f ? O / L : 0.f);
     } else {
-      const int64_t at = ((b * hkv + hk) * a.chunks + c) * G + h;
+      const int64_t at = ((b * a.hkv + hk) * a.chunks + c) * G + h;
       a.part[at * kHeadDim + d] = O;
       if (d == 0) {
         a.ml[at * 2] = M;
@@ -415,41 +392,22 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t
   }
 }
 
-// Bytes of dynamic LDS the work list of `pairs` (sequence, KV head) pairs
-// takes: first[pairs + 1] and tail_pair[pairs] (int32), tail_key[pairs]
-// (bytes), for pairs rounded up to a multiple of kPairClass.
-inline int attn_list_lds(int pairs) {
-  const int cap = (pairs + kPairClass - 1) / kPairClass * kPairClass;
-  return (4 * (cap + 1) + 4 * cap + cap + 15) / 16 * 16;
-}
-
-// OCC: waves per SIMD the compiler must leave room for (the second bound):
-// three up to four query heads per KV head (fp8 167 VGPRs, bf16 157, with the
-// query operand in LDS; four spilled 11-41), two for eight. Without a bound
-// the G = 8 kernels take 256 VGPRs plus accumulation registers, one wave per
-// SIMD. The work list lives in dynamic LDS sized to the launch's pairs, so
-// that LDS (29.7 KB of tiles plus 2.3 KB of list at 256 pairs) does not cap
-// the occupancy first; with the list at its old fixed 4096 pairs and the
-// query operand in registers, both LDS and VGPRs held it at two.
-template <int G, bool FP8, bool F16, int HKV, int OCC>
-__global__ __launch_bounds__(kAttnThreads, OCC) void attn_chunk_kernel(AttnArgs a) {
+template <int G, bool FP8, bool F16>
+// two workgroups per CU: without the bound the G = 8 kernels take 256 VGPRs
+// plus accumulation registers, one wave per SIMD
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   __shared__ float p_lds[kAttnWaves][kIterTokens][16];  // [wave][token][head] probabilities
   __shared__ float al_lds[kAttnWaves][16];              // [wave][head] rescale factor
   __shared__ float m_w[kAttnWaves][G], l_w[kAttnWaves][G];
   __shared__ __attribute__((aligned(16))) float o_w[kAttnWaves][G][kHeadDim];
-  __shared__ u32x4 q_lds[8][64];  // the query heads' MFMA operand, per step and lane
   // The work list, the same in every workgroup: first the full 1024-token
   // chunks of all (sequence, KV head) pairs, pair-major, then each pair's
   // last, shorter chunk (or the zeros of an empty pair) with the longest
   // first, so that the short items fill the end of the launch.
-  // dynamic LDS (attn_list_lds(a.pairs) bytes): first[pairs + 1], the first
-  // full-chunk item of each pair; tail_pair[pairs], the pairs with a short
-  // chunk, longest first; tail_key[pairs], its length class or kTailNone
-  extern __shared__ __attribute__((aligned(16))) int32_t attn_list[];
-  int32_t* const first = attn_list;
-  int32_t* const tail_pair = attn_list + a.pairs + 1;
-  uint8_t* const tail_key = reinterpret_cast<uint8_t*>(tail_pair + a.pairs);
+  __shared__ int32_t first[kMaxPairs + 1];  // first full-chunk item of each pair
+  __shared__ int32_t tail_pair[kMaxPairs];  // pairs with a short chunk, longest first
+  __shared__ uint8_t tail_key[kMaxPairs];   // its length class, or kTailNone
   __shared__ int32_t class_at[kTailClasses];         // next free slot of each class
   __shared__ int32_t class_wave[kAttnWaves][kTailClasses];
   __shared__ int32_t wave_tot[kAttnWaves];
@@ -464,8 +422,7 @@ __global__ __launch_bounds__(kAttnThreads, OCC) void attn_chunk_kernel(AttnArgs 
     const int pr = base + tid;
     int32_t cnt = 0;
     if (pr < a.pairs) {
-      const int32_t hkv = HKV ? HKV : a.hkv;
-      const int64_t len = attn_len(a, pr / hkv, blockIdx.x == 0 && pr % hkv == 0);
+      const int64_t len = attn_len(a, pr / a.hkv, blockIdx.x == 0 && pr % a.hkv == 0);
       cnt = (int32_t)(len / kChunk);
       const int32_t rem = (int32_t)(len % kChunk);
       const bool tail = rem != 0 || len == 0;  // an empty pair still zeroes its output
@@ -566,12 +523,11 @@ __global__ __launch_bounds__(kAttnThreads, OCC) void attn_chunk_kernel(AttnArgs 
     }
     pair = __builtin_amdgcn_readfirstlane(pair);
     c = __builtin_amdgcn_readfirstlane(c);
-    const int32_t hkv = HKV ? HKV : a.hkv;
-    const int64_t b = pair / hkv, hk = pair % hkv;
+    const int64_t b = pair / a.hkv, hk = pair % a.hkv;
     const int64_t len = attn_len(a, b, false);
     if (c < 0) c = (int32_t)(len / kChunk);
-    attn_chunk<G, FP8, F16, HKV>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w,
-                                 l_w, o_w, q_lds);
+    attn_chunk<G, FP8, F16>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w, l_w,
+                       o_w);
   }
 }
 
@@ -617,52 +573,34 @@ inline int64_t attn_chunks(int32_t max_seq_len) {
   return ((int64_t)max_seq_len + kChunk - 1) / kChunk;
 }
 
-// Waves per SIMD the chunk kernel is compiled for (see attn_chunk_kernel).
-template <int G, bool FP8>
-constexpr int attn_occ() { return G <= 4 ? 3 : 2; }
-
 // Workgroups of the chunk kernel: as many as are resident at once (CUs x the
-// kernel's occupancy with the launch's work-list LDS), so that every
+// kernel's occupancy, 2 per CU for four query heads), so that every
 // workgroup's static first item starts at once and the counter hands out the
-// rest in list order. A grid of 4 per CU, when only 2 were resident, left the
-// second half's first items, full chunks, to the end of the launch: 304.7
-// against 295.4 us per bf16 launch at batch 256, 102.4 against 100.4 us in
-// the serving workload. Cached per device and list size class.
-template <int G, bool FP8, bool F16, int HKV>
-int attn_grid(int pairs) {
-  constexpr int kClasses = kMaxPairs / kPairClass;
-  static int grid[64][kClasses] = {};
+// rest in list order. A grid of 4 per CU left the second half's first items,
+// full chunks, to the end of the launch: 304.7 against 295.4 us per bf16
+// launch at batch 256, 102.4 against 100.4 us in the serving workload.
+template <int G, bool FP8, bool F16>
+int attn_grid() {
+  static int grid[64] = {};
   int dev = 0;
-  const int cls = pairs <= 0 ? 0 : (pairs - 1) / kPairClass;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || cls >= kClasses) return 512;
-  if (grid[dev][cls] == 0) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (grid[dev] == 0) {
     int n = 0, per = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per, attn_chunk_kernel<G, FP8, F16, HKV, attn_occ<G, FP8>()>, kAttnThreads,
-            attn_list_lds((cls + 1) * kPairClass)) != hipSuccess ||
-        per <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_chunk_kernel<G, FP8, F16>,
+                                                     kAttnThreads, 0) != hipSuccess || per <= 0)
       per = 2;
-    grid[dev][cls] = n * per;
+    grid[dev] = n * per;
   }
-  return grid[dev][cls];
+  return grid[dev];
 }
 
 template <int G, bool FP8, bool F16>
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  // one KV head, and for fp8 scale planes aligned for 16-byte loads
-  const bool one =
-      a.hkv == 1 && (!FP8 || ((uintptr_t)a.ks % 16 == 0 && (uintptr_t)a.vs % 16 == 0));
-  if (one)
-    hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16, 1, attn_occ<G, FP8>()>),
-                       dim3((unsigned)attn_grid<G, FP8, F16, 1>(a.pairs)), dim3(kAttnThreads),
-                       attn_list_lds(a.pairs), st, a);
-  else
-    hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16, 0, attn_occ<G, FP8>()>),
-                       dim3((unsigned)attn_grid<G, FP8, F16, 0>(a.pairs)), dim3(kAttnThreads),
-                       attn_list_lds(a.pairs), st, a);
+  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16>), dim3((unsigned)attn_grid<G, FP8, F16>()),
+                     dim3(kAttnThreads), 0, st, a);
   // the merge kernel also resets the work counter: one workgroup when no
   // sequence spans two chunks
   hipLaunchKernelGGL((attn_merge_kernel<G, F16>), dim3(a.chunks > 1 ? (unsigned)(a.pairs * G) : 1u),

@@ -312,9 +312,9 @@ def test_fp8_decode_config_shape_against_oracle():
 
 @pytest.mark.parametrize("batch,Hkv", [(4096, 1), (1500, 2), (300, 1)])
 def test_work_list_sizes(batch, Hkv):
-    # the chunk kernel's work list lives in LDS sized to batch x KV heads (in
-    # steps of 256 pairs, up to 4096): every size class, including the
-    # largest, where LDS caps the occupancy, over bf16 and fp8 pools
+    # the chunk kernel's work list (one entry per sequence and KV head, up to
+    # 4096, in LDS) at its largest, at more than one round of its 256-pair
+    # passes and at one round, over bf16 and fp8 pools
     rng = np.random.default_rng(37 + batch)
     lens = rng.integers(0, 1200, batch)
     lens[::97] = 2048 + rng.integers(0, 2048, len(lens[::97]))  # some two- and three-chunk pairs
