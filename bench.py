@@ -567,7 +567,7 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
                              ratios.get("append_fp8_kernel")),
             _kernel_roofline("append_fp8_kernel<1> (mkv_append_fp8, one launch per layer)",
                              append_bytes, _timed(per_layer, "append") / L,
-                             ratios.get("append_fp8_kernel"))],
+                             ratios.get("append_fp8_kernel_per_layer"))],
             "fp8_prefill_hbm_counters.md"),
     }
     if with_cpu:
