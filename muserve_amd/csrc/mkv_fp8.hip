@@ -104,10 +104,12 @@ __device__ __forceinline__ u32x4 quantise_row(const u32x4 r0, const u32x4 r1, fl
 // the rows, grid.y is layer * 2 + K|V. The slot and both source loads are
 // issued together; a group whose row is past the end exits as a whole, so the
 // shuffles only ever read lanes of the same live row. Source rows are read
-// once and pool rows are not read back this step: non-temporal loads and
-// stores (6 % faster than ordinary ones on the chunked-prefill shape; more
-// rows per group, K and V in one workgroup, two rows per group, 128- or
-// 512-thread workgroups and a persistent grid measured no faster).
+// once and pool rows are not read back this step: non-temporal loads and code
+// stores, 6 % faster than ordinary ones on the chunked-prefill shape. The
+// scales take ordinary stores, 1.3 % faster there than non-temporal ones (a
+// page's 16 scales arrive as four 16-byte pieces from four waves). More rows
+// per group, K and V in one workgroup, two rows per group, 128- or 512-thread
+// workgroups and a persistent grid measured no faster.
 // HEADS is the head count when it is 1 or 2 (0: any, read from the
 // arguments): a runtime 32-bit division ahead of the first load made the
 // one-head launch 10 % slower on the chunked-prefill shape.
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void append_fp8_kernel(AppendFp8Args a) {
   if (lane == 0) {
     float* sp = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(is_v ? a.v_scale : a.k_scale) +
                                          (int64_t)l * a.scale_layer_stride);
-    __builtin_nontemporal_store(scale, sp + slot * nh + h);
+    sp[slot * nh + h] = scale;
   }
 }
 
