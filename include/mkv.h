@@ -658,7 +658,8 @@ int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_
  * (device uint64, caller-zeroed): [0] v_cvt_pk_fp8_f32 results that differ
  * from RNE e4m3fn (|x| <= 448, or not NaN for NaN), [1] v_cvt_pk_bf16_f32
  * results that differ from RNE bf16, [2] v_cvt_pk_f32_fp8 decodes that differ
- * from the OCP value, [3] fp8 codes where the quantiser's reciprocal divide
+ * from the OCP value, and v_cvt_scalef32_pk_bf16_fp8 (scale 1) decodes that
+ * differ from its bf16, [3] fp8 codes where the quantiser's reciprocal divide
  * differs from x / scale, [4] such quotients with |x/scale| >= 2^-12 whose
  * bits differ, [5] fp32 patterns checked (2^32), [6] (absmax, x) pairs
  * checked. Every mismatch count is 0 on a correct gfx950. No reference

@@ -5,8 +5,9 @@
 // halves) with the integer RNE encoder of mkv_common.h (which equals torch's
 // CPU cast on all 2^32 inputs) for |x| <= 448 and NaN, and v_cvt_pk_bf16_f32
 // with round-to-nearest-even bf16; v_cvt_pk_f32_fp8 (both halves) with the
-// OCP decode of all 256 codes; and div_by_recip with IEEE division over the
-// fp8 quantiser's whole domain (every non-negative bf16 absmax pattern,
+// OCP decode of all 256 codes, and v_cvt_scalef32_pk_bf16_fp8 at scale 1
+// (both halves) with the bf16 of that decode; and div_by_recip with IEEE
+// division over the fp8 quantiser's whole domain (every non-negative bf16 absmax pattern,
 // inf and NaN included, as divisor source; every bf16 x with |x| <= absmax,
 // or every x for a NaN absmax; NaN codes compare equal). Runs in a few
 // milliseconds.
@@ -65,6 +66,20 @@ __global__ __launch_bounds__(256) void check_conversions_kernel(unsigned long lo
     const float got[4] = {lo.x, lo.y, hi.x, hi.y};
     for (int k = 0; k < 4; ++k)
       c[kDecode] += (want != want) ? (got[k] == got[k]) : (f32_bits(got[k]) != f32_bits(want));
+    // and straight to bf16 through v_cvt_scalef32_pk_bf16_fp8 at scale 1 (the
+    // decode attention's K operand): every e4m3fn value is a bf16 value, so
+    // the result must be exact; the four bytes of the word hold four codes
+    const uint32_t codes[4] = {code, code ^ 0x55u, code ^ 0xaau, code ^ 0xffu};
+    const int mixed = (int)(codes[0] | (codes[1] << 8) | (codes[2] << 16) | (codes[3] << 24));
+    const uint32_t b_lo = __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(mixed, 1.0f, false));
+    const uint32_t b_hi = __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(mixed, 1.0f, true));
+    const uint32_t bgot[4] = {b_lo & 0xffffu, b_lo >> 16, b_hi & 0xffffu, b_hi >> 16};
+    for (int k = 0; k < 4; ++k) {
+      const float w = e4m3fn_to_f32(codes[k]);
+      c[kDecode] += (w != w) ? !bf16_is_nan(bgot[k]) : (bgot[k] != f32_to_bf16_rne(w));
+    }
   }
   // division: absmax bf16 pattern in the high 16 bits of v (all non-negative
   // patterns: finite, +inf and the NaNs), x in the low 16
