@@ -1185,9 +1185,9 @@ def run_decode_attn(steps: int, warmup: int, with_cpu: bool, fp8: bool = False) 
         "tokens_per_s": round(B / step_s, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": ("mkv_decode_attention_fp8 = attn_chunk_kernel<4, true> + "
+            "kernel": ("mkv_decode_attention_fp8 = attn_span_kernel<4, true> + "
                        "attn_merge_kernel<4>" if fp8 else
-                       "mkv_decode_attention_bf16 = attn_chunk_kernel<4, false> + "
+                       "mkv_decode_attention_bf16 = attn_span_kernel<4, false> + "
                        "attn_merge_kernel<4>"),
             "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -1482,9 +1482,9 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
     achieved = attn_b / attn_launches / (attn_ms / 1e3) / 1e9
     ratio = None if hybrid else counter_ratios("sched_serving_kernel_trace.md").get(
         "attn_fp8" if fp8 else "attn")
-    kernel = ("mkv_decode_attention_fp8 = attn_chunk_kernel<4, true> + attn_merge_kernel<4>"
+    kernel = ("mkv_decode_attention_fp8 = attn_span_kernel<4, true> + attn_merge_kernel<4>"
               if fp8 else
-              "mkv_decode_attention_bf16 = attn_chunk_kernel<4, false> + attn_merge_kernel<4>")
+              "mkv_decode_attention_bf16 = attn_span_kernel<4, false> + attn_merge_kernel<4>")
     res = {
         "metric": ("achieved HBM GB/s (% of 8 TB/s) of continuous-batching serving steps "
                    "(scheduler step plan + KV append + paged decode attention"

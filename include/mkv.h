@@ -524,19 +524,20 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
  *   k_cache, v_cache: [num_pages, 16, num_kv_heads, 256] bf16 (one layer's
  *            planes of the pool), 16-byte aligned;
  *   page_table: [batch][table_stride] int32, table_width valid columns;
- *   max_seq_len: an upper bound of seq_lens that sizes the launch (1024-token
- *            chunks per sequence); longer sequences are cut to it;
+ *   max_seq_len: an upper bound of seq_lens; longer sequences are cut to it;
  *   workspace: mkv_decode_attention_workspace_bytes(...) bytes, 16-byte
- *            aligned and zero-filled before its first use: it holds the work
- *            counters (every call leaves them zero again) and, when
- *            max_seq_len > 1024, the 1024-token chunks' partial softmax states
- *            that a second kernel merges. Calls that share a workspace must
- *            be ordered (one stream).
+ *            aligned, contents irrelevant between calls: it receives the
+ *            pairs' page prefix and the partial softmax states of pairs cut
+ *            between the waves' page spans, which a second kernel merges.
+ *            Calls that share a workspace must be ordered (one stream).
  * head_dim must be 256, G one of 1, 2, 4, 8, batch * num_kv_heads at most
- * 4096 and max_seq_len at most 2^24 (MKV_E_UNSUPPORTED). A page id
- * outside [0, num_pages) skips that page's tokens and sets MKV_DEVERR_PAGE; a
- * length above 16*table_width or max_seq_len is cut to it and sets
- * MKV_DEVERR_TABLE; a sequence of length 0 gets zeros.
+ * 4096, max_seq_len at most 2^24 and batch * num_kv_heads * ceil(max_seq_len
+ * / 16) below 2^31 (MKV_E_UNSUPPORTED). A page id outside [0, num_pages)
+ * skips that page's tokens and sets MKV_DEVERR_PAGE; a length above
+ * 16*table_width or max_seq_len is cut to it and sets MKV_DEVERR_TABLE; a
+ * sequence of length 0 gets zeros. The workspace size depends on the pair
+ * count and G (and the current device's CU count), not on max_seq_len; it
+ * returns -1 for an unsupported shape.
  */
 int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t num_kv_heads,
                                              int32_t num_q_heads, int32_t max_seq_len);
@@ -550,20 +551,20 @@ int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_
 
 /*
  * mkv_decode_attention_bf16 without a workspace argument and without any
- * allocation: the work counters and chunk partials live in a file-scope
- * device array of the library (48 MiB, one copy per GPU, held until the
- * process ends), whose address the first call on each device looks up with
- * that device current. No counterpart in the reference: it is for callers
- * that cannot call hipMalloc (code under HIP graph capture, tight serving
- * loops, harnesses that forbid allocation). The caller still passes the
- * inputs, out and err. Limit: batch x num_q_heads x ceil(max_seq_len / 1024)
- * chunk states must fit the array (at most 48,770 of them when max_seq_len >
- * 1024, e.g. batch 256 x 4 query heads up to 47 x 1024 tokens); a larger call
- * returns MKV_E_UNSUPPORTED and launches nothing. Calls on one GPU share the
- * array: calls that overlap on one GPU (different streams, or threads without
- * ordering) race and must not be issued; calls ordered on one stream are
- * safe. Results are bit-for-bit those of mkv_decode_attention_bf16 (the same
- * kernels). Same arguments, limits and error bits otherwise.
+ * allocation: the page prefix and partial states live in a file-scope device
+ * array of the library (48 MiB, one copy per GPU, held until the process
+ * ends), whose address the first call on each device looks up with that
+ * device current. No counterpart in the reference: it is for callers that
+ * cannot call hipMalloc (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). The caller still passes the inputs, out
+ * and err. Limit: mkv_decode_attention_workspace_bytes(...) of the call must
+ * fit the array (on MI355X every supported shape needs at most ~17 MB); an
+ * unsupported shape or a larger need returns MKV_E_UNSUPPORTED and launches
+ * nothing. Calls on one GPU share the array: calls that overlap on one GPU
+ * (different streams, or threads without ordering) race and must not be
+ * issued; calls ordered on one stream are safe. Results are bit-for-bit
+ * those of mkv_decode_attention_bf16 (the same kernels). Same arguments,
+ * limits and error bits otherwise.
  */
 int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_cache, const void* v_cache,
                                       int64_t num_pages, int32_t num_kv_heads,
@@ -608,6 +609,24 @@ int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_c
                              int32_t max_seq_len, float softmax_scale, void* out,
                              void* workspace, int64_t workspace_bytes, int32_t* err,
                              void* stream);
+
+/*
+ * Decode attention over contiguous per-sequence caches instead of the pool:
+ * k_cache / v_cache are [batch, seq_rows, num_kv_heads, 256] (fp16 != 0: fp16,
+ * else bf16; q and out of the same type), sequence b attending to its first
+ * seq_lens[b] rows. This is attn_decode with page_table None (the reference
+ * forwards None to its kernel, muserve/kernels/attention.py:33-42), e.g. over
+ * the padded [B, Lpad, H, D] layout mkv_gather_bf16 writes. Rows past
+ * seq_rows are never read: lengths above seq_rows (or max_seq_len) are cut
+ * and set MKV_DEVERR_TABLE. Same workspace, limits and numerics as
+ * mkv_decode_attention_bf16.
+ */
+int mkv_decode_attention_contig(const void* q, const void* k_cache, const void* v_cache,
+                                int32_t fp16, int32_t num_kv_heads, int32_t num_q_heads,
+                                int32_t head_dim, int64_t seq_rows, const int32_t* seq_lens,
+                                int32_t batch, int32_t max_seq_len, float softmax_scale,
+                                void* out, void* workspace, int64_t workspace_bytes,
+                                int32_t* err, void* stream);
 
 /* ---- self-test ------------------------------------------------------------ */
 

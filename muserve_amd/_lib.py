@@ -97,6 +97,8 @@ SIGNATURES: dict[str, list] = {
                                  _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
                                  _I32, _I32, _F32, _P, _P, _I64, _P, _P],
+    "mkv_decode_attention_contig": [_P, _P, _P, _I32, _I32, _I32, _I32, _I64, _P, _I32, _I32, _F32,
+                                    _P, _P, _I64, _P, _P],
 }
 _INT64_RESULT = {"mkv_bm_state_bytes", "mkv_decode_attention_workspace_bytes",
                  "mkv_prefill_attention_workspace_bytes"}

@@ -2,34 +2,45 @@
 //
 // One decode query token per sequence attends to the first seq_lens[b] cached
 // tokens of its block table: for each of the G query heads sharing a KV head,
-// softmax(q k^T * scale) v over the sequence, computed in fp32, written as
-// bf16. This is the interface of the paged decode kernel the reference wraps
-// (muserve/kernels/attention.py:29-42) and the math of its contiguous decode
-// path (muserve/model/qwen35_layer_v2.py:493-502), without the padded gather.
+// softmax(q k^T * scale) v over the sequence, computed in fp32, written in
+// the pool's 16-bit type. This is the interface of the paged decode kernel the
+// reference wraps (muserve/kernels/attention.py:29-42) and the math of its
+// contiguous decode path (muserve/model/qwen35_layer_v2.py:493-502), without
+// the padded gather.
 //
-// Each K/V row is read once, 4 flop per byte at G = 4, so the bound is HBM.
-// A workgroup (4 waves) takes a 1024-token chunk of one sequence and KV head;
-// a wave takes one 16-token page at a time:
-//   * scores on MFMA (v_mfma_f32_16x16x32_bf16, 8 steps over head_dim 256):
-//     A = the K page, 16 contiguous bytes of a K row per lane loaded straight
-//     from the pool (row = lane % 16, 16-byte chunk 4*step + lane / 16);
-//     B = the G query heads (columns >= G zero) in the same dim order, held
-//     in registers for the whole chunk; C = 4 scores per lane (tokens
-//     4*(lane/16) + i, head lane % 16);
-//   * online softmax per head in fp32 (exp2, log2(e) folded into the scale);
-//     the page's probabilities go through a wave-private LDS tile;
-//   * P V on the VALU: a lane owns dims 4*lane .. 4*lane+3 of all G heads, so
-//     a V row is one coalesced 512-byte load per wave, with no transpose;
-//   * the waves' partial softmax states merge in LDS. A one-chunk sequence
-//     writes its normalised output; longer ones write (max, sum, unnormalised
-//     output) per chunk to the caller's workspace and a second kernel merges
-//     them, one workgroup per (sequence, query head).
-// The chunks of all sequences form one list (sequence-major; every workgroup
-// computes the prefix of the chunk counts in LDS) that a grid of a few
-// workgroups per CU drains: the first item of each workgroup is its own
-// index, the rest come from an atomic counter. No workgroup is launched for a
-// chunk beyond its sequence's end, and the load balances whatever the
-// lengths. The merge kernel, which runs next, resets the counter.
+// Each cached K/V byte is read once and carries G flop, so the bound is HBM.
+// What decides the rate is how many page reads are in flight and how they are
+// issued (on MI355X random 8 KiB page reads stream at 6.8 TB/s only with the
+// non-temporal bit set; without it ~6.0 TB/s whatever the depth):
+//   * Work split: the (sequence, KV head) pairs' pages form one flat list
+//     (pair-major, pages in table order). Every wave of the grid (the
+//     resident workgroups, 4 waves each) takes an equal contiguous span of
+//     it. No counters, no atomics, no tail of short items: spans differ by
+//     at most one page. Each workgroup computes the pairs' page prefix in LDS
+//     in its prologue; workgroup 0 also leaves it in the workspace.
+//   * Loads: a wave streams its span's K and V planes page by page straight
+//     into its own LDS slots with global_load_lds_dwordx4 (16 bytes a lane,
+//     1 KiB per instruction, non-temporal). The next page's K is issued as
+//     soon as this page's scores have read the K slot, its V as soon as P V
+//     has read the V slot, so up to a page is in flight per wave while the
+//     wave computes. Completion is tracked with exact vmcnt waits. A pair's
+//     query rows ride the same stream, ahead of its first K plane. Page ids
+//     come from the table through scalar loads, which do not touch vmcnt.
+//   * LDS layout: chunk c of a cached row r is stored at chunk c ^ (r & 15)
+//     of that row (the DMA lanes fetch the permuted chunks), so the MFMA
+//     operand reads of 16 rows x 16 bytes hit 16 distinct bank groups.
+//   * Scores on MFMA (v_mfma_f32_16x16x32_{bf16,f16}; fp8 codes converted
+//     exactly to bf16): A = the 16 K rows of the page from LDS, B = the G
+//     query heads (zero columns above G) held in registers for the pair.
+//     Online softmax per head in fp32 (exp2 with log2 e folded into the
+//     scale); the page's probabilities go through a wave-private LDS tile.
+//   * P V on the VALU: a lane owns 8 dims of every head over 8 of the 16
+//     tokens (half waves take the two halves of the page); a V row is one
+//     16-byte LDS read per lane. The halves are summed at the segment's end.
+//   * A pair wholly inside one span is finished by its wave (normalised
+//     output). A pair cut by span boundaries leaves (max, sum, unnormalised
+//     output) per piece in the workspace, at most two per wave; a second
+//     kernel merges them and also writes the zeros of empty pairs.
 #include <math.h>
 
 #include <mutex>
@@ -45,35 +56,34 @@ typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHeadDim = 256;
-constexpr int kRowBytes = kHeadDim * 2;  // one bf16 K or V row of one KV head
+constexpr int kRowBytes = kHeadDim * 2;  // one 16-bit K or V row of one KV head
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kPageTokens = 16;
-constexpr int kChunk = 1024;  // tokens per work item (512 measured 3 % slower, 2048 4 %)
-constexpr int kChunkPages = kChunk / kPageTokens;
-constexpr int kMaxPairs = 4096;  // batch x KV heads whose chunk prefix fits in LDS
-constexpr int kPagesPerIter = 1;  // pages per wave iteration (2 measured 1.5 % slower on fp8)
-constexpr int kIterTokens = kPagesPerIter * kPageTokens;
-constexpr int kTailClasses = 32;  // length classes of the short chunks (32 tokens each)
-constexpr int kTailNone = 255;    // a pair without a short chunk
+constexpr int kMaxPairs = 4096;  // batch x KV heads whose page prefix fits in LDS
+constexpr int64_t kHeaderBytes = 256;
+constexpr size_t kLdsPerCu = 160 * 1024;  // MI355X
 
 struct AttnArgs {
-  const uint8_t* q;  // [B, Hkv * G, 256] bf16
-  const uint8_t* k;  // [P, 16, Hkv, 256] bf16, or e4m3fn codes
+  const uint8_t* q;  // [B, Hkv * G, 256] 16-bit
+  const uint8_t* k;  // [P, 16, Hkv, 256] 16-bit or e4m3fn codes; contiguous mode [B, S, Hkv, 256]
   const uint8_t* v;
   const float* ks;   // fp8 caches: [P, 16, Hkv] fp32 scales of K and V
   const float* vs;
-  const int32_t* table;  // [B, tstride] int32
+  const int32_t* table;  // [B, tstride] int32 (paged mode)
   const int32_t* lens;   // [B] int32
-  uint8_t* out;          // [B, Hkv * G, 256] bf16
-  float* part;           // [B, Hkv, chunks, G, 256] unnormalised chunk outputs
-  float* ml;             // [B, Hkv, chunks, G, 2] chunk (max, sum), log2 units
-  int32_t* queue;        // [1]: next dynamic work item (zero between calls)
+  uint8_t* out;          // [B, Hkv * G, 256] 16-bit
+  int64_t* hdr;          // workspace header: [0] span S (pages per wave), [1] total pages T
+  int32_t* pre;          // [pairs + 1]: exclusive prefix of the pairs' page counts
+  float* part;           // [waves, 2, G, 256] unnormalised outputs of cut pairs' pieces
+  float* ml;             // [waves, 2, G, 2] their (max, sum), log2 units
   int64_t num_pages, tstride;
-  int32_t twidth, hkv, chunks, max_len, pairs;
-  float scale_log2;  // softmax_scale * log2(e)
+  int64_t seq_rows;      // contiguous mode: rows per sequence (0: paged)
+  int32_t twidth, hkv, max_len, pairs;
+  float scale_log2;      // softmax_scale * log2(e)
   int32_t* err;
 };
 
@@ -117,321 +127,133 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The sequence length the kernels use: clamped to what the table holds and
-// to the launch's bound (MKV_DEVERR_TABLE when clamped), 0 if negative.
-__device__ __forceinline__ int64_t attn_len(const AttnArgs& a, int64_t b, bool report) {
-  int64_t len = ld_const(a.lens + b);
-  const int64_t cap = (int64_t)a.twidth * kPageTokens < a.max_len
-                          ? (int64_t)a.twidth * kPageTokens
-                          : (int64_t)a.max_len;
-  if (len > cap || len < 0) {
-    if (report) raise_err(a.err, MKV_DEVERR_TABLE);
-    len = len < 0 ? 0 : cap;
-  }
-  return len;
-}
-
 // Eight e4m3fn codes (little-endian bytes of lo, hi) as eight bf16: exact,
 // every e4m3fn value is a bf16 value. gfx950 converts a code pair straight to
-// a bf16 pair (v_cvt_scalef32_pk_bf16_fp8, scale 1): four instructions per
-// eight codes instead of eight through fp32 (mkv_check_conversions checks it
-// on every code).
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
+// a bf16 pair (v_cvt_scalef32_pk_bf16_fp8, scale 1; mkv_check_conversions
+// checks it on every code).
+__device__ __forceinline__ u32x4 fp8x8_bf16(uint32_t lo, uint32_t hi) {
   const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)lo, 1.0f, false);
   const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)lo, 1.0f, true);
   const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)hi, 1.0f, false);
   const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)hi, 1.0f, true);
-  return bf16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+  return u32x4{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+               __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
 }
 
-// One 1024-token chunk of one (sequence, KV head). FP8: the caches hold
-// e4m3fn codes with an fp32 scale per (token, KV head); a token's score is
-// scale_k * (q . codes) and its V weight p * scale_v, so the codes convert
-// exactly to bf16 MFMA operands and no product is rounded before the fp32
-// accumulation. F16: q, caches and out are fp16 instead of bf16.
-template <int G, bool FP8, bool F16>
-__device__ __forceinline__ void attn_chunk(const AttnArgs& a, int64_t b, int64_t hk, int64_t c,
-                                           int64_t len, int64_t nch,
-                                           float (&p_lds)[kAttnWaves][kIterTokens][16],
-                                           float (&al_lds)[kAttnWaves][16],
-                                           float (&m_w)[kAttnWaves][G], float (&l_w)[kAttnWaves][G],
-                                           float (&o_w)[kAttnWaves][G][kHeadDim]) {
-  constexpr int kCodeRow = FP8 ? kHeadDim : kRowBytes;  // bytes of one cached K or V row
-  constexpr int PPI = kPagesPerIter;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar page ids
-  const int n = lane & 15, g = lane >> 4;
-  uint8_t* out = a.out + (b * a.hkv + hk) * G * kRowBytes;
-  if (len == 0) {  // nothing to attend to: zeros
-    for (int i = threadIdx.x; i < G * kRowBytes / 16; i += kAttnThreads)
-      st16(out + i * 16, u32x4{0u, 0u, 0u, 0u});
-    return;
-  }
+// ---- direct-to-LDS loads and their completion ---------------------------------
+//
+// The loads are issued from inline assembly, so the compiler neither inserts
+// waits for them nor reorders LDS accesses across them ("memory" clobber);
+// every wait on them is explicit below. M0 holds the LDS destination of the
+// lane-0 bytes (the hardware adds 16 or 4 bytes per lane); the compiler keeps
+// nothing in M0 across these statements in this file (no LDS DMA builtins,
+// GWS, message or movrel instructions). Before a slot is refilled, the wave's
+// earlier LDS reads of it must have returned: lgkmcnt(0) first.
 
-  // The G query heads as the B operand, in the K operand's dim order. Lane
-  // group g loads the 16-byte chunks 4r+g of a K row (a load instruction reads
-  // 64 contiguous bytes of each of the 16 rows): bf16, step s = r covers dims
-  // 8*(4s+g) .. +7; fp8, a chunk holds 16 codes, step s = 2r+h covers dims
-  // 16*(4r+g) + 8h .. +7, the q chunk 8r + 2g + h.
-  u32x4 qb[8];
-  const uint8_t* qrow = a.q + ((b * a.hkv + hk) * G + (n < G ? n : 0)) * kRowBytes;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
-    const u32x4 w = n < G ? ld16(qrow + chunk * 16) : u32x4{0u, 0u, 0u, 0u};
-    qb[s] = w;
-  }
-  float m_run = -INFINITY, l_run = 0.f;  // head n
-  float o[G][4];
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[h][j] = 0.f;
-
-  const int64_t tok_stride = (int64_t)a.hkv * kCodeRow;
-  const int64_t pages = (len + kPageTokens - 1) / kPageTokens;
-  const int64_t p_end = (c + 1) * (int64_t)kChunkPages < pages ? (c + 1) * (int64_t)kChunkPages : pages;
-  const int32_t* trow = a.table + b * a.tstride;
-  // This wave's pages are p0 + 4q, q < np: their ids in one load, lane q
-  // holding page q. A page id outside the pool is flagged and its tokens
-  // masked (page 0 is read in its place), so the loop below has no branches
-  // and the compiler's load counting stays exact.
-  static_assert(kChunkPages / kAttnWaves <= 32, "a wave's page validity fits a 32-bit mask");
-  const int64_t p0 = c * (int64_t)kChunkPages + wave;
-  const int np = p_end > p0 ? (int)((p_end - p0 + kAttnWaves - 1) / kAttnWaves) : 0;
-  const int32_t pid_raw = lane < np ? trow[p0 + (int64_t)kAttnWaves * lane] : 0;
-  const bool bad = lane < np && (pid_raw < 0 || pid_raw >= a.num_pages);
-  const uint32_t badmask = (uint32_t)__ballot(bad);
-  if (badmask && lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
-  const int32_t pid_v = bad ? 0 : pid_raw;
-  auto page_row = [&](int q) {  // page q's first (token, KV head) row; q >= np: page np-1
-    return (int64_t)__builtin_amdgcn_readlane(pid_v, q < np ? q : np - 1) * kPageTokens * a.hkv +
-           hk;
-  };
-  // Software pipeline over iterations of PPI pages: the next iteration's K
-  // (and scales) are loaded once the score MFMAs have read this one's, and its
-  // V rows one by one as P V consumes this one's, into the same registers.
-  // Past the wave's last page the loads repeat that page (cache hits) and the
-  // tokens are masked.
-  typedef u32x4 KReg;
-  typedef typename std::conditional<FP8, uint32_t, u32x2>::type VReg;
-  constexpr int kKRegs = FP8 ? 4 : 8;
-  KReg ka[PPI][kKRegs];
-  VReg vr[PPI][kPageTokens];
-  float sk[PPI][4], svs[PPI][4];  // fp8: scales of tokens 4g+i
-  auto load_k = [&](int u, int64_t row) {
-    const uint8_t* kp = a.k + row * kCodeRow + n * tok_stride;
-    if constexpr (FP8) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ka[u][r] = ld16(kp + 16 * (4 * r + g));
-      // (one load and shuffles instead: 1 % faster, 18 more VGPRs)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sk[u][i] = a.ks[row + (int64_t)(4 * g + i) * a.hkv];
-        svs[u][i] = a.vs[row + (int64_t)(4 * g + i) * a.hkv];
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) ka[u][s] = ld16(kp + (4 * s + g) * 16);
-    }
-  };
-  auto load_v = [&](int u, int64_t row, int t) {
-    const uint8_t* vp = a.v + row * kCodeRow + t * tok_stride;
-    if constexpr (FP8)
-      vr[u][t] = *reinterpret_cast<const uint32_t*>(vp + lane * 4);
-    else
-      vr[u][t] = *reinterpret_cast<const u32x2*>(vp + lane * 8);
-  };
-  if (np > 0) {
-#pragma unroll
-    for (int u = 0; u < PPI; ++u) {
-      const int64_t row = page_row(u);
-      load_k(u, row);
-#pragma unroll
-      for (int t = 0; t < kPageTokens; ++t) load_v(u, row, t);
-    }
-  }
-  for (int q0 = 0; q0 < np; q0 += PPI) {
-    int64_t nrow[PPI];
-    f32x4 sc[PPI];
-    float skj[PPI][4], svj[PPI][4];
-#pragma unroll
-    for (int u = 0; u < PPI; ++u) {
-      nrow[u] = page_row(q0 + PPI + u);
-      sc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (FP8) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].x, ka[u][r].y),
-                                                          __builtin_bit_cast(bf16x8, qb[2 * r]),
-                                                          sc[u], 0, 0, 0);
-          sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_bf16(ka[u][r].z, ka[u][r].w),
-                                                          __builtin_bit_cast(bf16x8, qb[2 * r + 1]),
-                                                          sc[u], 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          skj[u][i] = sk[u][i];
-          svj[u][i] = svs[u][i];
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-          sc[u] = mfma16<F16>(ka[u][s], qb[s], sc[u]);
-      }
-      load_k(u, nrow[u]);
-    }
-
-    // online softmax for head n over this iteration's tokens 16u + 4g + i
-    float sv[PPI][4], pm = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < PPI; ++u) {
-      const int q = q0 + u;
-      const bool ok = q < np && ((badmask >> q) & 1u) == 0;
-      const int64_t tok0 = (p0 + (int64_t)kAttnWaves * q) * kPageTokens + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float score = FP8 ? sc[u][i] * skj[u][i] : sc[u][i];
-        sv[u][i] = ok && tok0 + i < len ? score * a.scale_log2 : -INFINITY;
-        pm = fmaxf(pm, sv[u][i]);
-      }
-    }
-    pm = fmaxf(pm, __shfl_xor(pm, 16));
-    pm = fmaxf(pm, __shfl_xor(pm, 32));
-    const float m_new = fmaxf(m_run, pm);
-    // -inf only while every page so far was masked: exponents then stay -inf
-    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_fast(m_run - m_ref);
-    float ps = 0.f;
-#pragma unroll
-    for (int u = 0; u < PPI; ++u)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pv = exp2_fast(sv[u][i] - m_ref);
-        ps += pv;
-        p_lds[wave][16 * u + 4 * g + i][n] = FP8 ? pv * svj[u][i] : pv;
-      }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-    if (g == 0) al_lds[wave][n] = alpha;
-    wave_sync();
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float al = al_lds[wave][h];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) o[h][jj] *= al;
-    }
-#pragma unroll
-    for (int u = 0; u < PPI; ++u)
-#pragma unroll
-      for (int t = 0; t < kPageTokens; ++t) {
-        float v0, v1, v2, v3;
-        if constexpr (FP8) {
-          const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[u][t], false);
-          const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[u][t], true);
-          v0 = lo.x;
-          v1 = lo.y;
-          v2 = hi.x;
-          v3 = hi.y;
-        } else if constexpr (F16) {
-          v0 = f16_lo(vr[u][t].x);
-          v1 = f16_hi(vr[u][t].x);
-          v2 = f16_lo(vr[u][t].y);
-          v3 = f16_hi(vr[u][t].y);
-        } else {
-          v0 = bf16_lo(vr[u][t].x);
-          v1 = bf16_hi(vr[u][t].x);
-          v2 = bf16_lo(vr[u][t].y);
-          v3 = bf16_hi(vr[u][t].y);
-        }
-        load_v(u, nrow[u], t);
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          const float pt = p_lds[wave][16 * u + t][h];
-          o[h][0] += pt * v0;
-          o[h][1] += pt * v1;
-          o[h][2] += pt * v2;
-          o[h][3] += pt * v3;
-        }
-      }
-    wave_sync();  // the next iteration rewrites this wave's tiles
-  }
-
-  // merge the waves' (max, sum, output) per head
-  if (g == 0 && n < G) {
-    m_w[wave][n] = m_run;
-    l_w[wave][n] = l_run;
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-    *reinterpret_cast<f32x4*>(&o_w[wave][h][4 * lane]) = f32x4{o[h][0], o[h][1], o[h][2], o[h][3]};
-  __syncthreads();
-  const int d = threadIdx.x;  // one dim per thread
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, m_w[w][h]);
-    float O = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float f = m_w[w][h] == -INFINITY ? 0.f : exp2_fast(m_w[w][h] - M);
-      O += f * o_w[w][h][d];
-      L += f * l_w[w][h];
-    }
-    if (nch == 1) {
-      reinterpret_cast<uint16_t*>(out + h * kRowBytes)[d] = out_bits<F16>(L > 0.f ? O / L : 0.f);
-    } else {
-      const int64_t at = ((b * a.hkv + hk) * a.chunks + c) * G + h;
-      a.part[at * kHeadDim + d] = O;
-      if (d == 0) {
-        a.ml[at * 2] = M;
-        a.ml[at * 2 + 1] = L;
-      }
-    }
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// A wave-uniform pointer in scalar registers (the compiler cannot always
+// prove uniformity through the index arithmetic).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+// 16 bytes per lane from base + voff (saddr form: base scalar, voff per lane)
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform_ptr(base))
+               : "memory");
+}
+// 4 bytes per lane from a per-lane 64-bit address
+__device__ __forceinline__ void dma4(const void* addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off nt"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(addr)
+               : "memory");
+}
+__device__ __forceinline__ void lds_reads_done() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void vm_wait_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most n vector-memory operations of this wave are
+// outstanding (n wave-uniform). The loads return in issue order, so the
+// loads issued before the youngest n are then complete.
+__device__ __forceinline__ void vm_wait(int n) {
+  switch (n) {
+#define MKV_VMW(k) \
+  case k: vm_wait_n<k>(); break;
+    MKV_VMW(0) MKV_VMW(1) MKV_VMW(2) MKV_VMW(3) MKV_VMW(4) MKV_VMW(5) MKV_VMW(6) MKV_VMW(7)
+    MKV_VMW(8) MKV_VMW(9) MKV_VMW(10) MKV_VMW(11) MKV_VMW(12) MKV_VMW(13) MKV_VMW(14)
+    MKV_VMW(15) MKV_VMW(16) MKV_VMW(17) MKV_VMW(18) MKV_VMW(19) MKV_VMW(20)
+#undef MKV_VMW
+    default: vm_wait_n<0>(); break;  // never taken: at most 17 loads follow a waited one
   }
 }
 
+// Geometry of one pool kind (bf16 / fp16 / fp8) and query-group size G.
+template <int G, bool FP8>
+struct Geo {
+  static constexpr int kCodeRow = FP8 ? kHeadDim : kRowBytes;  // bytes of a cached row
+  static constexpr int kPlane = kPageTokens * kCodeRow;        // a page's K (or V) bytes
+  static constexpr int kChunks = kCodeRow / 16;                // 16-byte chunks per row
+  static constexpr int kRowsPerIns = 1024 / kCodeRow;          // rows per 1 KiB instruction
+  static constexpr int kPlaneIns = kPlane / 1024;              // instructions per plane
+  static constexpr int kQBytes = G * kRowBytes < 1024 ? 1024 : G * kRowBytes;
+  static constexpr int kQIns = kQBytes / 1024;
+  static constexpr int kScaleBytes = FP8 ? 256 : 0;  // K scales, V scales (64 B each) + copies
+  static constexpr int kScaleIns = FP8 ? 1 : 0;
+  // per-wave LDS: K slot, V slot, scales, query rows, probability tile
+  static constexpr int kOffK = 0;
+  static constexpr int kOffV = kOffK + kPlane;
+  static constexpr int kOffS = kOffV + kPlane;
+  static constexpr int kOffQ = kOffS + kScaleBytes;
+  static constexpr int kOffP = kOffQ + kQBytes;
+  static constexpr int kWaveBytes = kOffP + kPageTokens * G * 4;
+  static_assert(kWaveBytes % 16 == 0, "16-byte aligned slots");
+};
+
+// Dynamic LDS of one workgroup: the pairs' page prefix and lengths, then the
+// four waves' slots.
+template <int G, bool FP8>
+inline size_t attn_lds_bytes(int32_t pairs) {
+  const size_t meta = ((size_t)(pairs + 1) * 8 + 15) / 16 * 16;
+  return meta + (size_t)kAttnWaves * Geo<G, FP8>::kWaveBytes;
+}
+
 template <int G, bool FP8, bool F16>
-// two workgroups per CU: without the bound the G = 8 kernels take 256 VGPRs
-// plus accumulation registers, one wave per SIMD
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
-  __shared__ float p_lds[kAttnWaves][kIterTokens][16];  // [wave][token][head] probabilities
-  __shared__ float al_lds[kAttnWaves][16];              // [wave][head] rescale factor
-  __shared__ float m_w[kAttnWaves][G], l_w[kAttnWaves][G];
-  __shared__ __attribute__((aligned(16))) float o_w[kAttnWaves][G][kHeadDim];
-  // The work list, the same in every workgroup: first the full 1024-token
-  // chunks of all (sequence, KV head) pairs, pair-major, then each pair's
-  // last, shorter chunk (or the zeros of an empty pair) with the longest
-  // first, so that the short items fill the end of the launch.
-  __shared__ int32_t first[kMaxPairs + 1];  // first full-chunk item of each pair
-  __shared__ int32_t tail_pair[kMaxPairs];  // pairs with a short chunk, longest first
-  __shared__ uint8_t tail_key[kMaxPairs];   // its length class, or kTailNone
-  __shared__ int32_t class_at[kTailClasses];         // next free slot of each class
-  __shared__ int32_t class_wave[kAttnWaves][kTailClasses];
+  using Gm = Geo<G, FP8>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int32_t wave_tot[kAttnWaves];
-  __shared__ int32_t item_sh;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < kTailClasses) class_at[tid] = 0;
-  __syncthreads();
-  // pass 1, 256 pairs per round: full-chunk counts and their exclusive
-  // prefix, the short chunk's class and the class sizes
+  int32_t* pre_l = reinterpret_cast<int32_t*>(lds);  // [pairs + 1]
+  int32_t* len_l = pre_l + (a.pairs + 1);             // [pairs]
+  const size_t meta = ((size_t)(a.pairs + 1) * 8 + 15) / 16 * 16;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- prologue: lengths (clamped to the table and the launch's bound) and
+  // the exclusive prefix of the pairs' page counts, 256 pairs per round
+  const int64_t cap = (int64_t)a.twidth * kPageTokens < a.max_len
+                          ? (int64_t)a.twidth * kPageTokens
+                          : (int64_t)a.max_len;
   int32_t total = 0;
   for (int base = 0; base < a.pairs; base += kAttnThreads) {
     const int pr = base + tid;
     int32_t cnt = 0;
     if (pr < a.pairs) {
-      const int64_t len = attn_len(a, pr / a.hkv, blockIdx.x == 0 && pr % a.hkv == 0);
-      cnt = (int32_t)(len / kChunk);
-      const int32_t rem = (int32_t)(len % kChunk);
-      const bool tail = rem != 0 || len == 0;  // an empty pair still zeroes its output
-      const int key = tail ? kTailClasses - 1 - rem / (kChunk / kTailClasses) : kTailNone;
-      tail_key[pr] = (uint8_t)key;
-      if (tail) atomicAdd(&class_at[key], 1);
+      int64_t len = ld_const(a.lens + pr / a.hkv);
+      if (len > cap || len < 0) {
+        if (blockIdx.x == 0 && pr % a.hkv == 0) raise_err(a.err, MKV_DEVERR_TABLE);
+        len = len < 0 ? 0 : cap;
+      }
+      len_l[pr] = (int32_t)len;
+      cnt = (int32_t)((len + kPageTokens - 1) / kPageTokens);
     }
     int32_t incl = cnt;
 #pragma unroll
@@ -447,112 +269,392 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_chunk_kernel(AttnArgs a)
       at += w < wave ? wave_tot[w] : 0;
       round += wave_tot[w];
     }
-    if (pr < a.pairs) first[pr] = at;
+    if (pr < a.pairs) pre_l[pr] = at;
     total += round;
     __syncthreads();  // wave_tot is rewritten by the next round
   }
-  const int32_t total_full = total;
-  // class sizes -> their first slots (exclusive scan of 32 counts in wave 0)
-  if (wave == 0) {
-    const int32_t n_c = lane < kTailClasses ? class_at[lane] : 0;
-    int32_t incl = n_c;
-#pragma unroll
-    for (int dd = 1; dd < 64; dd <<= 1) {
-      const int32_t o = __shfl_up(incl, dd);
-      if (lane >= dd) incl += o;
-    }
-    if (lane < kTailClasses) class_at[lane] = incl - n_c;
-    if (lane == 63) item_sh = incl;  // number of short chunks
-  }
+  if (tid == 0) pre_l[a.pairs] = total;
   __syncthreads();
-  const int32_t n_tail = __builtin_amdgcn_readfirstlane(item_sh);
-  // pass 2: each short chunk's slot, stable by pair index within its class
-  for (int base = 0; base < a.pairs; base += kAttnThreads) {
-    const int pr = base + tid;
-    const int key = pr < a.pairs ? tail_key[pr] : kTailNone;
-    int my_rank = 0;
-    for (int c = 0; c < kTailClasses; ++c) {
-      const uint64_t m = __ballot(key == c);
-      if (key == c) my_rank = __popcll(m & ((1ull << lane) - 1));
-      if (lane == 0) class_wave[wave][c] = __popcll(m);
+  const int64_t T = total;
+  const int64_t W = (int64_t)gridDim.x * kAttnWaves;
+  const int64_t S = (T + W - 1) / W;
+  if (blockIdx.x == 0) {  // for the merge kernel
+    for (int p = tid; p <= a.pairs; p += kAttnThreads) a.pre[p] = pre_l[p];
+    if (tid == 0) {
+      a.hdr[0] = S;
+      a.hdr[1] = T;
     }
-    __syncthreads();
-    if (key != kTailNone) {
-      int32_t slot = class_at[key] + my_rank;
-#pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) slot += w < wave ? class_wave[w][key] : 0;
-      tail_pair[slot] = pr;
-    }
-    __syncthreads();  // class_at and class_wave are updated below / rewritten next round
-    if (tid < kTailClasses) {
-      int32_t add = 0;
-#pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) add += class_wave[w][tid];
-      class_at[tid] += add;
-    }
-    __syncthreads();
   }
-  if (tid == 0) first[a.pairs] = total_full;
-  // The first round is static: workgroup w takes item w. Later items come from
-  // the counter, offset by the grid, and only when there are more items than
-  // workgroups. A launch of 1024 workgroups all hitting one device-scope
-  // atomic at their start, and again at their exit, cost 4-12 us per launch
-  // (3-16 %) on short contexts.
-  const int32_t n_items = total_full + n_tail;
-  for (int32_t round = 0;; ++round) {
-    __syncthreads();  // the lists written; the previous item's LDS reads done
-    if (round > 0) {
-      if (n_items <= (int32_t)gridDim.x) break;  // uniform
-      if (tid == 0) item_sh = (int32_t)gridDim.x + atomicAdd(a.queue, 1);
-    } else if (tid == 0) {
-      item_sh = (int32_t)blockIdx.x;
+  const int64_t gw = (int64_t)blockIdx.x * kAttnWaves + wave;
+  const int64_t s0 = gw * S < T ? gw * S : T;
+  const int64_t s1 = s0 + S < T ? s0 + S : T;
+  if (s0 >= s1) return;  // no barrier follows: an idle wave may leave
+
+  uint8_t* wl = lds + meta + (size_t)wave * Gm::kWaveBytes;
+  uint8_t* kslot = wl + Gm::kOffK;
+  uint8_t* vslot = wl + Gm::kOffV;
+  uint8_t* sslot = wl + Gm::kOffS;
+  uint8_t* qslot = wl + Gm::kOffQ;
+  float* ptile = reinterpret_cast<float*>(wl + Gm::kOffP);  // [16 tokens][G]
+  const uint32_t kslot_a = lds_addr(kslot), vslot_a = lds_addr(vslot);
+  const uint32_t sslot_a = lds_addr(sslot), qslot_a = lds_addr(qslot);
+
+  // The pair holding flat page f: the last pair p with pre[p] <= f (empty
+  // pairs share their successor's prefix, so it is never empty).
+  auto pair_of = [&](int64_t f) {
+    int lo = 0, hi = a.pairs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre_l[mid] <= f) lo = mid; else hi = mid - 1;
     }
-    __syncthreads();
-    // work-item values are uniform: scalar registers (readfirstlane)
-    const int32_t item = __builtin_amdgcn_readfirstlane(item_sh);
-    if (item >= n_items || item < 0) break;  // uniform: every workgroup ends here
-    int32_t pair, c;
-    if (item < total_full) {  // the last pair whose full chunks start at or before `item`
-      int lo = 0, hi = a.pairs - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (first[mid] <= item) lo = mid; else hi = mid - 1;
-      }
-      pair = lo;
-      c = item - first[lo];
+    return __builtin_amdgcn_readfirstlane(lo);
+  };
+
+  // ---- lane constants of the DMA addressing and the LDS reads
+  const int64_t row_stride = (int64_t)a.hkv * Gm::kCodeRow;  // bytes between token rows
+  uint32_t voff[Gm::kPlaneIns];  // lane's byte offset in a page plane, per instruction
+#pragma unroll
+  for (int j = 0; j < Gm::kPlaneIns; ++j) {
+    const int p = 64 * j + lane;  // 16-byte position in the slot
+    const int r = p / Gm::kChunks;
+    const int c = (p % Gm::kChunks) ^ (r & 15);
+    voff[j] = (uint32_t)(r * row_stride + c * 16);
+  }
+  // fp8: lane t < 16 fetches token t's K scale, 16 <= lane < 32 the V scale
+  // (lanes 32-63 repeat them into the slot's unused half)
+  const int st = lane & 15;
+  const float* sbase = ((lane >> 4) & 1) ? a.vs : a.ks;
+  const int n = lane & 15, g = lane >> 4;     // MFMA lane roles: row / head n, group g
+  const int hf = lane >> 5, c8 = lane & 31;   // P V roles: token half, 8-dim chunk
+  uint32_t koff[FP8 ? 4 : 8];                 // K operand reads
+  if constexpr (FP8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) koff[r] = kslot_a + (n * 16 + ((4 * r + g) ^ n)) * 16;
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) koff[s] = kslot_a + (n * 32 + ((4 * s + g) ^ n)) * 16;
+  }
+  uint32_t voffr[8];  // V row reads: token 8 hf + k, chunk c8
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int t = 8 * hf + k;
+    if constexpr (FP8)
+      voffr[k] = vslot_a + (t * 16 + ((c8 >> 1) ^ t)) * 16 + (c8 & 1) * 8;
+    else
+      voffr[k] = vslot_a + (t * 32 + (c8 ^ t)) * 16;
+  }
+  auto lds_ld16 = [](uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(addr);
+  };
+  auto lds_ld8 = [](uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(addr);
+  };
+
+  // ---- the issue side: page f's K plane (after the pair's query rows when
+  // it starts a pair, and with the page's scales for fp8), then its V plane
+  int32_t ip = pair_of(s0);          // pair of the next page to issue
+  int64_t ipre1 = pre_l[ip + 1];     // its end
+  int64_t irow = 0;                  // first cached row of the page being issued
+  bool ibad = false;
+  auto locate = [&](int64_t f) {
+    const int64_t b = ip / a.hkv;
+    const int64_t j = f - pre_l[ip];
+    if (a.seq_rows > 0) {
+      irow = b * a.seq_rows + j * kPageTokens;
+      ibad = false;
     } else {
-      pair = tail_pair[item - total_full];
-      c = -1;  // the pair's last chunk, index len / kChunk
+      int32_t pid = ld_const(a.table + b * a.tstride + j);
+      ibad = pid < 0 || pid >= a.num_pages;
+      if (ibad) {
+        if (lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
+        pid = 0;
+      }
+      irow = (int64_t)pid * kPageTokens;
     }
-    pair = __builtin_amdgcn_readfirstlane(pair);
-    c = __builtin_amdgcn_readfirstlane(c);
-    const int64_t b = pair / a.hkv, hk = pair % a.hkv;
-    const int64_t len = attn_len(a, b, false);
-    if (c < 0) c = (int32_t)(len / kChunk);
-    attn_chunk<G, FP8, F16>(a, b, hk, c, len, (len + kChunk - 1) / kChunk, p_lds, al_lds, m_w, l_w,
-                       o_w);
+  };
+  // rows of a contiguous sequence's last page past its end are not read:
+  // clamp the lane's row to the last valid one (only that page)
+  auto plane_off = [&](int j, int64_t rows_left) -> uint32_t {
+    if (rows_left >= kPageTokens) return voff[j];
+    const int p = 64 * j + lane;
+    int r = p / Gm::kChunks;
+    const int c = (p % Gm::kChunks) ^ (r & 15);
+    if (r >= rows_left) r = (int)rows_left - 1;
+    return (uint32_t)(r * row_stride + c * 16);
+  };
+  auto issue_k = [&](int64_t f, bool with_q, int64_t rows_left) -> int {
+    lds_reads_done();
+    if (with_q) {
+      const uint8_t* qb = a.q + (int64_t)ip * G * kRowBytes;
+#pragma unroll
+      for (int j = 0; j < Gm::kQIns; ++j)
+        dma16(qb, (uint32_t)((j * 1024 + lane * 16) % (G * kRowBytes)), qslot_a + j * 1024);
+    }
+    const int64_t hk = ip % a.hkv;
+    const uint8_t* base = a.k + (irow * a.hkv + hk) * Gm::kCodeRow;
+#pragma unroll
+    for (int j = 0; j < Gm::kPlaneIns; ++j) dma16(base, plane_off(j, rows_left), kslot_a + j * 1024);
+    if constexpr (FP8) dma4(sbase + (irow + st) * a.hkv + hk, sslot_a);
+    return Gm::kPlaneIns + Gm::kScaleIns + (with_q ? Gm::kQIns : 0);
+  };
+  auto issue_v = [&](int64_t rows_left) {
+    lds_reads_done();
+    const int64_t hk = ip % a.hkv;
+    const uint8_t* base = a.v + (irow * a.hkv + hk) * Gm::kCodeRow;
+#pragma unroll
+    for (int j = 0; j < Gm::kPlaneIns; ++j) dma16(base, plane_off(j, rows_left), vslot_a + j * 1024);
+  };
+  // rows of the page being issued that lie inside a contiguous sequence's
+  // storage (16 in paged mode)
+  auto rows_in_seq = [&](int64_t f) -> int64_t {
+    if (a.seq_rows <= 0) return kPageTokens;
+    const int64_t left = a.seq_rows - (f - pre_l[ip]) * kPageTokens;
+    return left < kPageTokens ? left : kPageTokens;
+  };
+
+  // ---- the consume side
+  int32_t cp = ip;                 // pair of the page being consumed
+  int64_t cpre0 = pre_l[cp], cpre1 = ipre1;
+  int32_t clen = len_l[cp];
+  locate(s0);
+  bool cbad = ibad;
+  int64_t rows0 = rows_in_seq(s0);
+  issue_k(s0, true, rows0);
+  issue_v(rows0);
+
+  u32x4 qb[8];
+  float m_run = -INFINITY, l_run = 0.f;  // head n (lanes n < G)
+  float o[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+  bool seg_first = true;
+
+  for (int64_t f = s0; f < s1; ++f) {
+    // K plane (and query rows, scales) of page f: only its V plane was issued after it
+    vm_wait(Gm::kPlaneIns);
+    if (seg_first) {
+      // the pair's query heads as the B operand, in the K operand's dim
+      // order: bf16, step s covers dims 8*(4s+g) .. +7; fp8, K chunk 4r+g
+      // holds 16 codes, step s = 2r+h covers dims 16*(4r+g) + 8h .. +7
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
+        const u32x4 w = lds_ld16(qslot_a + (n < G ? n : 0) * kRowBytes + chunk * 16);
+        qb[s] = n < G ? w : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (FP8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const u32x4 kc = lds_ld16(koff[r]);
+        sc = mfma16<false>(fp8x8_bf16(kc.x, kc.y), qb[2 * r], sc);
+        sc = mfma16<false>(fp8x8_bf16(kc.z, kc.w), qb[2 * r + 1], sc);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sc = mfma16<F16>(lds_ld16(koff[s]), qb[s], sc);
+    }
+    float ksc[4], vsc[4];
+    if constexpr (FP8) {
+      const u32x4 kw = lds_ld16(sslot_a + 16 * g);
+      const u32x4 vw = lds_ld16(sslot_a + 64 + 16 * g);
+      ksc[0] = bits_f32(kw.x); ksc[1] = bits_f32(kw.y); ksc[2] = bits_f32(kw.z); ksc[3] = bits_f32(kw.w);
+      vsc[0] = bits_f32(vw.x); vsc[1] = bits_f32(vw.y); vsc[2] = bits_f32(vw.z); vsc[3] = bits_f32(vw.w);
+    }
+    // page f's tokens of its pair: valid rows (0 for a page id outside the pool)
+    const int64_t tok0 = (f - cpre0) * kPageTokens;
+    const int valid = cbad ? 0 : (int)(clen - tok0 < kPageTokens ? clen - tok0 : kPageTokens);
+    const bool seg_last = f + 1 == cpre1 || f + 1 == s1;
+
+    // issue page f+1's K plane now that the K slot has been read
+    int next_k = 0;
+    bool nbad = false;
+    if (f + 1 < s1) {
+      const bool new_pair = f + 1 == ipre1;
+      if (new_pair) {
+        ip = pair_of(f + 1);
+        ipre1 = pre_l[ip + 1];
+      }
+      locate(f + 1);
+      nbad = ibad;
+      next_k = issue_k(f + 1, new_pair, rows_in_seq(f + 1));
+    }
+
+    // online softmax for head n over the page's tokens 4g + i
+    float sv[4], pm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float score = FP8 ? sc[i] * ksc[i] : sc[i];
+      sv[i] = 4 * g + i < valid ? score * a.scale_log2 : -INFINITY;
+      pm = fmaxf(pm, sv[i]);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 16));
+    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    const float m_new = fmaxf(m_run, pm);
+    // -inf only while every token so far was masked: exponents stay -inf
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_fast(m_run - m_ref);
+    const bool rescale = __ballot(n < G && m_new != m_run) != 0;
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pv = exp2_fast(sv[i] - m_ref);
+      ps += pv;
+      if (n < G) ptile[(4 * g + i) * G + n] = FP8 ? (4 * g + i < valid ? pv * vsc[i] : 0.f) : pv;
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    if (rescale) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float al = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] *= al;
+      }
+    }
+
+    // V plane of page f: only page f+1's K plane (if any) was issued after it
+    vm_wait(next_k);
+    if (valid < kPageTokens) {
+      // rows past the sequence's end (or of a page id outside the pool) may
+      // hold anything: zero them so that 0-weight rows add exact zeros
+      for (int i = lane; i < (kPageTokens - valid) * Gm::kChunks; i += 64) {
+        const int r = valid + i / Gm::kChunks;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+            vslot_a + (r * Gm::kChunks + (i % Gm::kChunks)) * 16) = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    wave_sync();  // the probability tile and zeroed rows before the reads below
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int t = 8 * hf + k;
+      float vv[8];
+      if constexpr (FP8) {
+        const u32x2 w = lds_ld8(voffr[k]);
+        const f32x2 a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, false);
+        const f32x2 a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, true);
+        const f32x2 a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, false);
+        const f32x2 a3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, true);
+        vv[0] = a0.x; vv[1] = a0.y; vv[2] = a1.x; vv[3] = a1.y;
+        vv[4] = a2.x; vv[5] = a2.y; vv[6] = a3.x; vv[7] = a3.y;
+      } else {
+        const u32x4 w = lds_ld16(voffr[k]);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vv[2 * e] = F16 ? f16_lo(ww[e]) : bf16_lo(ww[e]);
+          vv[2 * e + 1] = F16 ? f16_hi(ww[e]) : bf16_hi(ww[e]);
+        }
+      }
+      float pt[G];
+      if constexpr (G >= 4) {
+#pragma unroll
+        for (int h4 = 0; h4 < G; h4 += 4) {
+          const f32x4 p4 = *reinterpret_cast<const f32x4*>(&ptile[t * G + h4]);
+          pt[h4] = p4[0]; pt[h4 + 1] = p4[1]; pt[h4 + 2] = p4[2]; pt[h4 + 3] = p4[3];
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < G; ++h) pt[h] = ptile[t * G + h];
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] += pt[h] * vv[e];
+    }
+    // issue page f+1's V plane now that the V slot has been read
+    if (f + 1 < s1) issue_v(rows_in_seq(f + 1));
+    wave_sync();  // the next page rewrites the probability tile
+
+    if (seg_last) {
+      // the two token halves of the page hold the same dims: sum them
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], 32);
+      const bool whole = cpre0 >= s0 && cpre1 <= s1;
+      if (whole) {
+        uint8_t* orow = a.out + (int64_t)cp * G * kRowBytes;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), h));
+          if (hf == 0) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w[e] = (uint32_t)out_bits<F16>(L > 0.f ? o[h][2 * e] / L : 0.f) |
+                     ((uint32_t)out_bits<F16>(L > 0.f ? o[h][2 * e + 1] / L : 0.f) << 16);
+            st16(orow + h * kRowBytes + c8 * 16, u32x4{w[0], w[1], w[2], w[3]});
+          }
+        }
+      } else {
+        // a piece of a pair cut by span boundaries: the span's first pair
+        // goes to slot 0, its last pair to slot 1
+        const int64_t at = (gw * 2 + (cpre0 <= s0 ? 0 : 1)) * G;
+        if (hf == 0) {
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            float* pr = a.part + (at + h) * kHeadDim + 8 * c8;
+            *reinterpret_cast<f32x4*>(pr) = f32x4{o[h][0], o[h][1], o[h][2], o[h][3]};
+            *reinterpret_cast<f32x4*>(pr + 4) = f32x4{o[h][4], o[h][5], o[h][6], o[h][7]};
+          }
+        }
+        if (lane < G) {
+          a.ml[(at + lane) * 2] = m_run;
+          a.ml[(at + lane) * 2 + 1] = l_run;
+        }
+      }
+      m_run = -INFINITY;
+      l_run = 0.f;
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+      if (f + 1 < s1) {
+        cp = ip;  // the issue side is already at page f+1's pair
+        cpre0 = pre_l[cp];
+        cpre1 = ipre1;
+        clen = len_l[cp];
+      }
+    }
+    seg_first = seg_last;
+    cbad = nbad;
   }
 }
 
-// Merges the chunk states of one (sequence, KV head, query head) of a
-// sequence longer than one chunk: the chunks' maximum by a block reduction,
-// then a thread per dim sums the rescaled partial rows (loads 8 chunks deep).
+// Merges the pieces of one (pair, query head) of a pair cut by span
+// boundaries, and writes the zeros of an empty pair: the pieces' maximum by
+// a block reduction, then a thread per dim sums the rescaled partial rows.
 template <int G, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
   __shared__ float red[kAttnWaves];
-  // the chunk kernel has finished (stream order): its counter starts from
-  // zero for the next call
-  if (blockIdx.x == 0 && threadIdx.x == 0) a.queue[0] = 0;
   const int64_t pr = blockIdx.x / G;
   const int h = blockIdx.x % G;
-  const int64_t b = pr / a.hkv;
-  const int64_t len = attn_len(a, b, false);
-  const int64_t nch = (len + kChunk - 1) / kChunk;
-  if (nch <= 1) return;  // written by the chunk kernel
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t at0 = pr * a.chunks * G + h;  // chunk c: at0 + c * G
+  const int64_t p0 = ld_const(a.pre + pr), p1 = ld_const(a.pre + pr + 1);
+  uint8_t* out = a.out + (pr * G + h) * kRowBytes;
+  if (p1 <= p0) {  // nothing to attend to: zeros
+    reinterpret_cast<uint16_t*>(out)[tid] = 0;
+    return;
+  }
+  const int64_t S = ld_const(a.hdr);
+  const int64_t w0 = p0 / S, w1 = (p1 - 1) / S;
+  if (w0 == w1) return;  // written by its wave
+  const int64_t n_seg = w1 - w0 + 1;
+  // piece i: wave w0 + i, slot 1 for the first piece unless the pair starts
+  // its span (then it is that span's first pair), slot 0 for the rest
+  auto at_of = [&](int64_t i) {
+    const int64_t w = w0 + i;
+    const int slot = (i == 0 && p0 != w0 * S) ? 1 : 0;
+    return (w * 2 + slot) * G + h;
+  };
   float M = -INFINITY;
-  for (int64_t c = tid; c < nch; c += kAttnThreads) M = fmaxf(M, a.ml[(at0 + c * G) * 2]);
+  for (int64_t i = tid; i < n_seg; i += kAttnThreads) M = fmaxf(M, a.ml[at_of(i) * 2]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
   if (lane == 0) red[wave] = M;
@@ -561,53 +663,150 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
   for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, red[w]);
   float O = 0.f, L = 0.f;
 #pragma unroll 8
-  for (int64_t c = 0; c < nch; ++c) {
-    const int64_t at = at0 + c * G;
+  for (int64_t i = 0; i < n_seg; ++i) {
+    const int64_t at = at_of(i);
     const float m = ld_const(a.ml + at * 2);
     const float f = m == -INFINITY ? 0.f : exp2_fast(m - M);
     O += f * a.part[at * kHeadDim + tid];
     L += f * ld_const(a.ml + at * 2 + 1);
   }
-  uint8_t* out = a.out + (pr * G + h) * kRowBytes;
   reinterpret_cast<uint16_t*>(out)[tid] = out_bits<F16>(L > 0.f ? O / L : 0.f);
 }
 
-inline int64_t attn_chunks(int32_t max_seq_len) {
-  return ((int64_t)max_seq_len + kChunk - 1) / kChunk;
-}
-
-// Workgroups of the chunk kernel: as many as are resident at once (CUs x the
-// kernel's occupancy, 2 per CU for four query heads), so that every
-// workgroup's static first item starts at once and the counter hands out the
-// rest in list order. A grid of 4 per CU left the second half's first items,
-// full chunks, to the end of the launch: 304.7 against 295.4 us per bf16
-// launch at batch 256, 102.4 against 100.4 us in the serving workload.
-template <int G, bool FP8, bool F16>
-int attn_grid() {
-  static int grid[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-  if (grid[dev] == 0) {
-    int n = 0, per = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_chunk_kernel<G, FP8, F16>,
-                                                     kAttnThreads, 0) != hipSuccess || per <= 0)
-      per = 2;
-    grid[dev] = n * per;
+// Workgroups of the span kernel: as many as are resident at once (CUs x the
+// kernel's occupancy at this launch's LDS size), so every wave's span starts
+// at once. The occupancy depends on the pair count only through the LDS
+// size; it is looked up once per (device, kernel, pair count).
+std::mutex g_grid_mu;
+struct GridKey {
+  int dev, kind, G, pairs;
+  bool operator==(const GridKey& o) const {
+    return dev == o.dev && kind == o.kind && G == o.G && pairs == o.pairs;
   }
-  return grid[dev];
+};
+constexpr int kGridMemo = 64;
+GridKey g_grid_key[kGridMemo];
+int g_grid_val[kGridMemo];
+int g_grid_n = 0;
+
+// Workgroups per CU that this launch's LDS allows (at most 4): an upper
+// bound of the kernel's occupancy computable on the host alone, which sizes
+// the workspace.
+template <int G, bool FP8>
+int occ_cap(int32_t pairs) {
+  const int by_lds = (int)(kLdsPerCu / attn_lds_bytes<G, FP8>(pairs));
+  return by_lds < 4 ? (by_lds < 1 ? 1 : by_lds) : 4;
+}
+
+// CUs of the current device (256, MI355X's count, when none can be queried).
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
 }
 
 template <int G, bool FP8, bool F16>
-void launch_attn(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_chunk_kernel<G, FP8, F16>), dim3((unsigned)attn_grid<G, FP8, F16>()),
+int attn_grid(int kind, int32_t pairs) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const GridKey key{dev, kind, G, pairs};
+  {
+    std::lock_guard<std::mutex> lock(g_grid_mu);
+    for (int i = 0; i < g_grid_n; ++i)
+      if (g_grid_key[i] == key) return g_grid_val[i];
+  }
+  // the slots of four waves need more than the default 64 KiB of dynamic LDS
+  // (the attribute is per kernel and device; it must be set before the
+  // occupancy query, which honours it)
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_span_kernel<G, FP8, F16>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024) != hipSuccess)
+    return -1;
+  int per = 0;
+  const size_t lds = attn_lds_bytes<G, FP8>(pairs);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_span_kernel<G, FP8, F16>,
+                                                   kAttnThreads, lds) != hipSuccess ||
+      per <= 0)
+    per = 1;
+  const int cap = occ_cap<G, FP8>(pairs);
+  const int grid = device_cus() * (per < cap ? per : cap);
+  std::lock_guard<std::mutex> lock(g_grid_mu);
+  const int slot = g_grid_n < kGridMemo ? g_grid_n++ : (int)((unsigned)pairs % kGridMemo);
+  g_grid_key[slot] = key;
+  g_grid_val[slot] = grid;
+  return grid;
+}
+
+template <int G, bool FP8, bool F16>
+int launch_attn(AttnArgs a, int grid, hipStream_t st) {
+  const size_t lds = attn_lds_bytes<G, FP8>(a.pairs);
+  hipLaunchKernelGGL((attn_span_kernel<G, FP8, F16>), dim3((unsigned)grid), dim3(kAttnThreads),
+                     lds, st, a);
+  hipLaunchKernelGGL((attn_merge_kernel<G, F16>), dim3((unsigned)(a.pairs * G)),
                      dim3(kAttnThreads), 0, st, a);
-  // the merge kernel also resets the work counter: one workgroup when no
-  // sequence spans two chunks
-  hipLaunchKernelGGL((attn_merge_kernel<G, F16>), dim3(a.chunks > 1 ? (unsigned)(a.pairs * G) : 1u),
-                     dim3(kAttnThreads), 0, st, a);
+  return MKV_OK;
+}
+
+// Element kinds of the pool the entry points read.
+enum AttnKind { kAttnBf16, kAttnFp8, kAttnF16 };
+
+template <int G>
+int grid_of(AttnKind kind, int32_t pairs) {
+  if (kind == kAttnFp8) return attn_grid<G, true, false>(kind, pairs);
+  if (kind == kAttnF16) return attn_grid<G, false, true>(kind, pairs);
+  return attn_grid<G, false, false>(kind, pairs);
+}
+
+// The span kernel's grid for a kind, G and pair count (cached per device).
+int span_grid(AttnKind kind, int32_t G, int32_t pairs) {
+  switch (G) {
+    case 1: return grid_of<1>(kind, pairs);
+    case 2: return grid_of<2>(kind, pairs);
+    case 4: return grid_of<4>(kind, pairs);
+    default: return grid_of<8>(kind, pairs);
+  }
+}
+
+// Workspace layout: header, page prefix, piece (max, sum), piece outputs.
+struct WsLayout {
+  int64_t pre, ml, part, total;
+};
+inline WsLayout ws_layout(int64_t pairs, int64_t G, int64_t waves) {
+  WsLayout w;
+  w.pre = kHeaderBytes;
+  w.ml = w.pre + ((pairs + 1) * 4 + 255) / 256 * 256;
+  w.part = w.ml + (waves * 2 * G * 2 * 4 + 255) / 256 * 256;
+  w.total = w.part + waves * 2 * G * kHeadDim * 4;
+  return w;
+}
+
+// Waves of the largest grid a kind's launch can use for this G and pair
+// count (the CUs times the LDS-bound occupancy); host-only, so the workspace
+// can be sized without a device.
+template <int G>
+int64_t kind_waves(AttnKind kind, int32_t pairs) {
+  const int cap = kind == kAttnFp8 ? occ_cap<G, true>(pairs) : occ_cap<G, false>(pairs);
+  return (int64_t)device_cus() * cap * kAttnWaves;
+}
+int64_t bound_waves(AttnKind kind, int32_t G, int32_t pairs) {
+  switch (G) {
+    case 1: return kind_waves<1>(kind, pairs);
+    case 2: return kind_waves<2>(kind, pairs);
+    case 4: return kind_waves<4>(kind, pairs);
+    default: return kind_waves<8>(kind, pairs);
+  }
+}
+
+// Workspace bytes a launch over one pool kind needs at most.
+int64_t kind_workspace_bytes(AttnKind kind, int32_t batch, int32_t num_kv_heads,
+                             int32_t num_q_heads) {
+  if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0) return -1;
+  const int32_t G = num_q_heads / num_kv_heads;
+  if (G * num_kv_heads != num_q_heads || !(G == 1 || G == 2 || G == 4 || G == 8)) return -1;
+  const int64_t pairs = (int64_t)batch * num_kv_heads;
+  if (pairs > kMaxPairs) return -1;
+  return ws_layout(pairs, G, bound_waves(kind, G, (int32_t)pairs)).total;
 }
 
 }  // namespace
@@ -615,39 +814,37 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
 
 using namespace mkv;
 
-constexpr int64_t kQueueBytes = 256;  // the work counters, at the workspace's start
-
 extern "C" int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t num_kv_heads,
                                                         int32_t num_q_heads, int32_t max_seq_len) {
-  if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || max_seq_len < 0) return -1;
-  const int64_t chunks = attn_chunks(max_seq_len);
-  return kQueueBytes + (chunks <= 1 ? 0 : (int64_t)batch * num_q_heads * chunks * (kHeadDim + 2) * 4);
+  if (max_seq_len < 0) return -1;
+  int64_t best = -1;
+  for (AttnKind k : {kAttnBf16, kAttnFp8, kAttnF16}) {
+    const int64_t n = kind_workspace_bytes(k, batch, num_kv_heads, num_q_heads);
+    if (n < 0) return -1;
+    if (n > best) best = n;
+  }
+  return best;
 }
 
 namespace {
 
-// Element kinds of the pool the entry points read.
-enum AttnKind { kAttnBf16, kAttnFp8, kAttnF16 };
-
 template <int G>
-void launch_kind(AttnKind kind, const AttnArgs& a, hipStream_t st) {
-  if (kind == kAttnFp8)
-    launch_attn<G, true, false>(a, st);
-  else if (kind == kAttnF16)
-    launch_attn<G, false, true>(a, st);
-  else
-    launch_attn<G, false, false>(a, st);
+int launch_kind(AttnKind kind, const AttnArgs& a, int grid, hipStream_t st) {
+  if (kind == kAttnFp8) return launch_attn<G, true, false>(a, grid, st);
+  if (kind == kAttnF16) return launch_attn<G, false, true>(a, grid, st);
+  return launch_attn<G, false, false>(a, grid, st);
 }
 
 // Shared by the entry points: `fn` names the caller in error messages; the
-// scale planes are null for 16-bit caches.
+// scale planes are null for 16-bit caches; seq_rows > 0 selects contiguous
+// caches [batch, seq_rows, num_kv_heads, 256] (no page table).
 int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k_cache,
                      const void* v_cache, const float* k_scales, const float* v_scales,
                      int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
                      int32_t head_dim, const int32_t* page_table, int64_t table_stride,
-                     int32_t table_width, const int32_t* seq_lens, int32_t batch,
-                     int32_t max_seq_len, float softmax_scale, void* out, void* workspace,
-                     int64_t workspace_bytes, int32_t* err, void* stream) {
+                     int32_t table_width, int64_t seq_rows, const int32_t* seq_lens,
+                     int32_t batch, int32_t max_seq_len, float softmax_scale, void* out,
+                     void* workspace, int64_t workspace_bytes, int32_t* err, void* stream) {
   clear_error();
   MKV_REQUIRE(batch >= 0 && num_pages > 0 && num_kv_heads > 0 && num_q_heads > 0 &&
                   table_width >= 0 && table_stride >= table_width && max_seq_len >= 0,
@@ -659,7 +856,7 @@ int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k
               MKV_E_UNSUPPORTED, "%s: %d query heads per KV head unsupported (1, 2, 4, 8)", fn,
               num_q_heads / num_kv_heads);
   if (batch == 0) return MKV_OK;
-  MKV_REQUIRE(q && k_cache && v_cache && page_table && seq_lens && out && err &&
+  MKV_REQUIRE(q && k_cache && v_cache && (seq_rows > 0 || page_table) && seq_lens && out && err &&
                   (kind != kAttnFp8 || (k_scales && v_scales)),
               MKV_E_INVALID, "%s: null pointer", fn);
   MKV_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out),
@@ -669,10 +866,15 @@ int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k
   MKV_REQUIRE((int64_t)batch * num_kv_heads <= kMaxPairs, MKV_E_UNSUPPORTED,
               "%s: batch x KV heads above %d", fn, kMaxPairs);
   MKV_REQUIRE(max_seq_len <= (1 << 24), MKV_E_UNSUPPORTED, "%s: max_seq_len above 2^24", fn);
-  const int64_t need = mkv_decode_attention_workspace_bytes(batch, num_kv_heads, num_q_heads,
-                                                            max_seq_len);
-  MKV_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace), MKV_E_INVALID,
-              "%s: workspace of %lld bytes (16-byte aligned) required", fn, (long long)need);
+  // the pages of all pairs are counted in 32 bits
+  MKV_REQUIRE((int64_t)batch * num_kv_heads * (((int64_t)max_seq_len + 15) / 16) < (1ll << 31),
+              MKV_E_UNSUPPORTED, "%s: batch x KV heads x pages above 2^31", fn);
+  const int32_t pairs = batch * num_kv_heads;
+  const int grid = span_grid(kind, G, pairs);
+  MKV_REQUIRE(grid > 0, MKV_E_LAUNCH, "%s: cannot size the grid (dynamic LDS attribute)", fn);
+  const WsLayout L = ws_layout(pairs, G, (int64_t)grid * kAttnWaves);
+  MKV_REQUIRE(workspace && workspace_bytes >= L.total && aligned16(workspace), MKV_E_INVALID,
+              "%s: workspace of %lld bytes (16-byte aligned) required", fn, (long long)L.total);
   AttnArgs a;
   a.q = static_cast<const uint8_t*>(q);
   a.k = static_cast<const uint8_t*>(k_cache);
@@ -682,27 +884,29 @@ int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k
   a.table = page_table;
   a.lens = seq_lens;
   a.out = static_cast<uint8_t*>(out);
-  const int64_t chunks = attn_chunks(max_seq_len);
-  const int64_t part_floats = (int64_t)batch * num_q_heads * chunks * kHeadDim;
-  a.queue = static_cast<int32_t*>(workspace);
-  a.part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kQueueBytes);
-  a.ml = a.part + part_floats;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  a.hdr = reinterpret_cast<int64_t*>(ws);
+  a.pre = reinterpret_cast<int32_t*>(ws + L.pre);
+  a.ml = reinterpret_cast<float*>(ws + L.ml);
+  a.part = reinterpret_cast<float*>(ws + L.part);
   a.num_pages = num_pages;
   a.tstride = table_stride;
+  a.seq_rows = seq_rows;
   a.twidth = table_width;
   a.hkv = num_kv_heads;
-  a.chunks = (int32_t)chunks;
   a.max_len = max_seq_len;
-  a.pairs = (int32_t)((int64_t)batch * num_kv_heads);
+  a.pairs = pairs;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.err = err;
   const hipStream_t st = as_stream(stream);
+  int rc;
   switch (G) {
-    case 1: launch_kind<1>(kind, a, st); break;
-    case 2: launch_kind<2>(kind, a, st); break;
-    case 4: launch_kind<4>(kind, a, st); break;
-    default: launch_kind<8>(kind, a, st); break;
+    case 1: rc = launch_kind<1>(kind, a, grid, st); break;
+    case 2: rc = launch_kind<2>(kind, a, grid, st); break;
+    case 4: rc = launch_kind<4>(kind, a, grid, st); break;
+    default: rc = launch_kind<8>(kind, a, grid, st); break;
   }
+  if (rc != MKV_OK) return rc;
   return check_launch(fn);
 }
 
@@ -718,8 +922,8 @@ extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, con
                                          int32_t* err, void* stream) {
   return decode_attention("mkv_decode_attention_bf16", kAttnBf16, q, k_cache, v_cache, nullptr,
                           nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
-                          out, workspace, workspace_bytes, err, stream);
+                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          softmax_scale, out, workspace, workspace_bytes, err, stream);
 }
 
 extern "C" int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_codes,
@@ -733,8 +937,8 @@ extern "C" int mkv_decode_attention_fp8(const void* q, const void* k_codes, cons
                                         int32_t* err, void* stream) {
   return decode_attention("mkv_decode_attention_fp8", kAttnFp8, q, k_codes, v_codes, k_scales,
                           v_scales, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
-                          out, workspace, workspace_bytes, err, stream);
+                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          softmax_scale, out, workspace, workspace_bytes, err, stream);
 }
 
 extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_cache,
@@ -747,7 +951,29 @@ extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, cons
                                         int32_t* err, void* stream) {
   return decode_attention("mkv_decode_attention_f16", kAttnF16, q, k_cache, v_cache, nullptr,
                           nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, seq_lens, batch, max_seq_len, softmax_scale,
+                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          softmax_scale, out, workspace, workspace_bytes, err, stream);
+}
+
+extern "C" int mkv_decode_attention_contig(const void* q, const void* k_cache,
+                                           const void* v_cache, int32_t fp16,
+                                           int32_t num_kv_heads, int32_t num_q_heads,
+                                           int32_t head_dim, int64_t seq_rows,
+                                           const int32_t* seq_lens, int32_t batch,
+                                           int32_t max_seq_len, float softmax_scale, void* out,
+                                           void* workspace, int64_t workspace_bytes,
+                                           int32_t* err, void* stream) {
+  static const char* fn = "mkv_decode_attention_contig";
+  clear_error();
+  MKV_REQUIRE(seq_rows > 0 && (int64_t)batch * seq_rows < (1ll << 40), MKV_E_INVALID,
+              "%s: seq_rows must be positive", fn);
+  // lengths are cut to the rows each sequence owns (MKV_DEVERR_TABLE past them)
+  const int64_t pages = (seq_rows + 15) / 16;
+  MKV_REQUIRE(pages <= INT32_MAX, MKV_E_UNSUPPORTED, "%s: seq_rows too large", fn);
+  const int32_t cap = max_seq_len < seq_rows ? max_seq_len : (int32_t)seq_rows;
+  return decode_attention(fn, fp16 ? kAttnF16 : kAttnBf16, q, k_cache, v_cache, nullptr, nullptr,
+                          (int64_t)batch * pages, num_kv_heads, num_q_heads, head_dim, nullptr,
+                          pages, (int32_t)pages, seq_rows, seq_lens, batch, cap, softmax_scale,
                           out, workspace, workspace_bytes, err, stream);
 }
 
@@ -758,9 +984,9 @@ extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, cons
 // ---------------------------------------------------------------------------
 namespace {
 
-// Room for the work counters and the chunk partials of batch x query heads x
-// chunks <= 48,770 (e.g. batch 256, 4 query heads, max_seq_len up to 47 x
-// 1024 tokens).
+// Room for the header, the page prefix of up to 4096 pairs and the pieces of
+// every resident wave (2048 waves x 2 pieces x 4 query heads x 1032 bytes at
+// four query heads per KV head on MI355X: 17 MB).
 constexpr int64_t kNoAllocScratchBytes = 48ll << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
@@ -768,18 +994,12 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxScratchDevices] = {};
 
-__global__ void zero_queue_kernel(int32_t* queue) {
-  if (threadIdx.x < kQueueBytes / 4) queue[threadIdx.x] = 0;
-}
-
 // The current device's copy of `scratch`. In host code the array's name is
 // only a stand-in for the symbol: its device address comes from
 // hipGetSymbolAddress, once per device (with that device current), and only
-// that address is ever handed to a kernel. The first call on a device also
-// zeroes the work counters on the caller's stream (a fill kernel, not a
-// memset node); every call leaves them zero again (the merge kernel resets
-// them), as it does for a caller's workspace.
-int scratch_of_current_device(const char* fn, hipStream_t st, void** out) {
+// that address is ever handed to a kernel. Nothing in it needs to start at
+// zero: every call writes the header and prefix before the pieces are read.
+int scratch_of_current_device(const char* fn, void** out) {
   int dev = -1;
   const hipError_t ge = hipGetDevice(&dev);
   if (ge != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
@@ -792,9 +1012,6 @@ int scratch_of_current_device(const char* fn, hipStream_t st, void** out) {
     if (e != hipSuccess || !p)
       return set_error(MKV_E_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", fn,
                        hipGetErrorString(e));
-    hipLaunchKernelGGL(zero_queue_kernel, dim3(1), dim3(64), 0, st, static_cast<int32_t*>(p));
-    const int rc = check_launch(fn);
-    if (rc != MKV_OK) return rc;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -813,23 +1030,25 @@ extern "C" int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_ca
                                                  void* out, int32_t* err, void* stream) {
   static const char* fn = "mkv_decode_attention_bf16_noalloc";
   clear_error();
-  const int64_t need =
-      mkv_decode_attention_workspace_bytes(batch, num_kv_heads, num_q_heads, max_seq_len);
+  const int64_t need = max_seq_len < 0 ? -1
+                                        : kind_workspace_bytes(kAttnBf16, batch, num_kv_heads,
+                                                               num_q_heads);
+  MKV_REQUIRE(need >= 0, MKV_E_UNSUPPORTED, "%s: unsupported shape (batch %d, %d KV heads, %d "
+              "query heads)", fn, batch, num_kv_heads, num_q_heads);
   MKV_REQUIRE(need <= kNoAllocScratchBytes, MKV_E_UNSUPPORTED,
-              "%s: batch %d x %d query heads x %lld chunks of 1024 tokens need %lld bytes of "
-              "scratch, the static scratch holds %lld",
-              fn, batch, num_q_heads, (long long)attn_chunks(max_seq_len), (long long)need,
+              "%s: batch %d x %d query heads need %lld bytes of scratch, the static scratch "
+              "holds %lld", fn, batch, num_q_heads, (long long)need,
               (long long)kNoAllocScratchBytes);
   if (batch == 0) return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr,
                                           num_pages, num_kv_heads, num_q_heads, head_dim,
-                                          page_table, table_stride, table_width, seq_lens, batch,
-                                          max_seq_len, softmax_scale, out, nullptr, 0, err,
-                                          stream);
+                                          page_table, table_stride, table_width, 0, seq_lens,
+                                          batch, max_seq_len, softmax_scale, out, nullptr, 0,
+                                          err, stream);
   void* ws = nullptr;
-  const int rc = scratch_of_current_device(fn, as_stream(stream), &ws);
+  const int rc = scratch_of_current_device(fn, &ws);
   if (rc != MKV_OK) return rc;
   return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr, num_pages,
                           num_kv_heads, num_q_heads, head_dim, page_table, table_stride,
-                          table_width, seq_lens, batch, max_seq_len, softmax_scale, out, ws,
+                          table_width, 0, seq_lens, batch, max_seq_len, softmax_scale, out, ws,
                           kNoAllocScratchBytes, err, stream);
 }

@@ -20,7 +20,6 @@ import torch
 from muserve_amd import _lib
 
 HEAD_DIM = 256
-CHUNK = 1024  # tokens per work item of the kernel (sizes the workspace)
 
 _errors: dict[torch.device, _lib.DeviceErrors] = {}
 _workspace: dict[torch.device, torch.Tensor] = {}
@@ -180,8 +179,13 @@ def attn_decode(
     """bf16 or fp16 caches (fp16 is the reference's default pool dtype,
     muserve/config.py:37), with q and the output in the caches' dtype.
     ``max_seqlen`` bounds ``cache_seqlens`` (default: what the page table
-    holds) and sizes the launch; a tighter bound launches fewer empty
-    workgroups. ``out`` may be given to write in place."""
+    holds). ``out`` may be given to write in place.
+
+    With ``page_table=None`` the caches are contiguous per sequence,
+    ``[B, S, NUM_KV_HEADS, HEAD_DIM]``, sequence b's first
+    ``cache_seqlens[b]`` rows attended (the reference forwards None to its
+    kernel the same way, muserve/kernels/attention.py:33-42): the padded
+    layout ``PagedKVCache.gather`` writes."""
     fns = {torch.bfloat16: "mkv_decode_attention_bf16", torch.float16: "mkv_decode_attention_f16"}
     if k_cache.dtype not in fns or v_cache.dtype != k_cache.dtype:
         raise TypeError("attn_decode takes bf16 or fp16 caches (attn_decode_fp8 reads fp8 ones)")
@@ -217,10 +221,48 @@ def attn_decode_fp8(
                    cache_seqlens, page_table, softmax_scale, max_seqlen, out)
 
 
+def _workspace_for(dev, need):
+    ws = _workspace.get(dev)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        _workspace[dev] = ws
+    return ws
+
+
+def _decode_contig(q, k_cache, v_cache, cache_seqlens, softmax_scale, max_seqlen, out):
+    dev = _lib.require_gpu(q, k_cache, v_cache, cache_seqlens)
+    B, one, Hq, D = q.shape
+    if k_cache.dim() != 4:
+        raise ValueError("without a page table the caches are [B, S, kv_heads, 256]")
+    Bk, S, Hkv, Dk = k_cache.shape
+    if one != 1 or D != HEAD_DIM or Dk != D or Bk != B or v_cache.shape != k_cache.shape:
+        raise ValueError(f"unsupported shapes q {tuple(q.shape)}, cache {tuple(k_cache.shape)}")
+    if cache_seqlens.dtype != torch.int32 or cache_seqlens.numel() != B:
+        raise TypeError("cache_seqlens must be int32 [B]")
+    if not (q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous()
+            and cache_seqlens.is_contiguous()):
+        raise ValueError("q, caches and cache_seqlens must be contiguous")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    if max_seqlen is None:
+        max_seqlen = S
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    ws = _workspace_for(dev, workspace_bytes(B, Hkv, Hq, max_seqlen))
+    _lib.call("mkv_decode_attention_contig", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              1 if k_cache.dtype == torch.float16 else 0, Hkv, Hq, D, S,
+              cache_seqlens.data_ptr(), B, int(min(max_seqlen, 1 << 24)), scale, out.data_ptr(),
+              ws.data_ptr(), ws.numel(), _errword(dev).ptr(), _lib.stream_of(dev))
+    return out
+
+
 def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_table,
             softmax_scale, max_seqlen, out):
     if page_table is None:
-        raise ValueError("attn_decode reads the paged pool: page_table is required")
+        if k_scales is not None:
+            raise ValueError("attn_decode_fp8 reads the paged pool: page_table is required")
+        return _decode_contig(q, k_cache, v_cache, cache_seqlens, softmax_scale, max_seqlen, out)
     dev = _lib.require_gpu(q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_table)
     B, one, Hq, D = q.shape
     P, page, Hkv, Dk = k_cache.shape
@@ -242,12 +284,7 @@ def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_tab
     elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped like q")
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
-    need = workspace_bytes(B, Hkv, Hq, max_seqlen)
-    ws = _workspace.get(dev)
-    if ws is None or ws.numel() < need:
-        # zero-filled once: the kernels keep its work counters at zero between calls
-        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
-        _workspace[dev] = ws
+    ws = _workspace_for(dev, workspace_bytes(B, Hkv, Hq, max_seqlen))
     # the workspace is reused by later calls on the stream: calls on one
     # device must be issued on one stream (or be ordered by the caller)
     scales = () if k_scales is None else (k_scales.data_ptr(), v_scales.data_ptr())

@@ -83,3 +83,17 @@ def test_check_unique_arguments():
     rc, msg = _rc("mkv_check_unique", FAKE, 8, 4, 100, FAKE, 3, FAKE, None)
     assert rc == -1 and "4 needed" in msg
     assert _rc("mkv_check_unique", None, 8, 0, 100, None, 0, None, None)[0] == 0
+
+
+def test_noalloc_attention_rejects_an_unsupported_shape():
+    # batch x KV heads above 4096: rejected on the host before the scratch
+    # lookup or any launch, so fake pointers are never used
+    rc, msg = _rc("mkv_decode_attention_bf16_noalloc", FAKE, FAKE, FAKE, 16, 1, 8, 256, FAKE, 1, 1,
+                  FAKE, 8192, 2048, 0.0625, FAKE, FAKE, None)
+    assert rc == -3 and "unsupported shape" in msg
+
+
+def test_attention_workspace_of_an_unsupported_shape():
+    lib = _lib.load()
+    assert lib.mkv_decode_attention_workspace_bytes(4097, 1, 4, 1024) == -1  # too many pairs
+    assert lib.mkv_decode_attention_workspace_bytes(8, 1, 3, 1024) == -1     # G = 3

@@ -324,3 +324,71 @@ def test_work_list_sizes(batch, Hkv):
     within_one_ulp(got, want)
     got, want = run_fp8(q, *quantize(k, v), lens, table)
     within_one_ulp(got, want)
+
+
+# ---- contiguous caches: attn_decode with page_table=None ----
+
+def contiguous_from_pages(x, lens, table, S, pad_value):
+    """[B, S, Hkv, 256] per-sequence rows from a paged pool; rows past a
+    sequence's length hold pad_value."""
+    B = len(lens)
+    out = torch.full((B, S) + tuple(x.shape[2:]), pad_value, dtype=x.dtype)
+    for b, n in enumerate(lens):
+        out[b, :n] = torch.from_numpy(att.gather_kv(x.float().numpy(), table[b], int(n))).to(x.dtype)
+    return out
+
+
+@pytest.mark.parametrize("Hq,Hkv,dtype", [(4, 1, torch.bfloat16), (8, 2, torch.bfloat16),
+                                          (4, 1, torch.float16)])
+def test_contiguous_caches_match_oracle(Hq, Hkv, dtype):
+    """page_table=None: caches [B, S, Hkv, 256] (S = 1000, not a multiple of
+    16, the last sequence using every row); rows past each length hold NaN,
+    which must not reach the output."""
+    lens = [1, 16, 17, 999, 0, 513, 1000]
+    case(f"decode attention over contiguous caches Hq={Hq} Hkv={Hkv} {dtype} lens {lens}")
+    q, k, v, lens, table = build(81 + Hq, lens, Hq, Hkv)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    S = 1000
+    kc = contiguous_from_pages(k, lens, table, S, float("nan"))
+    vc = contiguous_from_pages(v, lens, table, S, float("nan"))
+    out = A.attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV),
+                        torch.from_numpy(lens.astype(np.int32)).to(DEV), None)
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.decode_attention(q[:, 0].float().numpy(), k.float().numpy(), v.float().numpy(),
+                                lens, table, 256 ** -0.5, stats=True)
+    assert torch.isfinite(out.float()).all()
+    within_one_ulp(out[:, 0], want, **(F16 if dtype == torch.float16 else {}))
+
+
+def test_contiguous_equals_paged_on_the_gathered_layout():
+    """The padded gather's output [B, Lpad, 1, 256] read with page_table=None
+    gives the same bits as attention over the pool it was gathered from (the
+    same pages per sequence, so the same work split and summation order)."""
+    rng = np.random.default_rng(82)
+    lens = rng.integers(1, 3000, 40)
+    case(f"gather then contiguous decode attention vs paged, lens sum {int(lens.sum())}")
+    q, k, v, lens, table = build(82, lens, 4, 1)
+    cache = PagedKVCache(k.shape[0], num_layers=1, dtype=torch.bfloat16, device=DEV,
+                         verbose=False)
+    cache.cache[0, 0].copy_(k.to(DEV))
+    cache.cache[0, 1].copy_(v.to(DEV))
+    lt = torch.from_numpy(lens.astype(np.int32)).to(DEV)
+    tt = torch.from_numpy(table).to(DEV)
+    out_len = table.shape[1] * 16
+    kg, vg = cache.gather(0, tt, lt, out_len=out_len)
+    paged = A.attn_decode(q.to(DEV), *cache.get_kv_by_layer(0), lt, tt)
+    contig = A.attn_decode(q.to(DEV), kg, vg, lt, None)
+    torch.cuda.synchronize()
+    cache.check_errors()
+    A.check_errors(DEV)
+    assert torch.equal(paged.view(torch.int16), contig.view(torch.int16))
+
+
+def test_contiguous_length_past_the_rows_is_flagged():
+    case("decode attention over contiguous caches, a length past the rows")
+    q = torch.randn(2, 1, 4, 256).bfloat16().to(DEV)
+    kc = torch.randn(2, 40, 1, 256).bfloat16().to(DEV)
+    A.attn_decode(q, kc, kc, torch.tensor([40, 41], dtype=torch.int32, device=DEV), None)
+    with pytest.raises(_lib.MkvDeviceError, match="longer than its block table"):
+        A.check_errors(DEV)
