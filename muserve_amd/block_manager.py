@@ -95,7 +95,11 @@ class BlockManager:
         page_hashes: int64 device tensor of u64 page-hash bit patterns;
         hash_offsets: int64 [max_requests+1] offsets into it per request id;
         num_tokens: int32 [max_requests] prompt lengths."""
-        _lib.call("mkv_bm_step", *self._step_args(ops, page_hashes, hash_offsets, num_tokens))
+        if self._pending is not None:
+            raise RuntimeError("step while a step_begin awaits its step_end")
+        args, keep = self._step_args(ops, page_hashes, hash_offsets, num_tokens)
+        _lib.call("mkv_bm_step", *args)
+        self._keep = keep  # the launches read these buffers: keep them until the next step
 
     def step_begin(self, ops: torch.Tensor, page_hashes: torch.Tensor, hash_offsets: torch.Tensor,
                    num_tokens: torch.Tensor) -> None:
@@ -107,17 +111,19 @@ class BlockManager:
         number of admits in ops, ``step_end`` has nothing left to run."""
         if self._pending is not None:
             raise RuntimeError("step_begin twice without step_end")
-        args = self._step_args(ops, page_hashes, hash_offsets, num_tokens)
+        args, keep = self._step_args(ops, page_hashes, hash_offsets, num_tokens)
         _lib.call("mkv_bm_step_begin", *args)
-        self._pending = args
+        # the pending step's tensors stay with it: step_end's launches read them
+        self._pending = (args, keep)
 
     def step_end(self) -> None:
         """The second half of ``step``: the one-workgroup kernels over the ops
         the resolution left."""
         if self._pending is None:
             raise RuntimeError("step_end without step_begin")
-        args, self._pending = self._pending, None
+        (args, keep), self._pending = self._pending, None
         _lib.call("mkv_bm_step_end", *args)
+        self._keep = keep  # until the next step: the launches may still be running
 
     def spec_done_word(self) -> torch.Tensor:
         """Device view (int64, one element) of the running count of admits the
@@ -140,15 +146,16 @@ class BlockManager:
         if page_hashes.dtype != torch.int64:
             raise TypeError("page_hashes must hold u64 bit patterns in an int64 tensor")
         _lib.require_gpu(ops, hash_offsets, num_tokens, self.state)
-        # the tensors ride along (step_end's launch reads the same buffers)
-        self._keep = (ops, page_hashes, hash_offsets, num_tokens)
+        # the tensors the launches read go back with the arguments: the caller
+        # keeps them alive until the launches are ordered before any reuse
+        keep = (ops, page_hashes, hash_offsets, num_tokens)
         return (self.state.data_ptr(), self.num_pages, ops.data_ptr(),
                 ops.numel(), self.tables.shape[0], page_hashes.data_ptr(), hash_offsets.data_ptr(),
                 num_tokens.data_ptr(), self.tables.data_ptr(), self.tables.stride(0),
                 self.tables.shape[1], self.hits.data_ptr(), self.child_last.data_ptr(),
                 self.cow_src.data_ptr(), self.cow_dst.data_ptr(), self.status.data_ptr(),
                 self.evict_log.data_ptr(), self.evict_log_capacity, self.errors.ptr(),
-                _lib.stream_of(self.device))
+                _lib.stream_of(self.device)), keep
 
     def probe(self, page_hashes: torch.Tensor, hash_offsets: torch.Tensor
               ) -> tuple[torch.Tensor, torch.Tensor]:

@@ -188,33 +188,47 @@ __device__ __forceinline__ void vm_wait(int n) {
 #define MKV_VMW(k) \
   case k: vm_wait_n<k>(); break;
     MKV_VMW(0) MKV_VMW(1) MKV_VMW(2) MKV_VMW(3) MKV_VMW(4) MKV_VMW(5) MKV_VMW(6) MKV_VMW(7)
-    MKV_VMW(8) MKV_VMW(9) MKV_VMW(10) MKV_VMW(11) MKV_VMW(12) MKV_VMW(13) MKV_VMW(14)
-    MKV_VMW(15) MKV_VMW(16) MKV_VMW(17) MKV_VMW(18) MKV_VMW(19) MKV_VMW(20)
+    MKV_VMW(8) MKV_VMW(9) MKV_VMW(10) MKV_VMW(11) MKV_VMW(12) MKV_VMW(13) MKV_VMW(14) MKV_VMW(15)
+    MKV_VMW(16) MKV_VMW(17) MKV_VMW(18) MKV_VMW(19) MKV_VMW(20) MKV_VMW(21) MKV_VMW(22) MKV_VMW(23)
+    MKV_VMW(24) MKV_VMW(25) MKV_VMW(26) MKV_VMW(27) MKV_VMW(28) MKV_VMW(29) MKV_VMW(30) MKV_VMW(31)
+    MKV_VMW(32) MKV_VMW(33) MKV_VMW(34) MKV_VMW(35) MKV_VMW(36) MKV_VMW(37) MKV_VMW(38) MKV_VMW(39)
+    MKV_VMW(40) MKV_VMW(41) MKV_VMW(42) MKV_VMW(43) MKV_VMW(44) MKV_VMW(45) MKV_VMW(46) MKV_VMW(47)
+    MKV_VMW(48) MKV_VMW(49) MKV_VMW(50) MKV_VMW(51) MKV_VMW(52) MKV_VMW(53) MKV_VMW(54) MKV_VMW(55)
+    MKV_VMW(56) MKV_VMW(57) MKV_VMW(58) MKV_VMW(59) MKV_VMW(60) MKV_VMW(61) MKV_VMW(62) MKV_VMW(63)
 #undef MKV_VMW
-    default: vm_wait_n<0>(); break;  // never taken: at most 17 loads follow a waited one
+    default: vm_wait_n<0>(); break;  // never taken: a wave has at most 63 loads outstanding
   }
 }
 
 // Geometry of one pool kind (bf16 / fp16 / fp8) and query-group size G.
+// A wave's loads go through a ring of kRing unit slots: unit 2i is page i's K
+// plane (with the pair's query rows ahead of it when the page starts a pair,
+// and for fp8 the page's K and V scales), unit 2i+1 its V plane. Unit u+kRing
+// is issued as soon as unit u has been read, so kRing-1 units are in flight
+// while the wave computes on one.
 template <int G, bool FP8>
 struct Geo {
   static constexpr int kCodeRow = FP8 ? kHeadDim : kRowBytes;  // bytes of a cached row
   static constexpr int kPlane = kPageTokens * kCodeRow;        // a page's K (or V) bytes
   static constexpr int kChunks = kCodeRow / 16;                // 16-byte chunks per row
-  static constexpr int kRowsPerIns = 1024 / kCodeRow;          // rows per 1 KiB instruction
   static constexpr int kPlaneIns = kPlane / 1024;              // instructions per plane
+  static constexpr int kRing = 2;                              // unit slots per wave
+  // query-row slots: with two slots a pair's rows are issued after the pair
+  // two pairs back has read its own (at least four units earlier)
+  static constexpr int kQSlots = kRing == 2 ? 1 : 2;
   static constexpr int kQBytes = G * kRowBytes < 1024 ? 1024 : G * kRowBytes;
   static constexpr int kQIns = kQBytes / 1024;
   static constexpr int kScaleBytes = FP8 ? 256 : 0;  // K scales, V scales (64 B each) + copies
   static constexpr int kScaleIns = FP8 ? 1 : 0;
-  // per-wave LDS: K slot, V slot, scales, query rows, probability tile
-  static constexpr int kOffK = 0;
-  static constexpr int kOffV = kOffK + kPlane;
-  static constexpr int kOffS = kOffV + kPlane;
-  static constexpr int kOffQ = kOffS + kScaleBytes;
-  static constexpr int kOffP = kOffQ + kQBytes;
+  // per-wave LDS: unit slots, scale slots, query rows, probability tile
+  static constexpr int kOffU = 0;
+  static constexpr int kOffS = kOffU + kRing * kPlane;
+  static constexpr int kOffQ = kOffS + kRing * kScaleBytes;
+  static constexpr int kOffP = kOffQ + kQSlots * kQBytes;
   static constexpr int kWaveBytes = kOffP + kPageTokens * G * 4;
   static_assert(kWaveBytes % 16 == 0, "16-byte aligned slots");
+  static_assert(kPlaneIns + kScaleIns + kQIns <= 15, "a unit's loads fit a 4-bit count");
+  static_assert(kRing >= 2 && kRing <= 4, "ring of 2 to 4 units");
 };
 
 // Dynamic LDS of one workgroup: the pairs' page prefix and lengths, then the
@@ -226,9 +240,10 @@ inline size_t attn_lds_bytes(int32_t pairs) {
 }
 
 template <int G, bool FP8, bool F16>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   using Gm = Geo<G, FP8>;
+  constexpr int R = Gm::kRing;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int32_t wave_tot[kAttnWaves];
   int32_t* pre_l = reinterpret_cast<int32_t*>(lds);  // [pairs + 1]
@@ -289,15 +304,18 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
   const int64_t s0 = gw * S < T ? gw * S : T;
   const int64_t s1 = s0 + S < T ? s0 + S : T;
   if (s0 >= s1) return;  // no barrier follows: an idle wave may leave
+  // The two resident workgroups of a CU put one wave each on every SIMD, and
+  // the SIMD's arbiter favours the older wave: with equal spans the first
+  // workgroup's waves finished in ~180 us and the second's in ~220 us (batch
+  // 256 decode shape). The two waves take turns at the higher issue priority,
+  // page by page, by the parity of their hardware wave slot (HW_ID WAVE_ID).
+  const uint32_t wslot = __builtin_amdgcn_s_getreg((3 << 11) | 4) & 1u;
 
   uint8_t* wl = lds + meta + (size_t)wave * Gm::kWaveBytes;
-  uint8_t* kslot = wl + Gm::kOffK;
-  uint8_t* vslot = wl + Gm::kOffV;
-  uint8_t* sslot = wl + Gm::kOffS;
-  uint8_t* qslot = wl + Gm::kOffQ;
   float* ptile = reinterpret_cast<float*>(wl + Gm::kOffP);  // [16 tokens][G]
-  const uint32_t kslot_a = lds_addr(kslot), vslot_a = lds_addr(vslot);
-  const uint32_t sslot_a = lds_addr(sslot), qslot_a = lds_addr(qslot);
+  const uint32_t unit_a = lds_addr(wl + Gm::kOffU);         // slot i at unit_a + i * kPlane
+  const uint32_t scale_a = lds_addr(wl + Gm::kOffS);        // slot i at scale_a + i * 256
+  const uint32_t q_a = lds_addr(wl + Gm::kOffQ);            // slot i at q_a + i * kQBytes
 
   // The pair holding flat page f: the last pair p with pre[p] <= f (empty
   // pairs share their successor's prefix, so it is never empty).
@@ -310,7 +328,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
     return __builtin_amdgcn_readfirstlane(lo);
   };
 
-  // ---- lane constants of the DMA addressing and the LDS reads
+  // ---- lane constants of the DMA addressing and the LDS reads (relative to
+  // a slot's start)
   const int64_t row_stride = (int64_t)a.hkv * Gm::kCodeRow;  // bytes between token rows
   uint32_t voff[Gm::kPlaneIns];  // lane's byte offset in a page plane, per instruction
 #pragma unroll
@@ -329,19 +348,19 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
   uint32_t koff[FP8 ? 4 : 8];                 // K operand reads
   if constexpr (FP8) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) koff[r] = kslot_a + (n * 16 + ((4 * r + g) ^ n)) * 16;
+    for (int r = 0; r < 4; ++r) koff[r] = (n * 16 + ((4 * r + g) ^ n)) * 16;
   } else {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) koff[s] = kslot_a + (n * 32 + ((4 * s + g) ^ n)) * 16;
+    for (int s = 0; s < 8; ++s) koff[s] = (n * 32 + ((4 * s + g) ^ n)) * 16;
   }
   uint32_t voffr[8];  // V row reads: token 8 hf + k, chunk c8
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int t = 8 * hf + k;
     if constexpr (FP8)
-      voffr[k] = vslot_a + (t * 16 + ((c8 >> 1) ^ t)) * 16 + (c8 & 1) * 8;
+      voffr[k] = (t * 16 + ((c8 >> 1) ^ t)) * 16 + (c8 & 1) * 8;
     else
-      voffr[k] = vslot_a + (t * 32 + (c8 ^ t)) * 16;
+      voffr[k] = (t * 32 + (c8 ^ t)) * 16;
   }
   auto lds_ld16 = [](uint32_t addr) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(addr);
@@ -350,78 +369,121 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(addr);
   };
 
-  // ---- the issue side: page f's K plane (after the pair's query rows when
-  // it starts a pair, and with the page's scales for fp8), then its V plane
-  int32_t ip = pair_of(s0);          // pair of the next page to issue
-  int64_t ipre1 = pre_l[ip + 1];     // its end
-  int64_t irow = 0;                  // first cached row of the page being issued
-  bool ibad = false;
-  auto locate = [&](int64_t f) {
-    const int64_t b = ip / a.hkv;
-    const int64_t j = f - pre_l[ip];
-    if (a.seq_rows > 0) {
-      irow = b * a.seq_rows + j * kPageTokens;
-      ibad = false;
+  // ---- the issue side walks the span's units in order
+  const int64_t nunits = 2 * (s1 - s0);
+  int64_t iu = 0;                    // next unit to issue
+  int32_t ip = pair_of(s0);          // pair of the page being issued
+  int64_t ipre0 = pre_l[ip], ipre1 = pre_l[ip + 1];
+  int64_t irow = 0;                  // first cached row of that page
+  int64_t irows = kPageTokens;       // its rows inside a contiguous sequence's storage
+  uint32_t iqn = 0;                  // pairs whose query rows were issued
+  uint32_t badbits = 0;              // bit (f - s0) & 31: page id outside the pool
+  // unit sizes in flight (4 bits each, oldest lowest) and their sum
+  uint32_t fifo = 0;
+  int fifo_n = 0, fifo_total = 0;
+  // one page plane into a slot; rows of a contiguous sequence's last page
+  // past its end are not read (the lane's row is clamped to the last valid
+  // one, only on that page)
+  auto issue_plane = [&](const uint8_t* base, uint32_t slot_a) {
+    if (irows >= kPageTokens) {
+#pragma unroll
+      for (int jj = 0; jj < Gm::kPlaneIns; ++jj) dma16(base, voff[jj], slot_a + jj * 1024);
     } else {
-      int32_t pid = ld_const(a.table + b * a.tstride + j);
-      ibad = pid < 0 || pid >= a.num_pages;
-      if (ibad) {
-        if (lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
-        pid = 0;
+#pragma unroll
+      for (int jj = 0; jj < Gm::kPlaneIns; ++jj) {
+        const int p = 64 * jj + lane;
+        int r = p / Gm::kChunks;
+        const int c = (p % Gm::kChunks) ^ (r & 15);
+        if (r >= irows) r = (int)irows - 1;
+        dma16(base, (uint32_t)(r * row_stride + c * 16), slot_a + jj * 1024);
       }
-      irow = (int64_t)pid * kPageTokens;
     }
   };
-  // rows of a contiguous sequence's last page past its end are not read:
-  // clamp the lane's row to the last valid one (only that page)
-  auto plane_off = [&](int j, int64_t rows_left) -> uint32_t {
-    if (rows_left >= kPageTokens) return voff[j];
-    const int p = 64 * j + lane;
-    int r = p / Gm::kChunks;
-    const int c = (p % Gm::kChunks) ^ (r & 15);
-    if (r >= rows_left) r = (int)rows_left - 1;
-    return (uint32_t)(r * row_stride + c * 16);
-  };
-  auto issue_k = [&](int64_t f, bool with_q, int64_t rows_left) -> int {
-    lds_reads_done();
-    if (with_q) {
-      const uint8_t* qb = a.q + (int64_t)ip * G * kRowBytes;
+  auto issue_next = [&]() {
+    const int64_t u = iu++;
+    const int64_t f = s0 + (u >> 1);
+    const uint32_t slot = (uint32_t)(u % R);
+    lds_reads_done();  // the slot's (and query slot's) earlier readers have their data
+    int size = Gm::kPlaneIns;
+    const int64_t hk = ip % a.hkv;
+    if ((u & 1) == 0) {
+      bool new_pair = u == 0;
+      if (f == ipre1) {
+        ip = pair_of(f);
+        ipre0 = pre_l[ip];
+        ipre1 = pre_l[ip + 1];
+        new_pair = true;
+      }
+      const int64_t b = ip / a.hkv;
+      const int64_t j = f - ipre0;
+      bool bad = false;
+      if (a.seq_rows > 0) {
+        irow = b * a.seq_rows + j * kPageTokens;
+        const int64_t left = a.seq_rows - j * kPageTokens;
+        irows = left < kPageTokens ? left : kPageTokens;
+      } else {
+        int32_t pid = ld_const(a.table + b * a.tstride + j);
+        bad = pid < 0 || pid >= a.num_pages;
+        if (bad) {
+          if (lane == 0) raise_err(a.err, MKV_DEVERR_PAGE);
+          pid = 0;
+        }
+        irow = (int64_t)pid * kPageTokens;
+        irows = kPageTokens;
+      }
+      const uint32_t bit = 1u << ((f - s0) & 31);
+      badbits = bad ? (badbits | bit) : (badbits & ~bit);
+      const int64_t hk2 = ip % a.hkv;
+      if (new_pair) {
+        const uint8_t* qb = a.q + (int64_t)ip * G * kRowBytes;
+        const uint32_t qs = q_a + (iqn % Gm::kQSlots) * Gm::kQBytes;
+        ++iqn;
 #pragma unroll
-      for (int j = 0; j < Gm::kQIns; ++j)
-        dma16(qb, (uint32_t)((j * 1024 + lane * 16) % (G * kRowBytes)), qslot_a + j * 1024);
+        for (int jj = 0; jj < Gm::kQIns; ++jj)
+          dma16(qb, (uint32_t)((jj * 1024 + lane * 16) % (G * kRowBytes)), qs + jj * 1024);
+        size += Gm::kQIns;
+      }
+      issue_plane(a.k + (irow * a.hkv + hk2) * Gm::kCodeRow, unit_a + slot * Gm::kPlane);
+      if constexpr (FP8) {
+        dma4(sbase + (irow + st) * a.hkv + hk2, scale_a + slot * Gm::kScaleBytes);
+        size += Gm::kScaleIns;
+      }
+    } else {
+      issue_plane(a.v + (irow * a.hkv + hk) * Gm::kCodeRow, unit_a + slot * Gm::kPlane);
     }
-    const int64_t hk = ip % a.hkv;
-    const uint8_t* base = a.k + (irow * a.hkv + hk) * Gm::kCodeRow;
-#pragma unroll
-    for (int j = 0; j < Gm::kPlaneIns; ++j) dma16(base, plane_off(j, rows_left), kslot_a + j * 1024);
-    if constexpr (FP8) dma4(sbase + (irow + st) * a.hkv + hk, sslot_a);
-    return Gm::kPlaneIns + Gm::kScaleIns + (with_q ? Gm::kQIns : 0);
+    fifo |= (uint32_t)size << (4 * fifo_n);
+    ++fifo_n;
+    fifo_total += size;
   };
-  auto issue_v = [&](int64_t rows_left) {
-    lds_reads_done();
-    const int64_t hk = ip % a.hkv;
-    const uint8_t* base = a.v + (irow * a.hkv + hk) * Gm::kCodeRow;
-#pragma unroll
-    for (int j = 0; j < Gm::kPlaneIns; ++j) dma16(base, plane_off(j, rows_left), vslot_a + j * 1024);
+  // waits for the oldest unit in flight (its loads and every earlier one)
+  auto wait_oldest = [&]() {
+    const int younger = fifo_total - (int)(fifo & 15u);
+    if constexpr (R == 2) {
+      // at most one younger unit: a V plane, a K plane (+ scales), or that
+      // with a pair's query rows
+      constexpr int kK = Gm::kPlaneIns + Gm::kScaleIns;
+      if (younger == 0) vm_wait_n<0>();
+      else if (younger == Gm::kPlaneIns) vm_wait_n<Gm::kPlaneIns>();
+      else if (younger == kK) vm_wait_n<kK>();
+      else if (younger == kK + Gm::kQIns) vm_wait_n<kK + Gm::kQIns>();
+      else vm_wait(younger);
+    } else {
+      vm_wait(younger);
+    }
   };
-  // rows of the page being issued that lie inside a contiguous sequence's
-  // storage (16 in paged mode)
-  auto rows_in_seq = [&](int64_t f) -> int64_t {
-    if (a.seq_rows <= 0) return kPageTokens;
-    const int64_t left = a.seq_rows - (f - pre_l[ip]) * kPageTokens;
-    return left < kPageTokens ? left : kPageTokens;
+  auto retire_and_refill = [&]() {
+    fifo_total -= (int)(fifo & 15u);
+    fifo >>= 4;
+    --fifo_n;
+    if (iu < nunits) issue_next();
   };
+  for (int k = 0; k < R && iu < nunits; ++k) issue_next();
 
   // ---- the consume side
-  int32_t cp = ip;                 // pair of the page being consumed
-  int64_t cpre0 = pre_l[cp], cpre1 = ipre1;
+  int32_t cp = pair_of(s0);        // pair of the page being consumed
+  int64_t cpre0 = pre_l[cp], cpre1 = pre_l[cp + 1];
   int32_t clen = len_l[cp];
-  locate(s0);
-  bool cbad = ibad;
-  int64_t rows0 = rows_in_seq(s0);
-  issue_k(s0, true, rows0);
-  issue_v(rows0);
-
+  uint32_t cqn = 0;                // pairs whose query rows were read
   u32x4 qb[8];
   float m_run = -INFINITY, l_run = 0.f;  // head n (lanes n < G)
   float o[G][8];
@@ -432,55 +494,55 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
   bool seg_first = true;
 
   for (int64_t f = s0; f < s1; ++f) {
-    // K plane (and query rows, scales) of page f: only its V plane was issued after it
-    vm_wait(Gm::kPlaneIns);
+    const int64_t uk = 2 * (f - s0);
+    const uint32_t kslot = unit_a + (uint32_t)(uk % R) * Gm::kPlane;
+    const uint32_t sslot = scale_a + (uint32_t)(uk % R) * Gm::kScaleBytes;
+    const uint32_t vslot = unit_a + (uint32_t)((uk + 1) % R) * Gm::kPlane;
+    __builtin_amdgcn_s_setprio(0);
+    if ((((uint32_t)(f - s0) & 1u) ^ wslot) != 0) __builtin_amdgcn_s_setprio(1);
+    // K plane (and query rows, scales) of page f
+    wait_oldest();
     if (seg_first) {
       // the pair's query heads as the B operand, in the K operand's dim
       // order: bf16, step s covers dims 8*(4s+g) .. +7; fp8, K chunk 4r+g
       // holds 16 codes, step s = 2r+h covers dims 16*(4r+g) + 8h .. +7
+      const uint32_t qs = q_a + (cqn % Gm::kQSlots) * Gm::kQBytes;
+      ++cqn;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         const int chunk = FP8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
-        const u32x4 w = lds_ld16(qslot_a + (n < G ? n : 0) * kRowBytes + chunk * 16);
+        const u32x4 w = lds_ld16(qs + (n < G ? n : 0) * kRowBytes + chunk * 16);
         qb[s] = n < G ? w : u32x4{0u, 0u, 0u, 0u};
       }
     }
-    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (FP8) {
+    // the page's K operand rows (and scales) into registers; the K slot is
+    // then free and the ring is refilled before the MFMAs run
+    u32x4 kr[FP8 ? 4 : 8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const u32x4 kc = lds_ld16(koff[r]);
-        sc = mfma16<false>(fp8x8_bf16(kc.x, kc.y), qb[2 * r], sc);
-        sc = mfma16<false>(fp8x8_bf16(kc.z, kc.w), qb[2 * r + 1], sc);
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) sc = mfma16<F16>(lds_ld16(koff[s]), qb[s], sc);
-    }
+    for (int s = 0; s < (FP8 ? 4 : 8); ++s) kr[s] = lds_ld16(kslot + koff[s]);
     float ksc[4], vsc[4];
     if constexpr (FP8) {
-      const u32x4 kw = lds_ld16(sslot_a + 16 * g);
-      const u32x4 vw = lds_ld16(sslot_a + 64 + 16 * g);
+      const u32x4 kw = lds_ld16(sslot + 16 * g);
+      const u32x4 vw = lds_ld16(sslot + 64 + 16 * g);
       ksc[0] = bits_f32(kw.x); ksc[1] = bits_f32(kw.y); ksc[2] = bits_f32(kw.z); ksc[3] = bits_f32(kw.w);
       vsc[0] = bits_f32(vw.x); vsc[1] = bits_f32(vw.y); vsc[2] = bits_f32(vw.z); vsc[3] = bits_f32(vw.w);
     }
     // page f's tokens of its pair: valid rows (0 for a page id outside the pool)
     const int64_t tok0 = (f - cpre0) * kPageTokens;
+    const bool cbad = (badbits >> ((f - s0) & 31)) & 1u;
     const int valid = cbad ? 0 : (int)(clen - tok0 < kPageTokens ? clen - tok0 : kPageTokens);
     const bool seg_last = f + 1 == cpre1 || f + 1 == s1;
-
-    // issue page f+1's K plane now that the K slot has been read
-    int next_k = 0;
-    bool nbad = false;
-    if (f + 1 < s1) {
-      const bool new_pair = f + 1 == ipre1;
-      if (new_pair) {
-        ip = pair_of(f + 1);
-        ipre1 = pre_l[ip + 1];
+    retire_and_refill();
+    f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (FP8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc = mfma16<false>(fp8x8_bf16(kr[r].x, kr[r].y), qb[2 * r], sc);
+        sc = mfma16<false>(fp8x8_bf16(kr[r].z, kr[r].w), qb[2 * r + 1], sc);
       }
-      locate(f + 1);
-      nbad = ibad;
-      next_k = issue_k(f + 1, new_pair, rows_in_seq(f + 1));
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sc = mfma16<F16>(kr[s], qb[s], sc);
     }
 
     // online softmax for head n over the page's tokens 4g + i
@@ -512,39 +574,50 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
     if (rescale) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float al = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+        const float al = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[h][e] *= al;
       }
     }
 
-    // V plane of page f: only page f+1's K plane (if any) was issued after it
-    vm_wait(next_k);
+    // V plane of page f
+    wait_oldest();
     if (valid < kPageTokens) {
       // rows past the sequence's end (or of a page id outside the pool) may
       // hold anything: zero them so that 0-weight rows add exact zeros
       for (int i = lane; i < (kPageTokens - valid) * Gm::kChunks; i += 64) {
         const int r = valid + i / Gm::kChunks;
         *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
-            vslot_a + (r * Gm::kChunks + (i % Gm::kChunks)) * 16) = u32x4{0u, 0u, 0u, 0u};
+            vslot + (r * Gm::kChunks + (i % Gm::kChunks)) * 16) = u32x4{0u, 0u, 0u, 0u};
       }
     }
     wave_sync();  // the probability tile and zeroed rows before the reads below
+    // the page's V rows into registers; the V slot is then free and the ring
+    // is refilled before the FMAs run
+    typedef typename std::conditional<FP8, u32x2, u32x4>::type VRow;
+    VRow vr[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if constexpr (FP8)
+        vr[k] = lds_ld8(vslot + voffr[k]);
+      else
+        vr[k] = lds_ld16(vslot + voffr[k]);
+    }
+    retire_and_refill();
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int t = 8 * hf + k;
       float vv[8];
       if constexpr (FP8) {
-        const u32x2 w = lds_ld8(voffr[k]);
-        const f32x2 a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, false);
-        const f32x2 a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, true);
-        const f32x2 a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, false);
-        const f32x2 a3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, true);
+        const f32x2 a0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[k].x, false);
+        const f32x2 a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[k].x, true);
+        const f32x2 a2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[k].y, false);
+        const f32x2 a3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)vr[k].y, true);
         vv[0] = a0.x; vv[1] = a0.y; vv[2] = a1.x; vv[3] = a1.y;
         vv[4] = a2.x; vv[5] = a2.y; vv[6] = a3.x; vv[7] = a3.y;
       } else {
-        const u32x4 w = lds_ld16(voffr[k]);
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t ww[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           vv[2 * e] = F16 ? f16_lo(ww[e]) : bf16_lo(ww[e]);
@@ -567,8 +640,6 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[h][e] += pt[h] * vv[e];
     }
-    // issue page f+1's V plane now that the V slot has been read
-    if (f + 1 < s1) issue_v(rows_in_seq(f + 1));
     wave_sync();  // the next page rewrites the probability tile
 
     if (seg_last) {
@@ -582,7 +653,8 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
         uint8_t* orow = a.out + (int64_t)cp * G * kRowBytes;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), h));
+          const float L = __builtin_bit_cast(
+              float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_run), h));
           if (hf == 0) {
             uint32_t w[4];
 #pragma unroll
@@ -615,15 +687,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_span_kernel(AttnArgs a) 
       for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
-      if (f + 1 < s1) {
-        cp = ip;  // the issue side is already at page f+1's pair
+      if (f + 1 < s1) {  // the next pair with pages
+        cp = pair_of(f + 1);
         cpre0 = pre_l[cp];
-        cpre1 = ipre1;
+        cpre1 = pre_l[cp + 1];
         clen = len_l[cp];
       }
     }
     seg_first = seg_last;
-    cbad = nbad;
   }
 }
 

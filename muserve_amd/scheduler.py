@@ -186,6 +186,15 @@ class ContinuousBatchScheduler:
         if state_pool is not None and state_pool.num_slots < max_batch_size:
             raise ValueError(f"state pool has {state_pool.num_slots} slots for "
                              f"{max_batch_size} batch rows")
+        if state_pool is not None and block_manager is not None:
+            # a prefix hit skips prefill of the hit pages, but the GDN layers'
+            # recurrent and conv states at the end of that prefix are not
+            # cached (the reference keeps them with each prefix entry,
+            # muserve/model/prefix_cache.py:74-79,98-105): the request would
+            # start its recurrent layers from zero states partway through its
+            # prompt. Prefix reuse is therefore for attention-only stacks.
+            raise ValueError("prefix reuse (block_manager=) does not cache GDN states: it "
+                             "cannot be combined with a state_pool")
         self.state_pool = state_pool
         self.block_manager = block_manager
         self.bm_held = 0          # sum of fb over requests admitted to the block manager

@@ -193,3 +193,23 @@ def test_max_seq_len_finishes_a_request():
         s.complete_step(p)
     # prompt 16, then decodes at positions 16 and 17; the cache is full at 18
     assert r.is_done and r.seq.seq_len == 18 and len(r.generated_tokens) == 3
+
+
+def test_prefix_reuse_with_gdn_states_is_rejected():
+    """A prefix hit skips prefill of its pages, but GDN states are not cached
+    with the pages: a scheduler with both a state pool and a block manager
+    would run the recurrent layers from zero states mid-prompt."""
+    from types import SimpleNamespace
+
+    from muserve_amd.scheduler import ContinuousBatchScheduler
+    with pytest.raises(ValueError, match="does not cache GDN states"):
+        ContinuousBatchScheduler(max_batch_size=4, state_pool=SimpleNamespace(num_slots=8),
+                                 block_manager=object())
+
+
+def test_block_manager_step_refuses_a_pending_half_step():
+    from muserve_amd.block_manager import BlockManager
+    bm = BlockManager.__new__(BlockManager)  # no device state: the guard comes first
+    bm._pending = ((), ())
+    with pytest.raises(RuntimeError, match="awaits its step_end"):
+        bm.step(None, None, None, None)
