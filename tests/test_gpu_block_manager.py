@@ -114,13 +114,18 @@ def synthetic_keys(n, seed, alphabet, max_pages, skew):
 
 
 def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=False,
-        ops_fn=bench.prefix_ops, keys=None, split=False):
+        ops_fn=bench.prefix_ops, keys=None, split=False, data_layers=2):
     """Drives the manager through ops_fn's steps and checks it against the
     model; returns the statuses, the model and the final snapshot. `keys` =
     (token counts, per-request key lists) replaces the hashed prompts.
     split: each step as step_begin + step_end; where the committed-admit
     count grew by the step's admits, their results read between the halves
-    are checked too (snap["early_steps"] counts those steps)."""
+    are checked too (snap["early_steps"] counts those steps).
+    with_data: a bf16 pool of data_layers layers holds random pages and each
+    step's copy-on-write pairs are copied by the library. The expected pool
+    applies the model's pairs (torch indexing: on the CPU for small pools, on
+    the device for large ones), and every page of the pool is compared at the
+    end."""
     if keys is None:
         reqs = bench.prefix_requests(n, seed=seed, n_templates=n_templates,
                                      template_len=template_len, suffix=suffix)
@@ -129,8 +134,8 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         flat = torch.from_numpy(np.concatenate(reqs)).to(DEV)
         hashes, cu_pages = page_hashes(flat, cu)
         hu = as_u64(hashes)
-        for r in (0, n // 2, n - 1):  # the GPU hashes are the prefix keys
-            assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r])
+        for r in range(n):  # every request's GPU page hashes are its hashlib prefix keys
+            assert hu[cu_pages[r]:cu_pages[r + 1]].tolist() == cpu_page_hashes(reqs[r]), r
     else:
         lens, kl = keys
         cu_pages = np.concatenate([[0], np.cumsum([len(k) for k in kl])]).astype(np.int64)
@@ -142,13 +147,19 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     model = BlockManagerModel(P, free)
     cache = cpu = None
     if with_data:
-        cache = PagedKVCache(P, num_layers=2, dtype=torch.bfloat16, device=DEV, verbose=False)
-        cpu = torch.randn(cache.cache.shape, generator=torch.Generator().manual_seed(seed)).bfloat16()
-        cache.cache.copy_(cpu.to(DEV))
+        cache = PagedKVCache(P, num_layers=data_layers, dtype=torch.bfloat16, device=DEV,
+                             verbose=False)
+        if data_layers <= 2:
+            cpu = torch.randn(cache.cache.shape,
+                              generator=torch.Generator().manual_seed(seed)).bfloat16()
+            cache.cache.copy_(cpu.to(DEV))
+        else:  # a full-size pool: random pages made on the device, the expected pool too
+            cache.cache.normal_(generator=torch.Generator(device=DEV).manual_seed(seed))
+            cpu = cache.cache.clone()
     off = torch.from_numpy(cu_pages).to(DEV)
     ntok = torch.tensor(lens, dtype=torch.int32, device=DEV)
     want = {}
-    early_steps = 0
+    early_steps = cow_pairs = 0
     for ops in ops_fn(n, batch):
         admits = [o for o in ops if o >= 0]  # consecutive request ids
         mid = None
@@ -178,8 +189,11 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
                     assert mid[2][op, :-(-lens[op] // 16)].tolist() == want[op]["table"], op
         if with_data and admits:
             bm.copy_on_write(cache, min(admits), min(admits) + len(admits))
-            for s, d in pairs:
-                cpu[:, :, d] = cpu[:, :, s]
+            if pairs:  # a fresh destination is never another pair's source
+                src = torch.tensor([p[0] for p in pairs], device=cpu.device)
+                dst = torch.tensor([p[1] for p in pairs], device=cpu.device)
+                cpu[:, :, dst] = cpu[:, :, src]
+            cow_pairs += len(pairs)
     bm.check_errors()
     ctr = bm.counters()
     print(f"speculation: {ctr[7]} admits resolved, {ctr[8]} left to the sequential kernels",
@@ -209,7 +223,10 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
     log = bm.evict_log.cpu().tolist()[:snap["log_len"]]
     assert log == model.evicted
     if with_data:
-        assert torch.equal(bits16(cache.cache), cpu.view(torch.int16))
+        if cpu.device.type == "cpu":
+            assert torch.equal(bits16(cache.cache), cpu.view(torch.int16))
+        else:
+            assert torch.equal(cache.cache.view(torch.int16), cpu.view(torch.int16))
         cache.check_errors()
     # read-only probe of every request against the final table
     pages, hit = bm.probe(hashes, off)
@@ -223,6 +240,7 @@ def run(P, n, batch, seed, n_templates, template_len, suffix, width, with_data=F
         assert hit[r] == lead, r
     assert bm.snapshot()["lru"] == snap["lru"]  # nothing moved
     snap["early_steps"] = early_steps
+    snap["cow_pairs"] = cow_pairs
     return status, model, snap
 
 

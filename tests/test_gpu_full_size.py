@@ -217,15 +217,21 @@ def test_gdn_config_gather_scatter_identities():
     pool.check_errors()
 
 
+@pytest.mark.timeout(900)
 def test_prefix_config_full_trace_against_model():
     # 4096 requests (Zipf(1.1) over 64 templates of 4096 ids + 64..1024-token
-    # suffixes), batches of 256, 65536 pages: every admit, table, hit count,
-    # copy-on-write pair, the 89k-entry eviction order and the final state
-    case("full size: prefix cache, 4096 requests, 65536 pages, batches of 256")
+    # suffixes), batches of 256, 65536 pages: every request's page hashes
+    # against hashlib, every admit, table, hit count, copy-on-write pair, the
+    # 89k-entry eviction order and the final state; the copies run on a real
+    # 15-layer bf16 pool of 65536 pages (16 GB of random pages), compared page
+    # for page at the end with the model's pairs applied to a copy of it
+    case("full size: prefix cache, 4096 requests, 65536 pages x 15 layers, batches of 256")
     status, model, snap = run_block_manager(P=65536, n=4096, batch=256, seed=104, n_templates=64,
-                                      template_len=4096, suffix=(64, 1024), width=320)
+                                      template_len=4096, suffix=(64, 1024), width=320,
+                                      with_data=True, data_layers=15)
     assert len(model.evicted) > 50000
     assert snap["spec_done"] + snap["spec_left"] == 4096  # every admit was speculated
+    assert snap["cow_pairs"] > 3000  # copy-on-write pairs copied and checked
 
 
 @pytest.mark.timeout(600)
