@@ -42,6 +42,7 @@ LAYERS = 15
 HEAD_DIM = 256
 ROW = HEAD_DIM * 2  # bytes per token row (1 head, bf16)
 SEED = 102
+PLACEMENT = "shuffled"  # fp8_prefill page placement (--placement)
 
 
 def log(msg: str) -> None:
@@ -455,7 +456,9 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
     pages = R * CTX // 16 + 16
     cache = PagedKVCache(pages, num_layers=L, kv_heads=1, head_dim=HEAD_DIM,
                          dtype=torch.float8_e4m3fn, device=dev, verbose=False)
-    cache.shuffle_free_list(torch.Generator().manual_seed(103))
+    if PLACEMENT == "shuffled":
+        cache.shuffle_free_list(torch.Generator().manual_seed(103))
+    # "contiguous": the LIFO free list hands each request consecutive pages
     gen = torch.Generator(device=dev).manual_seed(103)
 
     def kv_batch(t: int) -> torch.Tensor:
@@ -555,7 +558,8 @@ def run_fp8_prefill(steps: int, warmup: int, with_cpu: bool) -> dict:
         "data": "synthetic (seeded ~N(0,1) bf16 K/V with 1% x20 outliers)",
         "config": {"workload": ("fp8 chunked prefill: 32 requests x 2048-token chunks into 128k "
                                 "contexts, 15 layers, 1 KV head x 256, e4m3fn + fp32 per-token "
-                                "scale, then dequant-gather of the last 8192 tokens; seed 103")},
+                                "scale, then dequant-gather of the last 8192 tokens; seed 103"),
+                   "page_placement": PLACEMENT},
         "appended_tokens_per_s": round(T / step_s, 1),
         "step_time": _step_stats(step_spans),
         "pct_of_hbm_peak": round(100 * step_bytes_ / step_s / 1e9 / HBM_PEAK_GBS, 2),
@@ -1283,6 +1287,9 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
         pool.conv.normal_(generator=gen)
     s = ContinuousBatchScheduler(max_batch_size=SCHED_BATCH, max_seq_len=max_seq, kv_cache=cache,
                                  chunked_prefill_size=chunk, state_pool=pool, block_manager=bm)
+    # pages several running requests may read: the block manager's cached
+    # prompt pages [0, bm_pages); the private tail and decode pages lie above
+    shared = bm.num_pages if bm is not None else 0
     for i in range(n_req):
         ids = token_ids[i].tolist() if prefix else [0] * int(prompts[i])
         s.add_request(InferenceRequest(request_id=str(i), input_ids=ids,
@@ -1383,10 +1390,11 @@ def run_sched(steps: int, warmup: int, with_cpu: bool, fp8: bool = False,
                 sp = stamps.span(stream) if rec is not None else None
                 if fp8:
                     A.attn_decode_fp8(q[l, :nd], kp, vp, cache.scales[l, 0], cache.scales[l, 1],
-                                      plan.seq_lens[:nd], plan.block_tables[:nd], out=out[l, :nd])
+                                      plan.seq_lens[:nd], plan.block_tables[:nd], out=out[l, :nd],
+                                      shared_pages=shared)
                 else:
                     A.attn_decode(q[l, :nd], kp, vp, plan.seq_lens[:nd], plan.block_tables[:nd],
-                                  out=out[l, :nd])
+                                  out=out[l, :nd], shared_pages=shared)
                 if rec is not None:
                     rec.append(("attn", sp.end(stream)))
             if n > nd:  # the prefill chunks attend to their prefix and themselves
@@ -1956,6 +1964,9 @@ def main() -> int:
     ap.add_argument("--serial-prefill", action="store_true",
                     help="sched workloads: prefill attention on the main stream, after the "
                          "decode attention (default: beside it on a second stream)")
+    ap.add_argument("--placement", choices=("shuffled", "contiguous"), default="shuffled",
+                    help="fp8_prefill: pool pages from a shuffled free list (default) or "
+                         "consecutive pages per request (to measure what the scatter costs)")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
@@ -1963,6 +1974,8 @@ def main() -> int:
                              "prefill_attn"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
+    global PLACEMENT
+    PLACEMENT = args.placement
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this path has no cross-GPU traffic "
               "(each tensor-parallel rank owns its own pool); run with --gpus 1",

@@ -524,6 +524,12 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
  *   k_cache, v_cache: [num_pages, 16, num_kv_heads, 256] bf16 (one layer's
  *            planes of the pool), 16-byte aligned;
  *   page_table: [batch][table_stride] int32, table_width valid columns;
+ *   shared_pages: page ids below it may be read by several sequences (a
+ *            prefix shared through the block manager, whose page range is
+ *            [0, its num_pages)): their K/V are loaded through the caches so
+ *            the readers share them; every other page streams past the caches
+ *            (non-temporal loads, faster for pages one sequence reads). 0: no
+ *            page is shared. Results do not depend on it;
  *   max_seq_len: an upper bound of seq_lens; longer sequences are cut to it;
  *   workspace: mkv_decode_attention_workspace_bytes(...) bytes, 16-byte
  *            aligned, contents irrelevant between calls: it receives the
@@ -542,8 +548,9 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
 int64_t mkv_decode_attention_workspace_bytes(int32_t batch, int32_t num_kv_heads,
                                              int32_t num_q_heads, int32_t max_seq_len);
 int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
-                              int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
-                              int32_t head_dim, const int32_t* page_table, int64_t table_stride,
+                              int64_t num_pages, int64_t shared_pages, int32_t num_kv_heads,
+                              int32_t num_q_heads, int32_t head_dim, const int32_t* page_table,
+                              int64_t table_stride,
                               int32_t table_width, const int32_t* seq_lens, int32_t batch,
                               int32_t max_seq_len, float softmax_scale, void* out,
                               void* workspace, int64_t workspace_bytes, int32_t* err,
@@ -583,8 +590,9 @@ int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_cache, const 
  * as mkv_decode_attention_bf16.
  */
 int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_cache,
-                             int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
-                             int32_t head_dim, const int32_t* page_table, int64_t table_stride,
+                             int64_t num_pages, int64_t shared_pages, int32_t num_kv_heads,
+                             int32_t num_q_heads, int32_t head_dim, const int32_t* page_table,
+                             int64_t table_stride,
                              int32_t table_width, const int32_t* seq_lens, int32_t batch,
                              int32_t max_seq_len, float softmax_scale, void* out,
                              void* workspace, int64_t workspace_bytes, int32_t* err,
@@ -603,7 +611,8 @@ int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_c
  */
 int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_codes,
                              const float* k_scales, const float* v_scales, int64_t num_pages,
-                             int32_t num_kv_heads, int32_t num_q_heads, int32_t head_dim,
+                             int64_t shared_pages, int32_t num_kv_heads, int32_t num_q_heads,
+                             int32_t head_dim,
                              const int32_t* page_table, int64_t table_stride,
                              int32_t table_width, const int32_t* seq_lens, int32_t batch,
                              int32_t max_seq_len, float softmax_scale, void* out,

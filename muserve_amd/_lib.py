@@ -89,14 +89,14 @@ SIGNATURES: dict[str, list] = {
                         _P, _I64, _P, _P],
     "mkv_hash_probe": [_P, _I32, _P, _P, _I32, _P, _P, _P, _P],
     "mkv_decode_attention_workspace_bytes": [_I32, _I32, _I32, _I32],
-    "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
-                                  _I32, _F32, _P, _P, _I64, _P, _P],
+    "mkv_decode_attention_bf16": [_P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
+                                  _I32, _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_bf16_noalloc": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
                                           _I32, _I32, _F32, _P, _P, _P],
-    "mkv_decode_attention_f16": [_P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P, _I32,
-                                 _I32, _F32, _P, _P, _I64, _P, _P],
-    "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
+    "mkv_decode_attention_f16": [_P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _I64, _I32, _P,
                                  _I32, _I32, _F32, _P, _P, _I64, _P, _P],
+    "mkv_decode_attention_fp8": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _I64, _I32,
+                                 _P, _I32, _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_contig": [_P, _P, _P, _I32, _I32, _I32, _I32, _I64, _P, _I32, _I32, _F32,
                                     _P, _P, _I64, _P, _P],
 }

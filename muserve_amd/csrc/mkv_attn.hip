@@ -81,6 +81,7 @@ struct AttnArgs {
   float* part;           // [waves, 2, G, 256] unnormalised outputs of cut pairs' pieces
   float* ml;             // [waves, 2, G, 2] their (max, sum), log2 units
   int64_t num_pages, tstride;
+  int64_t shared_below;  // page ids below it are loaded through the caches
   int64_t seq_rows;      // contiguous mode: rows per sequence (0: paged)
   int32_t twidth, hkv, max_len, pairs;
   float scale_log2;      // softmax_scale * log2(e)
@@ -168,6 +169,14 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
                : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform_ptr(base))
                : "memory");
 }
+// the same through the caches (pages several sequences read: a prefix
+// shared through the block manager)
+__device__ __forceinline__ void dma16_cached(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(uniform_ptr(base))
+               : "memory");
+}
 // 4 bytes per lane from a per-lane 64-bit address
 __device__ __forceinline__ void dma4(const void* addr, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off nt"
@@ -239,7 +248,10 @@ inline size_t attn_lds_bytes(int32_t pairs) {
   return meta + (size_t)kAttnWaves * Geo<G, FP8>::kWaveBytes;
 }
 
-template <int G, bool FP8, bool F16>
+// SHARED: some pages (ids below shared_below) are read through the caches;
+// without it every page streams (the launch picks the variant, so a batch
+// with no shared pages carries no code or registers for them).
+template <int G, bool FP8, bool F16, bool SHARED>
 __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   using Gm = Geo<G, FP8>;
@@ -319,7 +331,7 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
 
   // The pair holding flat page f: the last pair p with pre[p] <= f (empty
   // pairs share their successor's prefix, so it is never empty).
-  auto pair_of = [&](int64_t f) {
+  auto pair_of = [&](int64_t f) __attribute__((always_inline)) {
     int lo = 0, hi = a.pairs - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -362,20 +374,26 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
     else
       voffr[k] = (t * 32 + (c8 ^ t)) * 16;
   }
-  auto lds_ld16 = [](uint32_t addr) {
+  auto lds_ld16 = [](uint32_t addr) __attribute__((always_inline)) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(addr);
   };
-  auto lds_ld8 = [](uint32_t addr) {
+  auto lds_ld8 = [](uint32_t addr) __attribute__((always_inline)) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(addr);
   };
 
-  // ---- the issue side walks the span's units in order
+  // ---- the issue side walks the span's units in order. Every lambda here
+  // is forced inline: a by-reference closure left out of line keeps the
+  // locals it captures (and a copy of the arguments) in scratch memory, and
+  // a scratch load waits for every outstanding page load (the 16-bit
+  // kernels ran 6x slower that way). Indices stay 32-bit where they can: a
+  // 64-bit modulo by the head count is a long software sequence per page.
   const int64_t nunits = 2 * (s1 - s0);
   int64_t iu = 0;                    // next unit to issue
   int32_t ip = pair_of(s0);          // pair of the page being issued
   int64_t ipre0 = pre_l[ip], ipre1 = pre_l[ip + 1];
   int64_t irow = 0;                  // first cached row of that page
   int64_t irows = kPageTokens;       // its rows inside a contiguous sequence's storage
+  bool icached = false;              // its planes through the caches (a shared page)
   uint32_t iqn = 0;                  // pairs whose query rows were issued
   uint32_t badbits = 0;              // bit (f - s0) & 31: page id outside the pool
   // unit sizes in flight (4 bits each, oldest lowest) and their sum
@@ -384,11 +402,14 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
   // one page plane into a slot; rows of a contiguous sequence's last page
   // past its end are not read (the lane's row is clamped to the last valid
   // one, only on that page)
-  auto issue_plane = [&](const uint8_t* base, uint32_t slot_a) {
-    if (irows >= kPageTokens) {
+  auto issue_plane = [&](const uint8_t* base, uint32_t slot_a) __attribute__((always_inline)) {
+    if (SHARED && icached) {  // uniform branches: one per plane
+#pragma unroll
+      for (int jj = 0; jj < Gm::kPlaneIns; ++jj) dma16_cached(base, voff[jj], slot_a + jj * 1024);
+    } else if (irows >= kPageTokens) {
 #pragma unroll
       for (int jj = 0; jj < Gm::kPlaneIns; ++jj) dma16(base, voff[jj], slot_a + jj * 1024);
-    } else {
+    } else {  // only a contiguous sequence's last page
 #pragma unroll
       for (int jj = 0; jj < Gm::kPlaneIns; ++jj) {
         const int p = 64 * jj + lane;
@@ -399,7 +420,7 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
       }
     }
   };
-  auto issue_next = [&]() {
+  auto issue_next = [&]() __attribute__((always_inline)) {
     const int64_t u = iu++;
     const int64_t f = s0 + (u >> 1);
     const uint32_t slot = (uint32_t)(u % R);
@@ -430,6 +451,7 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
         }
         irow = (int64_t)pid * kPageTokens;
         irows = kPageTokens;
+        icached = SHARED && pid < a.shared_below;
       }
       const uint32_t bit = 1u << ((f - s0) & 31);
       badbits = bad ? (badbits | bit) : (badbits & ~bit);
@@ -456,7 +478,7 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
     fifo_total += size;
   };
   // waits for the oldest unit in flight (its loads and every earlier one)
-  auto wait_oldest = [&]() {
+  auto wait_oldest = [&]() __attribute__((always_inline)) {
     const int younger = fifo_total - (int)(fifo & 15u);
     if constexpr (R == 2) {
       // at most one younger unit: a V plane, a K plane (+ scales), or that
@@ -471,7 +493,7 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
       vm_wait(younger);
     }
   };
-  auto retire_and_refill = [&]() {
+  auto retire_and_refill = [&]() __attribute__((always_inline)) {
     fifo_total -= (int)(fifo & 15u);
     fifo >>= 4;
     --fifo_n;
@@ -791,12 +813,16 @@ int attn_grid(int kind, int32_t pairs) {
   // the slots of four waves need more than the default 64 KiB of dynamic LDS
   // (the attribute is per kernel and device; it must be set before the
   // occupancy query, which honours it)
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_span_kernel<G, FP8, F16>),
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_span_kernel<G, FP8, F16, false>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024) != hipSuccess ||
+      hipFuncSetAttribute(reinterpret_cast<const void*>(attn_span_kernel<G, FP8, F16, true>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 159 * 1024) != hipSuccess)
     return -1;
   int per = 0;
   const size_t lds = attn_lds_bytes<G, FP8>(pairs);
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_span_kernel<G, FP8, F16>,
+  // the grid of the variant without shared pages (the other one has at least
+  // as many registers; the launch checks its own occupancy below)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_span_kernel<G, FP8, F16, false>,
                                                    kAttnThreads, lds) != hipSuccess ||
       per <= 0)
     per = 1;
@@ -812,8 +838,12 @@ int attn_grid(int kind, int32_t pairs) {
 template <int G, bool FP8, bool F16>
 int launch_attn(AttnArgs a, int grid, hipStream_t st) {
   const size_t lds = attn_lds_bytes<G, FP8>(a.pairs);
-  hipLaunchKernelGGL((attn_span_kernel<G, FP8, F16>), dim3((unsigned)grid), dim3(kAttnThreads),
-                     lds, st, a);
+  if (a.shared_below > 0)
+    hipLaunchKernelGGL((attn_span_kernel<G, FP8, F16, true>), dim3((unsigned)grid),
+                       dim3(kAttnThreads), lds, st, a);
+  else
+    hipLaunchKernelGGL((attn_span_kernel<G, FP8, F16, false>), dim3((unsigned)grid),
+                       dim3(kAttnThreads), lds, st, a);
   hipLaunchKernelGGL((attn_merge_kernel<G, F16>), dim3((unsigned)(a.pairs * G)),
                      dim3(kAttnThreads), 0, st, a);
   return MKV_OK;
@@ -911,14 +941,15 @@ int launch_kind(AttnKind kind, const AttnArgs& a, int grid, hipStream_t st) {
 // caches [batch, seq_rows, num_kv_heads, 256] (no page table).
 int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k_cache,
                      const void* v_cache, const float* k_scales, const float* v_scales,
-                     int64_t num_pages, int32_t num_kv_heads, int32_t num_q_heads,
+                     int64_t num_pages, int64_t shared_pages, int32_t num_kv_heads, int32_t num_q_heads,
                      int32_t head_dim, const int32_t* page_table, int64_t table_stride,
                      int32_t table_width, int64_t seq_rows, const int32_t* seq_lens,
                      int32_t batch, int32_t max_seq_len, float softmax_scale, void* out,
                      void* workspace, int64_t workspace_bytes, int32_t* err, void* stream) {
   clear_error();
   MKV_REQUIRE(batch >= 0 && num_pages > 0 && num_kv_heads > 0 && num_q_heads > 0 &&
-                  table_width >= 0 && table_stride >= table_width && max_seq_len >= 0,
+                  table_width >= 0 && table_stride >= table_width && max_seq_len >= 0 &&
+                  shared_pages >= 0,
               MKV_E_INVALID, "%s: bad sizes", fn);
   MKV_REQUIRE(head_dim == kHeadDim, MKV_E_UNSUPPORTED, "%s: head_dim %d unsupported (256)", fn,
               head_dim);
@@ -961,6 +992,7 @@ int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k
   a.ml = reinterpret_cast<float*>(ws + L.ml);
   a.part = reinterpret_cast<float*>(ws + L.part);
   a.num_pages = num_pages;
+  a.shared_below = shared_pages;
   a.tstride = table_stride;
   a.seq_rows = seq_rows;
   a.twidth = table_width;
@@ -984,45 +1016,48 @@ int decode_attention(const char* fn, AttnKind kind, const void* q, const void* k
 }  // namespace
 
 extern "C" int mkv_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
-                                         int64_t num_pages, int32_t num_kv_heads,
-                                         int32_t num_q_heads, int32_t head_dim,
-                                         const int32_t* page_table, int64_t table_stride,
-                                         int32_t table_width, const int32_t* seq_lens,
-                                         int32_t batch, int32_t max_seq_len, float softmax_scale,
-                                         void* out, void* workspace, int64_t workspace_bytes,
-                                         int32_t* err, void* stream) {
+                                         int64_t num_pages, int64_t shared_pages,
+                                         int32_t num_kv_heads, int32_t num_q_heads,
+                                         int32_t head_dim, const int32_t* page_table,
+                                         int64_t table_stride, int32_t table_width,
+                                         const int32_t* seq_lens, int32_t batch,
+                                         int32_t max_seq_len, float softmax_scale, void* out,
+                                         void* workspace, int64_t workspace_bytes, int32_t* err,
+                                         void* stream) {
   return decode_attention("mkv_decode_attention_bf16", kAttnBf16, q, k_cache, v_cache, nullptr,
-                          nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          nullptr, num_pages, shared_pages, num_kv_heads, num_q_heads, head_dim,
+                          page_table, table_stride, table_width, 0, seq_lens, batch, max_seq_len,
                           softmax_scale, out, workspace, workspace_bytes, err, stream);
 }
 
 extern "C" int mkv_decode_attention_fp8(const void* q, const void* k_codes, const void* v_codes,
                                         const float* k_scales, const float* v_scales,
-                                        int64_t num_pages, int32_t num_kv_heads,
-                                        int32_t num_q_heads, int32_t head_dim,
-                                        const int32_t* page_table, int64_t table_stride,
-                                        int32_t table_width, const int32_t* seq_lens,
-                                        int32_t batch, int32_t max_seq_len, float softmax_scale,
-                                        void* out, void* workspace, int64_t workspace_bytes,
-                                        int32_t* err, void* stream) {
+                                        int64_t num_pages, int64_t shared_pages,
+                                        int32_t num_kv_heads, int32_t num_q_heads,
+                                        int32_t head_dim, const int32_t* page_table,
+                                        int64_t table_stride, int32_t table_width,
+                                        const int32_t* seq_lens, int32_t batch,
+                                        int32_t max_seq_len, float softmax_scale, void* out,
+                                        void* workspace, int64_t workspace_bytes, int32_t* err,
+                                        void* stream) {
   return decode_attention("mkv_decode_attention_fp8", kAttnFp8, q, k_codes, v_codes, k_scales,
-                          v_scales, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          v_scales, num_pages, shared_pages, num_kv_heads, num_q_heads, head_dim,
+                          page_table, table_stride, table_width, 0, seq_lens, batch, max_seq_len,
                           softmax_scale, out, workspace, workspace_bytes, err, stream);
 }
 
 extern "C" int mkv_decode_attention_f16(const void* q, const void* k_cache, const void* v_cache,
-                                        int64_t num_pages, int32_t num_kv_heads,
-                                        int32_t num_q_heads, int32_t head_dim,
-                                        const int32_t* page_table, int64_t table_stride,
-                                        int32_t table_width, const int32_t* seq_lens,
-                                        int32_t batch, int32_t max_seq_len, float softmax_scale,
-                                        void* out, void* workspace, int64_t workspace_bytes,
-                                        int32_t* err, void* stream) {
+                                        int64_t num_pages, int64_t shared_pages,
+                                        int32_t num_kv_heads, int32_t num_q_heads,
+                                        int32_t head_dim, const int32_t* page_table,
+                                        int64_t table_stride, int32_t table_width,
+                                        const int32_t* seq_lens, int32_t batch,
+                                        int32_t max_seq_len, float softmax_scale, void* out,
+                                        void* workspace, int64_t workspace_bytes, int32_t* err,
+                                        void* stream) {
   return decode_attention("mkv_decode_attention_f16", kAttnF16, q, k_cache, v_cache, nullptr,
-                          nullptr, num_pages, num_kv_heads, num_q_heads, head_dim, page_table,
-                          table_stride, table_width, 0, seq_lens, batch, max_seq_len,
+                          nullptr, num_pages, shared_pages, num_kv_heads, num_q_heads, head_dim,
+                          page_table, table_stride, table_width, 0, seq_lens, batch, max_seq_len,
                           softmax_scale, out, workspace, workspace_bytes, err, stream);
 }
 
@@ -1043,7 +1078,7 @@ extern "C" int mkv_decode_attention_contig(const void* q, const void* k_cache,
   MKV_REQUIRE(pages <= INT32_MAX, MKV_E_UNSUPPORTED, "%s: seq_rows too large", fn);
   const int32_t cap = max_seq_len < seq_rows ? max_seq_len : (int32_t)seq_rows;
   return decode_attention(fn, fp16 ? kAttnF16 : kAttnBf16, q, k_cache, v_cache, nullptr, nullptr,
-                          (int64_t)batch * pages, num_kv_heads, num_q_heads, head_dim, nullptr,
+                          (int64_t)batch * pages, 0, num_kv_heads, num_q_heads, head_dim, nullptr,
                           pages, (int32_t)pages, seq_rows, seq_lens, batch, cap, softmax_scale,
                           out, workspace, workspace_bytes, err, stream);
 }
@@ -1111,14 +1146,14 @@ extern "C" int mkv_decode_attention_bf16_noalloc(const void* q, const void* k_ca
               "holds %lld", fn, batch, num_q_heads, (long long)need,
               (long long)kNoAllocScratchBytes);
   if (batch == 0) return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr,
-                                          num_pages, num_kv_heads, num_q_heads, head_dim,
+                                          num_pages, 0, num_kv_heads, num_q_heads, head_dim,
                                           page_table, table_stride, table_width, 0, seq_lens,
                                           batch, max_seq_len, softmax_scale, out, nullptr, 0,
                                           err, stream);
   void* ws = nullptr;
   const int rc = scratch_of_current_device(fn, &ws);
   if (rc != MKV_OK) return rc;
-  return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr, num_pages,
+  return decode_attention(fn, kAttnBf16, q, k_cache, v_cache, nullptr, nullptr, num_pages, 0,
                           num_kv_heads, num_q_heads, head_dim, page_table, table_stride,
                           table_width, 0, seq_lens, batch, max_seq_len, softmax_scale, out, ws,
                           kNoAllocScratchBytes, err, stream);

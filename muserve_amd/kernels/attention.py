@@ -175,11 +175,19 @@ def attn_decode(
     *,
     max_seqlen: int | None = None,
     out: torch.Tensor | None = None,
+    shared_pages: int = 0,
 ) -> torch.Tensor:                      # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16 / fp16
     """bf16 or fp16 caches (fp16 is the reference's default pool dtype,
     muserve/config.py:37), with q and the output in the caches' dtype.
     ``max_seqlen`` bounds ``cache_seqlens`` (default: what the page table
     holds). ``out`` may be given to write in place.
+
+    ``shared_pages``: page ids below it may be read by several sequences of
+    the batch (prompt pages shared through prefix reuse, e.g. a
+    ``BlockManager``'s page range): they are loaded through the GPU caches so
+    that their readers share them. Every other page streams past the caches,
+    which is faster for pages one sequence reads (the default: 0, no page
+    shared).
 
     With ``page_table=None`` the caches are contiguous per sequence,
     ``[B, S, NUM_KV_HEADS, HEAD_DIM]``, sequence b's first
@@ -192,7 +200,7 @@ def attn_decode(
     if q.dtype != k_cache.dtype:
         raise TypeError(f"q is {q.dtype}, the caches {k_cache.dtype}: they must match")
     return _decode(fns[k_cache.dtype], q, k_cache, v_cache, None, None, cache_seqlens,
-                   page_table, softmax_scale, max_seqlen, out)
+                   page_table, softmax_scale, max_seqlen, out, shared_pages)
 
 
 def attn_decode_fp8(
@@ -207,6 +215,7 @@ def attn_decode_fp8(
     *,
     max_seqlen: int | None = None,
     out: torch.Tensor | None = None,
+    shared_pages: int = 0,
 ) -> torch.Tensor:                      # [B, 1, NUM_Q_HEADS, HEAD_DIM] bf16
     """``attn_decode`` over an fp8 pool (codes plus one fp32 scale per token and
     KV head, as ``PagedKVCache`` appends them), with the dequantisation fused:
@@ -218,7 +227,7 @@ def attn_decode_fp8(
         if s.dtype != torch.float32 or s.shape != k_cache.shape[:3] or not s.is_contiguous():
             raise ValueError(f"{name} must be contiguous fp32 {tuple(k_cache.shape[:3])}")
     return _decode("mkv_decode_attention_fp8", q, k_cache, v_cache, k_scales, v_scales,
-                   cache_seqlens, page_table, softmax_scale, max_seqlen, out)
+                   cache_seqlens, page_table, softmax_scale, max_seqlen, out, shared_pages)
 
 
 def _workspace_for(dev, need):
@@ -258,7 +267,7 @@ def _decode_contig(q, k_cache, v_cache, cache_seqlens, softmax_scale, max_seqlen
 
 
 def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_table,
-            softmax_scale, max_seqlen, out):
+            softmax_scale, max_seqlen, out, shared_pages=0):
     if page_table is None:
         if k_scales is not None:
             raise ValueError("attn_decode_fp8 reads the paged pool: page_table is required")
@@ -288,8 +297,10 @@ def _decode(fn, q, k_cache, v_cache, k_scales, v_scales, cache_seqlens, page_tab
     # the workspace is reused by later calls on the stream: calls on one
     # device must be issued on one stream (or be ordered by the caller)
     scales = () if k_scales is None else (k_scales.data_ptr(), v_scales.data_ptr())
+    if shared_pages < 0:
+        raise ValueError("shared_pages must be >= 0")
     _lib.call(fn, q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *scales,
-              P, Hkv, Hq, D, page_table.data_ptr(), page_table.stride(0), width,
+              P, int(shared_pages), Hkv, Hq, D, page_table.data_ptr(), page_table.stride(0), width,
               cache_seqlens.data_ptr(), B, max_seqlen, scale, out.data_ptr(),
               ws.data_ptr(), ws.numel(), _errword(dev).ptr(), _lib.stream_of(dev))
     return out

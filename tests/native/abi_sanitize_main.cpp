@@ -60,11 +60,14 @@ int main() {
                                          E, N));
   expect_rejected("hash_probe", mkv_hash_probe(N, 16, nullptr, nullptr, 1, nullptr, nullptr, E, N));
   expect_rejected("attention_bf16",
-                  mkv_decode_attention_bf16(N, N, N, 4, 1, 4, 256, nullptr, 4, 4, nullptr, 1, 64,
-                                            0.0625f, N, N, 0, E, N));
+                  mkv_decode_attention_bf16(N, N, N, 4, 0, 1, 4, 256, nullptr, 4, 4, nullptr, 1,
+                                            64, 0.0625f, N, N, 0, E, N));
   expect_rejected("attention_fp8",
-                  mkv_decode_attention_fp8(N, N, N, nullptr, nullptr, 4, 1, 4, 256, nullptr, 4, 4,
-                                           nullptr, 1, 64, 0.0625f, N, N, 0, E, N));
+                  mkv_decode_attention_fp8(N, N, N, nullptr, nullptr, 4, 0, 1, 4, 256, nullptr, 4,
+                                           4, nullptr, 1, 64, 0.0625f, N, N, 0, E, N));
+  expect_rejected("attention_contig", mkv_decode_attention_contig(N, N, N, 0, 1, 4, 256, 0,
+                                                                  nullptr, 1, 64, 0.0625f, N, N,
+                                                                  0, E, N));
   expect_rejected("prefill_attention", mkv_prefill_attention_bf16(N, N, N, 4, 1, 4, 256, nullptr, 0, 0, nullptr, nullptr, nullptr, 1, 16, 16, 0.0625f, 1, 1, 0, N, N, 0, E, N));
   expect_rejected("prefill_attention split", mkv_prefill_attention_bf16(N, N, N, 4, 1, 4, 256, nullptr, 0, 0, nullptr, nullptr, nullptr, 1, 16, 16, 0.0625f, 1, 4, 33, N, N, 0, E, N));
   if (mkv_prefill_attention_workspace_bytes(100, 4, 1) != 0 || mkv_prefill_attention_workspace_bytes(100, 4, 3) <= 0) ++failures;

@@ -392,3 +392,33 @@ def test_contiguous_length_past_the_rows_is_flagged():
     A.attn_decode(q, kc, kc, torch.tensor([40, 41], dtype=torch.int32, device=DEV), None)
     with pytest.raises(_lib.MkvDeviceError, match="longer than its block table"):
         A.check_errors(DEV)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_shared_pages_bound_changes_only_the_load_policy(fp8):
+    """shared_pages (pages below it loaded through the caches, the rest
+    streamed past them) gives the same bits as without it, with sequences
+    sharing a common prefix of pages as prefix reuse makes them."""
+    rng = np.random.default_rng(91)
+    lens = rng.integers(300, 2500, 48)
+    case(f"decode attention, shared prefix pages, shared_pages bound, fp8={fp8}")
+    q, k, v, lens, table = build(91, lens, 4, 1, spare=40)
+    table = table.copy()
+    table[::3, :16] = np.arange(16, dtype=np.int32)  # a third share the pool's first 16 pages
+    lt = torch.from_numpy(lens.astype(np.int32)).to(DEV)
+    tt = torch.from_numpy(table).to(DEV)
+    P = k.shape[0]
+    if fp8:
+        kc, ks, vc, vs = quantize(k, v)
+        f8 = torch.float8_e4m3fn
+        args = (q.to(DEV), kc.view(f8).to(DEV), vc.view(f8).to(DEV), ks.to(DEV), vs.to(DEV), lt, tt)
+        fn = A.attn_decode_fp8
+    else:
+        args = (q.to(DEV), k.to(DEV), v.to(DEV), lt, tt)
+        fn = A.attn_decode
+    base = fn(*args)
+    for bound in (16, P // 2, P):
+        got = fn(*args, shared_pages=bound)
+        torch.cuda.synchronize()
+        A.check_errors(DEV)
+        assert torch.equal(got.view(torch.int16), base.view(torch.int16)), bound

@@ -35,7 +35,9 @@ def _inputs(seed, lens, Hq=4, Hkv=1):
 
 
 def _call(fn, q, k, v, lens, table, max_len, out, ws=None):
-    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), k.shape[0], k.shape[2], q.shape[2], 256,
+    shared = [] if ws is None else [0]  # the workspace entry point's shared_pages bound
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), k.shape[0], *shared, k.shape[2],
+            q.shape[2], 256,
             table.data_ptr(), table.stride(0), table.shape[1], lens.data_ptr(), q.shape[0],
             max_len, 256 ** -0.5, out.data_ptr()]
     if ws is not None:
