@@ -934,6 +934,25 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
     page_bytes = 16 * HEAD_DIM * 2
     cow_bytes = cow * 2 * LAYERS * 2 * page_bytes  # read + write, 15 layers x K,V
     us_req = elapsed / n_req * 1e6
+    # What a plain contiguous device copy of one batch's copy-on-write bytes
+    # takes on this GPU (torch's copy_, same stream and events): the ceiling
+    # for a copy of this size, launch and drain included. Each copy takes the
+    # next of 16 slices of 2 x ~1 GB buffers, so that (like the pool pages)
+    # its source is not in the 256 MB last-level cache from the copy before.
+    half = max(1, cow_bytes // len(ops_dev) // 2)
+    slices = 16
+    src_buf = torch.zeros(slices * half, dtype=torch.uint8, device=dev)
+    dst_buf = torch.zeros_like(src_buf)
+    spans = []
+    for i in range(2 * slices):
+        o = (i % slices) * half
+        sp = stamps.span(stream)
+        dst_buf[o:o + half].copy_(src_buf[o:o + half])
+        spans.append(sp.end(stream))
+    torch.cuda.synchronize()
+    plain_ms = float(np.median([sp.ms() for sp in spans[slices:]]))
+    del src_buf, dst_buf
+    cow_ratio = counter_ratios("copy_on_write_hbm_counters.md").get("cow")
     res = {
         "metric": "prefix-cache admission: us per request (page hashing + lookup/refcount/"
                   "eviction + copy-on-write)",
@@ -967,8 +986,14 @@ def run_prefix(steps: int, warmup: int, with_cpu: bool) -> dict:
             {"kernel": "mkv_bm_step (release run, speculation, group and step kernels)",
              "bound": "latency (a chain of small launches per batch)",
              "us_per_request": round(step_ms * 1e3 / n_req, 3)},
-            _kernel_roofline("copy_pages_kernel (mkv_copy_blocks)", cow_bytes / len(ops_dev),
-                             cow_ms / len(ops_dev))]},
+            dict(_kernel_roofline("copy_pages_kernel (mkv_copy_blocks)", cow_bytes / len(ops_dev),
+                                  cow_ms / len(ops_dev), cow_ratio),
+                 plain_copy_same_bytes={
+                     "note": "torch copy_ of one batch's bytes between contiguous slices of 2 x 16 "
+                             "batches, each slice cold in cache; median of 16, same events",
+                     "us": round(plain_ms * 1e3, 2),
+                     "achieved": round(2 * half / (plain_ms / 1e3) / 1e9, 2),
+                     "frac": round(2 * half / (plain_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4)})]},
     }
     if with_cpu:
         from oracle.blocks import BlockManagerModel

@@ -407,7 +407,7 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * the counters (16 int64: free-stack top, ring head, ring tail, next stamp,
  * evictable pages, tombstones, eviction-log length, then the running totals
  * of admits the many-workgroup passes committed and of admits they covered
- * but left to the one-workgroup kernels), the table (C entries of
+ * but left to the one-workgroup tail kernel), the table (C entries of
  * {u64 key, i32 page, i32 copy of the page's refcount}), the page records (P x 32 bytes: i32 refcount, i32
  * flags with bit 0 = cached, u32 LRU stamp, i32 table slot, u64 hash), the
  * free stack (P int32), the LRU ring (Q x u64: page | stamp << 32), the
@@ -472,7 +472,7 @@ int mkv_bm_step(void* state, int32_t num_pages, const int32_t* ops, int32_t num_
  * (no counterpart in the reference). Called with the same arguments, in this
  * order, on one stream, they are mkv_bm_step. _begin launches the release run
  * and the many-workgroup resolution (nothing for a step of at most 8 ops);
- * _end the one-workgroup kernels, which run every op left (none when the
+ * _end the one-workgroup tail kernel, which runs every op left (none when the
  * counter of committed admits grew by the number of admits in ops). Between the two, the committed admits' tables,
  * hits, status and copy-on-write pairs are final, so a caller may copy them
  * out before _end, whose workgroup needs 96 KiB of LDS and can wait for

@@ -117,8 +117,8 @@ class BlockManager:
         self._pending = (args, keep)
 
     def step_end(self) -> None:
-        """The second half of ``step``: the one-workgroup kernels over the ops
-        the resolution left."""
+        """The second half of ``step``: the one-workgroup tail kernel over the
+        ops the resolution left."""
         if self._pending is None:
             raise RuntimeError("step_end without step_begin")
         (args, keep), self._pending = self._pending, None

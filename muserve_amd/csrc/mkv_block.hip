@@ -7,9 +7,13 @@
 // a request: every page hash of a request is probed at once, pins and
 // refcount updates are one lane per page, and allocation / release positions
 // come from wavefront ballots + popcount prefix ranks. A leading run of
-// releases is retired on many CUs; the admits after it go eight at a time
-// through the group kernel (one round of loads for the eight, then a
-// sequential resolution in LDS); the step kernel runs whatever is left.
+// releases is retired on many CUs, and the admits after it are resolved
+// speculatively on many CUs up to the first one the speculation cannot
+// vouch for. The tail kernel takes the rest: admits eight at a time in its
+// group pass (one round of loads for the eight, then a sequential resolution
+// in LDS), then whatever is left one op at a time in its step pass. A step is
+// ten launches: setup (one workgroup), drop, mark, push + probe, hits,
+// window, victims, commit, finish, tail (one workgroup).
 //
 // A request costs a few dependent memory round trips, so the layout keeps
 // that chain short:
@@ -72,20 +76,28 @@ constexpr int32_t kEmpty = -1, kTomb = -2, kBusy = -3;
 constexpr int64_t kEntBytes = 16, kRecBytes = 32;
 
 // A leading run of release ops is retired by multi-workgroup kernels before
-// the one-workgroup step runs the rest (see the run kernels below); its
+// the one-workgroup tail kernel runs the rest (see the run kernels below); its
 // scratch lives in the state buffer.
 constexpr int kRunMaxOps = 1024;               // releases retired in bulk per step
 constexpr int64_t kRunMaxElems = 1 << 20;      // their page references
 // The run takes a single leading release too: the speculation starts after
-// the run, so a release left to the step kernel would leave every admit
-// after it to the one-workgroup kernels.
+// the run, so a release left to the tail kernel would leave every admit
+// after it to the one-workgroup kernel.
 constexpr int kRunMinOps = 1;
-// A step of at most this many ops runs on the one-workgroup step kernel alone:
-// one launch, against fifteen dependent launches of a few microseconds each,
+// A step of at most this many ops runs on the one-workgroup tail kernel alone:
+// one launch, against ten dependent launches of a few microseconds each,
 // which a concurrent kernel that fills the GPU stretches to tens each.
 constexpr int kShortStepOps = 8;
 constexpr int64_t kRunMaxWords = kRunMaxElems / 32;
-enum RunCtr { kRunOps, kRunTotal, kRunTail, kRunStamp, kRunFree, kRunCompact, kRunSpan,
+// The run's elements (and the ring entries a compaction copies) are counted in
+// chunks of kRunChunk: a workgroup of the mark pass writes each chunk's set
+// bits per array and each bit word's count before it within the chunk, and a
+// workgroup of the push pass adds up the chunks before its own.
+constexpr int kRunChunk = 256;
+constexpr int64_t kRunMaxChunks = kRunMaxElems / kRunChunk;
+enum RunCtr { kRunOps, kRunTotal,
+              kRunTail0, kRunStamp0, kRunFree0, kRunEvict0,  // counters before the run
+              kRunCompact, kRunSpan,
               kRunNext,  // the first op left to the next stage (speculation, groups, step)
               kRunNumCtr = 16 };
 
@@ -114,12 +126,12 @@ struct BmLayout {
   int64_t C, Q;  // table and ring capacities (powers of two)
   int64_t off_ctr, off_ent, off_rec, off_free, off_ring, off_last, off_run, bytes;
   // inside the run scratch at off_run
-  int64_t run_ctr, run_off, run_child, run_page, run_bits, run_wpre;
-  // ring compaction scratch: a copy of the ring span, live bits, their prefix counts
-  int64_t cmp_ring, cmp_bits, cmp_pre;
+  int64_t run_ctr, run_off, run_child, run_page, run_bits, run_wpre, run_ccnt;
+  // ring compaction scratch: a copy of the ring span, live bits, their counts
+  int64_t cmp_ring, cmp_bits, cmp_pre, cmp_ccnt;
   // speculation scratch
   int64_t sp_ctr, sp_req, sp_ntok, sp_m, sp_h0, sp_k, sp_take, sp_pinned, sp_T, sp_p0, sp_fo,
-      sp_first, sp_evt, sp_late, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt, sp_wpre;
+      sp_first, sp_evt, sp_late, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -155,9 +167,11 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.run_page = take(kRunMaxElems * 4);
   l.run_bits = take(3 * kRunMaxWords * 4);
   l.run_wpre = take(2 * kRunMaxWords * 4);
+  l.run_ccnt = take(2 * kRunMaxChunks * 4);
   l.cmp_ring = take(l.Q * 8);
   l.cmp_bits = take(l.Q / 32 * 4);
   l.cmp_pre = take(l.Q / 32 * 4);
+  l.cmp_ccnt = take(l.Q / kRunChunk * 4);
   l.sp_ctr = take(kSpNumCtr * 8);
   l.sp_req = take(kSpecOps * 4);
   l.sp_ntok = take(kSpecOps * 4);
@@ -178,7 +192,6 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.sp_victim = take(kSpecWin * 4);
   l.sp_vpos = take(kSpecWin * 4);
   l.sp_wcnt = take(kWinChunks * 4);
-  l.sp_wpre = take(kWinChunks * 8);
   l.bytes = o;
   return l;
 }
@@ -195,10 +208,13 @@ struct BmState {
   int32_t* run_child;  // run: the op's child copy page, -1 none, -2 releases nothing
   int32_t* run_page;   // run: page id of each element
   uint32_t* run_bits;  // run: [3][kRunMaxWords] to the ring / free stack / last occurrence
-  uint32_t* run_wpre;  // run: [2][kRunMaxWords] exclusive prefix counts of the first two
+  uint32_t* run_wpre;  // run: [2][kRunMaxWords] the first two's counts before each word,
+                       //  within its chunk
+  uint32_t* run_ccnt;  // run: [2][kRunMaxChunks] their set bits per chunk
   uint64_t* cmp_ring;  // compaction: the ring span [head, tail) copied out
   uint32_t* cmp_bits;  // compaction: live bit per copied entry
-  uint32_t* cmp_pre;   // compaction: live entries before each bit word
+  uint32_t* cmp_pre;   // compaction: live entries before each bit word, within its chunk
+  uint32_t* cmp_ccnt;  // compaction: live entries per chunk
   // speculation (per admit j < kSpecOps, position i < kSpecPos)
   int64_t* sp_ctr;     // SpecCtr values
   int32_t* sp_req;     // request id
@@ -222,7 +238,6 @@ struct BmState {
   int32_t* sp_victim;  // [v] the v-th eviction's page
   int32_t* sp_vpos;    //     its window position
   int32_t* sp_wcnt;    // [c] victim candidates in window chunk c (kWinChunk entries)
-  int64_t* sp_wpre;    //     candidates before chunk c
   int64_t C, Q;
   int32_t P;
 };
@@ -243,9 +258,11 @@ inline BmState bm_state(void* base, int32_t P) {
   s.run_page = reinterpret_cast<int32_t*>(b + l.run_page);
   s.run_bits = reinterpret_cast<uint32_t*>(b + l.run_bits);
   s.run_wpre = reinterpret_cast<uint32_t*>(b + l.run_wpre);
+  s.run_ccnt = reinterpret_cast<uint32_t*>(b + l.run_ccnt);
   s.cmp_ring = reinterpret_cast<uint64_t*>(b + l.cmp_ring);
   s.cmp_bits = reinterpret_cast<uint32_t*>(b + l.cmp_bits);
   s.cmp_pre = reinterpret_cast<uint32_t*>(b + l.cmp_pre);
+  s.cmp_ccnt = reinterpret_cast<uint32_t*>(b + l.cmp_ccnt);
   s.sp_ctr = reinterpret_cast<int64_t*>(b + l.sp_ctr);
   s.sp_req = reinterpret_cast<int32_t*>(b + l.sp_req);
   s.sp_ntok = reinterpret_cast<int32_t*>(b + l.sp_ntok);
@@ -266,7 +283,6 @@ inline BmState bm_state(void* base, int32_t P) {
   s.sp_victim = reinterpret_cast<int32_t*>(b + l.sp_victim);
   s.sp_vpos = reinterpret_cast<int32_t*>(b + l.sp_vpos);
   s.sp_wcnt = reinterpret_cast<int32_t*>(b + l.sp_wcnt);
-  s.sp_wpre = reinterpret_cast<int64_t*>(b + l.sp_wpre);
   s.C = l.C;
   s.Q = l.Q;
   s.P = P;
@@ -332,7 +348,7 @@ struct BmArgs {
   int32_t* evict_log;
   int64_t evict_cap;
   int32_t* err;
-  int32_t from_start;  // the step kernel runs every op (a short step: no run, no speculation)
+  int32_t from_start;  // the tail kernel runs every op (a short step: no run, no speculation)
 };
 
 // Request metadata of a chunk of ops, staged in LDS.
@@ -343,7 +359,7 @@ struct OpMeta {
   int64_t h0[kOpChunk];     // admits: index of the first page hash
 };
 
-// LDS of the step kernel's admits: the pages taken for table positions below
+// LDS of the step pass's admits: the pages taken for table positions below
 // kBmThreads, and the table slots claimed by the current admit's inserts (a
 // set, open addressing, -1 empty; cleared when each op ends).
 struct AdmitLds {
@@ -367,7 +383,7 @@ struct Shared {
 __device__ __forceinline__ uint32_t slot_of(uint64_t h) { return (uint32_t)(h ^ (h >> 29)); }
 
 // Values every lane holds alike but that come from LDS or a reduction: kept
-// in scalar registers (VGPRs are the step kernel's scarce resource).
+// in scalar registers (VGPRs are the tail kernel's scarce resource).
 __device__ __forceinline__ int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int64_t uni64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -988,7 +1004,7 @@ __device__ __forceinline__ uint32_t class_of(uint64_t cls, int u) {
   return (uint32_t)(cls >> (8 * u)) & 0xffu;
 }
 
-// The next kGroup ops' request metadata, staged in LDS by the group kernel;
+// The next kGroup ops' request metadata, staged in LDS by the group pass;
 // a member is a valid admit of at most kBmThreads pages that fits its table.
 struct GroupMeta {
   int32_t op[kGroup], ntok[kGroup], nhash[kGroup], ok[kGroup];
@@ -1345,59 +1361,81 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
 // only fall, so a page reaches zero exactly at its last occurrence in L, and
 // only if the run drops all of its references. One workgroup walking L is
 // bound by how many scattered cache lines one CU can touch, so the run is
-// retired by five launches before the step kernel runs the remaining ops:
-//   setup (1 workgroup): the run (leading valid releases, at most kRunMaxOps
-//     ops and kRunMaxElems references), each op's status, child copy and
-//     reference count, their prefix sums, room on the ring;
+// retired by four passes before the speculation and the tail kernel run the
+// remaining ops:
+//   setup (the step's one-workgroup setup kernel): the run (leading valid
+//     releases, at most kRunMaxOps ops and kRunMaxElems references), each
+//     op's status, child copy and reference count, their prefix sums, room on
+//     the ring, the counters the run starts from;
 //   drop (many): every element subtracts its references from its page's
 //     refcount and records its position as the page's last occurrence;
 //   mark (many): an element is a zero-crossing iff it is its page's last
 //     occurrence and the refcount is now 0 (bit arrays: to the ring / to the
 //     free stack); a cached page's final refcount is mirrored into its entry;
-//   scan (1 workgroup): prefix counts of the bit words, the counters, the
-//     requests' statuses;
-//   push (many): every crossing written at its place in L order; the
-//     last-occurrence slots reset to -1.
+//     each chunk's counts (per array, and before each bit word);
+//   push (many, sharing its launch with the speculation's probe): every
+//     crossing written at its place in L order (its chunk's offset is the sum
+//     of the counts of the chunks before it, which each workgroup adds up
+//     itself); the last-occurrence slots reset to -1; the counters and the
+//     requests' statuses.
 // No kernel waits for another workgroup; the launches order the passes.
 // ---------------------------------------------------------------------------
 constexpr int kRunThreads = 256;
-constexpr int kRunGrid = 256;                  // workgroups of the many-CU passes
-constexpr int kRunUnroll = 4;
-constexpr int kRunChunk = kRunUnroll * kRunThreads;  // elements a workgroup takes at a time
+constexpr int kRunWaves = kRunThreads / 64;
+constexpr int kDropGrid = 256;   // drop: a workgroup takes kDropUnroll x kRunThreads elements at a time
+constexpr int kDropUnroll = 4;
+constexpr int kDropChunk = kDropUnroll * kRunThreads;
+constexpr int kPassGrid = 1024;  // mark and push: a workgroup takes a chunk at a time
+constexpr int kChunkWords = kRunChunk / 32;
+static_assert(kRunChunk == kRunThreads, "a chunk is one element per thread");
+static_assert(2 * kChunkWords <= kRunThreads, "a thread per bit word of a chunk");
 
 // The LRU ring is compacted (on many CUs, inside the run kernels) when more
 // than an eighth of its span is dead entries, and when a run's pushes might
 // not fit. Dead entries accumulate as admits pin cached pages, and a dense
 // ring lets an admit find its victims in one window. Live entries are
 // exactly the evictable pages, and a run leaves them live. One thread of the
-// setup kernel decides, on every path.
+// setup kernel decides, on every path, and keeps the counters the push pass
+// starts from (its workgroup 0 rewrites them while the others read).
 constexpr int64_t kCompactMinDead = 1024;
-__device__ void decide_compaction(const BmState& s, int64_t run_refs) {
+__device__ void run_counters(const BmState& s, int64_t run_refs) {
   const int64_t span = s.ctr[kTail] - s.ctr[kHead], dead = span - s.ctr[kEvictable];
   const int64_t pushes = run_refs < s.P ? run_refs : s.P;  // at most one per page
   const bool pays = dead > kCompactMinDead && dead * 8 > span;
   s.run_ctr[kRunCompact] = pays || span + pushes > s.Q;
   s.run_ctr[kRunSpan] = span;
+  s.run_ctr[kRunTail0] = s.ctr[kTail];
+  s.run_ctr[kRunStamp0] = s.ctr[kNextStamp];
+  s.run_ctr[kRunFree0] = s.ctr[kFreeTop];
+  s.run_ctr[kRunEvict0] = s.ctr[kEvictable];
 }
 
 __device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
   return op < 0 && -(op + 1) < a.num_requests;
 }
 
-__global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
+// LDS of the step's setup: a set of request ids (open addressing) with each
+// id's first op, for the run's releases and then for the admits; the run's
+// element offsets.
+struct SetupLds {
+  uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
+  int64_t off[kRunMaxOps + 1];
+  int64_t wave_tot[kBmWaves];
+  int32_t cut;
+};
+
+// The run's part of the setup. Returns its op count (0: no run), alike in
+// every thread.
+__device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
   constexpr int kOpt = kRunMaxOps / kBmThreads;  // consecutive ops per thread
   static_assert(kOpt * kBmThreads == kRunMaxOps, "ops split evenly over the threads");
-  __shared__ int32_t first_non;
-  __shared__ uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
-  __shared__ int64_t off[kRunMaxOps + 1];
-  __shared__ int64_t wave_tot[kBmWaves];
   const BmState& s = a.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int limit = a.num_ops < kRunMaxOps ? a.num_ops : kRunMaxOps;
-  if (tid == 0) first_non = limit;
+  if (tid == 0) sl.cut = limit;
   for (int i = tid; i < 2 * kRunMaxOps; i += kBmThreads) {
-    key[i] = 0xffffffffu;
-    firsti[i] = 0xffffffffu;
+    sl.key[i] = 0xffffffffu;
+    sl.firsti[i] = 0xffffffffu;
   }
   __syncthreads();
   int32_t r[kOpt], st[kOpt], nt[kOpt];
@@ -1410,24 +1448,24 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     nt[u] = 0;
     if (j < limit) {
       // the run also ends at an admitted request whose token count no longer
-      // fits its table (a caller error the step kernel handles as before)
+      // fits its table (a caller error the tail kernel handles as before)
       bool ok = valid_release(a, op);
       if (ok) {
         st[u] = a.status[r[u]];
         nt[u] = a.ntok[r[u]];
         ok = st[u] != kStOk || (nt[u] >= 0 && (nt[u] + 15) / 16 <= a.twidth);
       }
-      if (!ok) atomicMin(&first_non, j);
+      if (!ok) atomicMin(&sl.cut, j);
     }
   }
   __syncthreads();
-  int n = first_non;
+  int n = sl.cut;
   if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
-      decide_compaction(s, 0);
+      run_counters(s, 0);
     }
-    return;
+    return 0;
   }
   // a request released twice: the earliest op releases; sequentially a later
   // one finds it released (a caller error) unless it got OOM (silent)
@@ -1439,11 +1477,11 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     if (j < n) {
       uint32_t q = ((uint32_t)r[u] * 2654435761u) & (2 * kRunMaxOps - 1);
       for (;;) {  // at most n of 2 kRunMaxOps slots are taken
-        const uint32_t prev = atomicCAS(&key[q], 0xffffffffu, (uint32_t)r[u]);
+        const uint32_t prev = atomicCAS(&sl.key[q], 0xffffffffu, (uint32_t)r[u]);
         if (prev == 0xffffffffu || prev == (uint32_t)r[u]) break;
         q = (q + 1) & (2 * kRunMaxOps - 1);
       }
-      atomicMin(&firsti[q], (uint32_t)j);
+      atomicMin(&sl.firsti[q], (uint32_t)j);
       slot[u] = q;
     }
   }
@@ -1456,7 +1494,7 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     cnt[u] = 0;
     child[u] = -2;
     if (j < n) {
-      if (firsti[slot[u]] == (uint32_t)j && st[u] == kStOk) {
+      if (sl.firsti[slot[u]] == (uint32_t)j && st[u] == kStOk) {
         const bool cow = (nt[u] & 15) != 0;
         child[u] = cow ? a.child_last[r[u]] : -1;
         cnt[u] = (nt[u] + 15) / 16 + (cow ? 1 : 0);
@@ -1473,39 +1511,39 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
     const int64_t o = __shfl_up(incl, d);
     if (lane >= d) incl += o;
   }
-  if (lane == 63) wave_tot[wave] = incl;
+  if (lane == 63) sl.wave_tot[wave] = incl;
   __syncthreads();
   int64_t before = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kBmWaves; ++w) {
-    before += w < wave ? wave_tot[w] : 0;
-    total += wave_tot[w];
+    before += w < wave ? sl.wave_tot[w] : 0;
+    total += sl.wave_tot[w];
   }
   int64_t at = before + incl - mine;
 #pragma unroll
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
-    if (j < n) off[j] = at;
+    if (j < n) sl.off[j] = at;
     at += cnt[u];
   }
-  if (tid == 0) off[n] = total;
+  if (tid == 0) sl.off[n] = total;
   __syncthreads();
   if (total > kRunMaxElems) {  // the longest prefix of ops that fits
     int lo = 0, hi = n;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (off[mid] <= kRunMaxElems) lo = mid; else hi = mid - 1;
+      if (sl.off[mid] <= kRunMaxElems) lo = mid; else hi = mid - 1;
     }
-    n = lo;  // ops after it are the step kernel's (it repeats any error bit)
+    n = lo;  // ops after it are the tail kernel's (it repeats any error bit)
   }
   if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
-      decide_compaction(s, 0);
+      run_counters(s, 0);
     }
-    return;
+    return 0;
   }
-  for (int j = tid; j <= n; j += kBmThreads) s.run_off[j] = off[j];
+  for (int j = tid; j <= n; j += kBmThreads) s.run_off[j] = sl.off[j];
 #pragma unroll
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
@@ -1513,9 +1551,10 @@ __global__ __launch_bounds__(kBmThreads) void run_setup_kernel(BmArgs a) {
   }
   if (tid == 0) {
     s.run_ctr[kRunOps] = n;
-    s.run_ctr[kRunTotal] = off[n];
-    decide_compaction(s, off[n]);
+    s.run_ctr[kRunTotal] = sl.off[n];
+    run_counters(s, sl.off[n]);
   }
+  return n;
 }
 
 // The run's per-op tables, staged in a pass workgroup's LDS.
@@ -1561,18 +1600,18 @@ __global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
   const int64_t total = s.run_ctr[kRunTotal];
-  if (n < kRunMinOps || (int64_t)blockIdx.x * kRunChunk >= total) return;
+  if (n < kRunMinOps || (int64_t)blockIdx.x * kDropChunk >= total) return;
   run_stage(a, n, ro);
-  for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
-       c0 += (int64_t)gridDim.x * kRunChunk) {
-    int32_t pg[kRunUnroll], dr[kRunUnroll];
+  for (int64_t c0 = (int64_t)blockIdx.x * kDropChunk; c0 < total;
+       c0 += (int64_t)gridDim.x * kDropChunk) {
+    int32_t pg[kDropUnroll], dr[kDropUnroll];
 #pragma unroll
-    for (int u = 0; u < kRunUnroll; ++u) {
+    for (int u = 0; u < kDropUnroll; ++u) {
       const int64_t e = c0 + u * kRunThreads + threadIdx.x;
       run_elem(a, ro, n, e < total ? e : total - 1, pg[u], dr[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kRunUnroll; ++u) {
+    for (int u = 0; u < kDropUnroll; ++u) {
       const int64_t e = c0 + u * kRunThreads + threadIdx.x;
       if (e < total) {
         s.run_page[e] = pg[u];
@@ -1585,50 +1624,76 @@ __global__ __launch_bounds__(kRunThreads) void run_drop_kernel(BmArgs a) {
   }
 }
 
+// A chunk's per-word set bits (wc[k][w], filled by the waves' lane 0) become
+// each word's count before it within the chunk (pre[k]) and the chunk's
+// total (ccnt[k]), for NB arrays; barriers before and after.
+template <int NB>
+__device__ __forceinline__ void chunk_counts(uint32_t (&wc)[2][kChunkWords], int64_t c,
+                                             uint32_t* const (&pre)[NB],
+                                             uint32_t* const (&ccnt)[NB]) {
+  __syncthreads();
+  if (threadIdx.x < NB * kChunkWords) {
+    const int k = threadIdx.x / kChunkWords, w = threadIdx.x % kChunkWords;
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int v = 0; v < kChunkWords; ++v) {
+      const uint32_t x = wc[k][v];
+      before += v < w ? x : 0;
+      all += x;
+    }
+    pre[k][c * kChunkWords + w] = before;
+    if (w == 0) ccnt[k][c] = all;
+  }
+  __syncthreads();  // wc is rewritten by the next chunk
+}
+
 __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
+  __shared__ uint32_t wc[2][kChunkWords];
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
   const int64_t total = n < kRunMinOps ? 0 : s.run_ctr[kRunTotal];
-  const int lane = threadIdx.x & 63;
-  for (int64_t c0 = (int64_t)blockIdx.x * kRunChunk; c0 < total;
-       c0 += (int64_t)gridDim.x * kRunChunk) {
-    RecHead h[kRunUnroll];
-    int32_t lst[kRunUnroll];
-#pragma unroll
-    for (int u = 0; u < kRunUnroll; ++u) {
-      const int64_t e = c0 + u * kRunThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  {
+    uint32_t* const pre[2] = {s.run_wpre, s.run_wpre + kRunMaxWords};
+    uint32_t* const ccnt[2] = {s.run_ccnt, s.run_ccnt + kRunMaxChunks};
+    for (int64_t c = blockIdx.x; c * kRunChunk < total; c += gridDim.x) {
+      const int64_t e = c * kRunChunk + threadIdx.x;  // a wave: 64 aligned elements
       const int32_t pg = s.run_page[e < total ? e : total - 1];
-      h[u] = rec_head(s, pg);
-      lst[u] = s.last[pg];
-    }
-#pragma unroll
-    for (int u = 0; u < kRunUnroll; ++u) {
-      const int64_t e = c0 + u * kRunThreads + threadIdx.x;  // a wave: 64 aligned elements
-      const bool is_last = e < total && lst[u] == (int32_t)e;
-      const bool zero = is_last && h[u].ref == 0;
-      const bool cached = (h[u].flag & 1) != 0;
-      if (is_last && cached) *ent_ref(s, h[u].slot) = h[u].ref;
+      const RecHead h = rec_head(s, pg);
+      const bool is_last = e < total && s.last[pg] == (int32_t)e;
+      const bool zero = is_last && h.ref == 0;
+      const bool cached = (h.flag & 1) != 0;
+      if (is_last && cached) *ent_ref(s, h.slot) = h.ref;
       const uint64_t ml = __ballot(is_last), mr = __ballot(zero && cached),
                      mf = __ballot(zero && !cached);
-      if (lane == 0 && e < total) {
-        const int64_t w = e >> 5;
-        uint32_t* b = s.run_bits;
-        b[w] = (uint32_t)mr;
-        b[w + 1] = (uint32_t)(mr >> 32);
-        b[kRunMaxWords + w] = (uint32_t)mf;
-        b[kRunMaxWords + w + 1] = (uint32_t)(mf >> 32);
-        b[2 * kRunMaxWords + w] = (uint32_t)ml;
-        b[2 * kRunMaxWords + w + 1] = (uint32_t)(ml >> 32);
+      if (lane == 0) {
+        const int wi = wave * 2;  // the wave's first word in the chunk
+        wc[0][wi] = __popc((uint32_t)mr);
+        wc[0][wi + 1] = __popc((uint32_t)(mr >> 32));
+        wc[1][wi] = __popc((uint32_t)mf);
+        wc[1][wi + 1] = __popc((uint32_t)(mf >> 32));
+        if (e < total) {
+          const int64_t w = e >> 5;
+          uint32_t* b = s.run_bits;
+          b[w] = (uint32_t)mr;
+          b[w + 1] = (uint32_t)(mr >> 32);
+          b[kRunMaxWords + w] = (uint32_t)mf;
+          b[kRunMaxWords + w + 1] = (uint32_t)(mf >> 32);
+          b[2 * kRunMaxWords + w] = (uint32_t)ml;
+          b[2 * kRunMaxWords + w + 1] = (uint32_t)(ml >> 32);
+        }
       }
+      chunk_counts<2>(wc, c, pre, ccnt);
     }
   }
   // Compaction: the ring span [head, tail) is copied out, with a bit per entry
   // that stays live (an entry of a page this run pushes again does not).
   if (s.run_ctr[kRunCompact] == 0) return;
   const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
-  for (int64_t b0 = (int64_t)blockIdx.x * kRunThreads; b0 < span;
-       b0 += (int64_t)gridDim.x * kRunThreads) {
-    const int64_t i = b0 + threadIdx.x;  // a wave: 64 aligned entries
+  uint32_t* const pre[1] = {s.cmp_pre};
+  uint32_t* const ccnt[1] = {s.cmp_ccnt};
+  for (int64_t c = blockIdx.x; c * kRunChunk < span; c += gridDim.x) {
+    const int64_t i = c * kRunChunk + threadIdx.x;  // a wave: 64 aligned entries
     bool keep = false;
     if (i < span) {
       const uint64_t e = s.ring[(head + i) & qm];
@@ -1637,132 +1702,136 @@ __global__ __launch_bounds__(kRunThreads) void run_mark_kernel(BmArgs a) {
       keep = live(rec_head(s, pg), (uint32_t)(e >> 32)) && (n < kRunMinOps || s.last[pg] < 0);
     }
     const uint64_t m = __ballot(keep);
-    if (lane == 0 && i < span) {
-      s.cmp_bits[i >> 5] = (uint32_t)m;
-      s.cmp_bits[(i >> 5) + 1] = (uint32_t)(m >> 32);
+    if (lane == 0) {
+      const int wi = wave * 2;
+      wc[0][wi] = __popc((uint32_t)m);
+      wc[0][wi + 1] = __popc((uint32_t)(m >> 32));
+      if (i < span) {
+        s.cmp_bits[i >> 5] = (uint32_t)m;
+        s.cmp_bits[(i >> 5) + 1] = (uint32_t)(m >> 32);
+      }
     }
+    chunk_counts<1>(wc, c, pre, ccnt);
   }
 }
 
-// Exclusive prefix counts of up to three bit arrays of nw words (per thread a
-// contiguous slice of words, then a wavefront scan and the waves' totals);
-// every thread gets the totals. NB bit arrays; pre[k][w] receives the count
-// of set bits before word w of array k.
-template <int NB>
-__device__ void scan_bits(const uint32_t* const (&bits)[NB], uint32_t* const (&pre)[NB], int64_t nw,
-                          int64_t (&tot)[NB], int64_t (&wave_tot)[NB][kBmWaves]) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t per = (nw + kBmThreads - 1) / kBmThreads;  // words per thread
-  const int64_t w0 = tid * per, w1 = w0 + per < nw ? w0 + per : nw;
-  int64_t cnt[NB], incl[NB];
-#pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    cnt[k] = 0;
-    for (int64_t w = w0; w < w1; ++w) cnt[k] += __popc(bits[k][w]);
-    incl[k] = cnt[k];
+// The sum of cnt[lo, hi) over the workgroup (every thread gets it), two
+// arrays at once; red is LDS for the waves' partial sums.
+__device__ __forceinline__ void range_sum2(const uint32_t* c0, const uint32_t* c1, int64_t lo,
+                                           int64_t hi, int64_t (&red)[2][kRunWaves],
+                                           int64_t& t0, int64_t& t1) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t v0 = 0, v1 = 0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kRunThreads) {
+    v0 += c0[i];
+    v1 += c1 ? c1[i] : 0;
   }
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      const int64_t o = __shfl_up(incl[k], d);
-      if (lane >= d) incl[k] += o;
-    }
+  for (int off = 32; off >= 1; off >>= 1) {
+    v0 += __shfl_xor(v0, off);
+    v1 += __shfl_xor(v1, off);
   }
-  if (lane == 63) {
-#pragma unroll
-    for (int k = 0; k < NB; ++k) wave_tot[k][wave] = incl[k];
+  if (lane == 0) {
+    red[0][wave] = v0;
+    red[1][wave] = v1;
   }
   __syncthreads();
+  t0 = t1 = 0;
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    int64_t before = incl[k] - cnt[k];
-    tot[k] = 0;
-#pragma unroll
-    for (int w = 0; w < kBmWaves; ++w) {
-      before += w < wave ? wave_tot[k][w] : 0;
-      tot[k] += wave_tot[k][w];
-    }
-    for (int64_t w = w0; w < w1; ++w) {
-      pre[k][w] = (uint32_t)before;
-      before += __popc(bits[k][w]);
-    }
+  for (int w = 0; w < kRunWaves; ++w) {
+    t0 += red[0][w];
+    t1 += red[1][w];
   }
+  __syncthreads();  // red is rewritten by the next sum
 }
 
-__global__ __launch_bounds__(kBmThreads) void run_scan_kernel(BmArgs a) {
-  __shared__ int64_t wave_tot[2][kBmWaves];
-  const BmState& s = a.s;
-  const int n = (int)s.run_ctr[kRunOps];
-  const bool cmp = s.run_ctr[kRunCompact] != 0;
-  if (n < kRunMinOps && !cmp) return;
-  const int tid = threadIdx.x;
-  int64_t n_lru = 0, n_free = 0, n_kept = 0;
-  if (n >= kRunMinOps) {
-    const uint32_t* const bits[2] = {s.run_bits, s.run_bits + kRunMaxWords};
-    uint32_t* const pre[2] = {s.run_wpre, s.run_wpre + kRunMaxWords};
-    int64_t tot[2];
-    scan_bits<2>(bits, pre, (s.run_ctr[kRunTotal] + 31) >> 5, tot, wave_tot);
-    n_lru = tot[0];
-    n_free = tot[1];
-  }
-  if (cmp) {
-    if (n >= kRunMinOps) __syncthreads();  // wave_tot is reused
-    const uint32_t* const bits[1] = {s.cmp_bits};
-    uint32_t* const pre[1] = {s.cmp_pre};
-    int64_t tot[1];
-    int64_t(&wt)[1][kBmWaves] = reinterpret_cast<int64_t(&)[1][kBmWaves]>(wave_tot);
-    scan_bits<1>(bits, pre, (s.run_ctr[kRunSpan] + 31) >> 5, tot, wt);
-    n_kept = tot[0];
-  }
-  if (tid == 0) {
-    // pushes go after the kept entries (compacted from the head) or the tail
-    const int64_t base = cmp ? s.ctr[kHead] + n_kept : s.ctr[kTail];
-    s.run_ctr[kRunTail] = base;
-    s.run_ctr[kRunStamp] = s.ctr[kNextStamp];
-    s.run_ctr[kRunFree] = s.ctr[kFreeTop];
-    s.ctr[kTail] = base + n_lru;
-    s.ctr[kNextStamp] += n_lru;
-    s.ctr[kEvictable] += n_lru;
-    s.ctr[kFreeTop] += n_free;
-  }
-  for (int j = tid; j < (n >= kRunMinOps ? n : 0); j += kBmThreads)
-    if (s.run_child[j] != -2) a.status[-(a.ops[j] + 1)] = kStReleased;
-}
+__device__ void spec_probe(const BmArgs& a, int32_t wg, int32_t nwg);
 
+// Workgroups [0, kPassGrid) push the run; the rest run the speculation's probe
+// (it reads only the table, which the push does not touch, and the setup's
+// admit list).
 __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
+  __shared__ int64_t red[2][kRunWaves];
+  if (blockIdx.x >= kPassGrid) {
+    spec_probe(a, blockIdx.x - kPassGrid, gridDim.x - kPassGrid);
+    return;
+  }
   const BmState& s = a.s;
   const int n = (int)s.run_ctr[kRunOps];
   const int64_t total = n < kRunMinOps ? 0 : s.run_ctr[kRunTotal];
-  if (s.run_ctr[kRunCompact] != 0) {  // the kept entries, from the head in order
-    const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
-    for (int64_t i = (int64_t)blockIdx.x * kRunThreads + threadIdx.x; i < span;
-         i += (int64_t)gridDim.x * kRunThreads) {
-      const uint32_t bits = s.cmp_bits[i >> 5], bit = 1u << (i & 31);
-      if (bits & bit)
-        s.ring[(head + s.cmp_pre[i >> 5] + __popc(bits & (bit - 1u))) & qm] = s.cmp_ring[i];
+  const bool cmp = s.run_ctr[kRunCompact] != 0;
+  const int64_t head = s.ctr[kHead], span = s.run_ctr[kRunSpan], qm = s.Q - 1;
+  const int64_t nch = (total + kRunChunk - 1) / kRunChunk;
+  const int64_t ncc = cmp ? (span + kRunChunk - 1) / kRunChunk : 0;
+  const int64_t b = blockIdx.x;
+  if (b != 0 && b >= nch && b >= ncc && b * kRunThreads >= n) return;
+  for (int64_t j = b * kRunThreads + threadIdx.x; j < (n >= kRunMinOps ? n : 0);
+       j += (int64_t)kPassGrid * kRunThreads)
+    if (s.run_child[j] != -2) a.status[-(a.ops[j] + 1)] = kStReleased;
+  int64_t t0, t1;
+  // the kept entries, from the head in order
+  int64_t n_kept = 0;
+  if (cmp) {
+    range_sum2(s.cmp_ccnt, nullptr, 0, ncc, red, n_kept, t1);
+    int64_t before;
+    range_sum2(s.cmp_ccnt, nullptr, 0, b < ncc ? b : ncc, red, before, t1);
+    for (int64_t c = b; c < ncc; c += kPassGrid) {
+      const int64_t i = c * kRunChunk + threadIdx.x;
+      if (i < span) {
+        const uint32_t bits = s.cmp_bits[i >> 5], bit = 1u << (i & 31);
+        if (bits & bit)
+          s.ring[(head + before + s.cmp_pre[i >> 5] + __popc(bits & (bit - 1u))) & qm] =
+              s.cmp_ring[i];
+      }
+      const int64_t next = c + kPassGrid < ncc ? c + kPassGrid : ncc;
+      range_sum2(s.cmp_ccnt, nullptr, c, next, red, t0, t1);
+      before += t0;
     }
   }
-  const int64_t tail0 = s.run_ctr[kRunTail], stamp0 = s.run_ctr[kRunStamp];
-  const int64_t free0 = s.run_ctr[kRunFree], qm = s.Q - 1;
-  const uint32_t* b = s.run_bits;
-  for (int64_t e = (int64_t)blockIdx.x * kRunThreads + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * kRunThreads) {
+  // pushes go after the kept entries (compacted from the head) or the tail
+  const int64_t tail0 = cmp ? head + n_kept : s.run_ctr[kRunTail0];
+  const int64_t stamp0 = s.run_ctr[kRunStamp0], free0 = s.run_ctr[kRunFree0];
+  const uint32_t* bw = s.run_bits;
+  const uint32_t *cl = s.run_ccnt, *cf = s.run_ccnt + kRunMaxChunks;
+  int64_t bl, bf;
+  range_sum2(cl, cf, 0, b < nch ? b : nch, red, bl, bf);
+  for (int64_t c = b; c < nch; c += kPassGrid) {
+    const int64_t e = c * kRunChunk + threadIdx.x;
     const int64_t w = e >> 5;
     const uint32_t bit = 1u << (e & 31), below = bit - 1u;
-    const uint32_t br = b[w], bf = b[kRunMaxWords + w], bl = b[2 * kRunMaxWords + w];
-    if (!((br | bf | bl) & bit)) continue;
-    const int32_t pg = s.run_page[e];
-    if (bl & bit) s.last[pg] = -1;
-    if (br & bit) {
-      const int64_t rank = s.run_wpre[w] + __popc(br & below);
-      const uint32_t stamp = (uint32_t)(stamp0 + rank);
-      s.ring[(tail0 + rank) & qm] = (uint32_t)pg | (uint64_t)stamp << 32;
-      *rec_stamp(s, pg) = stamp;
+    const uint32_t br = e < total ? bw[w] : 0u, bfw = e < total ? bw[kRunMaxWords + w] : 0u,
+                   bl_w = e < total ? bw[2 * kRunMaxWords + w] : 0u;
+    if ((br | bfw | bl_w) & bit) {
+      const int32_t pg = s.run_page[e];
+      if (bl_w & bit) s.last[pg] = -1;
+      if (br & bit) {
+        const int64_t rank = bl + s.run_wpre[w] + __popc(br & below);
+        const uint32_t stamp = (uint32_t)(stamp0 + rank);
+        s.ring[(tail0 + rank) & qm] = (uint32_t)pg | (uint64_t)stamp << 32;
+        *rec_stamp(s, pg) = stamp;
+      }
+      if (bfw & bit) {
+        const int64_t rank = bf + s.run_wpre[kRunMaxWords + w] + __popc(bfw & below);
+        s.free_list[free0 + rank] = pg;
+      }
     }
-    if (bf & bit) {
-      const int64_t rank = s.run_wpre[kRunMaxWords + w] + __popc(bf & below);
-      s.free_list[free0 + rank] = pg;
+    const int64_t next = c + kPassGrid < nch ? c + kPassGrid : nch;
+    range_sum2(cl, cf, c, next, red, t0, t1);
+    bl += t0;
+    bf += t1;
+  }
+  if (b == 0) {  // the counters after the run, and the speculation's starting point
+    int64_t n_lru, n_free;
+    range_sum2(cl, cf, 0, nch, red, n_lru, n_free);
+    if (threadIdx.x == 0) {
+      const int64_t ev = s.run_ctr[kRunEvict0] + n_lru, fr = free0 + n_free;
+      s.ctr[kTail] = tail0 + n_lru;
+      s.ctr[kNextStamp] = stamp0 + n_lru;
+      s.ctr[kEvictable] = ev;
+      s.ctr[kFreeTop] = fr;
+      s.sp_ctr[kSpF] = fr;
+      s.sp_ctr[kSpLive] = ev;
+      s.sp_ctr[kSpHead] = head;
     }
   }
 }
@@ -1787,7 +1856,7 @@ __global__ __launch_bounds__(kRunThreads) void run_push_kernel(BmArgs a) {
 //     (sequentially it would be that admit's victim);
 //   - a window or first-occurrence table too small.
 // The admits before the first violation are exactly what the sequential order
-// gives, and are committed on many CUs; the group kernel takes the rest.
+// gives, and are committed on many CUs; the tail kernel takes the rest.
 //
 // Refcounts: a hit adds 2 (parent and child), a taken page its base (2, 1
 // for a partial last page the child copies, 1 for a copy-on-write page), by
@@ -1892,26 +1961,21 @@ __device__ __forceinline__ void spec_clear_scratch(const BmState& s, int64_t g, 
 
 // 1. The admits to speculate: the leading valid admits after the release run
 //    (at most kSpecOps, of at most kSpecPos pages), cut before a request that
-//    repeats; their metadata and the step's starting counters.
-__global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
+//    repeats; their metadata. The counters they start from come from the
+//    push pass, after the run.
+__device__ void spec_setup(const BmArgs& a, int32_t start, SetupLds& sl) {
   constexpr int kOpt = kSpecOps / kSpecThreads;
   static_assert(kOpt * kSpecThreads == kSpecOps, "ops split evenly over the threads");
-  __shared__ int32_t cut;
-  __shared__ uint32_t key[2 * kSpecOps], firsti[2 * kSpecOps];
+  static_assert(kSpecOps == kRunMaxOps && kSpecThreads == kBmThreads, "the run's set and threads");
   const BmState& s = a.s;
   const int tid = threadIdx.x;
-  if (s.ctr[kTombs] > s.C / 4) {  // tombstones past a quarter of the table: rebuild it
-    Ctrs c;
-    tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
-    if (tid == 0) s.ctr[kTombs] = 0;
-  }
-  const int32_t start = (int32_t)s.run_ctr[kRunOps];
   const int32_t left = a.num_ops - start;
   const int limit = left < kSpecOps ? left : kSpecOps;
-  if (tid == 0) cut = limit;
+  __syncthreads();  // the run's reads of the set are done
+  if (tid == 0) sl.cut = limit;
   for (int i = tid; i < 2 * kSpecOps; i += kSpecThreads) {
-    key[i] = 0xffffffffu;
-    firsti[i] = 0xffffffffu;
+    sl.key[i] = 0xffffffffu;
+    sl.firsti[i] = 0xffffffffu;
   }
   __syncthreads();
   int32_t r[kOpt], n[kOpt], m[kOpt];
@@ -1933,10 +1997,10 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
       ok = n[u] >= 0 && mm == n[u] / 16 && np <= a.twidth && np <= kSpecPos;
       m[u] = (int32_t)mm;
     }
-    if (!ok) atomicMin(&cut, j);
+    if (!ok) atomicMin(&sl.cut, j);
   }
   __syncthreads();
-  const int lim2 = cut;
+  const int lim2 = sl.cut;
   // a request admitted twice: the speculation stops before the second
   uint32_t slot[kOpt];
 #pragma unroll
@@ -1946,21 +2010,21 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
     if (j >= lim2) continue;
     uint32_t q = ((uint32_t)r[u] * 2654435761u) & (2 * kSpecOps - 1);
     for (;;) {  // at most kSpecOps of 2 kSpecOps slots are taken
-      const uint32_t prev = atomicCAS(&key[q], 0xffffffffu, (uint32_t)r[u]);
+      const uint32_t prev = atomicCAS(&sl.key[q], 0xffffffffu, (uint32_t)r[u]);
       if (prev == 0xffffffffu || prev == (uint32_t)r[u]) break;
       q = (q + 1) & (2 * kSpecOps - 1);
     }
-    atomicMin(&firsti[q], (uint32_t)j);
+    atomicMin(&sl.firsti[q], (uint32_t)j);
     slot[u] = q;
   }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
-    if (j < lim2 && firsti[slot[u]] != (uint32_t)j) atomicMin(&cut, j);
+    if (j < lim2 && sl.firsti[slot[u]] != (uint32_t)j) atomicMin(&sl.cut, j);
   }
   __syncthreads();
-  const int nspec = cut;
+  const int nspec = sl.cut;
 #pragma unroll
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
@@ -1973,21 +2037,34 @@ __global__ __launch_bounds__(kSpecThreads) void spec_setup_kernel(BmArgs a) {
   if (tid == 0) {
     s.sp_ctr[kSpN] = nspec;
     s.sp_ctr[kSpBad] = nspec;
-    s.sp_ctr[kSpF] = s.ctr[kFreeTop];
-    s.sp_ctr[kSpLive] = s.ctr[kEvictable];
-    s.sp_ctr[kSpHead] = s.ctr[kHead];
     s.sp_ctr[kSpWin] = 0;
     s.sp_ctr[kSpReused] = 0;
     s.run_ctr[kRunNext] = start;
   }
 }
 
+// The step's setup, one workgroup: the table rebuilt when tombstones pass a
+// quarter of it (no pass of the step holds a slot across this launch), the
+// release run's setup, then the admits after the run.
+__global__ __launch_bounds__(kBmThreads) void step_setup_kernel(BmArgs a) {
+  __shared__ SetupLds sl;
+  const BmState& s = a.s;
+  if (s.ctr[kTombs] > s.C / 4) {
+    Ctrs c;
+    tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
+    if (threadIdx.x == 0) s.ctr[kTombs] = 0;
+  }
+  const int32_t start = run_setup(a, sl);
+  spec_setup(a, start, sl);
+}
+
 // 2. Every speculated admit's page hashes looked up at S (a workgroup per
-//    admit); keys absent at S enter the first-occurrence table.
-__global__ __launch_bounds__(256) void spec_probe_kernel(BmArgs a) {
+//    admit, in the push pass's launch); keys absent at S enter the
+//    first-occurrence table.
+__device__ void spec_probe(const BmArgs& a, int32_t wg, int32_t nwg) {
   const BmState& s = a.s;
   const int32_t n = (int32_t)s.sp_ctr[kSpN];
-  for (int32_t j = blockIdx.x; j < n; j += gridDim.x) {
+  for (int32_t j = wg; j < n; j += nwg) {
     const int32_t m = s.sp_m[j];
     const int64_t h0 = s.sp_h0[j];
     int2* out = s.sp_p0 + (int64_t)j * kSpecPos;
@@ -2154,17 +2231,29 @@ __device__ __forceinline__ int32_t spec_owner(const int64_t* T, int32_t n, int64
   return lo;
 }
 
-// 5. One workgroup: the takes' prefix sums, the OOM checks, and the
-//    candidates before each window chunk (the window too short for the
-//    evictions wanted makes the admit that lacks one a violation).
-__global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
-  constexpr int kOpt = kSpecOps / kSpecThreads;
+// 5. Per window chunk (many CUs), after the takes' prefix sums, which every
+//    workgroup computes for itself (workgroup 0 also keeps them, checks each
+//    admit for OOM, and checks that the window holds the evictions wanted: if
+//    it is too short, the admit that lacks one is a violation). Victim v, the
+//    (v+1)-th candidate in window order, is take F + v, which belongs to the
+//    admit whose prefix range holds it; a live entry pinned in the step is
+//    passed by the admit owning the take index it is passed at, a violation
+//    if that admit comes before its first pinner (sequentially it would have
+//    evicted it). A hit is never a victim (pinned, or not in the LRU at all),
+//    so only pages held past a first miss can be read after their eviction.
+__global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
+  constexpr int kWaves = kWinChunk / 64;
+  constexpr int kOpt = kSpecOps / kWinChunk;  // consecutive admits per thread
+  static_assert(kOpt * kWinChunk == kSpecOps, "admits split evenly over the threads");
   __shared__ int64_t T[kSpecOps + 1];
-  __shared__ int64_t wave_tot[2][kBmWaves];
+  __shared__ int64_t wave_tot[2][kWaves];
+  __shared__ int32_t cnt[kWaves];
   const BmState& s = a.s;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool lead = blockIdx.x == 0;
   const int32_t n = (int32_t)s.sp_ctr[kSpN];
-  if (n == 0) return;
+  const int64_t W = s.sp_ctr[kSpWin];
+  if (n == 0 || (!lead && (int64_t)blockIdx.x * kWinChunk >= W)) return;  // no chunk here
   const int64_t F = s.sp_ctr[kSpF], live0 = s.sp_ctr[kSpLive];
   // exclusive prefix sums of takes and pins, kOpt consecutive admits per thread
   int64_t tk[kOpt], pn[kOpt], st = 0, sp = 0;
@@ -2172,7 +2261,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
     tk[u] = j < n ? s.sp_take[j] : 0;
-    pn[u] = j < n ? s.sp_pinned[j] : 0;
+    pn[u] = lead && j < n ? s.sp_pinned[j] : 0;
     st += tk[u];
     sp += pn[u];
   }
@@ -2192,7 +2281,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
   __syncthreads();
   int64_t bt = it - st, bp = ip - sp;
 #pragma unroll
-  for (int w = 0; w < kBmWaves; ++w) {
+  for (int w = 0; w < kWaves; ++w) {
     bt += w < wave ? wave_tot[0][w] : 0;
     bp += w < wave ? wave_tot[1][w] : 0;
   }
@@ -2201,73 +2290,51 @@ __global__ __launch_bounds__(kSpecThreads) void spec_scan_kernel(BmArgs a) {
     const int j = tid * kOpt + u;
     if (j < n) {
       T[j] = bt;
-      s.sp_T[j] = bt;
-      // OOM: the takes exceed the free stack left plus the evictable pages
-      // left, minus the ones this admit pins
-      const int64_t free_j = F - bt > 0 ? F - bt : 0;
-      const int64_t ev_j = live0 - bp - (bt - F > 0 ? bt - F : 0);
-      if (tk[u] > free_j + ev_j - pn[u]) atomicMin(spec_bad(s), j);
+      if (lead) {
+        s.sp_T[j] = bt;
+        // OOM: the takes exceed the free stack left plus the evictable pages
+        // left, minus the ones this admit pins
+        const int64_t free_j = F - bt > 0 ? F - bt : 0;
+        const int64_t ev_j = live0 - bp - (bt - F > 0 ? bt - F : 0);
+        if (tk[u] > free_j + ev_j - pn[u]) atomicMin(spec_bad(s), j);
+      }
     }
     bt += tk[u];
     bp += pn[u];
   }
-  if (tid == kSpecThreads - 1) {
+  if (tid == kWinChunk - 1) {
     T[n] = bt;  // the last thread's running sum covers every admit
-    s.sp_T[n] = bt;
+    if (lead) s.sp_T[n] = bt;
   }
   __syncthreads();
-  const int64_t total = T[n];
-  const int64_t E = total - F > 0 ? total - F : 0;  // evictions wanted
-  const int64_t W = s.sp_ctr[kSpWin];
-  const int32_t nch = (int32_t)((W + kWinChunk - 1) / kWinChunk);  // <= kWinChunks
-  static_assert(kWinChunks <= kSpecThreads, "a chunk per thread");
-  const int64_t cc = tid < nch ? s.sp_wcnt[tid] : 0;
-  int64_t inc = cc;
+  const int64_t E = T[n] - F > 0 ? T[n] - F : 0;  // evictions wanted
+  const int64_t nch = (W + kWinChunk - 1) / kWinChunk;
+  // the candidates in window chunks [lo, hi), summed over the workgroup
+  auto cand = [&](int64_t lo, int64_t hi) __attribute__((always_inline)) {
+    int64_t v = 0;
+    for (int64_t c = lo + tid; c < hi; c += kWinChunk) v += s.sp_wcnt[c];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int64_t o = __shfl_up(inc, d);
-    if (lane >= d) inc += o;
-  }
-  __syncthreads();  // wave_tot is reused
-  if (lane == 63) wave_tot[0][wave] = inc;
-  __syncthreads();
-  int64_t before = inc - cc, ncand = 0;
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    __syncthreads();  // wave_tot's last readers are done
+    if (lane == 0) wave_tot[0][wave] = v;
+    __syncthreads();
+    int64_t t = 0;
 #pragma unroll
-  for (int w = 0; w < kBmWaves; ++w) {
-    before += w < wave ? wave_tot[0][w] : 0;
-    ncand += wave_tot[0][w];
+    for (int w = 0; w < kWaves; ++w) t += wave_tot[0][w];
+    return t;
+  };
+  if (lead) {
+    const int64_t ncand = cand(0, nch);
+    if (tid == 0 && ncand < E) atomicMin(spec_bad(s), spec_owner(T, n, F + ncand));
   }
-  if (tid < nch) s.sp_wpre[tid] = before;
-  if (tid == 0 && ncand < E) atomicMin(spec_bad(s), spec_owner(T, n, F + ncand));
-}
-
-// 6. Per window chunk (many CUs): victim v, the (v+1)-th candidate in window
-//    order, is take F + v, which belongs to the admit whose prefix range holds
-//    it; a live entry pinned in the step is passed by the admit owning the
-//    take index it is passed at, a violation if that admit comes before its
-//    first pinner (sequentially it would have evicted it). A hit is never a
-//    victim (pinned, or not in the LRU at all), so only pages held past a
-//    first miss can be read after their eviction.
-__global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
-  constexpr int kWaves = kWinChunk / 64;
-  __shared__ int64_t T[kSpecOps + 1];
-  __shared__ int32_t cnt[kWaves];
-  const BmState& s = a.s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int32_t n = (int32_t)s.sp_ctr[kSpN];
-  const int64_t W = s.sp_ctr[kSpWin];
-  if (n == 0 || (int64_t)blockIdx.x * kWinChunk >= W) return;  // no chunk here
-  for (int32_t j = tid; j <= n; j += kWinChunk) T[j] = s.sp_T[j];
-  __syncthreads();
-  const int64_t F = s.sp_ctr[kSpF];
-  const int64_t E = T[n] - F > 0 ? T[n] - F : 0;
-  for (int64_t c = blockIdx.x; c * kWinChunk < W; c += gridDim.x) {
+  int64_t pre = cand(0, (int64_t)blockIdx.x < nch ? blockIdx.x : nch);
+  for (int64_t c = blockIdx.x; c < nch; c += gridDim.x) {
     const int64_t w = c * kWinChunk + tid;
     const uint8_t f = w < W ? s.sp_wflag[w] : 0;
     const uint64_t bal = __ballot(f == 1);
     if (lane == 0) cnt[wave] = __popcll(bal);
     __syncthreads();
-    int64_t before = s.sp_wpre[c] + __popcll(bal & ((1ull << lane) - 1ull));
+    int64_t before = pre + __popcll(bal & ((1ull << lane) - 1ull));
 #pragma unroll
     for (int v = 0; v < kWaves; ++v) before += v < wave ? cnt[v] : 0;
     if (f == 1 && before < E) {
@@ -2284,10 +2351,12 @@ __global__ __launch_bounds__(kWinChunk) void spec_victims_kernel(BmArgs a) {
       if (u < s.sp_first[s.sp_wpg[w]]) atomicMin(spec_bad(s), u);
     }
     __syncthreads();  // cnt is rewritten
+    const int64_t next = c + gridDim.x < nch ? c + gridDim.x : nch;
+    pre += cand(c, next);
   }
 }
 
-// 7. The admits before the first violation, a workgroup per admit: tables,
+// 6. The admits before the first violation, a workgroup per admit: tables,
 //    refcounts, cached flags and hashes, registrations (insertion by
 //    compare-and-swap at the slot found at S), results.
 __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
@@ -2348,7 +2417,7 @@ __global__ __launch_bounds__(kSpecThreads) void spec_commit_kernel(BmArgs a) {
                         (unsigned long long)reused);
 }
 
-// 8. The evictions' tombstones and log, the cached pages' refcounts copied
+// 7. The evictions' tombstones and log, the cached pages' refcounts copied
 //    into their table entries, the counters, and the scratch cleared.
 __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
   const BmState& s = a.s;
@@ -2393,14 +2462,10 @@ __global__ __launch_bounds__(kSpecThreads) void spec_finish_kernel(BmArgs a) {
   }
 }
 
-// The admits after the leading run of releases, in groups, while they are
-// valid and at most kBmThreads pages long; the step kernel takes the ops from
-// the first one that is not (kRunNext). A kernel of its own, so that the
-// single-request path's registers do not crowd the group's.
-__global__ __launch_bounds__(kBmThreads) void bm_group_kernel(BmArgs a) {
-  __shared__ Shared sh;
-  __shared__ GroupLds gl;
-  __shared__ GroupMeta gm;
+// The tail kernel's group pass: the admits after the speculated ones, in
+// groups, while they are valid and at most kBmThreads pages long; the step
+// pass takes the ops from the first one that is not (kRunNext).
+__device__ void group_pass(const BmArgs& a, Shared& sh, GroupLds& gl, GroupMeta& gm) {
   const BmState& s = a.s;
   int32_t t = (int32_t)s.run_ctr[kRunNext];  // after the run and the speculated admits
   if (s.P > kGroupMaxPages) {  // the page bitmaps do not fit in LDS
@@ -2454,10 +2519,7 @@ __global__ __launch_bounds__(kBmThreads) void bm_group_kernel(BmArgs a) {
   }
 }
 
-__global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
-  __shared__ Shared sh;
-  __shared__ OpMeta om;
-  __shared__ AdmitLds al;
+__device__ void step_pass(const BmArgs& a, Shared& sh, OpMeta& om, AdmitLds& al) {
   int buf = 0;
   Ctrs c;
   c.free_top = a.s.ctr[kFreeTop];
@@ -2474,12 +2536,12 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
   }
   for (int i = threadIdx.x; i < kSetSize; i += kBmThreads) al.claims[i] = -1;
   uint64_t cur[kHeld] = {}, nxt[kHeld] = {};
-  if (a.from_start && c.tombs > a.s.C / 4) {  // what the speculation's setup does otherwise
+  if (a.from_start && c.tombs > a.s.C / 4) {  // what the step's setup does otherwise
     tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
     if (threadIdx.x == 0) a.s.ctr[kTombs] = 0;
   }
   // the leading run of releases (if any) was retired by the run kernels, and
-  // the admits after it by the speculation and the group kernel
+  // the admits after it by the speculation and the group pass
   const int32_t start = a.from_start ? 0 : (int32_t)a.s.run_ctr[kRunNext];
   for (int32_t base = start; base < a.num_ops; base += kOpChunk) {
     const int cnt = a.num_ops - base < kOpChunk ? a.num_ops - base : kOpChunk;
@@ -2537,6 +2599,30 @@ __global__ __launch_bounds__(kBmThreads) void bm_step_kernel(BmArgs a) {
     a.s.ctr[kTombs] = c.tombs;
     a.s.ctr[kLogLen] = c.log_len;
   }
+}
+
+// The ops the release run and the speculation left, in order: admits in
+// groups while they qualify, then one op at a time (a short step: every op,
+// one at a time). One kernel, the two passes' LDS overlaid.
+union TailLds {
+  struct {
+    GroupLds gl;
+    GroupMeta gm;
+  } g;
+  struct {
+    OpMeta om;
+    AdmitLds al;
+  } o;
+};
+
+__global__ __launch_bounds__(kBmThreads) void bm_tail_kernel(BmArgs a) {
+  __shared__ Shared sh;
+  __shared__ TailLds tl;
+  if (!a.from_start) {
+    group_pass(a, sh, tl.g.gl, tl.g.gm);
+    __syncthreads();  // its counters and LDS reads are done before the step pass
+  }
+  step_pass(a, sh, tl.o.om, tl.o.al);
 }
 
 // Read-only lookup (mkv_hash_probe): one workgroup per request probes its page
@@ -2667,16 +2753,12 @@ int bm_step_args(BmArgs& a, const char* fn, void* state, int32_t num_pages, cons
 // nothing for a short step.
 void launch_bm_begin(const BmArgs& a, hipStream_t st) {
   if (a.from_start) return;
-  hipLaunchKernelGGL(run_setup_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
-  hipLaunchKernelGGL(run_drop_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
-  hipLaunchKernelGGL(run_mark_kernel, dim3(kRunGrid), dim3(kRunThreads), 0, st, a);
-  hipLaunchKernelGGL(run_scan_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
-  hipLaunchKernelGGL(run_push_kernel, dim3(kRunGrid * kRunUnroll), dim3(kRunThreads), 0, st, a);
-  hipLaunchKernelGGL(spec_setup_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
-  hipLaunchKernelGGL(spec_probe_kernel, dim3(kSpecGrid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(step_setup_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+  hipLaunchKernelGGL(run_drop_kernel, dim3(kDropGrid), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(run_mark_kernel, dim3(kPassGrid), dim3(kRunThreads), 0, st, a);
+  hipLaunchKernelGGL(run_push_kernel, dim3(kPassGrid + kSpecGrid), dim3(kRunThreads), 0, st, a);
   hipLaunchKernelGGL(spec_hits_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_window_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
-  hipLaunchKernelGGL(spec_scan_kernel, dim3(1), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_victims_kernel, dim3(kSpecGrid), dim3(kWinChunk), 0, st, a);
   hipLaunchKernelGGL(spec_commit_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
   hipLaunchKernelGGL(spec_finish_kernel, dim3(kSpecGrid), dim3(kSpecThreads), 0, st, a);
@@ -2685,8 +2767,7 @@ void launch_bm_begin(const BmArgs& a, hipStream_t st) {
 // The ops the speculation left, in order: admits in groups, then one at a time
 // (a short step: every op, one at a time).
 void launch_bm_end(const BmArgs& a, hipStream_t st) {
-  if (!a.from_start) hipLaunchKernelGGL(bm_group_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
-  hipLaunchKernelGGL(bm_step_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
+  hipLaunchKernelGGL(bm_tail_kernel, dim3(1), dim3(kBmThreads), 0, st, a);
 }
 
 }  // namespace
