@@ -414,10 +414,10 @@ int mkv_block_hash_sha256(const void* tokens, const int64_t* tok_offsets,
  * last-occurrence slots (P int32, -1 between steps), the scratch of the
  * many-workgroup passes (4.6 MiB for a release run of up to 2^20 page
  * references: counters, per-op offsets, page ids, bit arrays; plus 8.25 x Q
- * bytes for compacting the ring; plus 26.2 MiB + 12 x P bytes for resolving up
+ * bytes for compacting the ring; plus 26.2 MiB + 8 x P bytes for resolving up
  * to 1024 admits of up to 2048 pages at once: per-admit metadata,
  * per-position probe results, a first-occurrence table of absent hashes,
- * per-page first pinner and eviction, the LRU window and its victims), and
+ * per-page first pinner and late holder, the LRU window and its victims), and
  * the total size.
  *
  * mkv_bm_step runs ops[0..num_ops) with the effect of running them in order

@@ -131,7 +131,7 @@ struct BmLayout {
   int64_t cmp_ring, cmp_bits, cmp_pre, cmp_ccnt;
   // speculation scratch
   int64_t sp_ctr, sp_req, sp_ntok, sp_m, sp_h0, sp_k, sp_take, sp_pinned, sp_T, sp_p0, sp_fo,
-      sp_first, sp_evt, sp_late, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt;
+      sp_first, sp_late, sp_wpg, sp_wslot, sp_wflag, sp_victim, sp_vpos, sp_wcnt;
 };
 
 __host__ __device__ inline int64_t next_pow2(int64_t x) {
@@ -184,7 +184,6 @@ __host__ __device__ inline BmLayout bm_layout(int32_t P) {
   l.sp_p0 = take((int64_t)kSpecOps * kSpecPos * 8);
   l.sp_fo = take(kFoCap * 16);
   l.sp_first = take((int64_t)P * 4);
-  l.sp_evt = take((int64_t)P * 4);
   l.sp_late = take((int64_t)P * 4);
   l.sp_wpg = take(kSpecWin * 4);
   l.sp_wslot = take(kSpecWin * 4);
@@ -230,7 +229,6 @@ struct BmState {
                        //  of an earlier admit; table slot | kTombBit}
   uint8_t* sp_fo;      // first-occurrence table: {u64 key, i32 first occurrence, i32 -}
   int32_t* sp_first;   // [P] first admit pinning the page (INT_MAX none)
-  int32_t* sp_evt;     // [P] admit evicting the page (INT_MAX none)
   int32_t* sp_late;    // [P] first admit holding the page (found at S) past its first miss
   int32_t* sp_wpg;     // [w] LRU window: page
   int32_t* sp_wslot;   //     its key's table slot
@@ -275,7 +273,6 @@ inline BmState bm_state(void* base, int32_t P) {
   s.sp_p0 = reinterpret_cast<int2*>(b + l.sp_p0);
   s.sp_fo = b + l.sp_fo;
   s.sp_first = reinterpret_cast<int32_t*>(b + l.sp_first);
-  s.sp_evt = reinterpret_cast<int32_t*>(b + l.sp_evt);
   s.sp_late = reinterpret_cast<int32_t*>(b + l.sp_late);
   s.sp_wpg = reinterpret_cast<int32_t*>(b + l.sp_wpg);
   s.sp_wslot = reinterpret_cast<int32_t*>(b + l.sp_wslot);
@@ -1382,8 +1379,8 @@ __device__ int group_admit(const BmArgs& a, const GroupMeta& om, int g, Ctrs& c,
 // ---------------------------------------------------------------------------
 constexpr int kRunThreads = 256;
 constexpr int kRunWaves = kRunThreads / 64;
-constexpr int kDropGrid = 256;   // drop: a workgroup takes kDropUnroll x kRunThreads elements at a time
-constexpr int kDropUnroll = 4;
+constexpr int kDropGrid = 512;   // drop: a workgroup takes kDropUnroll x kRunThreads elements at a time
+constexpr int kDropUnroll = 2;
 constexpr int kDropChunk = kDropUnroll * kRunThreads;
 constexpr int kPassGrid = 1024;  // mark and push: a workgroup takes a chunk at a time
 constexpr int kChunkWords = kRunChunk / 32;
@@ -1398,35 +1395,92 @@ static_assert(2 * kChunkWords <= kRunThreads, "a thread per bit word of a chunk"
 // setup kernel decides, on every path, and keeps the counters the push pass
 // starts from (its workgroup 0 rewrites them while the others read).
 constexpr int64_t kCompactMinDead = 1024;
-__device__ void run_counters(const BmState& s, int64_t run_refs) {
-  const int64_t span = s.ctr[kTail] - s.ctr[kHead], dead = span - s.ctr[kEvictable];
+// c: the counters at the step's start (as the setup kernel loaded them)
+__device__ void run_counters(const BmState& s, const Ctrs& c, int64_t run_refs) {
+  const int64_t span = c.tail - c.head, dead = span - c.evictable;
   const int64_t pushes = run_refs < s.P ? run_refs : s.P;  // at most one per page
   const bool pays = dead > kCompactMinDead && dead * 8 > span;
   s.run_ctr[kRunCompact] = pays || span + pushes > s.Q;
   s.run_ctr[kRunSpan] = span;
-  s.run_ctr[kRunTail0] = s.ctr[kTail];
-  s.run_ctr[kRunStamp0] = s.ctr[kNextStamp];
-  s.run_ctr[kRunFree0] = s.ctr[kFreeTop];
-  s.run_ctr[kRunEvict0] = s.ctr[kEvictable];
+  s.run_ctr[kRunTail0] = c.tail;
+  s.run_ctr[kRunStamp0] = c.next_stamp;
+  s.run_ctr[kRunFree0] = c.free_top;
+  s.run_ctr[kRunEvict0] = c.evictable;
 }
 
 __device__ __forceinline__ bool valid_release(const BmArgs& a, int32_t op) {
   return op < 0 && -(op + 1) < a.num_requests;
 }
 
-// LDS of the step's setup: a set of request ids (open addressing) with each
+// LDS of the step's setup: the first kStageOps ops with their requests'
+// metadata (the run's releases and the admits after them both lie there,
+// loaded in one round); a set of request ids (open addressing) with each
 // id's first op, for the run's releases and then for the admits; the run's
 // element offsets.
+constexpr int kStageOps = 2048;
+static_assert(kStageOps >= 2 * kRunMaxOps, "the run and the admits after it");
 struct SetupLds {
+  int32_t op[kStageOps];
+  int32_t ntok[kStageOps];    // the request's tokens (0 if the op names no request)
+  int32_t status[kStageOps];  // releases: the request's status (kStBad if invalid)
+  int32_t child[kStageOps];   // releases: the request's child_last
+  int32_t m[kStageOps];       // admits: its page-hash count
+  int64_t h0[kStageOps];      // admits: its first page hash
   uint32_t key[2 * kRunMaxOps], firsti[2 * kRunMaxOps];
   int64_t off[kRunMaxOps + 1];
   int64_t wave_tot[kBmWaves];
   int32_t cut;
 };
 
+// Stages ops [0, min(num_ops, kStageOps)) and their requests' metadata (every
+// load depends only on its op) and loads the counters, all in one round.
+__device__ void setup_stage(const BmArgs& a, SetupLds& sl, Ctrs& c) {
+  constexpr int kPer = kStageOps / kBmThreads;
+  const int nst = a.num_ops < kStageOps ? a.num_ops : kStageOps;
+  c.free_top = a.s.ctr[kFreeTop];
+  c.head = a.s.ctr[kHead];
+  c.tail = a.s.ctr[kTail];
+  c.next_stamp = a.s.ctr[kNextStamp];
+  c.evictable = a.s.ctr[kEvictable];
+  c.tombs = a.s.ctr[kTombs];
+  c.log_len = 0;  // unused here
+  int32_t op[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = threadIdx.x + u * kBmThreads;
+    op[u] = j < nst ? a.ops[j] : 0;
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = threadIdx.x + u * kBmThreads;
+    if (j >= nst) continue;
+    const int32_t o = op[u], r = o >= 0 ? o : -(o + 1);
+    const bool ok = r < a.num_requests;
+    int32_t nt = 0, st = kStBad, ch = -1, m = 0;
+    int64_t h0 = 0;
+    if (ok) {
+      nt = a.ntok[r];
+      if (o < 0) {
+        st = a.status[r];
+        ch = a.child_last[r];
+      } else {
+        h0 = a.hash_off[r];
+        m = (int32_t)(a.hash_off[r + 1] - h0);
+      }
+    }
+    sl.op[j] = o;
+    sl.ntok[j] = nt;
+    sl.status[j] = st;
+    sl.child[j] = ch;
+    sl.m[j] = m;
+    sl.h0[j] = h0;
+  }
+  __syncthreads();
+}
+
 // The run's part of the setup. Returns its op count (0: no run), alike in
 // every thread.
-__device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
+__device__ int32_t run_setup(const BmArgs& a, const Ctrs& c0, SetupLds& sl) {
   constexpr int kOpt = kRunMaxOps / kBmThreads;  // consecutive ops per thread
   static_assert(kOpt * kBmThreads == kRunMaxOps, "ops split evenly over the threads");
   const BmState& s = a.s;
@@ -1438,21 +1492,23 @@ __device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
     sl.firsti[i] = 0xffffffffu;
   }
   __syncthreads();
-  int32_t r[kOpt], st[kOpt], nt[kOpt];
+  int32_t r[kOpt], st[kOpt], nt[kOpt], ch[kOpt];
 #pragma unroll
   for (int u = 0; u < kOpt; ++u) {
     const int j = tid * kOpt + u;
-    const int32_t op = j < limit ? a.ops[j] : 0;
+    const int32_t op = j < limit ? sl.op[j] : 0;
     r[u] = -(op + 1);
     st[u] = kStBad;
     nt[u] = 0;
+    ch[u] = -1;
     if (j < limit) {
       // the run also ends at an admitted request whose token count no longer
       // fits its table (a caller error the tail kernel handles as before)
       bool ok = valid_release(a, op);
       if (ok) {
-        st[u] = a.status[r[u]];
-        nt[u] = a.ntok[r[u]];
+        st[u] = sl.status[j];
+        nt[u] = sl.ntok[j];
+        ch[u] = sl.child[j];
         ok = st[u] != kStOk || (nt[u] >= 0 && (nt[u] + 15) / 16 <= a.twidth);
       }
       if (!ok) atomicMin(&sl.cut, j);
@@ -1463,7 +1519,7 @@ __device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
   if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
-      run_counters(s, 0);
+      run_counters(s, c0, 0);
     }
     return 0;
   }
@@ -1496,7 +1552,7 @@ __device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
     if (j < n) {
       if (sl.firsti[slot[u]] == (uint32_t)j && st[u] == kStOk) {
         const bool cow = (nt[u] & 15) != 0;
-        child[u] = cow ? a.child_last[r[u]] : -1;
+        child[u] = cow ? ch[u] : -1;
         cnt[u] = (nt[u] + 15) / 16 + (cow ? 1 : 0);
       } else if (st[u] != kStOom) {
         raise_err(a.err, MKV_DEVERR_BM);
@@ -1539,7 +1595,7 @@ __device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
   if (n < kRunMinOps) {
     if (tid == 0) {
       s.run_ctr[kRunOps] = 0;
-      run_counters(s, 0);
+      run_counters(s, c0, 0);
     }
     return 0;
   }
@@ -1552,7 +1608,7 @@ __device__ int32_t run_setup(const BmArgs& a, SetupLds& sl) {
   if (tid == 0) {
     s.run_ctr[kRunOps] = n;
     s.run_ctr[kRunTotal] = sl.off[n];
-    run_counters(s, sl.off[n]);
+    run_counters(s, c0, sl.off[n]);
   }
   return n;
 }
@@ -1954,7 +2010,6 @@ __device__ __forceinline__ void spec_clear_scratch(const BmState& s, int64_t g, 
     *reinterpret_cast<u32x4*>(s.sp_fo + i * 16) = u32x4{0u, 0u, (uint32_t)INT_MAX, 0u};
   for (int64_t p = g; p < s.P; p += stride) {
     s.sp_first[p] = INT_MAX;
-    s.sp_evt[p] = INT_MAX;
     s.sp_late[p] = INT_MAX;
   }
 }
@@ -1987,13 +2042,13 @@ __device__ void spec_setup(const BmArgs& a, int32_t start, SetupLds& sl) {
     n[u] = m[u] = 0;
     h0[u] = 0;
     if (j >= limit) continue;
-    const int32_t op = a.ops[start + j];
+    const int32_t op = sl.op[start + j];  // start + j < kStageOps: start <= kRunMaxOps
     bool ok = op >= 0 && op < a.num_requests;
     if (ok) {
       r[u] = op;
-      n[u] = a.ntok[op];
-      h0[u] = a.hash_off[op];
-      const int64_t mm = a.hash_off[op + 1] - h0[u], np = ((int64_t)n[u] + 15) / 16;
+      n[u] = sl.ntok[start + j];
+      h0[u] = sl.h0[start + j];
+      const int64_t mm = sl.m[start + j], np = ((int64_t)n[u] + 15) / 16;
       ok = n[u] >= 0 && mm == n[u] / 16 && np <= a.twidth && np <= kSpecPos;
       m[u] = (int32_t)mm;
     }
@@ -2048,13 +2103,13 @@ __device__ void spec_setup(const BmArgs& a, int32_t start, SetupLds& sl) {
 // release run's setup, then the admits after the run.
 __global__ __launch_bounds__(kBmThreads) void step_setup_kernel(BmArgs a) {
   __shared__ SetupLds sl;
-  const BmState& s = a.s;
-  if (s.ctr[kTombs] > s.C / 4) {
-    Ctrs c;
-    tab_rebuild(a, c);  // ends with a barrier, after every thread read the count
-    if (threadIdx.x == 0) s.ctr[kTombs] = 0;
+  Ctrs c;
+  setup_stage(a, sl, c);  // ends with a barrier, after every thread read the counters
+  if (c.tombs > a.s.C / 4) {
+    tab_rebuild(a, c);  // ends with a barrier
+    if (threadIdx.x == 0) a.s.ctr[kTombs] = 0;
   }
-  const int32_t start = run_setup(a, sl);
+  const int32_t start = run_setup(a, c, sl);
   spec_setup(a, start, sl);
 }
 
