@@ -394,13 +394,40 @@ def test_contiguous_length_past_the_rows_is_flagged():
         A.check_errors(DEV)
 
 
+@pytest.mark.parametrize("Hq,Hkv,lens", [
+    (4, 1, [1, 2, 15, 16, 17, 31, 33, 200, 511, 512, 513, 1000, 1023, 1024, 1025, 1500, 2049, 3000,
+            4097, 0, 7]),
+    (8, 2, [1, 17, 513, 2049, 0, 3000, 64]),
+    (1, 1, [30000]),                    # one sequence over many waves
+    (4, 1, [16] * 1500 + [300, 0, 5]),  # more sequences than half the waves: unaligned spans
+])
+def test_shared_pages_shapes(Hq, Hkv, lens):
+    """The shared-page variant (every page below the bound through the
+    caches; each sequence's pages start a wave's span while the sequences
+    number at most half the waves) against the oracle."""
+    case(f"decode attention, shared_pages = pool, Hq={Hq} Hkv={Hkv}, {len(lens)} sequences, "
+         f"max {max(lens)}")
+    q, k, v, lens, table = build(95 + Hq + 10 * Hkv, lens, Hq, Hkv)
+    out = A.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV),
+                        torch.from_numpy(lens.astype(np.int32)).to(DEV),
+                        torch.from_numpy(table).to(DEV), shared_pages=k.shape[0])
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    want = att.decode_attention(q[:, 0].float().numpy(), k.float().numpy(), v.float().numpy(),
+                                lens, table, 256 ** -0.5, stats=True)
+    within_one_ulp(out[:, 0], want)
+
+
 @pytest.mark.parametrize("fp8", [False, True])
-def test_shared_pages_bound_changes_only_the_load_policy(fp8):
+def test_shared_pages_bound(fp8):
     """shared_pages (pages below it loaded through the caches, the rest
-    streamed past them) gives the same bits as without it, with sequences
-    sharing a common prefix of pages as prefix reuse makes them."""
+    streamed past them; every sequence's pages start a wave's span) against
+    the oracle, with sequences sharing a common prefix of pages as prefix
+    reuse makes them. Bounds 16, P/2 and P give the same bits: they change
+    only which loads go through the caches."""
     rng = np.random.default_rng(91)
     lens = rng.integers(300, 2500, 48)
+    lens[5] = 0  # an empty sequence among them
     case(f"decode attention, shared prefix pages, shared_pages bound, fp8={fp8}")
     q, k, v, lens, table = build(91, lens, 4, 1, spare=40)
     table = table.copy()
@@ -413,12 +440,19 @@ def test_shared_pages_bound_changes_only_the_load_policy(fp8):
         f8 = torch.float8_e4m3fn
         args = (q.to(DEV), kc.view(f8).to(DEV), vc.view(f8).to(DEV), ks.to(DEV), vs.to(DEV), lt, tt)
         fn = A.attn_decode_fp8
+        want = att.decode_attention(q[:, 0].float().numpy(), kc.numpy(), vc.numpy(), lens, table,
+                                    256 ** -0.5, ks.numpy(), vs.numpy(), stats=True)
     else:
         args = (q.to(DEV), k.to(DEV), v.to(DEV), lt, tt)
         fn = A.attn_decode
-    base = fn(*args)
+        want = att.decode_attention(q[:, 0].float().numpy(), k.float().numpy(),
+                                    v.float().numpy(), lens, table, 256 ** -0.5, stats=True)
+    first = None
     for bound in (16, P // 2, P):
         got = fn(*args, shared_pages=bound)
         torch.cuda.synchronize()
         A.check_errors(DEV)
-        assert torch.equal(got.view(torch.int16), base.view(torch.int16)), bound
+        within_one_ulp(got[:, 0], want)
+        if first is None:
+            first = got
+        assert torch.equal(got.view(torch.int16), first.view(torch.int16)), bound
