@@ -528,8 +528,14 @@ int mkv_hash_probe(const void* state, int32_t num_pages, const uint64_t* page_ha
  *            prefix shared through the block manager, whose page range is
  *            [0, its num_pages)): their K/V are loaded through the caches so
  *            the readers share them; every other page streams past the caches
- *            (non-temporal loads, faster for pages one sequence reads). 0: no
- *            page is shared. Results do not depend on it;
+ *            (non-temporal loads, faster for pages one sequence reads). With
+ *            shared_pages > 0, while the pairs (sequence, KV head) number at
+ *            most half the kernel's waves, each pair's pages also start a
+ *            wave's span, so that the pairs sharing a page read it at the same
+ *            time. 0: no page is shared. Results are within the same bound for
+ *            every value, bit-identical for every value above 0, and can
+ *            differ from those of 0 in the last bits (the pages' split among
+ *            the waves, and so the merge order, changes);
  *   max_seq_len: an upper bound of seq_lens; longer sequences are cut to it;
  *   workspace: mkv_decode_attention_workspace_bytes(...) bytes, 16-byte
  *            aligned, contents irrelevant between calls: it receives the
