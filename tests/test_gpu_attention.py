@@ -400,11 +400,13 @@ def test_contiguous_length_past_the_rows_is_flagged():
     (8, 2, [1, 17, 513, 2049, 0, 3000, 64]),
     (1, 1, [30000]),                    # one sequence over many waves
     (4, 1, [16] * 1500 + [300, 0, 5]),  # more sequences than half the waves: unaligned spans
+    (4, 1, [0] * 1000 + [700] * 90 + [3, 17]),  # aligned spans, too many pairs to sort
 ])
 def test_shared_pages_shapes(Hq, Hkv, lens):
     """The shared-page variant (every page below the bound through the
     caches; each sequence's pages start a wave's span while the sequences
-    number at most half the waves) against the oracle."""
+    number at most half the waves, in the order of their first page id up to
+    1024 pairs) against the oracle."""
     case(f"decode attention, shared_pages = pool, Hq={Hq} Hkv={Hkv}, {len(lens)} sequences, "
          f"max {max(lens)}")
     q, k, v, lens, table = build(95 + Hq + 10 * Hkv, lens, Hq, Hkv)
