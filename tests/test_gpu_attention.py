@@ -458,3 +458,50 @@ def test_shared_pages_bound(fp8):
         if first is None:
             first = got
         assert torch.equal(got.view(torch.int16), first.view(torch.int16)), bound
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_against_oracle(seed):
+    """Seeded sweep: pool kind (bf16 / fp16 / fp8), query heads per KV head,
+    one or two KV heads, batch size, lengths (empty, one token, page
+    boundaries, long), sequences sharing leading pages, and shared_pages off
+    or covering the pool; each case against the float64 oracle."""
+    rng = np.random.default_rng(1000 + seed)
+    kind = ("bf16", "f16", "fp8")[seed % 3]
+    Hkv = 2 if seed % 4 == 3 and kind != "fp8" else 1
+    G = int(rng.choice([1, 2, 4, 8]))
+    B = int(rng.integers(1, 64))
+    lens = rng.integers(0, 3000, B)
+    special = [0, 1, 15, 16, 17, 4096 + 3]
+    for i in range(min(B, 3)):
+        lens[int(rng.integers(0, B))] = special[int(rng.integers(0, len(special)))]
+    q, k, v, lens, table = build(2000 + seed, lens, G * Hkv, Hkv, spare=24)
+    if B > 2 and rng.random() < 0.7:  # some sequences share leading pages
+        table = table.copy()
+        share = int(rng.integers(1, 24))
+        for b in range(B):
+            if rng.random() < 0.5 and lens[b] > 16 * share:
+                table[b, :share] = table[0, :share] if lens[0] > 16 * share else np.arange(share)
+    shared = int(k.shape[0]) if seed % 2 else 0
+    case(f"decode attention sweep seed {seed}: {kind}, G={G}, Hkv={Hkv}, B={B}, "
+         f"max len {int(lens.max())}, shared_pages {shared}")
+    lt = torch.from_numpy(lens.astype(np.int32)).to(DEV)
+    tt = torch.from_numpy(table).to(DEV)
+    if kind == "fp8":
+        kc, ks, vc, vs = quantize(k, v)
+        f8 = torch.float8_e4m3fn
+        got = A.attn_decode_fp8(q.to(DEV), kc.view(f8).to(DEV), vc.view(f8).to(DEV), ks.to(DEV),
+                                vs.to(DEV), lt, tt, shared_pages=shared)
+        want = att.decode_attention(q[:, 0].float().numpy(), kc.numpy(), vc.numpy(), lens, table,
+                                    256 ** -0.5, ks.numpy(), vs.numpy(), stats=True)
+        tol = {}
+    else:
+        dt = torch.bfloat16 if kind == "bf16" else torch.float16
+        q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        got = A.attn_decode(q.to(DEV), k.to(DEV), v.to(DEV), lt, tt, shared_pages=shared)
+        want = att.decode_attention(q[:, 0].float().numpy(), k.float().numpy(),
+                                    v.float().numpy(), lens, table, 256 ** -0.5, stats=True)
+        tol = F16 if kind == "f16" else {}
+    torch.cuda.synchronize()
+    A.check_errors(DEV)
+    within_one_ulp(got[:, 0], want, **tol)
