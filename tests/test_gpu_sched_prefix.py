@@ -10,12 +10,15 @@ import pytest
 import torch
 
 from muserve_amd.block_manager import BlockManager
+from muserve_amd.kernels import attention as A
 from muserve_amd.kv_cache import PagedKVCache
 from muserve_amd.scheduler import ContinuousBatchScheduler, InferenceRequest
+from oracle import attention as oatt
 from oracle import paged as pg
 from oracle import sched as S
 from oracle.blocks import BlockManagerModel
 from tests.gpu_util import DEV, case
+from tests.test_gpu_attention import within_one_ulp
 from tests.test_gpu_sched import check_plan
 
 pytestmark = pytest.mark.gpu
@@ -112,7 +115,10 @@ def test_prefix_pages_hold_every_sequence_kv():
     """Serving steps with prefix reuse writing real K/V: after every step's
     append, every entry's sequence gathered through its block table (shared
     cached pages, its own tail and decode pages) equals the K/V of its own
-    tokens at their positions, bit for bit."""
+    tokens at their positions, bit for bit; and the step's decode attention
+    over those tables, with the block manager's pages as shared_pages (read
+    through the caches, the sequences' spans sorted by first page), is within
+    the oracle's tolerance."""
     case("prefix-reuse scheduler drives appends; every sequence gathered back each step")
     rng = np.random.default_rng(7)
     batch, max_seq, chunk, bm_pages, private = 6, 512, 96, 64, 64
@@ -127,7 +133,7 @@ def test_prefix_pages_hold_every_sequence_kv():
             for i, p in enumerate(prompts)]
     for r in reqs:
         s.add_request(r)
-    checked = 0
+    checked = attn_checked = 0
     for step in range(5000):
         plan = s.plan_step()
         if plan is None:
@@ -156,7 +162,22 @@ def test_prefix_pages_hold_every_sequence_kv():
         assert torch.equal(vg.cpu().view(torch.int16),
                            _kv(want_ids, want_pos, 0.07).view(torch.int16)), f"step {step}"
         checked += len(lens)
+        nd = plan.num_decode
+        if nd:
+            q = torch.from_numpy(rng.standard_normal((nd, 1, 4, 256)).astype(np.float32))
+            q = q.bfloat16().to(DEV)
+            kc, vc = cache.get_kv_by_layer(0)
+            out = A.attn_decode(q, kc, vc, plan.seq_lens[:nd], plan.block_tables[:nd],
+                                shared_pages=bm.num_pages)
+            torch.cuda.synchronize()
+            A.check_errors(DEV)
+            want = oatt.decode_attention(q[:, 0].float().cpu().numpy(),
+                                         kc.float().cpu().numpy(), vc.float().cpu().numpy(),
+                                         lens[:nd], plan.block_tables[:nd].cpu().numpy(),
+                                         256 ** -0.5, stats=True)
+            within_one_ulp(out[:, 0], want)
+            attn_checked += 1
         s.complete_step(plan, rng.integers(0, 64, plan.num_entries).tolist())
     s.check_errors()
     cache.check_errors()
-    assert s.is_idle and s.prefix_skipped > 0 and checked > 100
+    assert s.is_idle and s.prefix_skipped > 0 and checked > 100 and attn_checked > 20
