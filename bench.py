@@ -1937,6 +1937,121 @@ def run_calibration(reps: int = 5, nbytes: int = 1 << 30) -> dict:
             "bytes_written": nbytes, "launches": reps}
 
 
+def run_ceilings(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Access-pattern ceilings: the probe kernels (mkv_probe_*) and torch's own
+    copies move the bytes of the product kernels in the same placement and do
+    nothing else; each is timed with HIP events over `steps` launches after
+    `warmup`. The product kernels' own rates come from their workloads."""
+    from muserve_amd import _lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = _lib.stream_of(dev)
+    sink = torch.zeros(16384, dtype=torch.uint8, device=dev)
+    out: list[dict] = []
+
+    def timed(fn) -> float:  # mean us per call
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    def record(probe: str, pattern: str, nbytes: int, us: float, **extra) -> None:
+        gbs = nbytes / us / 1e3
+        out.append({"probe": probe, "pattern": pattern, "bytes_per_launch": int(nbytes),
+                    "mean_launch_us": round(us, 2), "GBps": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), **extra})
+        log(f"{probe} [{pattern}]: {us:.1f} us, {gbs:.0f} GB/s")
+
+    # decode attention and the gather's data tiles: the K and V planes of one
+    # layer's pages of the 256 lognormal sequences, every page once, shuffled
+    ctx = context_lengths()
+    npg = int(np.sum(-(-ctx // 16)))
+    perm = torch.randperm(npg, generator=torch.Generator().manual_seed(SEED))
+    perm_d = perm.to(torch.int32).to(dev)
+    for pb, pool in ((8192, "bf16"), (4096, "fp8")):
+        kp = torch.empty(npg * pb, dtype=torch.uint8, device=dev)
+        vp = torch.empty_like(kp)
+        for walk, nt, shape in ((0, 1, "a workgroup per page, non-temporal loads"),
+                                (1, 0, "a wave per page, resident grid, cached loads"),
+                                (1, 1, "a wave per page, resident grid, non-temporal loads")):
+            us = timed(lambda: _lib.call("mkv_probe_read_pages", kp.data_ptr(), vp.data_ptr(), pb,
+                                         npg, perm_d.data_ptr(), npg, walk, nt, sink.data_ptr(), sp))
+            record("mkv_probe_read_pages", f"{pool} pages ({pb} B K + {pb} B V), {npg} pages "
+                   f"shuffled, loads only: {shape}", 2 * npg * pb, us)
+        if pb == 8192:
+            # torch's copies of the same bytes (read and written): random pages
+            # gathered (index_select) and a contiguous copy
+            kp2, vp2 = kp.view(npg, pb), vp.view(npg, pb)
+            ko, vo = torch.empty_like(kp2), torch.empty_like(vp2)
+            idx = perm.to(dev)
+
+            def isel():
+                torch.index_select(kp2, 0, idx, out=ko)
+                torch.index_select(vp2, 0, idx, out=vo)
+
+            record("torch.index_select", f"{npg} shuffled 8 KiB pages of K and V gathered "
+                   "to contiguous rows", 4 * npg * pb, timed(isel))
+
+            def cpy():
+                ko.copy_(kp2)
+                vo.copy_(vp2)
+
+            record("torch.Tensor.copy_", f"the same {2 * npg * pb} bytes, contiguous",
+                   4 * npg * pb, timed(cpy))
+            del ko, vo
+        del kp, vp
+        torch.cuda.empty_cache()
+
+    # fp8 append: a 2048-token chunk of 32 requests (4096 pages) into a
+    # 262,160-page pool, 15 layers per launch and one, shuffled or
+    # consecutive pages; bf16 rows in (8 KiB a page), 4 KiB page rows out
+    R, CHUNK, CTX = 32, 2048, 131072
+    dpages = R * CTX // 16 + 16
+    cpages = R * CHUNK // 16
+    planes = 2 * LAYERS
+    src = torch.empty(planes, cpages * 8192, dtype=torch.uint8, device=dev)
+    dst = torch.empty(planes, dpages * 4096, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(SEED)
+    placements = {"shuffled": torch.randperm(dpages, generator=g)[:cpages],
+                  "consecutive": torch.arange(cpages) + dpages // 2}
+    for name, pg in placements.items():
+        assert int(pg.min()) >= 0 and int(pg.max()) < dpages
+        pg_d = pg.to(torch.int32).to(dev)
+        for per_launch in (planes, 2):
+            def scat():
+                for i in range(0, planes, per_launch):
+                    _lib.call("mkv_probe_scatter_pages", src[i].data_ptr(), src.stride(0),
+                              dst[i].data_ptr(), dst.stride(0), dpages, pg_d.data_ptr(), cpages,
+                              per_launch, sp)
+
+            us = timed(scat)
+            record("mkv_probe_scatter_pages", f"{cpages} pages {name}, {per_launch // 2} "
+                   f"layer(s) per launch", planes * cpages * (8192 + 4096), us,
+                   us_per_layer=round(us / LAYERS, 2))
+    del src, dst
+    torch.cuda.empty_cache()
+
+    # the padded gather's zero tiles: a 6 GiB streaming fill
+    fill = torch.empty(6 << 30, dtype=torch.uint8, device=dev)
+    record("mkv_probe_fill", "16-byte device-scope non-temporal stores, 6 GiB",
+           fill.numel(), timed(lambda: _lib.call("mkv_probe_fill", fill.data_ptr(),
+                                                 fill.numel(), sp)))
+    del fill
+    torch.cuda.empty_cache()
+    return {"metric": "access-pattern ceilings (probe kernels)", "value": None, "unit": "GB/s",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": True,
+            "dtype": "u8", "data": "synthetic (uninitialised planes, seeded page orders)",
+            "config": {"workload": "ceilings"}, "probes": out}
+
+
 def _summary(r: dict, keep: tuple[str, ...]) -> dict:
     """A secondary configuration's result, compacted for the headline line:
     its metric and value, the named extra keys, and per kernel the
@@ -2000,7 +2115,7 @@ def main() -> int:
                     choices=["decode", "fp8_prefill", "gdn_state", "plumbing", "prefix",
                              "decode_attn", "decode_attn_fp8", "offload", "gdn_decode",
                              "sched", "sched_fp8", "sched_hybrid", "sched_prefix",
-                             "prefill_attn"],
+                             "prefill_attn", "ceilings"],
                     help="decode (default, the headline metric) or another configuration")
     args = ap.parse_args()
     global PLACEMENT
@@ -2028,7 +2143,7 @@ def main() -> int:
                                                    serial_prefill=args.serial_prefill),
               "sched_prefix": lambda *a: run_sched(*a, prefix=True,
                                                    serial_prefill=args.serial_prefill),
-              "prefill_attn": run_prefill_attn}[args.workload]
+              "prefill_attn": run_prefill_attn, "ceilings": run_ceilings}[args.workload]
     steps, warmup = args.steps, args.warmup
     if args.workload == "fp8_prefill" and steps == 1000:
         steps, warmup = 12, 3  # 15 chunks of 2048 fit before the 8192-token window
@@ -2037,6 +2152,8 @@ def main() -> int:
     if args.workload == "offload" and steps == 1000:
         steps, warmup = 10, 2  # a step moves ~1.5 GB across the host link
     if args.workload == "prefill_attn" and (steps, warmup) == (1000, 20):
+        steps, warmup = 20, 3
+    if args.workload == "ceilings" and (steps, warmup) == (1000, 20):
         steps, warmup = 20, 3
     if args.workload.startswith("sched") and (steps, warmup) == (1000, 20):
         steps, warmup = 500, 300  # the warmup fills the 256-request batch

@@ -701,6 +701,42 @@ int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_
  */
 int mkv_check_conversions(uint64_t* counts, void* stream);
 
+/*
+ * Access-pattern probes. Each moves the bytes of one kernel above in the same
+ * placement and does nothing else, so that kernel's rate can be set against
+ * what its access pattern allows on the device at hand. None has a reference
+ * counterpart; they are measurement kernels only.
+ *
+ * mkv_probe_read_pages: reads the K and V planes (page_bytes 8192 or 4096
+ * each, page p at byte p * page_bytes of k_planes / v_planes, num_pages
+ * pages) of the n pages listed in pages[n] (int32 on the device; ids outside
+ * [0, num_pages) are skipped). walk 0: a workgroup per page; walk 1: the
+ * resident grid's waves walk the list, a wave per page, the next page's
+ * loads issued before the current one is consumed. nontemporal selects
+ * non-temporal or ordinary loads. Nothing is written; sink (16 KiB, 16-byte
+ * aligned) keeps the loads alive.
+ */
+int mkv_probe_read_pages(const void* k_planes, const void* v_planes, int32_t page_bytes,
+                         int64_t num_pages, const int32_t* pages, int64_t n, int32_t walk,
+                         int32_t nontemporal, void* sink, void* stream);
+
+/*
+ * mkv_probe_scatter_pages: for each of `planes` planes y and each listed page
+ * x < npages: reads 8 KiB of src at y * src_plane + x * 8192 and writes 4 KiB
+ * (the two 16-byte halves of every 32 bytes xor-ed) at y * dst_plane +
+ * pages[x] * 4096; ids outside [0, dst_pages) are skipped. The fp8 append's
+ * bytes (bf16 rows in, 4 KiB page rows out) without the quantisation.
+ */
+int mkv_probe_scatter_pages(const void* src, int64_t src_plane, void* dst, int64_t dst_plane,
+                            int64_t dst_pages, const int32_t* pages, int32_t npages,
+                            int32_t planes, void* stream);
+
+/*
+ * mkv_probe_fill: zeros `bytes` (a multiple of 4096) at dst with one 16-byte
+ * device-scope non-temporal store a thread, the padded gather's zero tiles.
+ */
+int mkv_probe_fill(void* dst, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -99,6 +99,9 @@ SIGNATURES: dict[str, list] = {
                                  _P, _I32, _I32, _F32, _P, _P, _I64, _P, _P],
     "mkv_decode_attention_contig": [_P, _P, _P, _I32, _I32, _I32, _I32, _I64, _P, _I32, _I32, _F32,
                                     _P, _P, _I64, _P, _P],
+    "mkv_probe_read_pages": [_P, _P, _I32, _I64, _P, _I64, _I32, _I32, _P, _P],
+    "mkv_probe_scatter_pages": [_P, _I64, _P, _I64, _I64, _P, _I32, _I32, _P],
+    "mkv_probe_fill": [_P, _I64, _P],
 }
 _INT64_RESULT = {"mkv_bm_state_bytes", "mkv_decode_attention_workspace_bytes",
                  "mkv_prefill_attention_workspace_bytes"}

@@ -72,6 +72,17 @@ def test_empty_calls_are_no_ops():
     assert _rc("mkv_copy_blocks", None, 0, 2, 4, 8192, None, None, 0, None, None)[0] == 0
 
 
+def test_probe_arguments():
+    rc, msg = _rc("mkv_probe_read_pages", FAKE, FAKE, 1000, 4, FAKE, 4, 0, 1, FAKE, None)
+    assert rc == -3 and "page_bytes must be 4096 or 8192" in msg
+    rc, msg = _rc("mkv_probe_scatter_pages", FAKE, 8192, FAKE, 4096, 1, FAKE, 2, 1, None)
+    assert rc == -1 and "shorter than its pages" in msg
+    rc, msg = _rc("mkv_probe_fill", FAKE, 100, None)
+    assert rc == -1 and "multiple of 4096" in msg
+    assert _rc("mkv_probe_read_pages", None, None, 8192, 0, None, 0, 1, 0, None, None)[0] == 0
+    assert _rc("mkv_probe_fill", None, 0, None)[0] == 0
+
+
 def test_call_raises_with_message():
     with pytest.raises(_lib.MkvError, match="token_bytes 3"):
         _lib.call("mkv_block_hash_sha256", FAKE, FAKE, FAKE, 1, 3, FAKE, FAKE, None)
