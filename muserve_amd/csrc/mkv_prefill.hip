@@ -367,11 +367,15 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   }
 }
 
-// Combines the key ranges of one (query token, query head): one workgroup of
-// 256 threads (a dim each) per query t < max_seqlen_q of sequence b (grid.y)
-// and head (grid.z). It writes exactly the rows the attention kernel wrote
-// ranges for: the same query offsets and bounds decide, so rows of `out`
-// outside every sequence's queries are left alone, as with one range.
+// Combines the key ranges of one query token's KV head: one workgroup of 256
+// threads per query t < max_seqlen_q of sequence b (grid.y) and KV head
+// (grid.z); its four waves take the head's four query heads, a lane four
+// dims (16-byte loads of the fp32 partial rows). It writes exactly the rows
+// the attention kernel wrote ranges for: the same query offsets and bounds
+// decide, so rows of `out` outside every sequence's queries are left alone,
+// as with one range. Each output element is summed over the ranges in range
+// order, as a thread per element did (one workgroup per query head was 4x
+// the workgroups for the same bytes).
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const int32_t b = blockIdx.y;
   const int32_t qs = a.cu_q[b];
@@ -380,19 +384,27 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const int32_t nq = q_ok ? (nq_raw < a.max_q ? nq_raw : a.max_q) : 0;
   const int32_t t = blockIdx.x;
   if (t >= nq) return;
-  const int64_t row = ((int64_t)qs + t) * ((int64_t)a.hkv * kPG) + blockIdx.z;
-  const int d = threadIdx.x;
+  const int64_t row = ((int64_t)qs + t) * ((int64_t)a.hkv * kPG) +
+                      (int64_t)blockIdx.z * kPG + (threadIdx.x >> 6);
+  const int d = (threadIdx.x & 63) * 4;
   const int64_t at0 = row * a.splits;
   float M = -INFINITY;
   for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, a.ml[(at0 + sp) * 2]);
-  float O = 0.f, L = 0.f;
+  float O[4] = {0.f, 0.f, 0.f, 0.f}, L = 0.f;
   for (int sp = 0; sp < a.splits; ++sp) {
     const float m = a.ml[(at0 + sp) * 2];
     const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-    O += f * a.part[(at0 + sp) * kPD + d];
+    const f32x4 p = *reinterpret_cast<const f32x4*>(a.part + (at0 + sp) * kPD + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) O[e] += f * p[e];
     L += f * a.ml[(at0 + sp) * 2 + 1];
   }
-  reinterpret_cast<uint16_t*>(a.out + row * kPRow)[d] = bf16_bits(L > 0.f ? O / L : 0.f);
+  uint32_t w[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    w[e] = (uint32_t)bf16_bits(L > 0.f ? O[2 * e] / L : 0.f) |
+           ((uint32_t)bf16_bits(L > 0.f ? O[2 * e + 1] / L : 0.f) << 16);
+  *reinterpret_cast<uint2*>(a.out + row * kPRow + d * 2) = uint2{w[0], w[1]};
 }
 
 }  // namespace
@@ -443,6 +455,8 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
               MKV_E_INVALID, "mkv_prefill_attention_bf16: null pointer");
   MKV_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), MKV_E_ALIGN,
               "mkv_prefill_attention_bf16: q, k, v and out must be 16-byte aligned");
+  MKV_REQUIRE(splits <= 1 || aligned16(workspace), MKV_E_ALIGN,
+              "mkv_prefill_attention_bf16: the workspace must be 16-byte aligned");
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
   a.k = static_cast<const uint8_t*>(k);
@@ -470,7 +484,7 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
   hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kPThreads), 0, as_stream(stream), a);
   if (splits > 1 && num_q_tokens > 0)
     hipLaunchKernelGGL(prefill_merge_kernel,
-                       dim3((unsigned)max_seqlen_q, (unsigned)batch, (unsigned)num_q_heads),
+                       dim3((unsigned)max_seqlen_q, (unsigned)batch, (unsigned)num_kv_heads),
                        dim3(256), 0, as_stream(stream), a);
   return check_launch("mkv_prefill_attention_bf16");
 }
