@@ -682,7 +682,8 @@ int mkv_prefill_attention_bf16(const void* q, const void* k, const void* v, int6
  * last key) that separate workgroups attend to, and a second kernel merges
  * their (max, sum, output) per query row and head, writing only the rows of
  * the sequences' queries. That fills the GPU when a step has few, short
- * chunks. No reference counterpart.
+ * chunks. With splits > 1 the workspace must be 16-byte aligned and hold
+ * these bytes (MKV_E_INVALID otherwise). No reference counterpart.
  */
 int64_t mkv_prefill_attention_workspace_bytes(int64_t num_q_tokens, int32_t num_q_heads,
                                               int32_t splits);

@@ -448,15 +448,14 @@ extern "C" int mkv_prefill_attention_bf16(const void* q, const void* k, const vo
   if (batch == 0 || max_seqlen_q == 0) return MKV_OK;
   const int64_t need = mkv_prefill_attention_workspace_bytes(num_q_tokens, num_q_heads, splits);
   MKV_REQUIRE(splits == 1 || (workspace && workspace_bytes >= need && aligned16(workspace)),
-              MKV_E_INVALID, "mkv_prefill_attention_bf16: workspace of %lld bytes required",
+              MKV_E_INVALID,
+              "mkv_prefill_attention_bf16: workspace of %lld bytes (16-byte aligned) required",
               (long long)need);
   MKV_REQUIRE(q && k && v && cu_seqlens_q && out && err &&
                   (page_table ? seq_lens_k != nullptr : cu_seqlens_k != nullptr),
               MKV_E_INVALID, "mkv_prefill_attention_bf16: null pointer");
   MKV_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), MKV_E_ALIGN,
               "mkv_prefill_attention_bf16: q, k, v and out must be 16-byte aligned");
-  MKV_REQUIRE(splits <= 1 || aligned16(workspace), MKV_E_ALIGN,
-              "mkv_prefill_attention_bf16: the workspace must be 16-byte aligned");
   PrefillArgs a;
   a.q = static_cast<const uint8_t*>(q);
   a.k = static_cast<const uint8_t*>(k);
