@@ -2076,8 +2076,9 @@ def _summary(r: dict, keep: tuple[str, ...]) -> dict:
 def run_secondary() -> dict:
     """The other configurations, after the headline (each on a fresh pool,
     with its default sizes): fp8 chunked prefill, GDN state slots in model
-    order (and MALL-cold), the prefix cache, and paged decode attention over
-    bf16 and fp8 pools at the headline's shape."""
+    order (and MALL-cold), the prefix cache, paged decode attention over
+    bf16 and fp8 pools at the headline's shape, and the continuous-batching
+    serving step driven by the scheduler's step plan."""
     out = {}
     for name, fn, steps, warmup, keep in (
             ("fp8_prefill", run_fp8_prefill, 12, 3, ("pct_of_hbm_peak", "appended_tokens_per_s")),
@@ -2086,7 +2087,9 @@ def run_secondary() -> dict:
                                           "page_hit_rate", "cow_copies")),
             ("decode_attn", run_decode_attn, 200, 10, ("pct_of_hbm_peak", "tokens_per_s")),
             ("decode_attn_fp8", lambda st, wu, cpu: run_decode_attn(st, wu, cpu, fp8=True), 200,
-             10, ("pct_of_hbm_peak", "tokens_per_s"))):
+             10, ("pct_of_hbm_peak", "tokens_per_s")),
+            ("sched", run_sched, 500, 300, ("tokens_per_s", "attn_us_per_layer",
+                                            "prefill_attn_us_per_layer"))):
         gc.collect()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
