@@ -880,47 +880,100 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
 }
 
 // Merges the pieces of one (pair, query head) of a pair cut by span
-// boundaries, and writes the zeros of an empty pair: the pieces' maximum by
-// a block reduction, then a thread per dim sums the rescaled partial rows.
+// boundaries, and writes the zeros of an empty pair. The pieces are dealt to
+// the four waves (piece i to wave i % 4); a wave keeps a running (max, sum,
+// output) over its pieces, four dims a lane, and the waves' results are
+// combined through LDS, a thread per dim. A wave reads its pieces in batches
+// of kMergeBatch with every load of a batch issued before the first is used:
+// its (max, sum) pairs by one load (lane u reads the batch's piece u),
+// broadcast from lanes 0..7, and one 16-byte load a lane per piece. An index
+// past the last piece re-reads the last one and adds 0 x -0 (x + -0 is x for
+// every x). The longest pairs (40-odd pieces at batch 256) take two batches
+// per wave; a thread per dim walking all of a pair's pieces waited on six.
+constexpr int kMergeBatch = 8;
+
 template <int G, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
-  __shared__ float red[kAttnWaves];
+  __shared__ __attribute__((aligned(16))) float wave_o[kAttnWaves][kHeadDim];
+  __shared__ float wave_ml[kAttnWaves][2];
   const int64_t pr = blockIdx.x / G;
   const int h = blockIdx.x % G;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t p0 = ld_const(a.pre + pr), p1 = ld_const(a.pend + pr);
+  // the span is loaded with the pair's bounds (the empty asm keeps the
+  // compiler from moving its load behind the branch below)
+  const int64_t span = ld_const(a.hdr);
+  const int32_t p0 = ld_const(a.pre + pr), p1 = ld_const(a.pend + pr);
+  asm volatile("" ::"s"(span));
   uint8_t* out = a.out + (pr * G + h) * kRowBytes;
   if (p1 <= p0) {  // nothing to attend to: zeros
     reinterpret_cast<uint16_t*>(out)[tid] = 0;
     return;
   }
-  const int64_t S = ld_const(a.hdr);
-  const int64_t w0 = p0 / S, w1 = (p1 - 1) / S;
+  // flat page indices are int32, and the span is at most the launch's pages
+  const uint32_t S = (uint32_t)span;
+  const uint32_t w0 = (uint32_t)p0 / S, w1 = (uint32_t)(p1 - 1) / S;
   if (w0 == w1) return;  // written by its wave
-  const int64_t n_seg = w1 - w0 + 1;
+  const int n_seg = (int)(w1 - w0 + 1);
   // piece i: wave w0 + i, slot 1 for the first piece unless the pair starts
   // its span (then it is that span's first pair), slot 0 for the rest
-  auto at_of = [&](int64_t i) {
-    const int64_t w = w0 + i;
-    const int slot = (i == 0 && p0 != w0 * S) ? 1 : 0;
+  auto at_of = [&](int i) __attribute__((always_inline)) {
+    const int64_t w = (int64_t)w0 + i;
+    const int slot = (i == 0 && (uint32_t)p0 != w0 * S) ? 1 : 0;
     return (w * 2 + slot) * G + h;
   };
-  float M = -INFINITY;
-  for (int64_t i = tid; i < n_seg; i += kAttnThreads) M = fmaxf(M, a.ml[at_of(i) * 2]);
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o_run = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i0 = wave; i0 < n_seg; i0 += kAttnWaves * kMergeBatch) {
+    const int mine = i0 + kAttnWaves * (lane & (kMergeBatch - 1));
+    const float2 ml =
+        *reinterpret_cast<const float2*>(a.ml + at_of(mine < n_seg ? mine : n_seg - 1) * 2);
+    f32x4 p[kMergeBatch];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-  if (lane == 0) red[wave] = M;
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int i = i0 + kAttnWaves * u;
+      p[u] = *reinterpret_cast<const f32x4*>(a.part + at_of(i < n_seg ? i : n_seg - 1) * kHeadDim +
+                                             4 * lane);
+    }
+    float m[kMergeBatch], l[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      m[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ml.x), u));
+      l[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ml.y), u));
+    }
+    float mb = m_run;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+      mb = fmaxf(mb, i0 + kAttnWaves * u < n_seg ? m[u] : -INFINITY);
+    // mb >= m_run; a wave's first batch starts from nothing
+    const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - mb);
+    l_run *= alpha;
+    o_run *= alpha;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const bool ok = i0 + kAttnWaves * u < n_seg;
+      const float f = !ok || m[u] == -INFINITY ? 0.f : exp2_fast(m[u] - mb);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o_run[e] += f * (ok ? p[u][e] : -0.f);
+      l_run += f * (ok ? l[u] : -0.f);
+    }
+    m_run = mb;
+  }
+  *reinterpret_cast<f32x4*>(&wave_o[wave][4 * lane]) = o_run;
+  if (lane == 0) {
+    wave_ml[wave][0] = m_run;
+    wave_ml[wave][1] = l_run;
+  }
   __syncthreads();
+  float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, red[w]);
+  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wave_ml[w][0]);
   float O = 0.f, L = 0.f;
-#pragma unroll 8
-  for (int64_t i = 0; i < n_seg; ++i) {
-    const int64_t at = at_of(i);
-    const float m = ld_const(a.ml + at * 2);
-    const float f = m == -INFINITY ? 0.f : exp2_fast(m - M);
-    O += f * a.part[at * kHeadDim + tid];
-    L += f * ld_const(a.ml + at * 2 + 1);
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) {
+    const float mw = wave_ml[w][0];
+    const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
+    O += f * wave_o[w][tid];
+    L += f * wave_ml[w][1];
   }
   reinterpret_cast<uint16_t*>(out)[tid] = out_bits<F16>(L > 0.f ? O / L : 0.f);
 }
