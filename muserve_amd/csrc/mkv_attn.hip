@@ -880,17 +880,50 @@ __global__ __launch_bounds__(kAttnThreads, G == 8 ? 1 : 2) void attn_span_kernel
 }
 
 // Merges the pieces of one (pair, query head) of a pair cut by span
-// boundaries, and writes the zeros of an empty pair. The pieces are dealt to
-// the four waves (piece i to wave i % 4); a wave keeps a running (max, sum,
-// output) over its pieces, four dims a lane, and the waves' results are
-// combined through LDS, a thread per dim. A wave reads its pieces in batches
-// of kMergeBatch with every load of a batch issued before the first is used:
-// its (max, sum) pairs by one load (lane u reads the batch's piece u),
-// broadcast from lanes 0..7, and one 16-byte load a lane per piece. An index
-// past the last piece re-reads the last one and adds 0 x -0 (x + -0 is x for
-// every x). The longest pairs (40-odd pieces at batch 256) take two batches
-// per wave; a thread per dim walking all of a pair's pieces waited on six.
-constexpr int kMergeBatch = 8;
+// boundaries, and writes the zeros of an empty pair. Every load of a batch
+// of pieces is issued before the first is used (a loop with a remainder
+// issued its last n % 8 loads a round trip apiece):
+// - at most kMergeExact pieces (most cut pairs): a thread per dim, exactly
+//   n pieces in one batch;
+// - more (the longest pairs, 43 pieces at batch 256, which set the launch's
+//   time): the pieces are dealt to the four waves (piece i to wave i % 4); a
+//   wave keeps a running (max, sum, output) over batches of kMergeBatch, four
+//   dims a lane, its (max, sum) pairs by one load broadcast by v_readlane,
+//   and the waves' results are combined through LDS, a thread per dim. An
+//   index past the last piece re-reads the last one and adds 0 x -0 (x + -0
+//   is x for every x).
+// The kernel stays at 44 VGPRs: the merge runs beside the prefill attention
+// in the serving step, and forms of 52-76 VGPRs (more pieces a batch, the
+// wave index not uniform) made the prefix-reuse serving step 1.7-2.6 %
+// slower while their merges were faster.
+constexpr int kMergeBatch = 4;   // pieces a wave loads at once (more pieces)
+constexpr int kMergeExact = 16;  // pieces merged by one thread per dim in one batch
+
+// The merge of a pair with exactly N pieces, a thread per dim: every load is
+// issued before the first is used, the maximum is the pieces', and the sums
+// run in piece order. Returns this thread's output value.
+template <int N, typename AtOf>
+__device__ __forceinline__ float merge_exact(const AttnArgs& a, AtOf at_of, int tid) {
+  float m[N], l[N], p[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int64_t at = at_of(u);
+    m[u] = ld_const(a.ml + at * 2);
+    l[u] = ld_const(a.ml + at * 2 + 1);
+    p[u] = a.part[at * kHeadDim + tid];
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < N; ++u) M = fmaxf(M, m[u]);
+  float O = 0.f, L = 0.f;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float f = m[u] == -INFINITY ? 0.f : exp2_fast(m[u] - M);
+    O += f * p[u];
+    L += f * l[u];
+  }
+  return L > 0.f ? O / L : 0.f;
+}
 
 template <int G, bool F16>
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
@@ -898,7 +931,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
   __shared__ float wave_ml[kAttnWaves][2];
   const int64_t pr = blockIdx.x / G;
   const int h = blockIdx.x % G;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: piece addresses in SGPRs
   // the span is loaded with the pair's bounds (the empty asm keeps the
   // compiler from moving its load behind the branch below)
   const int64_t span = ld_const(a.hdr);
@@ -921,6 +955,28 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(AttnArgs a) {
     const int slot = (i == 0 && (uint32_t)p0 != w0 * S) ? 1 : 0;
     return (w * 2 + slot) * G + h;
   };
+  if (n_seg <= kMergeExact) {  // most cut pairs: one round trip, no duplicate loads
+    float r;
+    switch (n_seg) {
+      case 2: r = merge_exact<2>(a, at_of, tid); break;
+      case 3: r = merge_exact<3>(a, at_of, tid); break;
+      case 4: r = merge_exact<4>(a, at_of, tid); break;
+      case 5: r = merge_exact<5>(a, at_of, tid); break;
+      case 6: r = merge_exact<6>(a, at_of, tid); break;
+      case 7: r = merge_exact<7>(a, at_of, tid); break;
+      case 8: r = merge_exact<8>(a, at_of, tid); break;
+      case 9: r = merge_exact<9>(a, at_of, tid); break;
+      case 10: r = merge_exact<10>(a, at_of, tid); break;
+      case 11: r = merge_exact<11>(a, at_of, tid); break;
+      case 12: r = merge_exact<12>(a, at_of, tid); break;
+      case 13: r = merge_exact<13>(a, at_of, tid); break;
+      case 14: r = merge_exact<14>(a, at_of, tid); break;
+      case 15: r = merge_exact<15>(a, at_of, tid); break;
+      default: r = merge_exact<16>(a, at_of, tid); break;
+    }
+    reinterpret_cast<uint16_t*>(out)[tid] = out_bits<F16>(r);
+    return;
+  }
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 o_run = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int i0 = wave; i0 < n_seg; i0 += kAttnWaves * kMergeBatch) {
