@@ -709,7 +709,8 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool, fused_conv: bool = Fa
     move_bytes = 2 * B * entry + 4 * B  # one gather or one scatter launch
     # in-place conv: the slot read and written, x in, out, the weights, the slots
     conv_bytes = 2 * B * C * 4 * 2 + 2 * B * C * 2 + C * 4 * 2 + 4 * B
-    ratios = counter_ratios("gdn_state_hbm_counters.md")
+    ratios = counter_ratios("gdn_decode_hbm_counters.md" if fused_conv else
+                            "gdn_state_hbm_counters.md")
     g_ms, s_ms, u_ms = _timed(recs, "gather"), _timed(recs, "scatter"), _timed(recs, "update")
     state_s = G * (g_ms + s_ms) / 1e3
     step_s = elapsed / steps
@@ -718,9 +719,11 @@ def run_gdn_state(steps: int, warmup: int, with_cpu: bool, fused_conv: bool = Fa
         _kernel_roofline("gdn_decode_gather_kernel<4> (mkv_gdn_decode_gather)" if fused_conv
                          else "state_move_kernel<true> (mkv_state_gather)",
                          move_bytes + (conv_bytes if fused_conv else 0), g_ms,
-                         None if fused_conv else ratios.get("state_move_kernel<true>")),
+                         ratios.get("gdn_decode_gather_kernel<4>" if fused_conv
+                                    else "state_move_kernel<true>")),
         _kernel_roofline("state_move_kernel<false> (mkv_state_scatter)", move_bytes, s_ms,
-                         None if fused_conv else ratios.get("state_move_kernel<false>"))]
+                         ratios.get("state_move_kernel<false> fused" if fused_conv
+                                    else "state_move_kernel<false>"))]
     res = {
         "metric": ("achieved HBM GB/s (% of 8 TB/s) for GDN decode-step state traffic: "
                    "recurrent slot gather+scatter, conv in place" if fused_conv else
