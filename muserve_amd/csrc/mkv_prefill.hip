@@ -375,7 +375,32 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
 // decide, so rows of `out` outside every sequence's queries are left alone,
 // as with one range. Each output element is summed over the ranges in range
 // order, as a thread per element did (one workgroup per query head was 4x
-// the workgroups for the same bytes).
+// the workgroups for the same bytes). Up to 8 ranges, every load
+// is issued before the first is used (a loop over the ranges waited a round
+// trip per range, twice); loads of ranges past the count are not issued, so
+// the bytes read are the ranges' own.
+template <int N>
+__device__ __forceinline__ void merge_ranges(const float2* ml, const float* part, float& L,
+                                             float (&O)[4]) {
+  float2 x[N];
+  f32x4 p[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    x[u] = ml[u];
+    p[u] = *reinterpret_cast<const f32x4*>(part + (int64_t)u * kPD);
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < N; ++u) M = fmaxf(M, x[u].x);
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float f = x[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(x[u].x - M);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) O[e] += f * p[u][e];
+    L += f * x[u].y;
+  }
+}
+
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const int32_t b = blockIdx.y;
   const int32_t qs = a.cu_q[b];
@@ -388,16 +413,29 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
                       (int64_t)blockIdx.z * kPG + (threadIdx.x >> 6);
   const int d = (threadIdx.x & 63) * 4;
   const int64_t at0 = row * a.splits;
-  float M = -INFINITY;
-  for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, a.ml[(at0 + sp) * 2]);
   float O[4] = {0.f, 0.f, 0.f, 0.f}, L = 0.f;
-  for (int sp = 0; sp < a.splits; ++sp) {
-    const float m = a.ml[(at0 + sp) * 2];
-    const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
-    const f32x4 p = *reinterpret_cast<const f32x4*>(a.part + (at0 + sp) * kPD + d);
+  const float2* ml = reinterpret_cast<const float2*>(a.ml) + at0;
+  const float* part = a.part + at0 * kPD + d;
+  switch (a.splits) {
+    case 2: merge_ranges<2>(ml, part, L, O); break;
+    case 3: merge_ranges<3>(ml, part, L, O); break;
+    case 4: merge_ranges<4>(ml, part, L, O); break;
+    case 5: merge_ranges<5>(ml, part, L, O); break;
+    case 6: merge_ranges<6>(ml, part, L, O); break;
+    case 7: merge_ranges<7>(ml, part, L, O); break;
+    case 8: merge_ranges<8>(ml, part, L, O); break;
+    default: {  // more than 8 ranges
+      float M = -INFINITY;
+      for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, a.ml[(at0 + sp) * 2]);
+      for (int sp = 0; sp < a.splits; ++sp) {
+        const float m = a.ml[(at0 + sp) * 2];
+        const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        const f32x4 p = *reinterpret_cast<const f32x4*>(a.part + (at0 + sp) * kPD + d);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) O[e] += f * p[e];
-    L += f * a.ml[(at0 + sp) * 2 + 1];
+        for (int e = 0; e < 4; ++e) O[e] += f * p[e];
+        L += f * a.ml[(at0 + sp) * 2 + 1];
+      }
+    }
   }
   uint32_t w[2];
 #pragma unroll
