@@ -101,9 +101,11 @@ __device__ __forceinline__ u32x4 quantise_row(const u32x4 r0, const u32x4 r1, fl
 }
 
 // One 16-lane group per (token, head) row of one (layer, K|V): grid.x covers
-// the rows, grid.y is layer * 2 + K|V. The slot and both source loads are
-// issued together; a group whose row is past the end exits as a whole, so the
-// shuffles only ever read lanes of the same live row. Source rows are read
+// the rows, grid.y is layer * 2 + K|V. The source loads do not depend on the
+// slot, but the compiler issues them after the slot check; issuing them with
+// the slot's load (pinned by an empty asm) measured no faster, the workgroups
+// in flight hiding the second round trip. A group whose row is past the end
+// exits as a whole, so the shuffles only ever read lanes of the same live row. Source rows are read
 // once and pool rows are not read back this step: non-temporal loads and code
 // stores, 6 % faster than ordinary ones on the chunked-prefill shape. The
 // scales take ordinary stores, 1.3 % faster there than non-temporal ones (a

@@ -65,16 +65,30 @@ __device__ __forceinline__ void move_piece(const StateArgs& a, uint32_t bx) {
   pool += plane * a.plane_stride;
   dense += plane * a.n * bytes;
   for (int64_t b = blockIdx.y; b < a.n; b += gridDim.y) {
-    const int32_t slot = a.slots[b];
+    const int32_t slot = ld_const(a.slots + b);
+    uint8_t* row = dense + b * bytes + base;
+    u32x4 v[kUnroll];
+    if (!GATHER && full) {
+      // scatter: the dense row does not depend on the slot, so it is loaded
+      // with the slot's (scalar) load; the empty asm keeps the compiler from
+      // moving these loads behind the slot check: one round trip, not two
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) v[u] = ld_nt(row + (u * kThreads + threadIdx.x) * 16);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) asm volatile("" : "+v"(v[u]));
+    }
     const bool ok = slot >= 0 && slot < a.pool_slots;
     if (!ok && threadIdx.x == 0 && piece == 0 && !second && plane == 0)
       raise_err(a.err, MKV_DEVERR_STATE_SLOT);
     if (!ok && !GATHER) continue;  // scatter: nothing to write for a bad slot
     uint8_t* entry = const_cast<uint8_t*>(pool) + (ok ? (int64_t)slot * bytes : 0) + base;
-    uint8_t* row = dense + b * bytes + base;
     const uint8_t* src = GATHER ? entry : row;
     uint8_t* dst = GATHER ? row : entry;
-    u32x4 v[kUnroll];
+    if (!GATHER && full) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) store<GATHER>(dst, (u * kThreads + threadIdx.x) * 16, v[u]);
+      continue;
+    }
     if (full && ok) {  // straight-line: every load issued before any store
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = ld_nt(src + (u * kThreads + threadIdx.x) * 16);
