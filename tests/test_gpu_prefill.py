@@ -203,7 +203,21 @@ def test_forced_key_splits_through_the_c_abi(split_len):
     the split chosen by the caller of the C ABI."""
     lens = [1, 63, 64, 65, 128, 129, 200, 383]
     case(f"mkv_prefill_attention_bf16 forced split_len {split_len}, lens {lens}")
-    g, cu = seqs(lens, 38 + split_len)
+    _forced_splits(lens, split_len, 38 + split_len)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4, 5, 6, 7, 8, 9])
+def test_every_merged_range_count(splits):
+    """64-key ranges, as many as `splits`: the merge reads each count from 2
+    to 8 with its own fixed number of loads and more than 8 through a loop;
+    sequences end inside, at and past the ranges' edges."""
+    lens = [1, 63, 64, 65, 64 * splits - 1, 64 * splits]
+    case(f"mkv_prefill_attention_bf16 {splits} ranges of 64 keys, lens {lens}")
+    _forced_splits(lens, 64, 60 + splits)
+
+
+def _forced_splits(lens, split_len, seed):
+    g, cu = seqs(lens, seed)
     T, max_k = int(cu[-1]), max(lens)
     q = torch.randn(T, 4, 256, generator=g).bfloat16().to(DEV)
     k = torch.randn(T, 1, 256, generator=g).bfloat16().to(DEV)
