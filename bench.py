@@ -94,8 +94,8 @@ CPU_STEPS = 3  # whole decode steps the CPU baseline times
 
 def cpu_threads() -> dict:
     """Sets torch's CPU threads to every core this process may run on (its
-    affinity set, capped by OMP_NUM_THREADS where the host sets it: a GPU box
-    gives one GPU's job a share of the host's cores) and describes them."""
+    affinity set, capped by OMP_NUM_THREADS where the host sets it: a shared
+    host gives one GPU's job a share of its cores) and describes them."""
     affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     omp = os.environ.get("OMP_NUM_THREADS", "")
     threads = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
@@ -110,7 +110,7 @@ def cpu_baseline_steps(cache, seqs, kin, vin, first: int, n_steps: int, gpu_step
     slot-mapped append and the padded gather of K and V: torch-CPU
     index_put_ / index_select, restating muserve/kv_cache.py:102-158 and the
     [B,S,H,D] layout of muserve/model/qwen35_model.py:223-249), on a copy of
-    the GPU pool taken after the timed loop, with the inputs of steps
+    the device KV pool taken after the timed loop, with the inputs of steps
     first .. first+n_steps-1. The GPU then runs the same steps (gpu_step) and
     its pool and last gather are compared with the CPU's byte for byte."""
     from oracle import paged as ref

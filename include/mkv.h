@@ -339,7 +339,7 @@ int mkv_gdn_decode_gather(const void* state_pool, int64_t state_bytes, void* sta
  * staging copy.
  * Replaces PrefixCache._to_storage / _to_device
  * (muserve/model/prefix_cache.py:36-44: tensor.cpu(), .to(device,
- * non_blocking=True)) for state kept in this build's pools, and caches KV
+ * non_blocking=True)) for state kept in the library's pools, and caches KV
  * pages, which the reference does not.
  * Requirements (otherwise MKV_E_INVALID / MKV_E_ALIGN):
  *   - pool, out/in, block_bytes and plane_stride are 16-byte aligned;

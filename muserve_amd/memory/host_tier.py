@@ -10,7 +10,7 @@ asynchronous (muserve/model/prefix_cache.py:36-44). Here:
   coalescing on free.
 * Dense tensors (the hidden state, per-layer GDN states) move by DMA
   (``copy_`` with ``non_blocking``, hipMemcpyAsync on pinned memory).
-* Blocks of this build's pools (the KV pages of a prefix, fp8 scales, a GDN
+* Blocks of the library's pools (the KV pages of a prefix, fp8 scales, a GDN
   state slot across layers) move with ``mkv_pack_blocks`` /
   ``mkv_unpack_blocks``: the kernel reads the scattered blocks from HBM and
   writes the pinned arena across the host link itself, or the reverse, with no

@@ -6,9 +6,9 @@ muserve/scheduler.py:54-123: a FIFO waiting queue, a running batch, and a
 step that decodes every running request and admits waiting requests while
 running + admitted < max_batch_size.
 
-``ChunkedSchedulerModel`` is the paged step the build drives from that
+``ChunkedSchedulerModel`` is the paged step the library drives from that
 scheduler. The reference has no chunked prefill in its scheduler, only the
-chunk size muserve/config.py:40; the policy below is this build's and is
+chunk size muserve/config.py:40; the policy below is the library's and is
 stated once here, token by token:
 
 1. Retire: FINISHED requests leave the running batch (its order), then the
